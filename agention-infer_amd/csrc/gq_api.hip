@@ -1,0 +1,376 @@
+// gq_api.hip -- the C ABI of libgq.so (declared in include/gq.h).
+//
+// Host-side runtime of the HIP backend: device selection, resident weight
+// handles (upload once, re-laid-out on the device), launch shims and the
+// synchronous Backend::matmul_dequant mirror.  Errors are negative codes
+// plus a per-thread message, mirroring GgufError::BackendError(String)
+// (src/error.rs:4-42).
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/gq.h"
+#include "gq_device.h"
+#include "gq_internal.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                \
+  do {                                                                               \
+    hipError_t e_ = (expr);                                                          \
+    if (e_ != hipSuccess)                                                            \
+      return fail(GQ_EHIP, "%s failed: %s", #expr, hipGetErrorString(e_));           \
+  } while (0)
+
+struct DeviceState {
+  bool ready = false;
+  int device = -1;
+  int num_cus = 0;
+  uint32_t *grid = nullptr;  // IQ3_XXS codebook, 256 u32 on the device
+  uint32_t grid_host[256];
+};
+
+std::mutex g_mu;
+DeviceState g_dev;
+
+// Placeholder IQ3_XXS codebook: ggml's magnitude alphabet
+// {4,12,20,28,36,44,52,62}, four magnitudes per entry chosen by a fixed
+// integer hash of the entry index.  Replaced by gq_set_iq3xxs_grid.
+void default_grid(uint32_t *g) {
+  static const uint8_t mags[8] = {4, 12, 20, 28, 36, 44, 52, 62};
+  for (uint32_t i = 0; i < 256; i++) {
+    uint32_t h = i * 0x9E3779B1u;
+    h ^= h >> 15;
+    uint32_t e = 0;
+    for (int k = 0; k < 4; k++) e |= (uint32_t)mags[(h >> (3 * k)) & 7] << (8 * k);
+    g[i] = e;
+  }
+}
+
+int init_locked(int device) {
+  if (g_dev.ready && g_dev.device == device) return GQ_OK;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0)
+    return fail(GQ_ENODEV, "no HIP device available");
+  if (device < 0 || device >= n) return fail(GQ_ENODEV, "device %d out of range (%d)", device, n);
+  HIP_TRY(hipSetDevice(device));
+  hipDeviceProp_t p;
+  HIP_TRY(hipGetDeviceProperties(&p, device));
+  if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+    return fail(GQ_ENODEV, "device %d is %s, this library is built for gfx950", device,
+                p.gcnArchName);
+  g_dev.device = device;
+  g_dev.num_cus = p.multiProcessorCount;
+  default_grid(g_dev.grid_host);
+  if (!g_dev.grid) HIP_TRY(hipMalloc(&g_dev.grid, 1024));
+  HIP_TRY(hipMemcpy(g_dev.grid, g_dev.grid_host, 1024, hipMemcpyHostToDevice));
+  g_dev.ready = true;
+  return GQ_OK;
+}
+
+int ensure_init() {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_dev.ready) return GQ_OK;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  return init_locked(dev);
+}
+
+bool supported(int t) {
+  return t == gq::T_Q8_0 || t == gq::T_Q4_K || t == gq::T_Q5_K || t == gq::T_Q6_K ||
+         t == gq::T_IQ3_XXS;
+}
+
+const char *type_name(int t) {
+  switch (t) {
+  case 0: return "F32";
+  case 1: return "F16";
+  case 8: return "Q8_0";
+  case 12: return "Q4_K";
+  case 13: return "Q5_K";
+  case 14: return "Q6_K";
+  case 18: return "IQ3_XXS";
+  case 30: return "BF16";
+  default: return "unknown";
+  }
+}
+
+int check_matvec(const gq_weight *w) {
+  if (!w) return fail(GQ_EINVAL, "null weight handle");
+  const int kpad = w->nb * gq::block_elems(w->dtype);
+  if (gq::matvec_lds_bytes(kpad) > 160 * 1024)
+    return fail(GQ_EINVAL, "in_dim %d too large for the LDS-staged matvec", w->in_dim);
+  return GQ_OK;
+}
+
+int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes, int in_dim,
+                  int out_dim, gq_weight **out) {
+  if (!out) return fail(GQ_EINVAL, "null output handle pointer");
+  *out = nullptr;
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (!supported(dtype))
+    return fail(GQ_EDTYPE, "matmul_dequant: unsupported dtype %s", type_name(dtype));
+  if (in_dim <= 0 || out_dim < 0) return fail(GQ_EINVAL, "bad shape %d x %d", out_dim, in_dim);
+  const int be = gq::block_elems(dtype);
+  const int nb = (in_dim + be - 1) / be;
+  const size_t row_bytes = (size_t)nb * gq::ggml_block_bytes(dtype);
+  const size_t need = row_bytes * (size_t)out_dim;
+  if (nbytes < need)
+    return fail(GQ_ESHORT, "%s upload: need %zu bytes, have %zu", type_name(dtype), need, nbytes);
+  if (out_dim > 0 && !src) return fail(GQ_EINVAL, "null weight data");
+
+  gq_weight *w = new gq_weight();
+  w->dtype = dtype;
+  w->in_dim = in_dim;
+  w->out_dim = out_dim;
+  w->nb = nb;
+  w->stride = (long)nb * gq::body_block_bytes(dtype);
+  w->ggml_bytes = need;
+  w->device = g_dev.device;
+  const size_t body_bytes = (size_t)w->stride * out_dim;
+  const size_t d_bytes = gq::has_d_array(dtype) ? (size_t)nb * out_dim * 2 : 0;
+  // One allocation: body, then the scale array (kept 256 B aligned).
+  const size_t d_off = (body_bytes + 255) & ~(size_t)255;
+  uint8_t *mem = nullptr;
+  if (hipMalloc(&mem, d_off + d_bytes + 256) != hipSuccess) {
+    delete w;
+    return fail(GQ_ENOMEM, "hipMalloc of %zu bytes failed", d_off + d_bytes);
+  }
+  w->body = mem;
+  w->d = d_bytes ? (uint16_t *)(mem + d_off) : nullptr;
+  hipError_t e = hipSuccess;
+  if (!gq::has_d_array(dtype)) {
+    if (need)
+      e = hipMemcpy(w->body, src, need, src_on_device ? hipMemcpyDeviceToDevice
+                                                      : hipMemcpyHostToDevice);
+  } else if (need) {
+    const uint8_t *raw = (const uint8_t *)src;
+    uint8_t *tmp = nullptr;
+    if (!src_on_device) {
+      e = hipMalloc(&tmp, need);
+      if (e == hipSuccess) e = hipMemcpy(tmp, src, need, hipMemcpyHostToDevice);
+      raw = tmp;
+    }
+    if (e == hipSuccess) e = gq::launch_repack(dtype, raw, out_dim, nb, w->body, w->d, 0);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (tmp) (void)hipFree(tmp);
+  }
+  if (e != hipSuccess) {
+    (void)hipFree(mem);
+    delete w;
+    return fail(GQ_EHIP, "weight upload failed: %s", hipGetErrorString(e));
+  }
+  *out = w;
+  return GQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gq_init(int device) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  return init_locked(device);
+}
+
+const char *gq_backend_name(void) { return "hip"; }
+
+const char *gq_last_error(void) { return g_err.c_str(); }
+
+size_t gq_type_size(int dtype, size_t n) {
+  const int bb = gq::ggml_block_bytes(dtype);
+  if (!bb) return 0;
+  const size_t be = gq::block_elems(dtype);
+  return ((n + be - 1) / be) * bb;
+}
+
+int gq_upload(int dtype, const void *w_host, size_t nbytes, int in_dim, int out_dim,
+              gq_weight **out) {
+  return upload_common(dtype, w_host, false, nbytes, in_dim, out_dim, out);
+}
+
+int gq_upload_device(int dtype, const void *w_dev, size_t nbytes, int in_dim, int out_dim,
+                     gq_weight **out) {
+  return upload_common(dtype, w_dev, true, nbytes, in_dim, out_dim, out);
+}
+
+int gq_weight_free(gq_weight *w) {
+  if (!w) return GQ_OK;
+  if (w->body) (void)hipFree(w->body);
+  delete w;
+  return GQ_OK;
+}
+
+int gq_weight_shape(const gq_weight *w, int *dtype, int *in_dim, int *out_dim) {
+  if (!w) return fail(GQ_EINVAL, "null weight handle");
+  if (dtype) *dtype = w->dtype;
+  if (in_dim) *in_dim = w->in_dim;
+  if (out_dim) *out_dim = w->out_dim;
+  return GQ_OK;
+}
+
+size_t gq_weight_bytes(const gq_weight *w) { return w ? w->ggml_bytes : 0; }
+
+int gq_matvec_multi(const gq_weight *const *ws, int count, const float *x_dev,
+                    float *const *y_dev, void *stream) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (count <= 0 || !ws || !y_dev) return fail(GQ_EINVAL, "empty weight list");
+  for (int i = 0; i < count; i++) {
+    if ((rc = check_matvec(ws[i]))) return rc;
+    if (ws[i]->dtype != ws[0]->dtype || ws[i]->in_dim != ws[0]->in_dim)
+      return fail(GQ_EINVAL, "gq_matvec_multi: weights must share dtype and in_dim");
+    if (ws[i]->out_dim > 0 && !y_dev[i]) return fail(GQ_EINVAL, "null output %d", i);
+  }
+  if (!x_dev) return fail(GQ_EINVAL, "null x");
+  const gq_weight *w0 = ws[0];
+  for (int base = 0; base < count; base += gq::MV_MAX_SEG) {
+    gq::MvArgs a{};
+    a.x = x_dev;
+    a.grid = g_dev.grid;
+    a.k = w0->in_dim;
+    a.nb = w0->nb;
+    a.kpad = w0->nb * gq::block_elems(w0->dtype);
+    int rows = 0, ns = 0;
+    for (int i = base; i < count && ns < gq::MV_MAX_SEG; i++, ns++) {
+      a.seg[ns] = gq::MvSeg{ws[i]->body, ws[i]->d, y_dev[i], ws[i]->stride, rows};
+      rows += ws[i]->out_dim;
+    }
+    a.nseg = ns;
+    a.total_rows = rows;
+    if (rows == 0) continue;
+    hipError_t e = gq::launch_matvec(a, w0->dtype, g_dev.num_cus, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(GQ_EHIP, "matvec launch failed: %s", hipGetErrorString(e));
+  }
+  return GQ_OK;
+}
+
+int gq_matvec(const gq_weight *w, const float *x_dev, float *y_dev, void *stream) {
+  const gq_weight *ws[1] = {w};
+  float *ys[1] = {y_dev};
+  return gq_matvec_multi(ws, 1, x_dev, ys, stream);
+}
+
+int gq_matmul_dequant_preloaded(const gq_weight *w, const float *x_host, float *out_host) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if ((rc = check_matvec(w))) return rc;
+  if (w->out_dim == 0) return GQ_OK;
+  if (!x_host || !out_host) return fail(GQ_EINVAL, "null x or out");
+  float *xd = nullptr, *yd = nullptr;
+  HIP_TRY(hipMalloc(&xd, (size_t)w->in_dim * 4));
+  if (hipMalloc(&yd, (size_t)w->out_dim * 4) != hipSuccess) {
+    (void)hipFree(xd);
+    return fail(GQ_ENOMEM, "hipMalloc failed");
+  }
+  hipError_t e = hipMemcpy(xd, x_host, (size_t)w->in_dim * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) {
+    rc = gq_matvec(w, xd, yd, nullptr);
+    if (!rc) e = hipMemcpy(out_host, yd, (size_t)w->out_dim * 4, hipMemcpyDeviceToHost);
+  }
+  (void)hipFree(xd);
+  (void)hipFree(yd);
+  if (rc) return rc;
+  if (e != hipSuccess) return fail(GQ_EHIP, "copy failed: %s", hipGetErrorString(e));
+  return GQ_OK;
+}
+
+int gq_matmul_dequant_host(int dtype, const void *w_host, size_t nbytes, const float *x_host,
+                           size_t in_dim, float *out_host, size_t out_dim) {
+  if (!supported(dtype) || dtype == gq::T_IQ3_XXS)
+    // Backend::matmul_dequant accepts the GPU_DEQUANT_DTYPES (ops/mod.rs:27-28).
+    return fail(GQ_EDTYPE, "matmul_dequant: unsupported dtype %s", type_name(dtype));
+  if (out_dim == 0) return GQ_OK;
+  gq_weight *w = nullptr;
+  int rc = gq_upload(dtype, w_host, nbytes, (int)in_dim, (int)out_dim, &w);
+  if (rc) return rc;
+  rc = gq_matmul_dequant_preloaded(w, x_host, out_host);
+  gq_weight_free(w);
+  return rc;
+}
+
+int gq_dequant_rows(const gq_weight *w, int row0, int nrows, float *out_dev, void *stream) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (!w) return fail(GQ_EINVAL, "null weight handle");
+  if (row0 < 0 || nrows < 0 || row0 + nrows > w->out_dim)
+    return fail(GQ_EINVAL, "row index %d out of range (tensor has %d rows)", row0 + nrows - 1,
+                w->out_dim);
+  if (nrows == 0) return GQ_OK;
+  hipError_t e = gq::launch_dequant(w, g_dev.grid, row0, nrows, out_dev, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(GQ_EHIP, "dequant launch failed: %s", hipGetErrorString(e));
+  return GQ_OK;
+}
+
+int gq_quantize_q8_32(const float *x_dev, int n, uint16_t *scale_dev, int8_t *q_dev,
+                      void *stream) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (n < 0 || n % 32) return fail(GQ_EINVAL, "n=%d must be a multiple of 32", n);
+  hipError_t e = gq::launch_quantize_q8_32(x_dev, n, scale_dev, q_dev, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(GQ_EHIP, "quantize launch failed: %s", hipGetErrorString(e));
+  return GQ_OK;
+}
+
+int gq_set_iq3xxs_grid(const uint32_t *grid_host) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (grid_host) memcpy(g_dev.grid_host, grid_host, 1024);
+  else default_grid(g_dev.grid_host);
+  HIP_TRY(hipMemcpy(g_dev.grid, g_dev.grid_host, 1024, hipMemcpyHostToDevice));
+  return GQ_OK;
+}
+
+int gq_get_iq3xxs_grid(uint32_t *grid_host) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (!grid_host) return fail(GQ_EINVAL, "null grid");
+  memcpy(grid_host, g_dev.grid_host, 1024);
+  return GQ_OK;
+}
+
+int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mode,
+            void *stream) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (!w) return fail(GQ_EINVAL, "null weight handle");
+  if (n < 0) return fail(GQ_EINVAL, "negative batch");
+  if (n == 0 || w->out_dim == 0) return GQ_OK;
+  if (mode != GQ_GEMM_BF16 && mode != GQ_GEMM_INT8) return fail(GQ_EINVAL, "bad gemm mode %d", mode);
+  const size_t ws = gq::gemm_workspace_bytes(w, n, mode);
+  if (ws == (size_t)-1)
+    return fail(GQ_EDTYPE, "gq_gemm: %s weights with in_dim %d not supported in this mode",
+                type_name(w->dtype), w->in_dim);
+  void *wsp = nullptr;
+  if (ws) HIP_TRY(hipMallocAsync(&wsp, ws, (hipStream_t)stream));
+  hipError_t e = gq::launch_gemm(w, X_dev, n, Y_dev, mode, wsp, ws, g_dev.num_cus,
+                                 (hipStream_t)stream);
+  if (wsp) (void)hipFreeAsync(wsp, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(GQ_EHIP, "gemm launch failed: %s", hipGetErrorString(e));
+  return GQ_OK;
+}
+
+int gq_sync(void *stream) {
+  HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
+  return GQ_OK;
+}
+
+}  // extern "C"

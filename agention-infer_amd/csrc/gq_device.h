@@ -1,0 +1,85 @@
+// gq_device.h -- device-side formats and helpers shared by the gq kernels.
+//
+// Device-resident weight layouts (chosen at upload; total bytes equal the
+// ggml tensor size, so HBM traffic per matvec is the algorithmic byte count):
+//
+//   Q4_K    ggml rows unchanged: 144 B blocks are 16 B aligned
+//           (d, dmin, scales[12] = one 16 B header, then qs[128]).
+//   Q5_K    ggml rows unchanged: 176 B blocks, 16 B aligned
+//           (16 B header, qh[32], qs[128]).
+//   Q6_K    body[row][blk] = ql[128] qh[64] scales[16] (208 B, 16 B aligned),
+//           d[row][blk] f16 in a separate array (ggml puts d last, making the
+//           210 B block unaligned for 128-bit loads).
+//   Q8_0    body[row][blk] = qs[32] int8, d[row][blk] f16 separate
+//           (the 34 B ggml block is unaligned).
+//   IQ3_XXS body[row][blk] = qs[64] aux[32] (96 B), d[row][blk] f16 separate.
+//
+// Arithmetic: the library is compiled with -ffp-contract=off, so an
+// expression such as d1 * q - m1 rounds exactly like the reference's Rust
+// (which never contracts).  Kernels that want a fused multiply-add say so
+// with fmaf().
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace gq {
+
+enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ3_XXS = 18 };
+
+// Device body bytes per block for each layout.
+__host__ __device__ constexpr int body_block_bytes(int t) {
+  return t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 208 : t == T_Q8_0 ? 32
+       : t == T_IQ3_XXS ? 96 : 0;
+}
+__host__ __device__ constexpr int ggml_block_bytes(int t) {
+  return t == T_Q4_K ? 144 : t == T_Q5_K ? 176 : t == T_Q6_K ? 210 : t == T_Q8_0 ? 34
+       : t == T_IQ3_XXS ? 98 : 0;
+}
+__host__ __device__ constexpr int block_elems(int t) { return t == T_Q8_0 ? 32 : 256; }
+__host__ __device__ constexpr bool has_d_array(int t) {
+  return t == T_Q6_K || t == T_Q8_0 || t == T_IQ3_XXS;
+}
+
+// IEEE binary16 -> binary32 (exact; v_cvt_f32_f16 keeps f16 subnormals).
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
+}
+
+// Byte k (0..11) of the 12 packed scale bytes held in three dwords.
+__device__ __forceinline__ uint32_t sbyte(uint32_t s0, uint32_t s1, uint32_t s2, int k) {
+  uint32_t w = k < 4 ? s0 : (k < 8 ? s1 : s2);
+  return (w >> ((k & 3) * 8)) & 0xffu;
+}
+
+// get_scale_min_k4 (src/quant/q4_k.rs:26-35) on the scale dwords.
+__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                             uint32_t &sc, uint32_t &m) {
+  if (j < 4) {
+    sc = sbyte(s0, s1, s2, j) & 63u;
+    m = sbyte(s0, s1, s2, j + 4) & 63u;
+  } else {
+    sc = (sbyte(s0, s1, s2, j + 4) & 0xFu) | ((sbyte(s0, s1, s2, j - 4) >> 6) << 4);
+    m = (sbyte(s0, s1, s2, j + 4) >> 4) | ((sbyte(s0, s1, s2, j) >> 6) << 4);
+  }
+}
+
+// ksigns_iq2xs[i]: 7 sign bits plus an even-parity 8th bit.
+__device__ __forceinline__ uint32_t ksign7(uint32_t i) {
+  return i | ((uint32_t)(__popc(i) & 1) << 7);
+}
+
+// Unsigned byte k of w as float (lowers to v_cvt_f32_ubyte{k}).
+template <int K>
+__device__ __forceinline__ float ub(uint32_t w) { return (float)((w >> (8 * K)) & 0xffu); }
+
+// sum_k ub(w, k) * x[k] over the 4 bytes of w, accumulated into acc.
+__device__ __forceinline__ float dot4u(uint32_t w, float4 x, float acc) {
+  acc = fmaf(ub<0>(w), x.x, acc);
+  acc = fmaf(ub<1>(w), x.y, acc);
+  acc = fmaf(ub<2>(w), x.z, acc);
+  acc = fmaf(ub<3>(w), x.w, acc);
+  return acc;
+}
+
+}  // namespace gq

@@ -1,0 +1,126 @@
+/*
+ * gq.h -- C ABI of libgq.so, the MI355X (gfx950) quantized dequant-matmul
+ * backend for gguf-rs.
+ *
+ * Every entry point returns 0 on success or a negative GQ_E* code; the
+ * message for the last failure on the calling thread is gq_last_error()
+ * (mirrors GgufError::BackendError(String), src/error.rs:4-42).
+ * Pointers named *_dev are device pointers; *_host are host pointers.
+ * `stream` is a hipStream_t (NULL = the default stream).
+ * Launch entry points (gq_matvec, gq_gemm, ...) are asynchronous on
+ * `stream`; the *_host entry points are synchronous.
+ */
+#ifndef GQ_H
+#define GQ_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GQ_OK 0
+#define GQ_EINVAL (-1)   /* bad argument / shape mismatch */
+#define GQ_EDTYPE (-2)   /* unsupported dtype ("unsupported dtype {other}") */
+#define GQ_ESHORT (-3)   /* buffer too short ("need N bytes, have M") */
+#define GQ_EHIP (-4)     /* HIP runtime error */
+#define GQ_ENOMEM (-5)   /* device allocation failed */
+#define GQ_ENODEV (-6)   /* no gfx950 device / not initialised */
+
+/* GgmlType ids, the on-disk tensor type ids (src/types.rs:9-46). */
+#define GQ_TYPE_Q8_0 8
+#define GQ_TYPE_Q4_K 12
+#define GQ_TYPE_Q5_K 13
+#define GQ_TYPE_Q6_K 14
+#define GQ_TYPE_IQ3_XXS 18
+
+/* gq_gemm modes (batched prefill). */
+#define GQ_GEMM_BF16 0  /* Q4_K tiles dequantized to bf16 in LDS, bf16 MFMA */
+#define GQ_GEMM_INT8 1  /* activations packed per-32 to Q8, int8 MFMA      */
+
+typedef struct gq_weight gq_weight;
+
+/* Select and initialise device `device` (BackendPreference::Hip arm of
+ * create_backend, src/ops/backend_select.rs:72-83, which is a CPU-fallback
+ * stub in the reference).  Fails with GQ_ENODEV if it is not a gfx950. */
+int gq_init(int device);
+
+/* Backend::name (src/ops/mod.rs:101): returns "hip". */
+const char *gq_backend_name(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *gq_last_error(void);
+
+/* GgmlType::type_size (src/types.rs:164-168): bytes of one row of n
+ * elements; 0 for an unknown dtype. */
+size_t gq_type_size(int dtype, size_t n);
+
+/* WgpuBackend::upload_weight (src/ops/wgpu_backend/mod.rs:61-92): copy a
+ * whole tensor (out_dim rows of type_size(in_dim) bytes, ggml block order)
+ * to the device once and keep it resident, re-laid-out for the kernels.
+ * All-zero blocks are valid (warmup, src/ops/backend_select.rs:133-139). */
+int gq_upload(int dtype, const void *w_host, size_t nbytes, int in_dim, int out_dim,
+              gq_weight **out);
+
+/* Same, from bytes already on the device (ggml block order). */
+int gq_upload_device(int dtype, const void *w_dev, size_t nbytes, int in_dim, int out_dim,
+                     gq_weight **out);
+
+/* Drop a handle (GpuWeightHandle's Drop). */
+int gq_weight_free(gq_weight *w);
+
+/* GpuWeightHandle::shape / out_dim (src/ops/wgpu_backend/mod.rs:914-922). */
+int gq_weight_shape(const gq_weight *w, int *dtype, int *in_dim, int *out_dim);
+
+/* Device bytes held by the handle (equals the ggml tensor size). */
+size_t gq_weight_bytes(const gq_weight *w);
+
+/* launch_only / launch_only_f32out (src/ops/wgpu_backend/resident.rs:13-69):
+ * y_dev[out_dim] = W . x_dev[in_dim], fp32 in and out, no readback. */
+int gq_matvec(const gq_weight *w, const float *x_dev, float *y_dev, void *stream);
+
+/* matmul_dequant_qkv / _multi / _ffn (src/ops/wgpu_backend/mod.rs:702-854):
+ * several weights sharing one input, one launch.  All weights must have
+ * the same in_dim; y_dev[i] receives out_dim(w[i]) floats. */
+int gq_matvec_multi(const gq_weight *const *w, int count, const float *x_dev,
+                    float *const *y_dev, void *stream);
+
+/* matmul_dequant_preloaded (src/ops/wgpu_backend/mod.rs:642-696):
+ * host x in, host out, synchronous. */
+int gq_matmul_dequant_preloaded(const gq_weight *w, const float *x_host, float *out_host);
+
+/* Backend::matmul_dequant (src/ops/mod.rs:105, cpu_backend.rs:38-65):
+ * w_host is the whole tensor (out_dim rows of type_size(in_dim) bytes);
+ * out_host[out_dim] is overwritten.  Uploads, runs, reads back. */
+int gq_matmul_dequant_host(int dtype, const void *w_host, size_t nbytes, const float *x_host,
+                           size_t in_dim, float *out_host, size_t out_dim);
+
+/* quant::dequant_row (src/quant/mod.rs:25-45) for rows [row0, row0+nrows):
+ * out_dev[nrows][in_dim] f32, bit-identical to the CPU dequant. */
+int gq_dequant_rows(const gq_weight *w, int row0, int nrows, float *out_dev, void *stream);
+
+/* launch_only_batch (src/ops/wgpu_backend/resident.rs:76-104) and the
+ * prefill path of WeightMap::matmul_batch_into (src/model/mod.rs:414-464):
+ * X_dev [n][in_dim] fp32 token-major -> Y_dev [n][out_dim] fp32.
+ * mode GQ_GEMM_BF16 or GQ_GEMM_INT8 (Q4_K weights). */
+int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mode, void *stream);
+
+/* Per-32 Q8 activation pack used by GQ_GEMM_INT8, identical to
+ * KvDtype::Q8_0::pack (src/model/mod.rs:574-583): scale_dev[n/32] f16
+ * bits, q_dev[n] int8 (n a multiple of 32). */
+int gq_quantize_q8_32(const float *x_dev, int n, uint16_t *scale_dev, int8_t *q_dev,
+                      void *stream);
+
+/* IQ3_XXS codebook (256 entries, 4 magnitude bytes each).  The reference
+ * has no IQ3_XXS implementation (src/quant/mod.rs:7,38-41); the default is
+ * a placeholder until the caller installs ggml's iq3xxs_grid. */
+int gq_set_iq3xxs_grid(const uint32_t *grid_host);
+int gq_get_iq3xxs_grid(uint32_t *grid_host);
+
+/* Wait for all work on `stream`. */
+int gq_sync(void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,677 @@
+/*
+ * gq_oracle.c -- CPU restatement of gguf-rs's quantized dequant-matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker and the timed CPU baseline.
+ * Nothing in the product library links or calls this file.
+ *
+ * Compiled with -O2 -ffp-contract=off: Rust never fuses a*b-c into an FMA,
+ * and the dequantized values must come out bit-identical to the reference.
+ * Citations are into the reference crate (src/...).
+ *
+ * Pinning (how each function is checked, in tests/test_oracle.py):
+ *   f16<->f32        exhaustive over 65536 patterns vs numpy float16.
+ *   Q8_0             q8_0.rs:109-170 known answers + brute-force fp64 dot.
+ *   get_scale_min_k4 q4_k.rs:228-241 known-answer vectors + bit-packing
+ *                    round trip over all 64x64 (sc, m) pairs.
+ *   Q4_K / Q5_K      closed-form dequant (numpy), q4_k.rs:243-259 fused ==
+ *                    dequant-then-dot, fp64 brute-force dot.
+ *   Q6_K             closed-form element mapping (numpy, written from the
+ *                    ggml layout independently), q6_k.rs:147-164.
+ *   Q8_K             q8_k.rs:97-138 invariants (bsums, zero block, padding,
+ *                    round-trip bound).
+ *   per-32 Q8 pack   model/mod.rs:574-583 restated in numpy.
+ *   IQ3_XXS          parity unpinned: the reference has no implementation
+ *                    (quant/mod.rs:7, :38-41).  This is a restatement of
+ *                    ggml's published dequantize_row_iq3_xxs; its codebook is
+ *                    a placeholder unless the caller installs the real one.
+ */
+#include "gq_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+/* ------------------------------------------------------------------ types */
+
+size_t gqo_block_size(int t) {
+    switch (t) {
+    case GQO_F32: case GQO_F16: case GQO_BF16: return 1;
+    case GQO_Q8_0: return 32;
+    case GQO_Q4_K: case GQO_Q5_K: case GQO_Q6_K: case GQO_Q8_K: case GQO_IQ3_XXS: return 256;
+    default: return 0;
+    }
+}
+
+size_t gqo_block_bytes(int t) {
+    switch (t) {
+    case GQO_F32: return 4;
+    case GQO_F16: case GQO_BF16: return 2;
+    case GQO_Q8_0: return 34;
+    case GQO_Q4_K: return 144;
+    case GQO_Q5_K: return 176;
+    case GQO_Q6_K: return 210;
+    case GQO_Q8_K: return 292;
+    case GQO_IQ3_XXS: return 98;
+    default: return 0;
+    }
+}
+
+size_t gqo_type_size(int t, size_t n) {
+    size_t bs = gqo_block_size(t);
+    if (!bs) return 0;
+    return ((n + bs - 1) / bs) * gqo_block_bytes(t);
+}
+
+/* ------------------------------------------------------------- f16 <-> f32 */
+
+/* IEEE binary16 -> binary32, exact (what half::f16::to_f32 computes). */
+float gqo_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h >> 15) << 31;
+    uint32_t exp = (h >> 10) & 0x1f;
+    uint32_t man = h & 0x3ff;
+    uint32_t bits;
+    if (exp == 0) {
+        if (man == 0) {
+            bits = sign;
+        } else { /* subnormal: normalise */
+            int e = -1;
+            do { man <<= 1; e++; } while (!(man & 0x400));
+            man &= 0x3ff;
+            bits = sign | ((uint32_t)(127 - 15 - e) << 23) | (man << 13);
+        }
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (man << 13);
+    } else {
+        bits = sign | ((exp + 127 - 15) << 23) | (man << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* binary32 -> binary16, round to nearest even (half::f16::from_f32). */
+uint16_t gqo_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000);
+    uint32_t exp = (x >> 23) & 0xff;
+    uint32_t man = x & 0x7fffff;
+    if (exp == 0xff) /* inf / nan (keep a quiet payload bit for nan) */
+        return sign | 0x7c00 | (man ? (0x200 | (man >> 13)) : 0);
+    int e = (int)exp - 127 + 15;
+    if (e >= 31) return sign | 0x7c00;
+    if (e <= 0) {
+        if (e < -10) return sign; /* below half the smallest subnormal */
+        man |= 0x800000;
+        int shift = 14 - e; /* 14..24 */
+        uint32_t hm = man >> shift;
+        uint32_t rem = man & ((1u << shift) - 1);
+        uint32_t half = 1u << (shift - 1);
+        if (rem > half || (rem == half && (hm & 1))) hm++;
+        return sign | (uint16_t)hm;
+    }
+    uint32_t hm = man >> 13;
+    uint32_t rem = man & 0x1fff;
+    uint16_t out = sign | (uint16_t)(e << 10) | (uint16_t)hm;
+    if (rem > 0x1000 || (rem == 0x1000 && (hm & 1))) out++; /* carry may bump exp: correct */
+    return out;
+}
+
+static inline float rd_f16(const uint8_t *p) { return gqo_f16_to_f32((uint16_t)(p[0] | (p[1] << 8))); }
+
+/* -------------------------------------------------------------------- Q8_0 */
+
+/* q8_0.rs:14-51 */
+int gqo_dequant_q8_0(const uint8_t *data, size_t nbytes, size_t n, float *out) {
+    size_t nb = (n + 31) / 32;
+    if (nbytes < nb * 34) return GQO_ESHORT;
+    size_t o = 0;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = data + b * 34;
+        float scale = rd_f16(blk);
+        size_t cnt = (b == nb - 1) ? n - b * 32 : 32;
+        for (size_t i = 0; i < cnt; i++) out[o++] = scale * (float)(int8_t)blk[2 + i];
+    }
+    return 0;
+}
+
+/* q8_0.rs:58-90: per block sequential sum of q*x, then acc += scale*block_dot */
+int gqo_dot_q8_0(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res) {
+    size_t nb = (n + 31) / 32;
+    if (nbytes < nb * 34) return GQO_ESHORT;
+    float acc = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = data + b * 34;
+        float scale = rd_f16(blk);
+        size_t start = b * 32;
+        size_t cnt = n - start < 32 ? n - start : 32;
+        float bd = 0.0f;
+        for (size_t i = 0; i < cnt; i++) bd += (float)(int8_t)blk[2 + i] * x[start + i];
+        acc += scale * bd;
+    }
+    *res = acc;
+    return 0;
+}
+
+/* -------------------------------------------------------------------- Q4_K */
+
+/* q4_k.rs:26-35 */
+void gqo_get_scale_min_k4(int j, const uint8_t *s, uint8_t *sc, uint8_t *m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (uint8_t)((s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4));
+        *m = (uint8_t)((s[j + 4] >> 4) | ((s[j] >> 6) << 4));
+    }
+}
+
+/* q4_k.rs:37-91 (also the Q5_K variant, q5_k.rs:41-99, when qh != NULL) */
+static void dequant_k4_block(const uint8_t *blk, const uint8_t *qh, const uint8_t *qs, float *y) {
+    float d = rd_f16(blk), dmin = rd_f16(blk + 2);
+    const uint8_t *scales = blk + 4;
+    int is = 0;
+    for (int j = 0; j < 256; j += 64) {
+        uint8_t sc0, m0, sc1, m1s;
+        gqo_get_scale_min_k4(is, scales, &sc0, &m0);
+        float d1 = d * (float)sc0, m1 = dmin * (float)m0;
+        gqo_get_scale_min_k4(is + 1, scales, &sc1, &m1s);
+        float d2 = d * (float)sc1, m2 = dmin * (float)m1s;
+        const uint8_t *q = qs + j / 2;
+        for (int l = 0; l < 32; l++) {
+            int hb = qh ? (((qh[l] >> is) & 1) << 4) : 0;
+            y[j + l] = d1 * (float)((q[l] & 0xF) + hb) - m1;
+        }
+        for (int l = 0; l < 32; l++) {
+            int hb = qh ? (((qh[l] >> (is + 1)) & 1) << 4) : 0;
+            y[j + 32 + l] = d2 * (float)((q[l] >> 4) + hb) - m2;
+        }
+        is += 2;
+    }
+}
+
+static int dequant_k4(const uint8_t *data, size_t nbytes, size_t n, float *out, int q5) {
+    size_t bb = q5 ? 176 : 144;
+    size_t nb = (n + 255) / 256;
+    if (nbytes < nb * bb) return GQO_ESHORT;
+    float tmp[256];
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = data + b * bb;
+        dequant_k4_block(blk, q5 ? blk + 16 : NULL, blk + (q5 ? 48 : 16), tmp);
+        size_t cnt = n - b * 256 < 256 ? n - b * 256 : 256;
+        memcpy(out + b * 256, tmp, cnt * sizeof(float));
+    }
+    return 0;
+}
+
+int gqo_dequant_q4_k(const uint8_t *d, size_t nb, size_t n, float *o) { return dequant_k4(d, nb, n, o, 0); }
+int gqo_dequant_q5_k(const uint8_t *d, size_t nb, size_t n, float *o) { return dequant_k4(d, nb, n, o, 1); }
+
+/* dot_q4_k_group (q4_k.rs:152-203) / dot_q5_k_group (q5_k.rs:249-317): an
+ * 8-lane f32 accumulator, lane k takes ((d1*lo - m1)*x_lo) then
+ * ((d2*hi - m2)*x_hi) for each of the 4 byte-octets, then a sequential
+ * horizontal sum.  Out-of-range x lanes read as 0.0 (load_f32x8_partial). */
+static float dot_k4_group(float d1, float m1, float d2, float m2, const uint8_t *qs,
+                          const uint8_t *qh, int sh1, int sh2, const float *x, size_t avail) {
+    float sum[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (size_t base = 0; base < 32; base += 8) {
+        for (int k = 0; k < 8; k++) {
+            uint8_t q = qs[base + k];
+            int h1 = qh ? (((qh[base + k] >> sh1) & 1) << 4) : 0;
+            int h2 = qh ? (((qh[base + k] >> sh2) & 1) << 4) : 0;
+            float lo = (float)((q & 0xF) | h1);
+            float hi = (float)((q >> 4) | h2);
+            float xl = (base + k < avail) ? x[base + k] : 0.0f;
+            float xh = (32 + base + k < avail) ? x[32 + base + k] : 0.0f;
+            float t = d1 * lo;
+            t = t - m1;
+            sum[k] = sum[k] + t * xl;
+            float u = d2 * hi;
+            u = u - m2;
+            sum[k] = sum[k] + u * xh;
+        }
+    }
+    float s = 0.0f; /* arr.iter().sum(): sequential */
+    for (int k = 0; k < 8; k++) s += sum[k];
+    return s;
+}
+
+/* q4_k.rs:95-147, q5_k.rs:189-247 */
+static int dot_k4(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res, int q5) {
+    size_t bb = q5 ? 176 : 144;
+    size_t nb = (n + 255) / 256;
+    if (nbytes < nb * bb) return GQO_ESHORT;
+    float acc = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = data + b * bb;
+        float d = rd_f16(blk), dmin = rd_f16(blk + 2);
+        const uint8_t *scales = blk + 4;
+        const uint8_t *qh = q5 ? blk + 16 : NULL;
+        const uint8_t *qs = blk + (q5 ? 48 : 16);
+        size_t bo = b * 256;
+        int is = 0;
+        for (int j = 0; j < 256; j += 64) {
+            uint8_t sc0, m0, sc1, m1s;
+            gqo_get_scale_min_k4(is, scales, &sc0, &m0);
+            float d1 = d * (float)sc0, m1 = dmin * (float)m0;
+            gqo_get_scale_min_k4(is + 1, scales, &sc1, &m1s);
+            float d2 = d * (float)sc1, m2 = dmin * (float)m1s;
+            size_t off = bo + j;
+            size_t avail = n > off ? n - off : 0;
+            acc += dot_k4_group(d1, m1, d2, m2, qs + j / 2, qh, is, is + 1, avail ? x + off : x, avail);
+            is += 2;
+        }
+    }
+    *res = acc;
+    return 0;
+}
+
+int gqo_dot_q4_k(const uint8_t *d, size_t nb, const float *x, size_t n, float *r) { return dot_k4(d, nb, x, n, r, 0); }
+int gqo_dot_q5_k(const uint8_t *d, size_t nb, const float *x, size_t n, float *r) { return dot_k4(d, nb, x, n, r, 1); }
+
+/* -------------------------------------------------------------------- Q6_K */
+
+/* q6_k.rs:25-32 */
+static inline void quads(const uint8_t *ql, const uint8_t *qh, int l, int q[4]) {
+    uint8_t h = qh[l];
+    q[0] = ((ql[l] & 0xF) | (((h >> 0) & 3) << 4)) - 32;
+    q[1] = ((ql[l + 32] & 0xF) | (((h >> 2) & 3) << 4)) - 32;
+    q[2] = ((ql[l] >> 4) | (((h >> 4) & 3) << 4)) - 32;
+    q[3] = ((ql[l + 32] >> 4) | (((h >> 6) & 3) << 4)) - 32;
+}
+
+/* q6_k.rs:34-77: y = (d * sc) * q */
+int gqo_dequant_q6_k(const uint8_t *data, size_t nbytes, size_t n, float *out) {
+    size_t nb = (n + 255) / 256;
+    if (nbytes < nb * 210) return GQO_ESHORT;
+    float tmp[256];
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = data + b * 210;
+        const int8_t *sc = (const int8_t *)(blk + 192);
+        float d = rd_f16(blk + 208);
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *ql = blk + h * 64, *qh = blk + 128 + h * 32;
+            for (int l = 0; l < 32; l++) {
+                int is = l / 16, q[4];
+                quads(ql, qh, l, q);
+                tmp[h * 128 + l] = d * (float)sc[h * 8 + is] * (float)q[0];
+                tmp[h * 128 + l + 32] = d * (float)sc[h * 8 + is + 2] * (float)q[1];
+                tmp[h * 128 + l + 64] = d * (float)sc[h * 8 + is + 4] * (float)q[2];
+                tmp[h * 128 + l + 96] = d * (float)sc[h * 8 + is + 6] * (float)q[3];
+            }
+        }
+        size_t cnt = n - b * 256 < 256 ? n - b * 256 : 256;
+        memcpy(out + b * 256, tmp, cnt * sizeof(float));
+    }
+    return 0;
+}
+
+/* q6_k.rs:82-131: acc += ((d*sc)*q)*x, one scalar accumulator, element order
+ * (h, l, quad). */
+int gqo_dot_q6_k(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res) {
+    size_t nb = (n + 255) / 256;
+    if (nbytes < nb * 210) return GQO_ESHORT;
+    float acc = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = data + b * 210;
+        const int8_t *sc = (const int8_t *)(blk + 192);
+        float d = rd_f16(blk + 208);
+        size_t bo = b * 256;
+        for (int h = 0; h < 2; h++) {
+            const uint8_t *ql = blk + h * 64, *qh = blk + 128 + h * 32;
+            size_t yh = bo + h * 128;
+            for (int l = 0; l < 32; l++) {
+                int is = l / 16, q[4];
+                quads(ql, qh, l, q);
+                for (int k = 0; k < 4; k++) {
+                    size_t idx = yh + l + 32 * k;
+                    if (idx < n) {
+                        float t = d * (float)sc[h * 8 + is + 2 * k];
+                        t = t * (float)q[k];
+                        acc += t * x[idx];
+                    } else {
+                        acc += 0.0f;
+                    }
+                }
+            }
+        }
+    }
+    *res = acc;
+    return 0;
+}
+
+/* ----------------------------------------------------------------- IQ3_XXS */
+
+/* The reference has no IQ3_XXS arithmetic (quant/mod.rs:7,38-41); this is a
+ * restatement of ggml's published dequantize_row_iq3_xxs:
+ *   block: f16 d | qs[64] grid indices | 8 x u32 aux (per 32 elements):
+ *   aux bits 0..27 = four 7-bit sign indices, bits 28..31 = scale s;
+ *   db = d * (0.5 + s) * 0.5;
+ *   signs7 -> 8 sign bits via even parity: ksigns[i] = i | (popcount(i)&1)<<7;
+ *   for each of 4 groups of 8: two grid entries (4 magnitude bytes each),
+ *   y[j] = db * mag[j] * (sign bit j ? -1 : 1).
+ * The codebook ggml ships (iq3xxs_grid) is not available here; the default
+ * below is a deterministic placeholder over ggml's magnitude alphabet
+ * {4,12,20,28,36,44,52,62}.  gqo_set_iq3xxs_grid installs another table.
+ * Parity unpinned. */
+static uint32_t g_iq3_grid[256];
+static int g_iq3_init = 0;
+
+static void iq3_default_grid(uint32_t *g) {
+    static const uint8_t mags[8] = {4, 12, 20, 28, 36, 44, 52, 62};
+    for (uint32_t i = 0; i < 256; i++) {
+        uint32_t h = i * 0x9E3779B1u;
+        h ^= h >> 15;
+        uint32_t e = 0;
+        for (int k = 0; k < 4; k++) e |= (uint32_t)mags[(h >> (3 * k)) & 7] << (8 * k);
+        g[i] = e;
+    }
+}
+
+static const uint32_t *iq3_grid(void) {
+    if (!g_iq3_init) { iq3_default_grid(g_iq3_grid); g_iq3_init = 1; }
+    return g_iq3_grid;
+}
+
+void gqo_set_iq3xxs_grid(const uint32_t *grid) {
+    if (grid) memcpy(g_iq3_grid, grid, sizeof(g_iq3_grid));
+    else iq3_default_grid(g_iq3_grid);
+    g_iq3_init = 1;
+}
+void gqo_get_iq3xxs_grid(uint32_t *grid) { memcpy(grid, iq3_grid(), sizeof(g_iq3_grid)); }
+
+static inline uint8_t ksign(uint32_t i) {
+    return (uint8_t)(i | ((uint32_t)(__builtin_popcount(i) & 1) << 7));
+}
+
+static void dequant_iq3_block(const uint8_t *blk, float *y) {
+    const uint32_t *grid = iq3_grid();
+    float d = rd_f16(blk);
+    const uint8_t *qs = blk + 2;
+    const uint8_t *sas = blk + 2 + 64;
+    for (int ib = 0; ib < 8; ib++) {
+        uint32_t aux = (uint32_t)sas[4 * ib] | ((uint32_t)sas[4 * ib + 1] << 8) |
+                       ((uint32_t)sas[4 * ib + 2] << 16) | ((uint32_t)sas[4 * ib + 3] << 24);
+        float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+        for (int l = 0; l < 4; l++) {
+            uint8_t signs = ksign((aux >> (7 * l)) & 127);
+            uint32_t g1 = grid[qs[8 * ib + 2 * l]], g2 = grid[qs[8 * ib + 2 * l + 1]];
+            for (int j = 0; j < 4; j++) {
+                float m1 = (float)((g1 >> (8 * j)) & 0xff), m2 = (float)((g2 >> (8 * j)) & 0xff);
+                y[32 * ib + 8 * l + j] = db * m1 * ((signs >> j) & 1 ? -1.0f : 1.0f);
+                y[32 * ib + 8 * l + j + 4] = db * m2 * ((signs >> (j + 4)) & 1 ? -1.0f : 1.0f);
+            }
+        }
+    }
+}
+
+int gqo_dequant_iq3_xxs(const uint8_t *data, size_t nbytes, size_t n, float *out) {
+    size_t nb = (n + 255) / 256;
+    if (nbytes < nb * 98) return GQO_ESHORT;
+    float tmp[256];
+    for (size_t b = 0; b < nb; b++) {
+        dequant_iq3_block(data + b * 98, tmp);
+        size_t cnt = n - b * 256 < 256 ? n - b * 256 : 256;
+        memcpy(out + b * 256, tmp, cnt * sizeof(float));
+    }
+    return 0;
+}
+
+/* The reference's generic dot_row fallback (quant/mod.rs:76-80):
+ * dequant then sequential sum of w*x. */
+int gqo_dot_iq3_xxs(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res) {
+    size_t nb = (n + 255) / 256;
+    if (nbytes < nb * 98) return GQO_ESHORT;
+    float tmp[256], acc = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        dequant_iq3_block(data + b * 98, tmp);
+        size_t cnt = n - b * 256 < 256 ? n - b * 256 : 256;
+        for (size_t i = 0; i < cnt; i++) acc += tmp[i] * x[b * 256 + i];
+    }
+    *res = acc;
+    return 0;
+}
+
+/* ------------------------------------------------------------- dispatchers */
+
+int gqo_dequant(int t, const uint8_t *d, size_t nb, size_t n, float *o) {
+    switch (t) {
+    case GQO_Q8_0: return gqo_dequant_q8_0(d, nb, n, o);
+    case GQO_Q4_K: return gqo_dequant_q4_k(d, nb, n, o);
+    case GQO_Q5_K: return gqo_dequant_q5_k(d, nb, n, o);
+    case GQO_Q6_K: return gqo_dequant_q6_k(d, nb, n, o);
+    case GQO_IQ3_XXS: return gqo_dequant_iq3_xxs(d, nb, n, o);
+    default: return GQO_EDTYPE;
+    }
+}
+
+/* quant/mod.rs:65-83 */
+int gqo_dot_row(int t, const uint8_t *d, size_t nb, const float *x, size_t n, float *r) {
+    switch (t) {
+    case GQO_Q8_0: return gqo_dot_q8_0(d, nb, x, n, r);
+    case GQO_Q4_K: return gqo_dot_q4_k(d, nb, x, n, r);
+    case GQO_Q5_K: return gqo_dot_q5_k(d, nb, x, n, r);
+    case GQO_Q6_K: return gqo_dot_q6_k(d, nb, x, n, r);
+    case GQO_IQ3_XXS: return gqo_dot_iq3_xxs(d, nb, x, n, r);
+    default: return GQO_EDTYPE;
+    }
+}
+
+/* -------------------------------------------------------------------- Q8_K */
+
+/* q8_k.rs:49-91 */
+void gqo_quantize_row_q8_k(const float *x, size_t n, float *d, int8_t *qs, int16_t *bsums) {
+    size_t nb = (n + 255) / 256;
+    memset(qs, 0, nb * 256);
+    for (size_t b = 0; b < nb; b++) {
+        size_t s = b * 256, e = s + 256 < n ? s + 256 : n;
+        float amax = 0.0f, mx = 0.0f;
+        for (size_t i = s; i < e; i++) {
+            float av = fabsf(x[i]);
+            if (av > amax) { amax = av; mx = x[i]; }
+        }
+        d[b] = 0.0f;
+        if (amax > 0.0f) {
+            float iscale = -127.0f / mx;
+            for (size_t i = s; i < e; i++) {
+                int r = (int)roundf(iscale * x[i]);
+                qs[i] = (int8_t)(r < 127 ? r : 127);
+            }
+            d[b] = 1.0f / iscale;
+        }
+        for (int g = 0; g < 16; g++) {
+            int16_t acc = 0;
+            for (int k = 0; k < 16; k++) acc = (int16_t)(acc + qs[b * 256 + g * 16 + k]);
+            bsums[b * 16 + g] = acc;
+        }
+    }
+}
+
+/* q5_k.rs:126-184 */
+int gqo_dot_q5_k_q8k(const uint8_t *data, size_t nbytes, size_t n, const float *dx8,
+                     const int8_t *xq, const int16_t *bsums, float *res) {
+    size_t nb = (n + 255) / 256;
+    if (nbytes < nb * 176) return GQO_ESHORT;
+    float sumf = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t *blk = data + b * 176;
+        float d = rd_f16(blk), dmin = rd_f16(blk + 2);
+        const uint8_t *scales = blk + 4, *qh = blk + 16, *qs = blk + 48;
+        const int8_t *xb = xq + b * 256;
+        const int16_t *bs = bsums + b * 16;
+        int32_t acc_pos = 0, acc_min = 0;
+        for (int is = 0; is < 8; is++) {
+            uint8_t sc, m;
+            gqo_get_scale_min_k4(is, scales, &sc, &m);
+            int32_t pos = 0;
+            for (int l = 0; l < 32; l++) {
+                uint8_t byte = qs[32 * (is / 2) + l];
+                int nib = (is % 2 == 0) ? (byte & 0xF) : (byte >> 4);
+                int hi = ((qh[l] >> is) & 1) << 4;
+                pos += (nib | hi) * (int32_t)xb[32 * is + l];
+            }
+            int32_t ms = (int32_t)bs[2 * is] + (int32_t)bs[2 * is + 1];
+            acc_pos += (int32_t)sc * pos;
+            acc_min += (int32_t)m * ms;
+        }
+        float t1 = d * (float)acc_pos;
+        float t2 = dmin * (float)acc_min;
+        sumf += dx8[b] * (t1 - t2);
+    }
+    *res = sumf;
+    return 0;
+}
+
+/* ------------------------------------------------------- per-32 Q8 pack */
+
+/* KvDtype::Q8_0::pack (model/mod.rs:574-583): scale = amax/127 (1.0 for an
+ * all-zero block), stored as f16; q = clamp(round(x / scale), -127, 127)
+ * with the f32 (unrounded) scale. */
+void gqo_quantize_q8_32(const float *x, size_t n, uint16_t *scale_f16, int8_t *q) {
+    size_t nb = (n + 31) / 32;
+    for (size_t b = 0; b < nb; b++) {
+        size_t s = b * 32, e = s + 32 < n ? s + 32 : n;
+        float amax = 0.0f;
+        for (size_t i = s; i < e; i++) amax = fmaxf(amax, fabsf(x[i]));
+        float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
+        scale_f16[b] = gqo_f32_to_f16(scale);
+        for (size_t i = s; i < e; i++) {
+            float r = roundf(x[i] / scale);
+            if (r < -127.0f) r = -127.0f;
+            if (r > 127.0f) r = 127.0f;
+            q[i] = (int8_t)r;
+        }
+        for (size_t i = e; i < s + 32; i++) q[i] = 0;
+    }
+}
+
+/* ------------------------------------------------------------ matmul_into */
+
+typedef struct {
+    int dtype;
+    const uint8_t *w;
+    size_t nbytes, in_dim, r0, r1, batch;
+    const float *x;
+    float *out;
+    int rc;
+} job_t;
+
+static void *matvec_job(void *p) {
+    job_t *j = (job_t *)p;
+    size_t rb = gqo_type_size(j->dtype, j->in_dim);
+    for (size_t r = j->r0; r < j->r1 && !j->rc; r++) {
+        size_t off = r * rb;
+        if (off + rb > j->nbytes) { j->rc = GQO_ESHORT; break; }
+        j->rc = gqo_dot_row(j->dtype, j->w + off, j->nbytes - off, j->x, j->in_dim, &j->out[r]);
+    }
+    return NULL;
+}
+
+static int hw_threads(int n) {
+    if (n > 0) return n;
+    long c = sysconf(_SC_NPROCESSORS_ONLN);
+    return c > 0 ? (int)c : 1;
+}
+
+static int run_jobs(job_t *proto, size_t rows, int nthreads, void *(*fn)(void *)) {
+    int nt = hw_threads(nthreads);
+    if ((size_t)nt > rows) nt = rows ? (int)rows : 1;
+    pthread_t th[256];
+    job_t jobs[256];
+    if (nt > 256) nt = 256;
+    size_t per = (rows + nt - 1) / nt;
+    for (int t = 0; t < nt; t++) {
+        jobs[t] = *proto;
+        jobs[t].r0 = (size_t)t * per < rows ? (size_t)t * per : rows;
+        jobs[t].r1 = jobs[t].r0 + per < rows ? jobs[t].r0 + per : rows;
+        jobs[t].rc = 0;
+        if (nt == 1) fn(&jobs[t]);
+        else pthread_create(&th[t], NULL, fn, &jobs[t]);
+    }
+    int rc = 0;
+    for (int t = 0; t < nt; t++) {
+        if (nt > 1) pthread_join(th[t], NULL);
+        if (jobs[t].rc && !rc) rc = jobs[t].rc;
+    }
+    return rc;
+}
+
+/* model/mod.rs:362-403 */
+int gqo_matmul_into(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
+                    float *out, size_t out_dim, int nthreads) {
+    if (!gqo_block_size(dtype) || dtype == GQO_F32 || dtype == GQO_F16 || dtype == GQO_BF16)
+        return GQO_EDTYPE;
+    job_t p = {dtype, w, nbytes, in_dim, 0, 0, 0, x, out, 0};
+    return run_jobs(&p, out_dim, nthreads, matvec_job);
+}
+
+/* cpu_backend.rs:38-65 */
+int gqo_matmul_dequant(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
+                       float *out, size_t out_dim) {
+    if (dtype != GQO_Q8_0 && dtype != GQO_Q4_K && dtype != GQO_Q5_K && dtype != GQO_Q6_K)
+        return GQO_EDTYPE;
+    size_t rb = gqo_type_size(dtype, in_dim);
+    for (size_t r = 0; r < out_dim; r++) {
+        size_t off = r * rb;
+        if (off > nbytes) return GQO_ESHORT;
+        int rc = gqo_dot_row(dtype, w + off, nbytes - off, x, in_dim, &out[r]);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+/* model/mod.rs:446-456: dequant row once, then per token a sequential sum */
+int gqo_matmul_batch_rows(int dtype, const uint8_t *w, size_t nbytes, const float *x,
+                          size_t in_dim, size_t batch, size_t r0, size_t r1, float *rowmajor) {
+    size_t rb = gqo_type_size(dtype, in_dim);
+    if (!rb) return GQO_EDTYPE;
+    float *wr = (float *)malloc(in_dim * sizeof(float));
+    int rc = 0;
+    for (size_t r = r0; r < r1 && !rc; r++) {
+        size_t off = r * rb;
+        if (off + rb > nbytes) { rc = GQO_ESHORT; break; }
+        rc = gqo_dequant(dtype, w + off, rb, in_dim, wr);
+        if (rc) break;
+        for (size_t t = 0; t < batch; t++) {
+            const float *xt = x + t * in_dim;
+            float s = 0.0f;
+            for (size_t i = 0; i < in_dim; i++) s += wr[i] * xt[i];
+            rowmajor[(r - r0) * batch + t] = s;
+        }
+    }
+    free(wr);
+    return rc;
+}
+
+static void *batch_job(void *p) {
+    job_t *j = (job_t *)p;
+    if (j->r1 > j->r0)
+        j->rc = gqo_matmul_batch_rows(j->dtype, j->w, j->nbytes, j->x, j->in_dim, j->batch, j->r0,
+                                      j->r1, j->out + j->r0 * j->batch);
+    return NULL;
+}
+
+/* model/mod.rs:414-464 */
+int gqo_matmul_batch_into(int dtype, const uint8_t *w, size_t nbytes, const float *x,
+                          size_t in_dim, size_t batch, float *out, size_t out_dim, int nthreads) {
+    float *rm = (float *)malloc(out_dim * batch * sizeof(float));
+    if (!rm) return GQO_ESHORT;
+    job_t p = {dtype, w, nbytes, in_dim, 0, 0, batch, x, rm, 0};
+    int rc = run_jobs(&p, out_dim, nthreads, batch_job);
+    if (!rc)
+        for (size_t r = 0; r < out_dim; r++)
+            for (size_t t = 0; t < batch; t++) out[t * out_dim + r] = rm[r * batch + t];
+    free(rm);
+    return rc;
+}
+
+/* sampler.rs:120-131 */
+size_t gqo_argmax(const float *xs, size_t n) {
+    size_t best = 0;
+    float bv = -INFINITY;
+    for (size_t i = 0; i < n; i++)
+        if (xs[i] > bv) { bv = xs[i]; best = i; }
+    return best;
+}

@@ -1,0 +1,97 @@
+/*
+ * gq_oracle.h -- CPU restatement of gguf-rs's quantized dequant-matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker and the
+ * timed CPU baseline.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it; the product library (libgq.so) never links
+ * or calls it.
+ *
+ * Every function restates one reference function (Rust crate gguf-rs,
+ * /root/reference/src/...) with the same arithmetic order, compiled with
+ * -ffp-contract=off so that no a*b+c is fused (Rust never contracts).
+ *
+ * Return codes: 0 = ok, GQO_ESHORT = buffer too short ("need N bytes"),
+ * GQO_EDTYPE = unsupported dtype, GQO_ERANGE = row out of range.
+ */
+#ifndef GQ_ORACLE_H
+#define GQ_ORACLE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GQO_ESHORT (-1)
+#define GQO_EDTYPE (-2)
+#define GQO_ERANGE (-3)
+
+/* GgmlType ids (types.rs:9-46). */
+enum { GQO_F32 = 0, GQO_F16 = 1, GQO_Q8_0 = 8, GQO_Q4_K = 12, GQO_Q5_K = 13,
+       GQO_Q6_K = 14, GQO_Q8_K = 15, GQO_IQ3_XXS = 18, GQO_BF16 = 30 };
+
+size_t gqo_block_size(int dtype);              /* types.rs:88-123 */
+size_t gqo_block_bytes(int dtype);             /* types.rs:126-161 */
+size_t gqo_type_size(int dtype, size_t n);     /* types.rs:164-168 */
+
+float    gqo_f16_to_f32(uint16_t h);           /* half::f16::to_f32 (exact) */
+uint16_t gqo_f32_to_f16(float f);              /* half::f16::from_f32 (RNE) */
+
+/* Per-format dequant of n elements from `data` (nbytes long). */
+int gqo_dequant_q8_0(const uint8_t *data, size_t nbytes, size_t n, float *out);
+int gqo_dequant_q4_k(const uint8_t *data, size_t nbytes, size_t n, float *out);
+int gqo_dequant_q5_k(const uint8_t *data, size_t nbytes, size_t n, float *out);
+int gqo_dequant_q6_k(const uint8_t *data, size_t nbytes, size_t n, float *out);
+int gqo_dequant_iq3_xxs(const uint8_t *data, size_t nbytes, size_t n, float *out);
+int gqo_dequant(int dtype, const uint8_t *data, size_t nbytes, size_t n, float *out);
+
+/* Fused dequant+dot of one row with x[n]. */
+int gqo_dot_q8_0(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res);
+int gqo_dot_q4_k(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res);
+int gqo_dot_q5_k(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res);
+int gqo_dot_q6_k(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res);
+int gqo_dot_iq3_xxs(const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res);
+int gqo_dot_row(int dtype, const uint8_t *data, size_t nbytes, const float *x, size_t n, float *res);
+
+/* Q4_K sub-block scale/min unpack (q4_k.rs:26-35). */
+void gqo_get_scale_min_k4(int j, const uint8_t *scales, uint8_t *sc, uint8_t *m);
+
+/* Q8_K activation quantizer (q8_k.rs:49-91): d[nblk], qs[nblk*256], bsums[nblk*16]. */
+void gqo_quantize_row_q8_k(const float *x, size_t n, float *d, int8_t *qs, int16_t *bsums);
+int  gqo_dot_q5_k_q8k(const uint8_t *data, size_t nbytes, size_t n, const float *d,
+                      const int8_t *qs, const int16_t *bsums, float *res);
+
+/* Per-32 Q8 activation pack (KvDtype::Q8_0::pack, model/mod.rs:574-583):
+ * scale_f16[n/32], q[n] (int8).  Used for the int8 prefill GEMM. */
+void gqo_quantize_q8_32(const float *x, size_t n, uint16_t *scale_f16, int8_t *q);
+
+/* IQ3_XXS codebook in use (256 x uint32, 4 magnitude bytes each). */
+void gqo_set_iq3xxs_grid(const uint32_t *grid);
+void gqo_get_iq3xxs_grid(uint32_t *grid);
+
+/* WeightMap::matmul_into (model/mod.rs:362-403): out[r] = dot_row(W, r, x),
+ * rows partitioned over nthreads (0 = hardware concurrency). */
+int gqo_matmul_into(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
+                    float *out, size_t out_dim, int nthreads);
+
+/* CpuBackend::matmul_dequant (cpu_backend.rs:38-65): serial row loop. */
+int gqo_matmul_dequant(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
+                       float *out, size_t out_dim);
+
+/* WeightMap::matmul_batch_into (model/mod.rs:414-464): X [batch][in_dim]
+ * token-major -> Y [batch][out_dim] token-major; dequant each row once,
+ * sequential f32 sum per token. */
+int gqo_matmul_batch_into(int dtype, const uint8_t *w, size_t nbytes, const float *x,
+                          size_t in_dim, size_t batch, float *out, size_t out_dim, int nthreads);
+
+/* Same, over rows [r0, r1) only, writing rowmajor[r - r0][batch]. */
+int gqo_matmul_batch_rows(int dtype, const uint8_t *w, size_t nbytes, const float *x,
+                          size_t in_dim, size_t batch, size_t r0, size_t r1, float *rowmajor);
+
+/* argmax, first maximum wins (sampler.rs:120-131). */
+size_t gqo_argmax(const float *xs, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

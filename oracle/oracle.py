@@ -1,0 +1,180 @@
+"""ctypes wrapper of liboracle.so -- TEST INFRASTRUCTURE ONLY.
+
+The CPU restatement of gguf-rs's quant path (gq_oracle.c).  Only tests/,
+__graft_entry__.smoke() and bench.py's cpu_baseline leg use it, always as
+the checker or the timed CPU baseline, never as the product path.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+_P, _I, _SZ = ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t
+
+
+def build():
+    subprocess.run(["make", "-B", "-C", _HERE, "liboracle.so"], check=True,
+                   capture_output=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        sig = {
+            "gqo_type_size": (_SZ, [_I, _SZ]),
+            "gqo_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
+            "gqo_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "gqo_dequant": (_I, [_I, _P, _SZ, _SZ, _P]),
+            "gqo_dot_row": (_I, [_I, _P, _SZ, _P, _SZ, _P]),
+            "gqo_get_scale_min_k4": (None, [_I, _P, _P, _P]),
+            "gqo_quantize_row_q8_k": (None, [_P, _SZ, _P, _P, _P]),
+            "gqo_dot_q5_k_q8k": (_I, [_P, _SZ, _SZ, _P, _P, _P, _P]),
+            "gqo_quantize_q8_32": (None, [_P, _SZ, _P, _P]),
+            "gqo_set_iq3xxs_grid": (None, [_P]),
+            "gqo_get_iq3xxs_grid": (None, [_P]),
+            "gqo_matmul_into": (_I, [_I, _P, _SZ, _P, _SZ, _P, _SZ, _I]),
+            "gqo_matmul_dequant": (_I, [_I, _P, _SZ, _P, _SZ, _P, _SZ]),
+            "gqo_matmul_batch_into": (_I, [_I, _P, _SZ, _P, _SZ, _SZ, _P, _SZ, _I]),
+            "gqo_argmax": (_SZ, [_P, _SZ]),
+        }
+        for n, (r, a) in sig.items():
+            f = getattr(L, n)
+            f.restype = r
+            f.argtypes = a
+        _lib = L
+    return _lib
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def _p(a):
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def _chk(rc):
+    if rc != 0:
+        raise OracleError({-1: "short buffer", -2: "unsupported dtype", -3: "row range"}.get(rc, rc))
+
+
+def f16_to_f32(bits):
+    return lib().gqo_f16_to_f32(int(bits))
+
+
+def f32_to_f16(v):
+    return lib().gqo_f32_to_f16(float(v))
+
+
+def type_size(dtype, n):
+    return lib().gqo_type_size(dtype, n)
+
+
+def dequant(dtype, data, n):
+    data = np.ascontiguousarray(data, np.uint8)
+    out = np.empty(n, np.float32)
+    _chk(lib().gqo_dequant(dtype, _p(data), data.nbytes, n, _p(out)))
+    return out
+
+
+def dequant_rows(dtype, w2d, in_dim):
+    return np.stack([dequant(dtype, w2d[r], in_dim) for r in range(w2d.shape[0])]) \
+        if w2d.shape[0] else np.zeros((0, in_dim), np.float32)
+
+
+def dot_row(dtype, data, x):
+    data = np.ascontiguousarray(data, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    r = np.zeros(1, np.float32)
+    _chk(lib().gqo_dot_row(dtype, _p(data), data.nbytes, _p(x), x.size, _p(r)))
+    return float(r[0])
+
+
+def get_scale_min_k4(j, scales):
+    s = np.ascontiguousarray(scales, np.uint8)
+    sc = np.zeros(1, np.uint8)
+    m = np.zeros(1, np.uint8)
+    lib().gqo_get_scale_min_k4(j, _p(s), _p(sc), _p(m))
+    return int(sc[0]), int(m[0])
+
+
+def quantize_row_q8_k(x):
+    x = np.ascontiguousarray(x, np.float32)
+    nb = (x.size + 255) // 256
+    d = np.zeros(nb, np.float32)
+    qs = np.zeros(nb * 256, np.int8)
+    bs = np.zeros(nb * 16, np.int16)
+    lib().gqo_quantize_row_q8_k(_p(x), x.size, _p(d), _p(qs), _p(bs))
+    return d, qs, bs
+
+
+def dot_q5_k_q8k(data, n, d, qs, bs):
+    data = np.ascontiguousarray(data, np.uint8)
+    r = np.zeros(1, np.float32)
+    _chk(lib().gqo_dot_q5_k_q8k(_p(data), data.nbytes, n, _p(d), _p(qs), _p(bs), _p(r)))
+    return float(r[0])
+
+
+def quantize_q8_32(x):
+    x = np.ascontiguousarray(x, np.float32)
+    nb = (x.size + 31) // 32
+    sc = np.zeros(nb, np.uint16)
+    q = np.zeros(nb * 32, np.int8)
+    lib().gqo_quantize_q8_32(_p(x), x.size, _p(sc), _p(q))
+    return sc, q[: x.size]
+
+
+def set_iq3xxs_grid(grid=None):
+    if grid is None:
+        lib().gqo_set_iq3xxs_grid(None)
+    else:
+        g = np.ascontiguousarray(grid, np.uint32)
+        lib().gqo_set_iq3xxs_grid(_p(g))
+
+
+def get_iq3xxs_grid():
+    g = np.zeros(256, np.uint32)
+    lib().gqo_get_iq3xxs_grid(_p(g))
+    return g
+
+
+def matmul_into(dtype, w, x, out_dim, nthreads=0):
+    """WeightMap::matmul_into: threaded row-parallel fused dot."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(out_dim, np.float32)
+    _chk(lib().gqo_matmul_into(dtype, _p(w), w.nbytes, _p(x), x.size, _p(out), out_dim, nthreads))
+    return out
+
+
+def matmul_dequant(dtype, w, x, out_dim):
+    """CpuBackend::matmul_dequant: serial rows."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(out_dim, np.float32)
+    _chk(lib().gqo_matmul_dequant(dtype, _p(w), w.nbytes, _p(x), x.size, _p(out), out_dim))
+    return out
+
+
+def matmul_batch_into(dtype, w, X, out_dim, nthreads=0):
+    """WeightMap::matmul_batch_into: X [batch][in_dim] -> [batch][out_dim]."""
+    w = np.ascontiguousarray(w, np.uint8)
+    X = np.ascontiguousarray(X, np.float32)
+    batch, in_dim = X.shape
+    out = np.zeros((batch, out_dim), np.float32)
+    _chk(lib().gqo_matmul_batch_into(dtype, _p(w), w.nbytes, _p(X), in_dim, batch, _p(out),
+                                     out_dim, nthreads))
+    return out
+
+
+def argmax(xs):
+    xs = np.ascontiguousarray(xs, np.float32)
+    return int(lib().gqo_argmax(_p(xs), xs.size))

@@ -1,0 +1,156 @@
+"""Independent numpy restatements of the ggml block formats (test helpers).
+
+Written from the block layouts (float32 arithmetic, one rounding per
+operation, no FMA), not from the C oracle, so that a mistake in either one
+shows up as a mismatch.  Used to pin the oracle and, on the GPU, as a second
+opinion on dequant.
+"""
+import numpy as np
+
+
+def f16(u16):
+    return np.asarray(u16, np.uint16).view(np.float16).astype(np.float32)
+
+
+def round_half_away(v):
+    v = np.asarray(v, np.float64)
+    return np.sign(v) * np.floor(np.abs(v) + 0.5)
+
+
+def unpack_k4_scales(s):
+    """s: uint8 [..., 12] -> (sc, m) uint8 [..., 8]; ggml's 6-bit packing."""
+    s = s.astype(np.uint8)
+    sc = np.empty(s.shape[:-1] + (8,), np.uint8)
+    m = np.empty_like(sc)
+    sc[..., :4] = s[..., 0:4] & 63
+    m[..., :4] = s[..., 4:8] & 63
+    sc[..., 4:] = (s[..., 8:12] & 0x0F) | ((s[..., 0:4] >> 6) << 4)
+    m[..., 4:] = (s[..., 8:12] >> 4) | ((s[..., 4:8] >> 6) << 4)
+    return sc, m
+
+
+def dequant_q8_0(data, n):
+    nb = (n + 31) // 32
+    b = np.asarray(data, np.uint8)[: nb * 34].reshape(nb, 34)
+    d = f16(b[:, 0:2].copy().view(np.uint16)[:, 0])
+    q = b[:, 2:].view(np.int8).astype(np.float32)
+    return (d[:, None] * q).reshape(-1)[:n]
+
+
+def dequant_k4(data, n, q5=False):
+    bb = 176 if q5 else 144
+    nb = (n + 255) // 256
+    b = np.asarray(data, np.uint8)[: nb * bb].reshape(nb, bb)
+    d = f16(b[:, 0:2].copy().view(np.uint16)[:, 0])
+    dmin = f16(b[:, 2:4].copy().view(np.uint16)[:, 0])
+    sc, m = unpack_k4_scales(b[:, 4:16])
+    qs = b[:, 48:176] if q5 else b[:, 16:144]
+    qh = b[:, 16:48] if q5 else None
+    y = np.empty((nb, 256), np.float32)
+    for g in range(4):                      # 64-element groups
+        byte = qs[:, 32 * g:32 * g + 32]
+        for half in range(2):               # low nibbles, then high nibbles
+            sub = 2 * g + half
+            q = (byte >> 4) if half else (byte & 0x0F)
+            if q5:
+                q = q | (((qh >> sub) & 1) << 4)
+            scale = d * sc[:, sub].astype(np.float32)
+            mn = dmin * m[:, sub].astype(np.float32)
+            y[:, 64 * g + 32 * half:64 * g + 32 * half + 32] = \
+                scale[:, None] * q.astype(np.float32) - mn[:, None]
+    return y.reshape(-1)[:n]
+
+
+def dequant_q6_k(data, n):
+    nb = (n + 255) // 256
+    b = np.asarray(data, np.uint8)[: nb * 210].reshape(nb, 210)
+    ql, qh = b[:, 0:128], b[:, 128:192]
+    sc = b[:, 192:208].view(np.int8).astype(np.float32)
+    d = f16(b[:, 208:210].copy().view(np.uint16)[:, 0])
+    y = np.empty((nb, 256), np.float32)
+    for half in range(2):
+        for quarter in range(4):            # 32-element run within the half
+            low = ql[:, 64 * half + 32 * (quarter & 1): 64 * half + 32 * (quarter & 1) + 32]
+            low = (low >> 4) if quarter >= 2 else (low & 0x0F)
+            high = (qh[:, 32 * half:32 * half + 32] >> (2 * quarter)) & 3
+            q = (low | (high << 4)).astype(np.int32) - 32
+            for sixteen in range(2):
+                s = sc[:, 8 * half + 2 * quarter + sixteen]
+                lo = 16 * sixteen
+                y[:, 128 * half + 32 * quarter + lo:128 * half + 32 * quarter + lo + 16] = \
+                    (d * s)[:, None] * q[:, lo:lo + 16].astype(np.float32)
+    return y.reshape(-1)[:n]
+
+
+def ksigns():
+    i = np.arange(128, dtype=np.uint32)
+    par = np.array([bin(v).count("1") & 1 for v in range(128)], np.uint32)
+    return (i | (par << 7)).astype(np.uint8)
+
+
+def dequant_iq3_xxs(data, n, grid):
+    nb = (n + 255) // 256
+    b = np.asarray(data, np.uint8)[: nb * 98].reshape(nb, 98)
+    d = f16(b[:, 0:2].copy().view(np.uint16)[:, 0])
+    qs = b[:, 2:66]
+    aux = b[:, 66:98].copy().view(np.uint32)          # [nb, 8]
+    mags = np.asarray(grid, np.uint32)[qs.astype(np.int64)]  # [nb, 64]
+    mag_bytes = mags.view(np.uint8).reshape(nb, 64, 4).astype(np.float32)  # 4 per index
+    ks = ksigns()
+    y = np.empty((nb, 256), np.float32)
+    for ib in range(8):
+        a = aux[:, ib]
+        db = d * (np.float32(0.5) + (a >> 28).astype(np.float32)) * np.float32(0.5)
+        for l in range(4):
+            sg = ks[(a >> (7 * l)) & 127]
+            for j in range(8):
+                mag = mag_bytes[:, 8 * ib + 2 * l + j // 4, j % 4]
+                sign = np.where((sg >> j) & 1, np.float32(-1), np.float32(1))
+                y[:, 32 * ib + 8 * l + j] = (db * mag) * sign
+    return y.reshape(-1)[:n]
+
+
+def dequant(dtype, data, n, grid=None):
+    if dtype == 8:
+        return dequant_q8_0(data, n)
+    if dtype == 12:
+        return dequant_k4(data, n)
+    if dtype == 13:
+        return dequant_k4(data, n, q5=True)
+    if dtype == 14:
+        return dequant_q6_k(data, n)
+    if dtype == 18:
+        return dequant_iq3_xxs(data, n, grid)
+    raise ValueError(dtype)
+
+
+def quantize_q8_32(x):
+    """KvDtype::Q8_0::pack (src/model/mod.rs:574-583)."""
+    x = np.asarray(x, np.float32).reshape(-1, 32)
+    amax = np.abs(x).max(axis=1)
+    scale = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    q = round_half_away((x / scale[:, None]).astype(np.float32))
+    q = np.clip(q, -127, 127).astype(np.int8)
+    return scale.astype(np.float16).view(np.uint16), q.reshape(-1)
+
+
+def quantize_row_q8_k(x):
+    """quantize_row_q8_k (src/quant/q8_k.rs:49-91)."""
+    x = np.asarray(x, np.float32)
+    n = x.size
+    nb = (n + 255) // 256
+    xp = np.zeros(nb * 256, np.float32)
+    xp[:n] = x
+    xb = xp.reshape(nb, 256)
+    d = np.zeros(nb, np.float32)
+    qs = np.zeros((nb, 256), np.int8)
+    for b in range(nb):
+        v = xb[b, : min(256, n - 256 * b)]
+        i = int(np.argmax(np.abs(v)))        # first index of the max |v|
+        if np.abs(v[i]) > 0:
+            iscale = np.float32(-127.0) / v[i]
+            r = round_half_away((iscale * v).astype(np.float32))
+            qs[b, : v.size] = np.minimum(r, 127).astype(np.int8)
+            d[b] = np.float32(1.0) / iscale
+    bs = qs.reshape(nb, 16, 16).astype(np.int16).sum(axis=2).reshape(-1)
+    return d, qs.reshape(-1), bs.astype(np.int16)
