@@ -70,6 +70,10 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise GqError(-6, f"{LIB_PATH} not built; run __graft_entry__.build()")
+        # Load torch (and with it torch's HIP runtime) first, so that libgq
+        # binds to the same libamdhip64 instance instead of loading a second
+        # HIP runtime into the process.
+        import torch  # noqa: F401
         L = ctypes.CDLL(LIB_PATH)
         for name, (res, args) in SIGNATURES.items():
             f = getattr(L, name)

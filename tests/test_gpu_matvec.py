@@ -188,7 +188,7 @@ def test_matmul_dequant_errors(backend):
 def test_iq3_custom_grid(backend, orc):
     import torch
     say("iq3 custom grid")
-    grid = (np.arange(256, dtype=np.uint32) * 2654435761 % (1 << 32)).astype(np.uint32)
+    grid = (np.arange(256, dtype=np.uint64) * 2654435761 % (1 << 32)).astype(np.uint32)
     grid = (grid & 0x3F3F3F3F).astype(np.uint32)
     backend.set_iq3xxs_grid(grid)
     orc.set_iq3xxs_grid(grid)
