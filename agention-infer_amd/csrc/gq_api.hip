@@ -12,6 +12,7 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <algorithm>
 
 #include "../../include/gq.h"
 #include "gq_device.h"
@@ -113,9 +114,9 @@ const char *type_name(int t) {
 
 int check_matvec(const gq_weight *w) {
   if (!w) return fail(GQ_EINVAL, "null weight handle");
-  const int kpad = w->nb * gq::block_elems(w->dtype);
-  if (gq::matvec_lds_bytes(kpad) > 160 * 1024)
-    return fail(GQ_EINVAL, "in_dim %d too large for the LDS-staged matvec", w->in_dim);
+  const int part = (w->L.rt * w->L.units + 63) / 64 * 64;
+  if (gq::matvec_lds_bytes(w->L.dtype, w->L.units, part) > 160 * 1024)
+    return fail(GQ_EINVAL, "in_dim %d too large for the LDS-staged matvec", w->L.k);
   return GQ_OK;
 }
 
@@ -137,17 +138,18 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   if (out_dim > 0 && !src) return fail(GQ_EINVAL, "null weight data");
 
   gq_weight *w = new gq_weight();
-  w->dtype = dtype;
-  w->in_dim = in_dim;
-  w->out_dim = out_dim;
-  w->nb = nb;
-  w->stride = (long)nb * gq::body_block_bytes(dtype);
+  w->L.dtype = dtype;
+  w->L.rows = out_dim;
+  w->L.k = in_dim;
+  w->L.units = (in_dim + 255) / 256;
+  w->L.chunks = gq::unit_chunks(dtype);
+  w->L.rt = gq::choose_rt(dtype, out_dim, w->L.units);
   w->ggml_bytes = need;
   w->device = g_dev.device;
-  const size_t body_bytes = (size_t)w->stride * out_dim;
-  const size_t d_bytes = gq::has_d_array(dtype) ? (size_t)nb * out_dim * 2 : 0;
-  // One allocation: body, then the scale array (kept 256 B aligned).
-  const size_t d_off = (body_bytes + 255) & ~(size_t)255;
+  const size_t body = (size_t)gq::body_bytes(w->L);
+  const bool has_d = dtype == gq::T_Q6_K || dtype == gq::T_IQ3_XXS;
+  const size_t d_bytes = has_d ? (size_t)w->L.rows * w->L.units * 2 : 0;
+  const size_t d_off = (body + 255) & ~(size_t)255;
   uint8_t *mem = nullptr;
   if (hipMalloc(&mem, d_off + d_bytes + 256) != hipSuccess) {
     delete w;
@@ -156,11 +158,7 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   w->body = mem;
   w->d = d_bytes ? (uint16_t *)(mem + d_off) : nullptr;
   hipError_t e = hipSuccess;
-  if (!gq::has_d_array(dtype)) {
-    if (need)
-      e = hipMemcpy(w->body, src, need, src_on_device ? hipMemcpyDeviceToDevice
-                                                      : hipMemcpyHostToDevice);
-  } else if (need) {
+  if (need) {
     const uint8_t *raw = (const uint8_t *)src;
     uint8_t *tmp = nullptr;
     if (!src_on_device) {
@@ -168,7 +166,7 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
       if (e == hipSuccess) e = hipMemcpy(tmp, src, need, hipMemcpyHostToDevice);
       raw = tmp;
     }
-    if (e == hipSuccess) e = gq::launch_repack(dtype, raw, out_dim, nb, w->body, w->d, 0);
+    if (e == hipSuccess) e = gq::launch_repack(w->L, raw, w->body, w->d, 0);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (tmp) (void)hipFree(tmp);
   }
@@ -220,9 +218,9 @@ int gq_weight_free(gq_weight *w) {
 
 int gq_weight_shape(const gq_weight *w, int *dtype, int *in_dim, int *out_dim) {
   if (!w) return fail(GQ_EINVAL, "null weight handle");
-  if (dtype) *dtype = w->dtype;
-  if (in_dim) *in_dim = w->in_dim;
-  if (out_dim) *out_dim = w->out_dim;
+  if (dtype) *dtype = w->L.dtype;
+  if (in_dim) *in_dim = w->L.k;
+  if (out_dim) *out_dim = w->L.rows;
   return GQ_OK;
 }
 
@@ -235,9 +233,9 @@ int gq_matvec_multi(const gq_weight *const *ws, int count, const float *x_dev,
   if (count <= 0 || !ws || !y_dev) return fail(GQ_EINVAL, "empty weight list");
   for (int i = 0; i < count; i++) {
     if ((rc = check_matvec(ws[i]))) return rc;
-    if (ws[i]->dtype != ws[0]->dtype || ws[i]->in_dim != ws[0]->in_dim)
+    if (ws[i]->L.dtype != ws[0]->L.dtype || ws[i]->L.k != ws[0]->L.k)
       return fail(GQ_EINVAL, "gq_matvec_multi: weights must share dtype and in_dim");
-    if (ws[i]->out_dim > 0 && !y_dev[i]) return fail(GQ_EINVAL, "null output %d", i);
+    if (ws[i]->L.rows > 0 && !y_dev[i]) return fail(GQ_EINVAL, "null output %d", i);
   }
   if (!x_dev) return fail(GQ_EINVAL, "null x");
   const gq_weight *w0 = ws[0];
@@ -245,18 +243,23 @@ int gq_matvec_multi(const gq_weight *const *ws, int count, const float *x_dev,
     gq::MvArgs a{};
     a.x = x_dev;
     a.grid = g_dev.grid;
-    a.k = w0->in_dim;
-    a.nb = w0->nb;
-    a.kpad = w0->nb * gq::block_elems(w0->dtype);
-    int rows = 0, ns = 0;
-    for (int i = base; i < count && ns < gq::MV_MAX_SEG; i++, ns++) {
-      a.seg[ns] = gq::MvSeg{ws[i]->body, ws[i]->d, y_dev[i], ws[i]->stride, rows};
-      rows += ws[i]->out_dim;
+    a.k = w0->L.k;
+    a.units = w0->L.units;
+    a.chunks = w0->L.chunks;
+    int tiles = 0, ns = 0, part = 64;
+    for (int i = base; i < count && ns < gq::MV_MAX_SEG; i++) {
+      const gq_weight *w = ws[i];
+      if (w->L.rows == 0) continue;
+      a.seg[ns++] = gq::MvSeg{w->body, w->d, y_dev[i], w->L.rows, w->L.rt, tiles};
+      tiles += gq::num_tiles(w->L);
+      const int uit = w->L.rt * w->L.units;
+      part = std::max(part, (uit + 63) / 64 * 64);
     }
+    if (ns == 0) continue;
     a.nseg = ns;
-    a.total_rows = rows;
-    if (rows == 0) continue;
-    hipError_t e = gq::launch_matvec(a, w0->dtype, g_dev.num_cus, (hipStream_t)stream);
+    a.total_tiles = tiles;
+    a.part_floats = part;
+    hipError_t e = gq::launch_matvec(a, w0->L.dtype, (hipStream_t)stream);
     if (e != hipSuccess) return fail(GQ_EHIP, "matvec launch failed: %s", hipGetErrorString(e));
   }
   return GQ_OK;
@@ -272,18 +275,18 @@ int gq_matmul_dequant_preloaded(const gq_weight *w, const float *x_host, float *
   int rc = ensure_init();
   if (rc) return rc;
   if ((rc = check_matvec(w))) return rc;
-  if (w->out_dim == 0) return GQ_OK;
+  if (w->L.rows == 0) return GQ_OK;
   if (!x_host || !out_host) return fail(GQ_EINVAL, "null x or out");
   float *xd = nullptr, *yd = nullptr;
-  HIP_TRY(hipMalloc(&xd, (size_t)w->in_dim * 4));
-  if (hipMalloc(&yd, (size_t)w->out_dim * 4) != hipSuccess) {
+  HIP_TRY(hipMalloc(&xd, (size_t)w->L.k * 4));
+  if (hipMalloc(&yd, (size_t)w->L.rows * 4) != hipSuccess) {
     (void)hipFree(xd);
     return fail(GQ_ENOMEM, "hipMalloc failed");
   }
-  hipError_t e = hipMemcpy(xd, x_host, (size_t)w->in_dim * 4, hipMemcpyHostToDevice);
+  hipError_t e = hipMemcpy(xd, x_host, (size_t)w->L.k * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
     rc = gq_matvec(w, xd, yd, nullptr);
-    if (!rc) e = hipMemcpy(out_host, yd, (size_t)w->out_dim * 4, hipMemcpyDeviceToHost);
+    if (!rc) e = hipMemcpy(out_host, yd, (size_t)w->L.rows * 4, hipMemcpyDeviceToHost);
   }
   (void)hipFree(xd);
   (void)hipFree(yd);
@@ -310,9 +313,9 @@ int gq_dequant_rows(const gq_weight *w, int row0, int nrows, float *out_dev, voi
   int rc = ensure_init();
   if (rc) return rc;
   if (!w) return fail(GQ_EINVAL, "null weight handle");
-  if (row0 < 0 || nrows < 0 || row0 + nrows > w->out_dim)
+  if (row0 < 0 || nrows < 0 || row0 + nrows > w->L.rows)
     return fail(GQ_EINVAL, "row index %d out of range (tensor has %d rows)", row0 + nrows - 1,
-                w->out_dim);
+                w->L.rows);
   if (nrows == 0) return GQ_OK;
   hipError_t e = gq::launch_dequant(w, g_dev.grid, row0, nrows, out_dev, (hipStream_t)stream);
   if (e != hipSuccess) return fail(GQ_EHIP, "dequant launch failed: %s", hipGetErrorString(e));
@@ -333,7 +336,13 @@ int gq_set_iq3xxs_grid(const uint32_t *grid_host) {
   int rc = ensure_init();
   if (rc) return rc;
   std::lock_guard<std::mutex> lk(g_mu);
-  if (grid_host) memcpy(g_dev.grid_host, grid_host, 1024);
+  if (grid_host) {
+    // magnitudes enter signed 8-bit dot products: each byte must be < 128
+    for (int i = 0; i < 256; i++)
+      if (grid_host[i] & 0x80808080u)
+        return fail(GQ_EINVAL, "IQ3_XXS grid entry %d has a magnitude byte >= 128", i);
+    memcpy(g_dev.grid_host, grid_host, 1024);
+  }
   else default_grid(g_dev.grid_host);
   HIP_TRY(hipMemcpy(g_dev.grid, g_dev.grid_host, 1024, hipMemcpyHostToDevice));
   return GQ_OK;
@@ -353,12 +362,12 @@ int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mod
   if (rc) return rc;
   if (!w) return fail(GQ_EINVAL, "null weight handle");
   if (n < 0) return fail(GQ_EINVAL, "negative batch");
-  if (n == 0 || w->out_dim == 0) return GQ_OK;
+  if (n == 0 || w->L.rows == 0) return GQ_OK;
   if (mode != GQ_GEMM_BF16 && mode != GQ_GEMM_INT8) return fail(GQ_EINVAL, "bad gemm mode %d", mode);
   const size_t ws = gq::gemm_workspace_bytes(w, n, mode);
   if (ws == (size_t)-1)
     return fail(GQ_EDTYPE, "gq_gemm: %s weights with in_dim %d not supported in this mode",
-                type_name(w->dtype), w->in_dim);
+                type_name(w->L.dtype), w->L.k);
   void *wsp = nullptr;
   if (ws) HIP_TRY(hipMallocAsync(&wsp, ws, (hipStream_t)stream));
   hipError_t e = gq::launch_gemm(w, X_dev, n, Y_dev, mode, wsp, ws, g_dev.num_cus,

@@ -13,97 +13,117 @@
 namespace gq {
 
 // ------------------------------------------------------------------ repack
-// One thread per (row, block): split the ggml block into the body and the
-// separate f16 scale array (Q6_K, Q8_0, IQ3_XXS); plain copy otherwise.
-__global__ void k_repack(int dtype, const uint8_t *raw, long nblocks, uint8_t *body,
-                         uint16_t *dd) {
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= nblocks) return;
-  const int gb = ggml_block_bytes(dtype), bb = body_block_bytes(dtype);
-  const uint8_t *src = raw + i * gb;
-  uint8_t *dst = body + i * bb;
-  int off = 0;
-  if (dtype == T_Q6_K) {
-    dd[i] = (uint16_t)(src[208] | (src[209] << 8));
-  } else if (dtype == T_Q8_0 || dtype == T_IQ3_XXS) {
-    dd[i] = (uint16_t)(src[0] | (src[1] << 8));
-    off = 2;
+// Byte o of the logical bytes of unit `u` of row r, read from the raw ggml
+// row (nb ggml blocks).  Q8_0 units past the row's last block read zero.
+__device__ inline uint8_t logical_byte(int dtype, const uint8_t *row, int nb, int u, int o) {
+  switch (dtype) {
+  case T_Q4_K: return row[u * 144 + o];
+  case T_Q5_K: return row[u * 176 + o];
+  case T_Q6_K: return row[u * 210 + o];
+  case T_IQ3_XXS: return row[u * 98 + 2 + o];
+  default: {  // Q8_0: qs of blocks 8u..8u+7, then their d's
+    const int b = 8 * u + (o < 256 ? o >> 5 : (o - 256) >> 1);
+    if (b >= nb) return 0;
+    return o < 256 ? row[b * 34 + 2 + (o & 31)] : row[b * 34 + ((o - 256) & 1)];
   }
-  for (int k = 0; k < bb; k++) dst[k] = src[off + k];
+  }
 }
 
-hipError_t launch_repack(int dtype, const uint8_t *raw, long rows, int nb, uint8_t *body,
-                         uint16_t *d, hipStream_t st) {
-  const long n = rows * nb;
+// One thread per (row, unit): scatter the unit's chunks into the layout.
+__global__ void k_repack(Layout L, const uint8_t *raw, long raw_row_bytes, int nb, uint8_t *body,
+                         uint16_t *dd) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)L.rows * L.units) return;
+  const int r = (int)(i / L.units), u = (int)(i % L.units);
+  const uint8_t *row = raw + (long)r * raw_row_bytes;
+  const int t = r / L.rt, j = (r % L.rt) * L.units + u;
+  for (int c = 0; c < L.chunks; c++) {
+    uint8_t *dst = body + chunk_offset(L, t, j, c);
+    for (int k = 0; k < 16; k++) dst[k] = logical_byte(L.dtype, row, nb, u, 16 * c + k);
+  }
+  if (dd) {
+    const uint8_t *b = L.dtype == T_Q6_K ? row + u * 210 + 208 : row + u * 98;
+    dd[unit_index(L, t, j)] = (uint16_t)(b[0] | (b[1] << 8));
+  }
+}
+
+hipError_t launch_repack(const Layout &L, const uint8_t *raw, uint8_t *body, uint16_t *d,
+                         hipStream_t st) {
+  const long n = (long)L.rows * L.units;
   if (n == 0) return hipSuccess;
-  const long blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(k_repack, dim3((unsigned)blocks), dim3(256), 0, st, dtype, raw, n, body, d);
+  const int be = block_elems(L.dtype);
+  const int nb = (L.k + be - 1) / be;
+  const long raw_row = (long)nb * ggml_block_bytes(L.dtype);
+  hipLaunchKernelGGL(k_repack, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, L, raw,
+                     raw_row, nb, body, d);
   return hipGetLastError();
 }
 
 // ----------------------------------------------------------------- dequant
-__device__ float dq_element(int dtype, const uint8_t *bp, const uint16_t *dp, int e,
-                            const uint32_t *grid) {
+// Element e (0..255) of a unit whose logical bytes are read through `lb`.
+template <typename LB>
+__device__ float dq_element(int dtype, const LB &lb, uint32_t dbits, int e, const uint32_t *grid) {
   if (dtype == T_Q8_0) {
-    const float scale = h2f(*dp);
-    return scale * (float)(int8_t)bp[e];
+    const int b = e >> 5;
+    const float scale = h2f(lb(256 + 2 * b) | (lb(257 + 2 * b) << 8));
+    return scale * (float)(int8_t)lb(e);
   }
   if (dtype == T_Q4_K || dtype == T_Q5_K) {
-    const float d = h2f(bp[0] | (bp[1] << 8)), dmin = h2f(bp[2] | (bp[3] << 8));
-    const uint32_t s0 = bp[4] | (bp[5] << 8) | (bp[6] << 16) | ((uint32_t)bp[7] << 24);
-    const uint32_t s1 = bp[8] | (bp[9] << 8) | (bp[10] << 16) | ((uint32_t)bp[11] << 24);
-    const uint32_t s2 = bp[12] | (bp[13] << 8) | (bp[14] << 16) | ((uint32_t)bp[15] << 24);
+    const float d = h2f(lb(0) | (lb(1) << 8)), dmin = h2f(lb(2) | (lb(3) << 8));
+    uint32_t sw[3];
+    for (int w = 0; w < 3; w++)
+      sw[w] = lb(4 + 4 * w) | (lb(5 + 4 * w) << 8) | (lb(6 + 4 * w) << 16) |
+              ((uint32_t)lb(7 + 4 * w) << 24);
     const int j = e / 64, w = e % 64, l = w % 32;
     const int is = 2 * j + (w >= 32);
     uint32_t sc, m;
-    scale_min_k4(is, s0, s1, s2, sc, m);
-    const uint8_t *qs = bp + (dtype == T_Q5_K ? 48 : 16) + 32 * j;
-    uint32_t q = w < 32 ? (qs[l] & 0xF) : (qs[l] >> 4);
-    if (dtype == T_Q5_K) q += ((bp[16 + l] >> is) & 1u) << 4;
+    scale_min_k4(is, sw[0], sw[1], sw[2], sc, m);
+    const int qs = (dtype == T_Q5_K ? 48 : 16) + 32 * j;
+    uint32_t q = w < 32 ? (lb(qs + l) & 0xF) : (lb(qs + l) >> 4);
+    if (dtype == T_Q5_K) q += ((lb(16 + l) >> is) & 1u) << 4;
     const float dl = d * (float)sc;
     const float ml = dmin * (float)m;
     return dl * (float)q - ml;
   }
   if (dtype == T_Q6_K) {
-    const float d = h2f(*dp);
+    const float d = h2f(dbits);
     const int h = e / 128, t = (e % 128) / 32, l = e % 32;
-    const uint8_t *ql = bp + 64 * h, *qh = bp + 128 + 32 * h;
-    const int8_t *sc = (const int8_t *)(bp + 192);
-    const int lo = (t & 1) ? ql[l + 32] : ql[l];
+    const int lo = (t & 1) ? lb(64 * h + l + 32) : lb(64 * h + l);
     const int nib = (t & 2) ? (lo >> 4) : (lo & 0xF);
-    const int q = (nib | (((qh[l] >> (2 * t)) & 3) << 4)) - 32;
-    return d * (float)sc[8 * h + l / 16 + 2 * t] * (float)q;
+    const int q = (nib | (((lb(128 + 32 * h + l) >> (2 * t)) & 3) << 4)) - 32;
+    const int sc = (int)(int8_t)lb(192 + 8 * h + l / 16 + 2 * t);
+    return d * (float)sc * (float)q;
   }
-  // IQ3_XXS
-  const float d = h2f(*dp);
+  // IQ3_XXS: logical bytes are ggml bytes 2..97
+  const float d = h2f(dbits);
   const int ib = e / 32, l = (e % 32) / 8, j = e % 8;
-  const uint8_t *aux8 = bp + 64 + 4 * ib;
-  const uint32_t aux = aux8[0] | (aux8[1] << 8) | (aux8[2] << 16) | ((uint32_t)aux8[3] << 24);
+  const uint32_t aux = lb(64 + 4 * ib) | (lb(65 + 4 * ib) << 8) | (lb(66 + 4 * ib) << 16) |
+                       ((uint32_t)lb(67 + 4 * ib) << 24);
   const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
   const uint32_t sg = ksign7((aux >> (7 * l)) & 127u);
-  const uint32_t g = grid[bp[8 * ib + 2 * l + (j >> 2)]];
+  const uint32_t g = grid[lb(8 * ib + 2 * l + (j >> 2))];
   const float mag = (float)((g >> (8 * (j & 3))) & 0xff);
   return db * mag * (((sg >> j) & 1u) ? -1.0f : 1.0f);
 }
 
-__global__ void k_dequant(gq_weight w, const uint32_t *grid, int row0, long total, float *out) {
+__global__ void k_dequant(Layout L, const uint8_t *body, const uint16_t *dd,
+                          const uint32_t *grid, int row0, long total, float *out) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
-  const int r = row0 + (int)(i / w.in_dim);
-  const int c = (int)(i % w.in_dim);
-  const int be = block_elems(w.dtype), bb = body_block_bytes(w.dtype);
-  const int b = c / be;
-  const uint8_t *bp = w.body + (long)r * w.stride + (long)b * bb;
-  const uint16_t *dp = w.d ? w.d + (long)r * w.nb + b : nullptr;
-  out[i] = dq_element(w.dtype, bp, dp, c % be, grid);
+  const int r = row0 + (int)(i / L.k);
+  const int c = (int)(i % L.k);
+  const int t = r / L.rt, j = (r % L.rt) * L.units + c / 256;
+  auto lb = [&](int o) -> uint32_t { return body[chunk_offset(L, t, j, o >> 4) + (o & 15)]; };
+  const uint32_t dbits = dd ? dd[unit_index(L, t, j)] : 0u;
+  out[i] = dq_element(L.dtype, lb, dbits, c % 256, grid);
 }
 
 hipError_t launch_dequant(const gq_weight *w, const uint32_t *grid, int row0, int nrows,
                           float *out, hipStream_t st) {
-  const long total = (long)nrows * w->in_dim;
+  const long total = (long)nrows * w->L.k;
   if (total == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_dequant, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, *w,
-                     grid, row0, total, out);
+  hipLaunchKernelGGL(k_dequant, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, w->L,
+                     (const uint8_t *)w->body, (const uint16_t *)w->d, grid, row0, total, out);
   return hipGetLastError();
 }
 

@@ -41,6 +41,25 @@ __host__ __device__ constexpr bool has_d_array(int t) {
   return t == T_Q6_K || t == T_Q8_0 || t == T_IQ3_XXS;
 }
 
+// Streaming (nontemporal) loads for weight bytes: each byte is read once
+// per launch, so they should not displace x or other cached data.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 ldw4(const void *p) {
+  const u32x4_t v = __builtin_nontemporal_load((const u32x4_t *)p);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 ldw2(const void *p) {
+  const u32x2_t v = __builtin_nontemporal_load((const u32x2_t *)p);
+  return make_uint2(v.x, v.y);
+}
+__device__ __forceinline__ uint32_t ldw1(const void *p) {
+  return __builtin_nontemporal_load((const uint32_t *)p);
+}
+__device__ __forceinline__ uint32_t ldh(const uint16_t *p) {
+  return __builtin_nontemporal_load(p);
+}
+
 // IEEE binary16 -> binary32 (exact; v_cvt_f32_f16 keeps f16 subnormals).
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));

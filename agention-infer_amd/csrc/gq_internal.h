@@ -1,17 +1,16 @@
 // gq_internal.h -- host/device structures shared by the gq translation units.
 #pragma once
 #include <hip/hip_runtime.h>
-#include <stdint.h>
 #include <stddef.h>
+#include <stdint.h>
+
+#include "gq_layout.h"
 
 // The public handle (opaque in gq.h).
 struct gq_weight {
-  int dtype;
-  int in_dim, out_dim;
-  int nb;            // blocks per row
-  long stride;       // device body bytes per row
-  uint8_t *body;     // device body (layout per dtype, see gq_device.h)
-  uint16_t *d;       // device per-block f16 scales, or nullptr
+  gq::Layout L;      // dtype, rows, k, units, chunks, rt
+  uint8_t *body;     // device body in the wave-tiled layout
+  uint16_t *d;       // per-unit f16 scales (Q6_K, IQ3_XXS), or nullptr
   size_t ggml_bytes; // size of the tensor in ggml block order
   int device;
 };
@@ -19,31 +18,36 @@ struct gq_weight {
 namespace gq {
 
 constexpr int MV_MAX_SEG = 4;
+constexpr float LIMB_RANGE = 8323072.0f;  // 127 * 65536: |X| <= this
 
 struct MvSeg {
   const uint8_t *body;
   const uint16_t *d;
   float *y;
-  long stride;
-  int row_begin;  // first global row of this segment
+  int rows;
+  int rt;
+  int tile_begin;  // first global tile (= wave) of this segment
 };
 
 struct MvArgs {
   const float *x;
   const uint32_t *grid;  // IQ3_XXS codebook (device)
-  int k, kpad, nb;
-  int total_rows;
+  int k, units, chunks;
+  int part_floats;       // LDS floats per wave for per-unit partial sums
+  int total_tiles;
   int nseg;
   MvSeg seg[MV_MAX_SEG];
 };
 
-size_t matvec_lds_bytes(int kpad);
-hipError_t launch_matvec(const MvArgs &a, int fmt, int num_cus, hipStream_t st);
+size_t matvec_lds_bytes(int dtype, int units, int part_floats);
+hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st);
 
-// Re-lay a ggml tensor that is already on the device into the handle's
-// device layout.
-hipError_t launch_repack(int dtype, const uint8_t *raw, long rows, int nb, uint8_t *body,
-                         uint16_t *d, hipStream_t st);
+// Rows per tile for a matrix (chosen at upload).
+int choose_rt(int dtype, int rows, int units);
+
+// Re-lay a ggml tensor already on the device into the wave-tiled layout.
+hipError_t launch_repack(const Layout &L, const uint8_t *raw, uint8_t *body, uint16_t *d,
+                         hipStream_t st);
 
 // Bit-exact dequant of rows [row0, row0+nrows) into out[nrows][in_dim].
 hipError_t launch_dequant(const gq_weight *w, const uint32_t *grid, int row0, int nrows,

@@ -3,334 +3,462 @@
 //
 // Replaces the reference's per-row dot kernels (src/quant/q8_0.rs:58-90,
 // q4_k.rs:95-212, q5_k.rs:189-317, q6_k.rs:82-131) driven row-parallel by
-// WeightMap::matmul_into (src/model/mod.rs:362-403), and the reference GPU
-// matvec (src/ops/kernels_wgpu.rs:1067-1706), which this does not follow.
+// WeightMap::matmul_into (src/model/mod.rs:362-403).  It does not follow
+// the reference GPU kernels (src/ops/kernels_wgpu.rs:1067-1706).
 //
-// Design (HBM-bound: every weight byte is read once):
-//  * A 256-thread block first stages x (fp32, zero-padded to whole blocks)
-//    and the sums of x over each 16-element run in LDS.  The runs let the
-//    kernels factor constant offsets out of the inner loop:
-//      Q4_K  sum (d*sc*q - dmin*m) x = d*sc*sum(q x) - dmin*m*sum(x)
-//      Q6_K  sum (q - 32) x          = sum(q x) - 32*sum(x)
-//      Q8_0  sum q x with q = u - 128, u = q ^ 0x80 unsigned byte
-//    so each weight element costs one byte->float convert and one FMA.
-//  * LPR lanes cooperate on one row; consecutive lanes read consecutive
-//    16-byte pieces of a weight block with 128-bit loads, so one load
-//    instruction of a wave covers 64/LPR rows x LPR*16 contiguous bytes.
-//  * Partial sums are reduced across the LPR lanes with xor shuffles.
-//  * The grid is capped and waves loop over row groups, so x is staged
-//    once per block rather than once per row group.
+// Design (HBM-bound; every weight byte is read exactly once):
+//  * Weights sit in the wave-tiled layout (gq_layout.h): one lane owns one
+//    256-element unit, and a wave-wide 128-bit load reads 1 KiB of
+//    contiguous HBM with a nontemporal hint.  Each lane keeps its next unit
+//    in flight while it computes the current one.
+//  * x is staged per block in LDS as fixed-point int8 "limbs": for each run
+//    of 32 elements, s = max|x| / (127 * 2^16), X = rint(x / s) (|X| <=
+//    127 * 2^16) and X = x2 * 2^16 + x1 * 2^8 + x0 with signed bytes.
+//    The representation error is <= s/2 (relative 6e-8 of the run's max,
+//    the same order as fp32 rounding).
+//  * The weight integers (nibbles, 6-bit codes, int8) meet the limbs in
+//    v_dot4_i32_i8: 32 elements cost 8 x 3 integer dot instructions, exact,
+//    and the block / sub-block scales are applied once per run:
+//      Q4_K  sum (d*sc*q - dmin*m) x = d*sc*s*sum(q X) - dmin*m*sum(x)
+//      Q6_K  sum d*sc*(q - 32) x     = d*sc*s*(sum(q X) - 32*sum(X))
+//      Q8_0  sum d*q*x               = d*s*sum(q X)
+//  * Per-unit partial sums go to LDS and are reduced per row in a fixed
+//    order (deterministic results).
+#include <cstdlib>
+
 #include "gq_device.h"
 #include "gq_internal.h"
 
 namespace gq {
 
-struct RowCtx {
-  const uint8_t *body;  // this segment's body
-  const uint16_t *d;    // per-block f16 scales (layouts with a d array)
-  long stride;          // body bytes per row
-  int nb;               // blocks per row
+constexpr int LIMB_STRIDE = 272;  // LDS bytes per 256-element block of one limb (16 B pad)
+
+struct Smem {
+  uint8_t *l2, *l1, *l0;  // limbs, LIMB_STRIDE bytes per 256 elements
+  float *sx;              // fixed-point step per 32-run
+  float *xsum;            // sum(x) per 32-run (Q4_K / Q5_K)
+  int *xs16;              // sum(X) per 16-run (Q6_K)
+  uint32_t *grid;         // IQ3_XXS codebook
+  float *part;            // per-wave per-unit partial sums
 };
 
-// ---------------------------------------------------------------- Q4_K
-// One unit = 16 B of qs: group j = s/2, half h = s%2.  Low nibbles are
-// elements 64j+16h+[0,16) (sub-block 2j), high nibbles +32 (sub-block 2j+1).
-template <int LPR>
-__device__ __forceinline__ float row_q4k(const RowCtx &c, int r, int sl, const float *xs,
-                                         const float *s16) {
-  const int s = sl & 7, bo = sl >> 3;
-  constexpr int step = LPR / 8;
-  const int j = s >> 1, h = s & 1;
-  const int e_lo = 64 * j + 16 * h;
-  const uint8_t *rp = c.body + (long)r * c.stride;
-  float acc = 0.f;
-#pragma unroll 2
-  for (int b = bo; b < c.nb; b += step) {
-    const uint4 hd = *(const uint4 *)(rp + b * 144);
-    const uint4 q = *(const uint4 *)(rp + b * 144 + 16 + 16 * s);
-    uint32_t sc0, m0, sc1, m1;
-    scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
-    scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
-    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-    const float *xl = xs + b * 256 + e_lo;
-    float sl_ = 0.f, sh_ = 0.f;
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t lo = qw[k] & 0x0F0F0F0Fu, hi = (qw[k] >> 4) & 0x0F0F0F0Fu;
-      sl_ = dot4u(lo, *(const float4 *)(xl + 4 * k), sl_);
-      sh_ = dot4u(hi, *(const float4 *)(xl + 32 + 4 * k), sh_);
-    }
-    const int g = (b * 256 + e_lo) >> 4;
-    acc = fmaf(d * (float)sc0, sl_, acc);
-    acc = fmaf(-(dmin * (float)m0), s16[g], acc);
-    acc = fmaf(d * (float)sc1, sh_, acc);
-    acc = fmaf(-(dmin * (float)m1), s16[g + 2], acc);
+__host__ __device__ inline size_t smem_layout(int units, int part_floats, Smem *s, char *base) {
+  size_t o = 0;
+  auto take = [&](size_t n) { size_t r = o; o += (n + 15) & ~(size_t)15; return r; };
+  const size_t limb = (size_t)units * LIMB_STRIDE;
+  const size_t o2 = take(limb), o1 = take(limb), o0 = take(limb);
+  const size_t osx = take((size_t)units * 8 * 4), osum = take((size_t)units * 8 * 4);
+  const size_t o16 = take((size_t)units * 16 * 4), og = take(1024);
+  const size_t op = take((size_t)4 * part_floats * 4);
+  if (s) {
+    s->l2 = (uint8_t *)(base + o2);
+    s->l1 = (uint8_t *)(base + o1);
+    s->l0 = (uint8_t *)(base + o0);
+    s->sx = (float *)(base + osx);
+    s->xsum = (float *)(base + osum);
+    s->xs16 = (int *)(base + o16);
+    s->grid = (uint32_t *)(base + og);
+    s->part = (float *)(base + op);
   }
-  return acc;
+  return o;
 }
 
-// ---------------------------------------------------------------- Q5_K
-// As Q4_K, plus the fifth bit from qh[l] (bit `is` of the 32-byte qh).
-template <int LPR>
-__device__ __forceinline__ float row_q5k(const RowCtx &c, int r, int sl, const float *xs,
-                                         const float *s16) {
-  const int s = sl & 7, bo = sl >> 3;
-  constexpr int step = LPR / 8;
-  const int j = s >> 1, h = s & 1;
-  const int e_lo = 64 * j + 16 * h;
-  const uint8_t *rp = c.body + (long)r * c.stride;
+// Dot of N weight dwords (4 int8 each, elements e..e+4N) with the limbs at
+// limb byte offset `off`; returns sum(q X) as float (exact integer parts,
+// one rounding when the three limb sums are combined).
+template <int N>
+__device__ __forceinline__ float limbdot(const uint32_t *w, const Smem &S, int off) {
+  int a2 = 0, a1 = 0, a0 = 0;
+#pragma unroll
+  for (int i = 0; i < N / 4; i++) {
+    const uint4 v2 = *(const uint4 *)(S.l2 + off + 16 * i);
+    const uint4 v1 = *(const uint4 *)(S.l1 + off + 16 * i);
+    const uint4 v0 = *(const uint4 *)(S.l0 + off + 16 * i);
+    a2 = __builtin_amdgcn_sdot4(w[4 * i + 0], v2.x, a2, false);
+    a2 = __builtin_amdgcn_sdot4(w[4 * i + 1], v2.y, a2, false);
+    a2 = __builtin_amdgcn_sdot4(w[4 * i + 2], v2.z, a2, false);
+    a2 = __builtin_amdgcn_sdot4(w[4 * i + 3], v2.w, a2, false);
+    a1 = __builtin_amdgcn_sdot4(w[4 * i + 0], v1.x, a1, false);
+    a1 = __builtin_amdgcn_sdot4(w[4 * i + 1], v1.y, a1, false);
+    a1 = __builtin_amdgcn_sdot4(w[4 * i + 2], v1.z, a1, false);
+    a1 = __builtin_amdgcn_sdot4(w[4 * i + 3], v1.w, a1, false);
+    a0 = __builtin_amdgcn_sdot4(w[4 * i + 0], v0.x, a0, false);
+    a0 = __builtin_amdgcn_sdot4(w[4 * i + 1], v0.y, a0, false);
+    a0 = __builtin_amdgcn_sdot4(w[4 * i + 2], v0.z, a0, false);
+    a0 = __builtin_amdgcn_sdot4(w[4 * i + 3], v0.w, a0, false);
+  }
+  return fmaf((float)a2, 65536.f, fmaf((float)a1, 256.f, (float)a0));
+}
+
+__device__ __forceinline__ uint32_t dw(const uint4 *ch, int k) {
+  const uint4 c = ch[k >> 2];
+  const int m = k & 3;
+  return m == 0 ? c.x : m == 1 ? c.y : m == 2 ? c.z : c.w;
+}
+
+// ---------------------------------------------------------------- Q4_K
+// ch[0] = d, dmin, scales[12]; Q4_K: ch[1..8] = qs[128];
+// Q5_K: ch[1..2] = qh[32], ch[3..10] = qs[128].
+__device__ __forceinline__ float unit_q4k(const uint4 *ch, int u, const Smem &S, int q5) {
+  const uint4 hd = ch[0];
+  const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+  const int qs0 = q5 ? 3 : 1;
   float acc = 0.f;
-#pragma unroll 2
-  for (int b = bo; b < c.nb; b += step) {
-    const uint8_t *bp = rp + b * 176;
-    const uint4 hd = *(const uint4 *)bp;
-    const uint4 qh = *(const uint4 *)(bp + 16 + 16 * h);
-    const uint4 q = *(const uint4 *)(bp + 48 + 16 * s);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
     uint32_t sc0, m0, sc1, m1;
     scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
     scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
-    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-    const float *xl = xs + b * 256 + e_lo;
-    float sl_ = 0.f, sh_ = 0.f;
-    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-    const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
+    uint32_t lo[8], hi[8];
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t lo = (qw[k] & 0x0F0F0F0Fu) | (((hw[k] >> (2 * j)) & 0x01010101u) << 4);
-      const uint32_t hi =
-          ((qw[k] >> 4) & 0x0F0F0F0Fu) | (((hw[k] >> (2 * j + 1)) & 0x01010101u) << 4);
-      sl_ = dot4u(lo, *(const float4 *)(xl + 4 * k), sl_);
-      sh_ = dot4u(hi, *(const float4 *)(xl + 32 + 4 * k), sh_);
+    for (int i = 0; i < 8; i++) {
+      const uint32_t q = dw(ch + qs0, 8 * j + i);
+      lo[i] = q & 0x0F0F0F0Fu;
+      hi[i] = (q >> 4) & 0x0F0F0F0Fu;
+      if (q5) {
+        const uint32_t h = dw(ch + 1, i);  // qh bytes 4i..4i+3: element 4i.. of each sub-block
+        lo[i] |= ((h >> (2 * j)) & 0x01010101u) << 4;
+        hi[i] |= ((h >> (2 * j + 1)) & 0x01010101u) << 4;
+      }
     }
-    const int g = (b * 256 + e_lo) >> 4;
-    acc = fmaf(d * (float)sc0, sl_, acc);
-    acc = fmaf(-(dmin * (float)m0), s16[g], acc);
-    acc = fmaf(d * (float)sc1, sh_, acc);
-    acc = fmaf(-(dmin * (float)m1), s16[g + 2], acc);
+    const int r0 = 8 * u + 2 * j;
+    const int off = u * LIMB_STRIDE + 64 * j;
+    const float slo = limbdot<8>(lo, S, off);
+    const float shi = limbdot<8>(hi, S, off + 32);
+    acc = fmaf(d * (float)sc0 * S.sx[r0], slo, acc);
+    acc = fmaf(-(dmin * (float)m0), S.xsum[r0], acc);
+    acc = fmaf(d * (float)sc1 * S.sx[r0 + 1], shi, acc);
+    acc = fmaf(-(dmin * (float)m1), S.xsum[r0 + 1], acc);
   }
   return acc;
 }
 
 // ---------------------------------------------------------------- Q6_K
-// One unit = half hh = s/2, l in [16*(s%2), +16): 16 B of ql at l, 16 B of
-// ql at l+32, 16 B of qh at l -> 64 elements in four runs of 16
-// (elements 128hh + l + 32t, t = 0..3), scale index 8hh + s%2 + 2t.
-template <int LPR>
-__device__ __forceinline__ float row_q6k(const RowCtx &c, int r, int sl, const float *xs,
-                                         const float *s16) {
-  const int s = sl & 3, bo = sl >> 2;
-  constexpr int step = LPR / 4;
-  const int hh = s >> 1, lh = s & 1;
-  const uint8_t *rp = c.body + (long)r * c.stride;
-  const uint16_t *dp = c.d + (long)r * c.nb;
+// ch[0..7] = ql[128], ch[8..11] = qh[64], ch[12] = scales[16]; d separate.
+// 16-run s (elements 16s..16s+15 of the unit) uses scale index s.
+__device__ __forceinline__ float unit_q6k(const uint4 *ch, uint32_t dbits, int u, const Smem &S) {
+  const float d = h2f(dbits);
   float acc = 0.f;
-#pragma unroll 2
-  for (int b = bo; b < c.nb; b += step) {
-    const uint8_t *bp = rp + b * 208;
-    const uint4 A = *(const uint4 *)(bp + 64 * hh + 16 * lh);
-    const uint4 B = *(const uint4 *)(bp + 64 * hh + 32 + 16 * lh);
-    const uint4 H = *(const uint4 *)(bp + 128 + 32 * hh + 16 * lh);
-    const uint4 SC = *(const uint4 *)(bp + 192);
-    const float d = h2f(dp[b]);
-    const uint32_t w0 = hh ? SC.z : SC.x, w1 = hh ? SC.w : SC.y;
-    const int sh = 8 * lh;
-    const float sc0 = (float)(int8_t)(w0 >> sh), sc1 = (float)(int8_t)(w0 >> (sh + 16));
-    const float sc2 = (float)(int8_t)(w1 >> sh), sc3 = (float)(int8_t)(w1 >> (sh + 16));
-    const uint32_t aw[4] = {A.x, A.y, A.z, A.w}, bw[4] = {B.x, B.y, B.z, B.w};
-    const uint32_t hw[4] = {H.x, H.y, H.z, H.w};
-    const float *xb = xs + b * 256 + 128 * hh + 16 * lh;
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const uint32_t q1 = (aw[k] & 0x0F0F0F0Fu) | ((hw[k] << 4) & 0x30303030u);
-      const uint32_t q2 = (bw[k] & 0x0F0F0F0Fu) | ((hw[k] << 2) & 0x30303030u);
-      const uint32_t q3 = ((aw[k] >> 4) & 0x0F0F0F0Fu) | (hw[k] & 0x30303030u);
-      const uint32_t q4 = ((bw[k] >> 4) & 0x0F0F0F0Fu) | ((hw[k] >> 2) & 0x30303030u);
-      s0 = dot4u(q1, *(const float4 *)(xb + 4 * k), s0);
-      s1 = dot4u(q2, *(const float4 *)(xb + 32 + 4 * k), s1);
-      s2 = dot4u(q3, *(const float4 *)(xb + 64 + 4 * k), s2);
-      s3 = dot4u(q4, *(const float4 *)(xb + 96 + 4 * k), s3);
+  for (int hh = 0; hh < 2; hh++) {
+#pragma unroll
+    for (int half = 0; half < 2; half++) {
+      uint32_t q[4][4];  // [t][i]
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int ii = 4 * half + i;
+        const uint32_t A = dw(ch, 16 * hh + ii), B = dw(ch, 16 * hh + 8 + ii);
+        const uint32_t H = dw(ch + 8, 8 * hh + ii);
+        q[0][i] = (A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+        q[1][i] = (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+        q[2][i] = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+        q[3][i] = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+      }
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        const int s = 8 * hh + 2 * t + half;  // 16-run within the unit = scale index
+        const float sc = (float)(int8_t)(dw(ch + 12, s >> 2) >> (8 * (s & 3)));
+        const float sqx = limbdot<4>(q[t], S, u * LIMB_STRIDE + 16 * s);
+        const float corr = sqx - 32.f * (float)S.xs16[16 * u + s];
+        acc = fmaf(sc * S.sx[8 * u + (s >> 1)], corr, acc);
+      }
     }
-    const int g = (b * 256 + 128 * hh + 16 * lh) >> 4;
-    float t = sc0 * fmaf(-32.f, s16[g], s0);
-    t = fmaf(sc1, fmaf(-32.f, s16[g + 2], s1), t);
-    t = fmaf(sc2, fmaf(-32.f, s16[g + 4], s2), t);
-    t = fmaf(sc3, fmaf(-32.f, s16[g + 6], s3), t);
-    acc = fmaf(d, t, acc);
   }
-  return acc;
+  return d * acc;
 }
 
 // ---------------------------------------------------------------- Q8_0
-// One unit = 16 int8 quants (half a block).
-template <int LPR>
-__device__ __forceinline__ float row_q80(const RowCtx &c, int r, int sl, const float *xs,
-                                         const float *s16) {
-  const uint8_t *rp = c.body + (long)r * c.stride;
-  const uint16_t *dp = c.d + (long)r * c.nb;
-  const int nc = 2 * c.nb;
+// ch[0..15] = qs of 8 blocks, ch[16] = their 8 f16 scales.
+__device__ __forceinline__ float unit_q80(const uint4 *ch, int u, const Smem &S) {
   float acc = 0.f;
-#pragma unroll 2
-  for (int u = sl; u < nc; u += LPR) {
-    const uint4 q = *(const uint4 *)(rp + 16 * u);
-    const float d = h2f(dp[u >> 1]);
-    const float *xb = xs + 16 * u;
-    float sum = 0.f;
-    sum = dot4u(q.x ^ 0x80808080u, *(const float4 *)(xb + 0), sum);
-    sum = dot4u(q.y ^ 0x80808080u, *(const float4 *)(xb + 4), sum);
-    sum = dot4u(q.z ^ 0x80808080u, *(const float4 *)(xb + 8), sum);
-    sum = dot4u(q.w ^ 0x80808080u, *(const float4 *)(xb + 12), sum);
-    acc = fmaf(d, fmaf(-128.f, s16[u], sum), acc);
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    uint32_t w[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) w[k] = dw(ch, 8 * i + k);
+    const float s = limbdot<8>(w, S, u * LIMB_STRIDE + 32 * i);
+    const float d = h2f(dw(ch + 16, i >> 1) >> (16 * (i & 1)));
+    acc = fmaf(d * S.sx[8 * u + i], s, acc);
   }
   return acc;
 }
 
 // ------------------------------------------------------------- IQ3_XXS
-// One unit = one 32-element sub-block ib = s: 8 grid indices + one aux word.
-template <int LPR>
-__device__ __forceinline__ float row_iq3(const RowCtx &c, int r, int sl, const float *xs,
-                                         const uint32_t *grid) {
-  const int s = sl & 7, bo = sl >> 3;
-  constexpr int step = LPR / 8;
-  const uint8_t *rp = c.body + (long)r * c.stride;
-  const uint16_t *dp = c.d + (long)r * c.nb;
+// ch[0..3] = 64 grid indices, ch[4..5] = 8 sign/scale words; d separate.
+// Signs are applied by splitting each group into its positive and negative
+// magnitudes (two dot products), so no byte negation can carry.
+__device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u, const Smem &S) {
+  const float d = h2f(dbits);
   float acc = 0.f;
-#pragma unroll 2
-  for (int b = bo; b < c.nb; b += step) {
-    const uint8_t *bp = rp + b * 96;
-    const uint2 qi = *(const uint2 *)(bp + 8 * s);
-    const uint32_t aux = *(const uint32_t *)(bp + 64 + 4 * s);
-    const float d = h2f(dp[b]);
-    const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
-    const float *xb = xs + b * 256 + 32 * s;
-    float sum = 0.f;
+#pragma unroll
+  for (int ib = 0; ib < 8; ib++) {
+    const uint32_t aux = dw(ch + 4, ib);
+    const uint32_t i0 = dw(ch, 2 * ib), i1 = dw(ch, 2 * ib + 1);
+    uint32_t pos[8], neg[8];
 #pragma unroll
     for (int l = 0; l < 4; l++) {
       const uint32_t sg = ksign7((aux >> (7 * l)) & 127u);
-      const uint32_t word = l < 2 ? qi.x : qi.y;
-      const uint32_t g1 = grid[(word >> (16 * (l & 1))) & 0xff];
-      const uint32_t g2 = grid[(word >> (16 * (l & 1) + 8)) & 0xff];
-      const float4 xa = *(const float4 *)(xb + 8 * l), xc = *(const float4 *)(xb + 8 * l + 4);
-      float4 ya, yc;
-      ya.x = __uint_as_float(__float_as_uint(xa.x) ^ ((sg & 1u) << 31));
-      ya.y = __uint_as_float(__float_as_uint(xa.y) ^ ((sg & 2u) << 30));
-      ya.z = __uint_as_float(__float_as_uint(xa.z) ^ ((sg & 4u) << 29));
-      ya.w = __uint_as_float(__float_as_uint(xa.w) ^ ((sg & 8u) << 28));
-      yc.x = __uint_as_float(__float_as_uint(xc.x) ^ ((sg & 16u) << 27));
-      yc.y = __uint_as_float(__float_as_uint(xc.y) ^ ((sg & 32u) << 26));
-      yc.z = __uint_as_float(__float_as_uint(xc.z) ^ ((sg & 64u) << 25));
-      yc.w = __uint_as_float(__float_as_uint(xc.w) ^ ((sg & 128u) << 24));
-      sum = dot4u(g1, ya, sum);
-      sum = dot4u(g2, yc, sum);
+      const uint32_t word = l < 2 ? i0 : i1;
+      const uint32_t g1 = S.grid[(word >> (16 * (l & 1))) & 0xff];
+      const uint32_t g2 = S.grid[(word >> (16 * (l & 1) + 8)) & 0xff];
+      const uint32_t m1 = (((sg & 15u) * 0x00204081u) & 0x01010101u) * 0xFFu;
+      const uint32_t m2 = (((sg >> 4) * 0x00204081u) & 0x01010101u) * 0xFFu;
+      pos[2 * l] = g1 & ~m1;
+      neg[2 * l] = g1 & m1;
+      pos[2 * l + 1] = g2 & ~m2;
+      neg[2 * l + 1] = g2 & m2;
     }
-    acc = fmaf(db, sum, acc);
+    const int off = u * LIMB_STRIDE + 32 * ib;
+    const float s = limbdot<8>(pos, S, off) - limbdot<8>(neg, S, off);
+    const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
+    acc = fmaf(db * S.sx[8 * u + ib], s, acc);
   }
   return acc;
 }
 
-// ------------------------------------------------------------- kernel
-template <int FMT, int LPR>
-__global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
-  extern __shared__ float smem[];
-  float *xs = smem;
-  float *s16 = smem + a.kpad;
-  uint32_t *grid = (uint32_t *)(s16 + a.kpad / 16);
-  const int tid = threadIdx.x;
-  for (int i = tid; i < a.kpad; i += 256) xs[i] = i < a.k ? a.x[i] : 0.f;
-  if (FMT == T_IQ3_XXS) grid[tid] = a.grid[tid];
-  __syncthreads();
-  for (int i = tid; i < a.kpad / 16; i += 256) {
-    const float4 *p = (const float4 *)(xs + 16 * i);
-    float s = 0.f;
+// ------------------------------------------------------------- staging
+// Thread t converts elements [4096p + 16t, +16) of x; 32-runs are thread
+// pairs (2m, 2m+1).  All threads execute the shuffles.
+__device__ __forceinline__ void stage_x(int kpad, int p, const float (&xv)[16], const Smem &S) {
+  const int e0 = 4096 * p + 16 * (int)threadIdx.x;
+  float amax = 0.f, sum = 0.f;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      const float4 v = p[k];
-      s += v.x; s += v.y; s += v.z; s += v.w;
-    }
-    s16[i] = s;
+  for (int i = 0; i < 16; i++) {
+    amax = fmaxf(amax, fabsf(xv[i]));
+    sum += xv[i];
   }
-  __syncthreads();
-
-  constexpr int RPW = 64 / LPR;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int sl = lane % LPR, rg = lane / LPR;
-  for (int row0 = (blockIdx.x * 4 + wave) * RPW; row0 < a.total_rows;
-       row0 += gridDim.x * 4 * RPW) {
-    const int r = row0 + rg;
-    float acc = 0.f;
-    int seg = 0;
-    if (r < a.total_rows) {
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  const float sum32 = sum + __shfl_xor(sum, 1, 64);
+  if (e0 >= kpad) return;
+  const float inv = amax > 0.f ? LIMB_RANGE / amax : 0.f;
+  uint32_t w2[4], w1[4], w0[4];
+  int xs = 0;
 #pragma unroll
-      for (int i = 1; i < MV_MAX_SEG; i++)
-        if (i < a.nseg && r >= a.seg[i].row_begin) seg = i;
-      const MvSeg &S = a.seg[seg];
-      const RowCtx c{S.body, S.d, S.stride, a.nb};
-      const int rr = r - S.row_begin;
-      if (FMT == T_Q4_K) acc = row_q4k<LPR>(c, rr, sl, xs, s16);
-      else if (FMT == T_Q5_K) acc = row_q5k<LPR>(c, rr, sl, xs, s16);
-      else if (FMT == T_Q6_K) acc = row_q6k<LPR>(c, rr, sl, xs, s16);
-      else if (FMT == T_Q8_0) acc = row_q80<LPR>(c, rr, sl, xs, s16);
-      else acc = row_iq3<LPR>(c, rr, sl, xs, grid);
+  for (int q = 0; q < 4; q++) {
+    uint32_t b2 = 0, b1 = 0, b0 = 0;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const int X = (int)rintf(xv[4 * q + r] * inv);
+      xs += X;
+      const int x0 = (int)(int8_t)(X & 0xff);
+      const int X1 = (X - x0) >> 8;
+      const int x1 = (int)(int8_t)(X1 & 0xff);
+      const int x2 = (X1 - x1) >> 8;
+      b0 |= (uint32_t)(x0 & 0xff) << (8 * r);
+      b1 |= (uint32_t)(x1 & 0xff) << (8 * r);
+      b2 |= (uint32_t)(x2 & 0xff) << (8 * r);
     }
+    w2[q] = b2;
+    w1[q] = b1;
+    w0[q] = b0;
+  }
+  const int lo = (e0 >> 8) * LIMB_STRIDE + (e0 & 255);
+  *(uint4 *)(S.l2 + lo) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+  *(uint4 *)(S.l1 + lo) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+  *(uint4 *)(S.l0 + lo) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+  if ((threadIdx.x & 1) == 0) {
+    S.sx[e0 >> 5] = amax / LIMB_RANGE;
+    S.xsum[e0 >> 5] = sum32;
+  }
+  S.xs16[e0 >> 4] = xs;
+}
+
+template <bool K4>
+__device__ __forceinline__ void load_x16(const float *x, int k, int e0, float (&xv)[16]) {
+  if (K4) {  // k % 4 == 0: clamped vector loads, zeroed past k
 #pragma unroll
-    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    if (sl == 0 && r < a.total_rows) a.seg[seg].y[r - a.seg[seg].row_begin] = acc;
+    for (int q = 0; q < 4; q++) {
+      const int e = e0 + 4 * q;
+      const float4 v = *(const float4 *)(x + min(e, k - 4));
+      const bool in = e < k;
+      xv[4 * q + 0] = in ? v.x : 0.f;
+      xv[4 * q + 1] = in ? v.y : 0.f;
+      xv[4 * q + 2] = in ? v.z : 0.f;
+      xv[4 * q + 3] = in ? v.w : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float v = x[min(e0 + i, k - 1)];
+      xv[i] = e0 + i < k ? v : 0.f;
+    }
   }
 }
 
-// ------------------------------------------------------------- launch
-template <int FMT, int LPR>
-static void launch_one(const MvArgs &a, int blocks, size_t lds, hipStream_t st) {
-  if (lds > 64 * 1024)
-    (void)hipFuncSetAttribute((const void *)k_matvec<FMT, LPR>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL((k_matvec<FMT, LPR>), dim3(blocks), dim3(256), lds, st, a);
+// ------------------------------------------------------------- kernel
+template <int FMT> struct Fmt;
+template <> struct Fmt<T_Q4_K> { static constexpr int C = 9; static constexpr bool HAS_D = false; };
+template <> struct Fmt<T_Q5_K> { static constexpr int C = 11; static constexpr bool HAS_D = false; };
+template <> struct Fmt<T_Q6_K> { static constexpr int C = 13; static constexpr bool HAS_D = true; };
+template <> struct Fmt<T_Q8_0> { static constexpr int C = 17; static constexpr bool HAS_D = false; };
+template <> struct Fmt<T_IQ3_XXS> { static constexpr int C = 6; static constexpr bool HAS_D = true; };
+
+template <int FMT>
+struct Unit {
+  uint4 ch[Fmt<FMT>::C];
+  uint32_t d;
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_unit(Unit<FMT> &U, const uint8_t *p, long cstride,
+                                          const uint16_t *dp) {
+#pragma unroll
+  for (int c = 0; c < Fmt<FMT>::C; c++) U.ch[c] = ldw4(p + c * cstride);
+  if (Fmt<FMT>::HAS_D) U.d = ldh(dp);
 }
 
 template <int FMT>
-static hipError_t launch_fmt(const MvArgs &a, int lpr, int blocks, size_t lds, hipStream_t st) {
-  switch (lpr) {
-  case 4:
-    if (FMT == T_Q6_K) { launch_one<FMT, 4>(a, blocks, lds, st); break; }
-    [[fallthrough]];  // the other formats need at least 8 lanes per row
-  case 8: launch_one<FMT, 8>(a, blocks, lds, st); break;
-  case 16: launch_one<FMT, 16>(a, blocks, lds, st); break;
-  case 32: launch_one<FMT, 32>(a, blocks, lds, st); break;
-  default: launch_one<FMT, 64>(a, blocks, lds, st); break;
+__device__ __forceinline__ float unit_dot(const Unit<FMT> &U, int u, const Smem &S) {
+  if constexpr (FMT == T_Q4_K) return unit_q4k(U.ch, u, S, 0);
+  else if constexpr (FMT == T_Q5_K) return unit_q4k(U.ch, u, S, 1);
+  else if constexpr (FMT == T_Q6_K) return unit_q6k(U.ch, U.d, u, S);
+  else if constexpr (FMT == T_Q8_0) return unit_q80(U.ch, u, S);
+  else return unit_iq3(U.ch, U.d, u, S);
+}
+
+// One wave = one tile of RT rows.  Blocks of 4 waves share the staged x.
+template <int FMT, bool K4>
+__global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
+  extern __shared__ __align__(16) char smem_raw[];
+  Smem S;
+  smem_layout(a.units, a.part_floats, &S, smem_raw);
+  constexpr int C = Fmt<FMT>::C;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int gw = blockIdx.x * 4 + wave;
+  const bool valid = gw < a.total_tiles;
+  const int gwc = valid ? gw : a.total_tiles - 1;
+
+  // Segment of this wave (wave-uniform selects over scalar arguments).
+  MvSeg sg = a.seg[0];
+#pragma unroll
+  for (int i = 1; i < MV_MAX_SEG; i++)
+    if (i < a.nseg && gwc >= a.seg[i].tile_begin) sg = a.seg[i];
+  const int t = gwc - sg.tile_begin;
+  const int U = a.units;
+  const int rows_here = min(sg.rt, sg.rows - t * sg.rt);
+  const int uit = rows_here * U;
+  const int iters = (uit + 63) >> 6;
+  const int nv_last = uit - 64 * (iters - 1);
+  const long tile_base = (long)t * sg.rt * U * C * 16;
+  const long dbase = (long)t * sg.rt * U;
+  auto unit_ptr = [&](int it, long &cstride, const uint16_t *&dp) -> const uint8_t * {
+    const bool last = it == iters - 1;
+    const int l = last ? min(lane, nv_last - 1) : lane;
+    cstride = last ? 16L * nv_last : 1024L;
+    dp = sg.d + dbase + 64 * it + l;
+    return sg.body + tile_base + (long)it * C * 1024 + 16 * l;
+  };
+
+  // x of the first pass, then the first weight unit, then the LDS stores:
+  // the wait before the stores leaves the weight loads in flight.
+  const int kpad = U * 256;
+  float xv[16];
+  load_x16<K4>(a.x, a.k, 16 * tid, xv);
+  uint32_t gword = 0;
+  if constexpr (FMT == T_IQ3_XXS) gword = a.grid[tid];
+  __builtin_amdgcn_sched_barrier(0);
+  Unit<FMT> A, B;
+  {
+    long cs;
+    const uint16_t *dp;
+    const uint8_t *p = unit_ptr(0, cs, dp);
+    load_unit<FMT>(A, p, cs, dp);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  stage_x(kpad, 0, xv, S);
+  for (int p = 1; 4096 * p < kpad; p++) {
+    load_x16<K4>(a.x, a.k, 4096 * p + 16 * tid, xv);
+    stage_x(kpad, p, xv, S);
+  }
+  if constexpr (FMT == T_IQ3_XXS) S.grid[tid] = gword;
+  __syncthreads();
+
+  float *part = S.part + wave * a.part_floats;
+  for (int it = 0; it < iters; it += 2) {
+    {
+      long cs;
+      const uint16_t *dp;
+      const uint8_t *p = unit_ptr(min(it + 1, iters - 1), cs, dp);
+      load_unit<FMT>(B, p, cs, dp);
+    }
+    {
+      const int j = 64 * it + lane;
+      const float v = unit_dot<FMT>(A, j % U, S);
+      if (j < uit) part[j] = v;
+    }
+    {
+      long cs;
+      const uint16_t *dp;
+      const uint8_t *p = unit_ptr(min(it + 2, iters - 1), cs, dp);
+      load_unit<FMT>(A, p, cs, dp);
+    }
+    if (it + 1 < iters) {
+      const int j = 64 * (it + 1) + lane;
+      const float v = unit_dot<FMT>(B, j % U, S);
+      if (j < uit) part[j] = v;
+    }
+  }
+  __syncthreads();
+
+  // Row sums: 64/RT lanes per row, fixed order.
+  const int lpr = 64 / sg.rt;
+  const int row = lane / lpr, sub = lane % lpr;
+  float v = 0.f;
+  if (row < rows_here)
+    for (int c = sub; c < U; c += lpr) v += part[row * U + c];
+  for (int off = lpr >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if (valid && sub == 0 && row < rows_here) sg.y[t * sg.rt + row] = v;
+}
+
+// ------------------------------------------------------------- launch
+size_t matvec_lds_bytes(int dtype, int units, int part_floats) {
+  (void)dtype;
+  return smem_layout(units, part_floats, nullptr, nullptr);
+}
+
+// Rows per tile: enough tiles (waves) to fill the GPU, few idle lanes in a
+// tile's last iteration.
+int choose_rt(int dtype, int rows, int units) {
+  (void)dtype;
+  if (const char *e = getenv("GQ_MV_RT")) return atoi(e);
+  int best = 1;
+  double best_score = -1;
+  for (int rt = 1; rt <= 64; rt *= 2) {
+    const long uit = (long)rt * units;
+    if (rt > 1 && uit > 2048) break;  // per-wave partial sums stay <= 8 KiB of LDS
+    const long iters = (uit + 63) / 64;
+    const double lane_eff = (double)uit / (64.0 * iters);
+    const long waves = (rows + rt - 1) / rt;
+    const double fill = waves >= 2048 ? 1.0 : (double)waves / 2048.0;
+    const double score = lane_eff * fill * (iters >= 2 ? 1.0 : 0.97);
+    if (score > best_score + 1e-9) { best_score = score; best = rt; }
+  }
+  return best;
+}
+
+template <int FMT, bool K4>
+static hipError_t launch_t(const MvArgs &a, hipStream_t st) {
+  const size_t lds = matvec_lds_bytes(FMT, a.units, a.part_floats);
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute((const void *)k_matvec<FMT, K4>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  const int blocks = (a.total_tiles + 3) / 4;
+  hipLaunchKernelGGL((k_matvec<FMT, K4>), dim3(blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
-size_t matvec_lds_bytes(int kpad) { return (size_t)kpad * 4 + (size_t)kpad / 16 * 4 + 1024; }
-
-// Lanes per row: the smallest that still gives >= ~8 waves per CU, but no
-// more lanes than units in a row.
-static int pick_lpr(int fmt, int rows, int nb) {
-  const int unit_lanes = fmt == T_Q6_K ? 4 : 8;
-  const int units = fmt == T_Q8_0 ? 2 * nb : nb * unit_lanes;  // units per row
-  int lpr = fmt == T_Q8_0 ? 8 : unit_lanes;
-  while (lpr < 64 && (long)rows * lpr / 64 < 2048 && units >= 2 * lpr) lpr *= 2;
-  return lpr;
+template <int FMT>
+static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
+  return a.k % 4 == 0 ? launch_t<FMT, true>(a, st) : launch_t<FMT, false>(a, st);
 }
 
-hipError_t launch_matvec(const MvArgs &a, int fmt, int num_cus, hipStream_t st) {
-  const int lpr = pick_lpr(fmt, a.total_rows, a.nb);
-  const int rows_per_block = 4 * (64 / lpr);
-  long blocks = (a.total_rows + rows_per_block - 1) / rows_per_block;
-  const size_t lds = matvec_lds_bytes(a.kpad);
-  // Blocks that fit per CU given LDS, times CUs: one resident wave of blocks.
-  long per_cu = (long)(160 * 1024 / lds);
-  if (per_cu > 8) per_cu = 8;
-  if (per_cu < 1) per_cu = 1;
-  const long cap = per_cu * num_cus;
-  if (blocks > cap) blocks = cap;
+hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st) {
   switch (fmt) {
-  case T_Q4_K: return launch_fmt<T_Q4_K>(a, lpr, (int)blocks, lds, st);
-  case T_Q5_K: return launch_fmt<T_Q5_K>(a, lpr, (int)blocks, lds, st);
-  case T_Q6_K: return launch_fmt<T_Q6_K>(a, lpr, (int)blocks, lds, st);
-  case T_Q8_0: return launch_fmt<T_Q8_0>(a, lpr, (int)blocks, lds, st);
-  case T_IQ3_XXS: return launch_fmt<T_IQ3_XXS>(a, lpr, (int)blocks, lds, st);
+  case T_Q4_K: return launch_f<T_Q4_K>(a, st);
+  case T_Q5_K: return launch_f<T_Q5_K>(a, st);
+  case T_Q6_K: return launch_f<T_Q6_K>(a, st);
+  case T_Q8_0: return launch_f<T_Q8_0>(a, st);
+  case T_IQ3_XXS: return launch_f<T_IQ3_XXS>(a, st);
   default: return hipErrorInvalidValue;
   }
 }
