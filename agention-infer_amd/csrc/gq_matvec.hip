@@ -33,11 +33,14 @@ namespace gq {
 
 constexpr int LIMB_STRIDE = 272;  // LDS bytes per 256-element block of one limb (16 B pad)
 
+constexpr int AUX_STRIDE = 144;   // LDS bytes per unit of the per-16-run records (16 B pad)
+
+// Per 16-run record: {s of its 32-run, c} with c = sum(x) of the 32-run
+// (Q4_K/Q5_K) or sum(X) of the 16-run as int bits (Q6_K).  The 16 B pads
+// put the records of consecutive units in different LDS bank groups.
 struct Smem {
   uint8_t *l2, *l1, *l0;  // limbs, LIMB_STRIDE bytes per 256 elements
-  float *sx;              // fixed-point step per 32-run
-  float *xsum;            // sum(x) per 32-run (Q4_K / Q5_K)
-  int *xs16;              // sum(X) per 16-run (Q6_K)
+  float2 *aux;            // AUX_STRIDE bytes per unit
   uint32_t *grid;         // IQ3_XXS codebook
   float *part;            // per-wave per-unit partial sums
 };
@@ -47,16 +50,13 @@ __host__ __device__ inline size_t smem_layout(int units, int part_floats, Smem *
   auto take = [&](size_t n) { size_t r = o; o += (n + 15) & ~(size_t)15; return r; };
   const size_t limb = (size_t)units * LIMB_STRIDE;
   const size_t o2 = take(limb), o1 = take(limb), o0 = take(limb);
-  const size_t osx = take((size_t)units * 8 * 4), osum = take((size_t)units * 8 * 4);
-  const size_t o16 = take((size_t)units * 16 * 4), og = take(1024);
+  const size_t oaux = take((size_t)units * AUX_STRIDE), og = take(1024);
   const size_t op = take((size_t)4 * part_floats * 4);
   if (s) {
     s->l2 = (uint8_t *)(base + o2);
     s->l1 = (uint8_t *)(base + o1);
     s->l0 = (uint8_t *)(base + o0);
-    s->sx = (float *)(base + osx);
-    s->xsum = (float *)(base + osum);
-    s->xs16 = (int *)(base + o16);
+    s->aux = (float2 *)(base + oaux);
     s->grid = (uint32_t *)(base + og);
     s->part = (float *)(base + op);
   }
@@ -90,6 +90,11 @@ __device__ __forceinline__ float limbdot(const uint32_t *w, const Smem &S, int o
   return fmaf((float)a2, 65536.f, fmaf((float)a1, 256.f, (float)a0));
 }
 
+// Record of 16-run r (0..15) of unit u.
+__device__ __forceinline__ float2 aux_at(const Smem &S, int u, int r) {
+  return *(const float2 *)((const char *)S.aux + u * AUX_STRIDE + 8 * r);
+}
+
 __device__ __forceinline__ uint32_t dw(const uint4 *ch, int k) {
   const uint4 c = ch[k >> 2];
   const int m = k & 3;
@@ -121,14 +126,14 @@ __device__ __forceinline__ float unit_q4k(const uint4 *ch, int u, const Smem &S,
         hi[i] |= ((h >> (2 * j + 1)) & 0x01010101u) << 4;
       }
     }
-    const int r0 = 8 * u + 2 * j;
     const int off = u * LIMB_STRIDE + 64 * j;
     const float slo = limbdot<8>(lo, S, off);
     const float shi = limbdot<8>(hi, S, off + 32);
-    acc = fmaf(d * (float)sc0 * S.sx[r0], slo, acc);
-    acc = fmaf(-(dmin * (float)m0), S.xsum[r0], acc);
-    acc = fmaf(d * (float)sc1 * S.sx[r0 + 1], shi, acc);
-    acc = fmaf(-(dmin * (float)m1), S.xsum[r0 + 1], acc);
+    const float2 alo = aux_at(S, u, 4 * j), ahi = aux_at(S, u, 4 * j + 2);
+    acc = fmaf(d * (float)sc0 * alo.x, slo, acc);
+    acc = fmaf(-(dmin * (float)m0), alo.y, acc);
+    acc = fmaf(d * (float)sc1 * ahi.x, shi, acc);
+    acc = fmaf(-(dmin * (float)m1), ahi.y, acc);
   }
   return acc;
 }
@@ -159,8 +164,9 @@ __device__ __forceinline__ float unit_q6k(const uint4 *ch, uint32_t dbits, int u
         const int s = 8 * hh + 2 * t + half;  // 16-run within the unit = scale index
         const float sc = (float)(int8_t)(dw(ch + 12, s >> 2) >> (8 * (s & 3)));
         const float sqx = limbdot<4>(q[t], S, u * LIMB_STRIDE + 16 * s);
-        const float corr = sqx - 32.f * (float)S.xs16[16 * u + s];
-        acc = fmaf(sc * S.sx[8 * u + (s >> 1)], corr, acc);
+        const float2 ax = aux_at(S, u, s);
+        const float corr = sqx - 32.f * (float)__float_as_int(ax.y);
+        acc = fmaf(sc * ax.x, corr, acc);
       }
     }
   }
@@ -178,7 +184,7 @@ __device__ __forceinline__ float unit_q80(const uint4 *ch, int u, const Smem &S)
     for (int k = 0; k < 8; k++) w[k] = dw(ch, 8 * i + k);
     const float s = limbdot<8>(w, S, u * LIMB_STRIDE + 32 * i);
     const float d = h2f(dw(ch + 16, i >> 1) >> (16 * (i & 1)));
-    acc = fmaf(d * S.sx[8 * u + i], s, acc);
+    acc = fmaf(d * aux_at(S, u, 2 * i).x, s, acc);
   }
   return acc;
 }
@@ -211,7 +217,7 @@ __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u
     const int off = u * LIMB_STRIDE + 32 * ib;
     const float s = limbdot<8>(pos, S, off) - limbdot<8>(neg, S, off);
     const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
-    acc = fmaf(db * S.sx[8 * u + ib], s, acc);
+    acc = fmaf(db * aux_at(S, u, 2 * ib).x, s, acc);
   }
   return acc;
 }
@@ -219,6 +225,7 @@ __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u
 // ------------------------------------------------------------- staging
 // Thread t converts elements [4096p + 16t, +16) of x; 32-runs are thread
 // pairs (2m, 2m+1).  All threads execute the shuffles.
+template <bool Q6>
 __device__ __forceinline__ void stage_x(int kpad, int p, const float (&xv)[16], const Smem &S) {
   const int e0 = 4096 * p + 16 * (int)threadIdx.x;
   float amax = 0.f, sum = 0.f;
@@ -256,11 +263,14 @@ __device__ __forceinline__ void stage_x(int kpad, int p, const float (&xv)[16], 
   *(uint4 *)(S.l2 + lo) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
   *(uint4 *)(S.l1 + lo) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
   *(uint4 *)(S.l0 + lo) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
-  if ((threadIdx.x & 1) == 0) {
-    S.sx[e0 >> 5] = amax / LIMB_RANGE;
-    S.xsum[e0 >> 5] = sum32;
-  }
-  S.xs16[e0 >> 4] = xs;
+  put_aux<Q6>(S, e0, amax / LIMB_RANGE, sum32, xs);
+}
+
+template <bool Q6>
+__device__ __forceinline__ void put_aux(const Smem &S, int e0, float sx, float sum32, int xs) {
+  const int u = e0 >> 8, r = (e0 & 255) >> 4;
+  *(float2 *)((char *)S.aux + u * AUX_STRIDE + 8 * r) =
+      make_float2(sx, Q6 ? __int_as_float(xs) : sum32);
 }
 
 template <bool K4>
@@ -317,8 +327,13 @@ __device__ __forceinline__ float unit_dot(const Unit<FMT> &U, int u, const Smem 
 }
 
 // One wave = one tile of RT rows.  Blocks of 4 waves share the staged x.
+template <int FMT> struct Occ { static constexpr int W = 3; };
+template <> struct Occ<T_Q4_K> { static constexpr int W = 4; };
+template <> struct Occ<T_IQ3_XXS> { static constexpr int W = 4; };
+
 template <int FMT, bool K4>
-__global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
+__global__ __launch_bounds__(256)
+void k_matvec(MvArgs a) {
   extern __shared__ __align__(16) char smem_raw[];
   Smem S;
   smem_layout(a.units, a.part_floats, &S, smem_raw);
@@ -365,38 +380,41 @@ __global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
     load_unit<FMT>(A, p, cs, dp);
   }
   __builtin_amdgcn_sched_barrier(0);
-  stage_x(kpad, 0, xv, S);
+  stage_x<FMT == T_Q6_K>(kpad, 0, xv, S);
   for (int p = 1; 4096 * p < kpad; p++) {
     load_x16<K4>(a.x, a.k, 4096 * p + 16 * tid, xv);
-    stage_x(kpad, p, xv, S);
+    stage_x<FMT == T_Q6_K>(kpad, p, xv, S);
   }
   if constexpr (FMT == T_IQ3_XXS) S.grid[tid] = gword;
   __syncthreads();
 
   float *part = S.part + wave * a.part_floats;
-  for (int it = 0; it < iters; it += 2) {
-    {
-      long cs;
-      const uint16_t *dp;
-      const uint8_t *p = unit_ptr(min(it + 1, iters - 1), cs, dp);
-      load_unit<FMT>(B, p, cs, dp);
-    }
-    {
-      const int j = 64 * it + lane;
-      const float v = unit_dot<FMT>(A, j % U, S);
-      if (j < uit) part[j] = v;
-    }
-    {
-      long cs;
-      const uint16_t *dp;
-      const uint8_t *p = unit_ptr(min(it + 2, iters - 1), cs, dp);
-      load_unit<FMT>(A, p, cs, dp);
-    }
-    if (it + 1 < iters) {
-      const int j = 64 * (it + 1) + lane;
-      const float v = unit_dot<FMT>(B, j % U, S);
-      if (j < uit) part[j] = v;
-    }
+  auto load_it = [&](Unit<FMT> &dst, int it) {
+    long cs;
+    const uint16_t *dp;
+    const uint8_t *p = unit_ptr(it, cs, dp);
+    load_unit<FMT>(dst, p, cs, dp);
+  };
+  auto consume = [&](const Unit<FMT> &src, int it) {
+    const int j = 64 * it + lane;
+    const float v = unit_dot<FMT>(src, j % U, S);
+    if (j < uit) part[j] = v;
+  };
+  // Steady state: two units in flight per lane; the tail is peeled so that
+  // no unit is ever loaded twice.
+  int it = 0;
+  for (; it + 2 < iters; it += 2) {
+    load_it(B, it + 1);
+    consume(A, it);
+    load_it(A, it + 2);
+    consume(B, it + 1);
+  }
+  if (it + 1 < iters) {
+    load_it(B, it + 1);
+    consume(A, it);
+    consume(B, it + 1);
+  } else {
+    consume(A, it);
   }
   __syncthreads();
 

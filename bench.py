@@ -1,14 +1,16 @@
 """Benchmark: Qwen2.5-7B-shaped Q4_K_M decode-layer matvecs on one MI355X.
 
 One step = one batch-1 pass over the decode matvecs of one layer plus the
-output head, with weights resident in HBM:
+output head, with weights resident in HBM (5 launches: qkv, o, gate+up,
+down, head -- same-input weights share a launch as in the reference's
+resident path):
     Wq 3584x3584, Wk 512x3584, Wv 512x3584, Wo 3584x3584,
     Wgate 18944x3584, Wup 18944x3584          (Q4_K)
     Wdown 3584x18944, head 152064x3584        (Q6_K)
 value = algorithmic bytes per step (weights + x + y) / step time, in GB/s.
-Every timed launch reads its weights cold from HBM: each matrix has enough
-device copies (>= 1 GiB per rotation set) that the 256 MB Infinity Cache
-cannot hold the working set, and steps rotate through the copies.
+Every timed launch reads its weights cold from HBM (two device copies per
+matrix, alternated; a step streams ~0.6 GB, more than twice the 256 MB
+Infinity Cache).  Each step is one captured HIP graph of the 8 launches.
 
 Prints ONE JSON line (rank 0).  --gpus above 1 exits: this build uses one GPU.
 """
@@ -30,7 +32,22 @@ MATS = [  # name, dtype, out_dim, in_dim
     ("Wo", Q4_K, HID, HID), ("Wgate", Q4_K, FFN, HID), ("Wup", Q4_K, FFN, HID),
     ("Wdown", Q6_K, HID, FFN), ("head", Q6_K, VOCAB, HID),
 ]
-ROTATION_BYTES = 1 << 30
+# Two device copies of every matrix, alternated step to step: between two
+# uses of a copy the step streams > 1 GB (the head alone is 447 MB), far
+# more than the 256 MB Infinity Cache, so every launch reads cold HBM.
+NCOPY = 2
+
+
+def measured_traffic():
+    """HBM bytes per head launch from the committed rocprof summary, or None."""
+    path = os.path.join(ROOT, "profiles", "matvec_q6k_head_and_q4k_layer.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def algo_bytes(gq, dtype, out_dim, in_dim):
@@ -64,6 +81,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="also run a plain 256 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
@@ -85,9 +104,8 @@ def main():
         host[name] = w
         nb = algo_bytes(gq, dtype, out_dim, in_dim)
         mats.append((name, dtype, out_dim, in_dim, nb))
-        ncopy = max(2, -(-ROTATION_BYTES // w.nbytes))
         dev = torch.from_numpy(w.reshape(-1)).cuda()
-        copies[name] = [be.upload_weight(dtype, dev, in_dim, out_dim) for _ in range(ncopy)]
+        copies[name] = [be.upload_weight(dtype, dev, in_dim, out_dim) for _ in range(NCOPY)]
         del dev
     for d in (HID, FFN):
         xs[d] = syn.make_x(d, seed=d)
@@ -96,53 +114,78 @@ def main():
           for name, _, out_dim, _, _ in mats}
     torch.cuda.synchronize()
 
-    def step(s, ev=None):
-        for name, dtype, out_dim, in_dim, _ in mats:
-            cs = copies[name]
-            if ev is not None and name == "head":
-                ev[0].record(stream)
-            cs[s % len(cs)].launch_only(xd[in_dim], yd[name])
-            if ev is not None and name == "head":
-                ev[1].record(stream)
+    # The decode layer launches matvecs the way the reference's resident path
+    # groups them: same-input weights share one launch
+    # (matmul_dequant_qkv / _ffn, src/ops/wgpu_backend/mod.rs:702-854).
+    GROUPS = [("Wq", "Wk", "Wv"), ("Wo",), ("Wgate", "Wup"), ("Wdown",), ("head",)]
+    dims = {name: in_dim for name, _, _, in_dim, _ in mats}
+    nbytes = {name: nb for name, *_, nb in mats}
 
+    def group_bytes(grp):  # weights + y of every member, x once
+        return sum(nbytes[n] - 4 * dims[n] for n in grp) + 4 * dims[grp[0]]
+    step_bytes = sum(group_bytes(g) for g in GROUPS)
+
+    def step(s):
+        for grp in GROUPS:
+            hs = [copies[n][s % NCOPY] for n in grp]
+            if len(grp) == 1:
+                hs[0].launch_only(xd[dims[grp[0]]], yd[grp[0]])
+            else:
+                be.matmul_dequant_multi(hs, xd[dims[grp[0]]], [yd[n] for n in grp])
+
+    # Warm up (also compiles nothing: kernels are prebuilt), then capture one
+    # HIP graph per copy parity so the timed loop is launch-overhead free.
     for s in range(args.warmup):
         step(s)
     torch.cuda.synchronize()
-
-    head_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-               for _ in range(args.steps)]
-    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    graphs = []
+    for r in range(NCOPY):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(r)
+        graphs.append(g)
+    for g in graphs:
+        g.replay()
     torch.cuda.synchronize()
+
+    t_start, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
-    t_start.record(stream)
+    t_start.record()
     for s in range(args.steps):
-        step(args.warmup + s, head_ev[s])
-    t_end.record(stream)
+        graphs[s % NCOPY].replay()
+    t_end.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms_total = t_start.elapsed_time(t_end)
     ms_step = ms_total / args.steps
-    step_bytes = sum(b for *_, b in mats)
     value = step_bytes / (ms_step * 1e-3) / 1e9
 
-    head_ms = float(np.mean([a.elapsed_time(b) for a, b in head_ev]))
-    head_bytes = [b for n, *_, b in mats if n == "head"][0]
-    achieved = head_bytes / (head_ms * 1e-3) / 1e9
-
-    # Per-matrix cold-cache kernel times (events bracket 20 back-to-back
-    # launches that rotate through the copies).
+    # Per-launch kernel time: a graph of REPS launches of one group,
+    # alternating the copies, bracketed by events on the replay stream.
     per = {}
-    for name, dtype, out_dim, in_dim, nb in mats:
-        cs = copies[name]
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = 20
-        e0.record(stream)
-        for r in range(reps):
-            cs[r % len(cs)].launch_only(xd[in_dim], yd[name])
-        e1.record(stream)
+    REPS = 20
+    for grp in GROUPS:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for r in range(REPS):
+                hs = [copies[n][r % NCOPY] for n in grp]
+                if len(grp) == 1:
+                    hs[0].launch_only(xd[dims[grp[0]]], yd[grp[0]])
+                else:
+                    be.matmul_dequant_multi(hs, xd[dims[grp[0]]], [yd[n] for n in grp])
+        g.replay()
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / reps
-        per[name] = {"us": round(us, 2), "GB/s": round(nb / (us * 1e-6) / 1e9, 1)}
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / REPS
+        nb = group_bytes(grp)
+        per["+".join(grp)] = {"us": round(us, 2), "GB/s": round(nb / (us * 1e-6) / 1e9, 1)}
+    head_bytes = [b for n, *_, b in mats if n == "head"][0]
+    head_us = per["head"]["us"]
+    achieved = head_bytes / (head_us * 1e-6) / 1e9
 
     out = {
         "metric": "Q4_K/Q6_K matvec HBM GB/s (% of peak); 7B-shape Q4_K_M decode tok/s",
@@ -159,14 +202,20 @@ def main():
         "data": "synthetic (seeded ggml blocks with the BASELINE distributions)",
         "config": {"workload": "Qwen2.5-7B-shaped Q4_K_M decode-layer matvecs, batch 1 "
                                "(Wq,Wk,Wv,Wo,Wgate,Wup Q4_K; Wdown,head Q6_K), cold HBM",
-                   "step_bytes": step_bytes, "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
+                   "step_bytes": step_bytes, "timing": "HIP graph per step", "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
                    "wall_s": round(wall, 4)},
         "roofline": {"bound": "hbm", "kernel": "k_matvec<Q6_K> (output head 152064x3584)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "launch_us": round(head_ms * 1e3, 2), "algo_bytes": head_bytes},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                     "launch_us": head_us, "algo_bytes": head_bytes},
         "per_kernel": per,
     }
+    if args.calib_copy:
+        src = torch.ones(64 * 1024 * 1024, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     if not args.no_cpu:
         nthreads = min(len(os.sched_getaffinity(0)), 16)
         out["cpu_baseline"] = cpu_baseline(mats, host, xs, nthreads, args.cpu_seconds)
