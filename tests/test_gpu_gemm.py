@@ -1,0 +1,129 @@
+"""GPU parity for the batched prefill GEMM (gq_gemm) against CPU references.
+
+Both modes change the operands' precision by definition, so each is
+compared against a CPU matmul of the *same* operands (tolerance
+max|err| <= 1e-4 * max|y_ref|, fp64 reference):
+  * GQ_GEMM_BF16: W = bf16(dequant(W)) (round to nearest even of the
+    bit-exact fp32 dequant), X = bf16(X).
+  * GQ_GEMM_INT8: W = dequant(W) exactly, X = per-32 Q8 pack of X
+    (KvDtype::Q8_0::pack, src/model/mod.rs:574-583), i.e. q * f16(scale).
+The distance to the fp32 CPU path (WeightMap::matmul_batch_into,
+src/model/mod.rs:414-464) is also checked, with a tolerance that reflects
+the operand rounding (bf16: 2^-9 relative per operand).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import gq_synth as syn
+
+pytestmark = pytest.mark.gpu
+
+Q4_K = 12
+TOL = 1e-4
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def bf16_round(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def run(backend, orc, rows, k, n, mode, seed):
+    import torch
+    import gq
+    w = syn.make_blocks(Q4_K, rows, k, seed=seed)
+    X = syn.make_x(k, seed=seed + 1, batch=n)
+    h = backend.upload_weight(Q4_K, w, k, rows)
+    Y = h.launch_only_batch(torch.from_numpy(X).cuda(), mode=mode)
+    torch.cuda.synchronize()
+    Wf = orc.dequant(Q4_K, w.reshape(-1), rows * k).reshape(rows, k) if k % 256 == 0 else \
+        orc.dequant_rows(Q4_K, w, k)
+    return w, X, Wf, Y.cpu().numpy()
+
+
+def check(y, ref, what, tol=TOL):
+    err = float(np.max(np.abs(y.astype(np.float64) - ref)))
+    bound = tol * float(np.max(np.abs(ref)))
+    say(f"{what}: max|err| {err:.3g} bound {bound:.3g}")
+    assert err <= bound, f"{what}: max|err| {err:.3g} > {bound:.3g}"
+
+
+SHAPES = [(331, 512, 37), (1024, 3584, 64), (160, 256, 256), (7, 300, 5), (2000, 1024, 300)]
+
+
+@pytest.mark.parametrize("rows,k,n", SHAPES)
+def test_gemm_bf16(backend, orc, rows, k, n):
+    import gq
+    say(f"gemm bf16 rows={rows} k={k} n={n}")
+    w, X, Wf, Y = run(backend, orc, rows, k, n, gq.GQ_GEMM_BF16, seed=rows + k)
+    ref = bf16_round(X).astype(np.float64) @ bf16_round(Wf).astype(np.float64).T
+    check(Y, ref, "bf16 vs same-operand fp64")
+    ref32 = orc.matmul_batch_into(Q4_K, w, X, rows)
+    check(Y, ref32, "bf16 vs fp32 CPU path", tol=1e-2)
+
+
+@pytest.mark.parametrize("rows,k,n", SHAPES)
+def test_gemm_int8(backend, orc, rows, k, n):
+    import gq
+    say(f"gemm int8 rows={rows} k={k} n={n}")
+    w, X, Wf, Y = run(backend, orc, rows, k, n, gq.GQ_GEMM_INT8, seed=rows + k + 1)
+    kp = (k + 31) // 32 * 32
+    Xq = np.zeros((n, k), np.float64)
+    for t in range(n):
+        sc, q = orc.quantize_q8_32(X[t])
+        s = np.repeat(sc.view(np.float16).astype(np.float64), 32)[:kp]
+        Xq[t] = (q.astype(np.float64) * s[: q.size])[:k]
+    ref = Xq @ Wf.astype(np.float64).T
+    check(Y, ref, "int8 vs same-operand fp64")
+    ref32 = orc.matmul_batch_into(Q4_K, w, X, rows)
+    check(Y, ref32, "int8 vs fp32 CPU path", tol=3e-2)
+
+
+def test_gemm_full_config(backend, orc):
+    """config 2: Q4_K 18944 x 3584 times 512 tokens, both modes."""
+    import gq
+    import torch
+    rows, k, n = 18944, 3584, 512
+    say("gemm full config 18944x3584x512")
+    w = syn.make_blocks(Q4_K, rows, k, seed=42)
+    X = syn.make_x(k, seed=43, batch=n)
+    h = backend.upload_weight(Q4_K, w, k, rows)
+    Xd = torch.from_numpy(X).cuda()
+    Yb = h.launch_only_batch(Xd, mode=gq.GQ_GEMM_BF16).cpu().numpy()
+    Yi = h.launch_only_batch(Xd, mode=gq.GQ_GEMM_INT8).cpu().numpy()
+    torch.cuda.synchronize()
+    Wf = orc.dequant(Q4_K, w.reshape(-1), rows * k).reshape(rows, k).astype(np.float64)
+    ref = bf16_round(X).astype(np.float64) @ bf16_round(Wf.astype(np.float32)).astype(np.float64).T
+    check(Yb, ref, "full bf16 vs same-operand fp64")
+    Xq = np.zeros((n, k), np.float64)
+    for t in range(n):
+        sc, q = orc.quantize_q8_32(X[t])
+        Xq[t] = q.astype(np.float64) * np.repeat(sc.view(np.float16).astype(np.float64), 32)
+    check(Yi, Xq @ Wf.T, "full int8 vs same-operand fp64")
+
+
+def test_gemm_errors_and_edges(backend):
+    import gq
+    import torch
+    w = syn.make_blocks(6 + 8, 4, 256, seed=1)  # Q6_K: no GEMM mode
+    h = backend.upload_weight(14, w, 256, 4)
+    with pytest.raises(gq.GqError, match="not supported"):
+        h.launch_only_batch(torch.zeros((2, 256), device="cuda"))
+    w4 = syn.make_blocks(Q4_K, 4, 256, seed=1)
+    h4 = backend.upload_weight(Q4_K, w4, 256, 4)
+    with pytest.raises(gq.GqError, match="mode"):
+        h4.launch_only_batch(torch.zeros((2, 256), device="cuda"), mode=7)
+    # n = 0 is a no-op; zero weights give zeros
+    h4.launch_only_batch(torch.zeros((0, 256), device="cuda"))
+    z = backend.upload_weight(Q4_K, syn.make_blocks(Q4_K, 9, 512, zero=True), 512, 9)
+    for mode in (gq.GQ_GEMM_BF16, gq.GQ_GEMM_INT8):
+        y = z.launch_only_batch(torch.randn((3, 512), device="cuda"), mode=mode)
+        torch.cuda.synchronize()
+        assert torch.all(y == 0)
