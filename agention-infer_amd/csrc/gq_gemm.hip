@@ -208,11 +208,13 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *body
 
   for (int kt = 0; kt < stages; kt++) {
     const int buf = kt & 1;
-    const bool more = kt + 1 < stages;
-    if (more) {
-      if (wtask) wr = load_w(L, body, m0 + wrow, (kt + 1) >> 2, (kt + 1) & 3);
-      load_x(kt + 1, xr);
-    }
+    // Straight-line stage body (no branch around the next stage's loads and
+    // dequant) so the scheduler can interleave the dequant VALU work with
+    // this stage's MFMAs; past the last stage it reloads the last stage into
+    // the unused buffer.
+    const int kn = min(kt + 1, stages - 1);
+    if (wtask) wr = load_w(L, body, m0 + wrow, kn >> 2, kn & 3);
+    load_x(kn, xr);
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
       const int kk = 32 * ks + 8 * (lane >> 4);
@@ -231,10 +233,8 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *body
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[i][j], 0, 0, 0);
       }
     }
-    if (more) {
-      if (wtask) dequant_sub_bf16(wr, (kt + 1) & 3, whi, &As[buf ^ 1][wrow * LDA + 32 * whi]);
-      store_x(buf ^ 1, xr);
-    }
+    if (wtask) dequant_sub_bf16(wr, kn & 3, whi, &As[buf ^ 1][wrow * LDA + 32 * whi]);
+    store_x(buf ^ 1, xr);
     __syncthreads();
   }
 

@@ -21,7 +21,7 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libgq.so")
+LIB_PATH = os.environ.get("GQ_LIBRARY") or os.path.join(_HERE, "libgq.so")
 
 GQ_GEMM_BF16 = 0
 GQ_GEMM_INT8 = 1
