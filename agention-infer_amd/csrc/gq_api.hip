@@ -121,7 +121,7 @@ int check_matvec(const gq_weight *w) {
 }
 
 int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes, int in_dim,
-                  int out_dim, gq_weight **out) {
+                  int out_dim, gq_weight **out, int rows_per_group = 0) {
   if (!out) return fail(GQ_EINVAL, "null output handle pointer");
   *out = nullptr;
   int rc = ensure_init();
@@ -144,6 +144,14 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   w->L.units = (in_dim + 255) / 256;
   w->L.chunks = gq::unit_chunks(dtype);
   w->L.rt = gq::choose_rt(dtype, out_dim, w->L.units);
+  // Stacked expert tensors: a tile must not straddle two experts, and only
+  // a few experts run per token, so tiles are small (at most three wave
+  // iterations: rt * units <= 192) to spread each expert over many waves.
+  if (rows_per_group > 0) {
+    w->L.rt = 1;
+    while (w->L.rt < 64 && 2 * w->L.rt * w->L.units <= 192 && rows_per_group % (2 * w->L.rt) == 0)
+      w->L.rt *= 2;
+  }
   w->ggml_bytes = need;
   w->device = g_dev.device;
   const size_t body = (size_t)gq::body_bytes(w->L);
@@ -207,6 +215,66 @@ int gq_upload(int dtype, const void *w_host, size_t nbytes, int in_dim, int out_
 int gq_upload_device(int dtype, const void *w_dev, size_t nbytes, int in_dim, int out_dim,
                      gq_weight **out) {
   return upload_common(dtype, w_dev, true, nbytes, in_dim, out_dim, out);
+}
+
+int gq_upload_experts(int dtype, const void *w_host, size_t nbytes, int in_dim,
+                      int rows_per_expert, int n_experts, gq_weight **out) {
+  if (rows_per_expert <= 0 || n_experts <= 0)
+    return fail(GQ_EINVAL, "bad expert shape %d x %d", n_experts, rows_per_expert);
+  return upload_common(dtype, w_host, false, nbytes, in_dim, rows_per_expert * n_experts, out,
+                       rows_per_expert);
+}
+
+int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, int n_experts,
+               const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
+               int *ids_dev, float *w_dev, void *stream) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (!gate || !up || !down) return fail(GQ_EINVAL, "null expert weight handle");
+  if (T < 0 || n_experts <= 0 || n_experts > 4096 || top_k <= 0 || top_k > n_experts)
+    return fail(GQ_EINVAL, "bad MoE shape T=%d experts=%d top_k=%d", T, n_experts, top_k);
+  if (T == 0) return GQ_OK;
+  const int h = gate->L.k, f = down->L.k;
+  if (gate->L.dtype != up->L.dtype || gate->L.dtype != down->L.dtype)
+    return fail(GQ_EINVAL, "expert tensors must share one dtype");
+  if (up->L.k != h || gate->L.rows != n_experts * f || up->L.rows != n_experts * f ||
+      down->L.rows != n_experts * h)
+    return fail(GQ_EINVAL, "expert shapes disagree: gate %dx%d up %dx%d down %dx%d, experts %d",
+                gate->L.rows, gate->L.k, up->L.rows, up->L.k, down->L.rows, down->L.k, n_experts);
+  if (gate->L.rt != up->L.rt || f % gate->L.rt || h % down->L.rt)
+    return fail(GQ_EINVAL, "expert tensors must be uploaded with gq_upload_experts");
+  if (!logits_dev || !x_dev || !out_dev) return fail(GQ_EINVAL, "null MoE buffer");
+  const int pairs = T * top_k;
+  const size_t ws = (size_t)pairs * (2 * (size_t)f + (size_t)h) * 4 + (size_t)pairs * 8 + 1024;
+  char *wsp = nullptr;
+  HIP_TRY(hipMallocAsync((void **)&wsp, ws, (hipStream_t)stream));
+  gq::MoeArgs a{};
+  a.fmt = gate->L.dtype;
+  a.n_experts = n_experts;
+  a.top_k = top_k;
+  a.h = h;
+  a.f = f;
+  a.gate = gate->body; a.up = up->body; a.down = down->body;
+  a.gate_d = gate->d; a.up_d = up->d; a.down_d = down->d;
+  a.rt_h = gate->L.rt;
+  a.rt_f = down->L.rt;
+  a.units_h = gate->L.units;
+  a.units_f = down->L.units;
+  a.part_h = (a.rt_h * a.units_h + 63) / 64 * 64;
+  a.part_f = (a.rt_f * a.units_f + 63) / 64 * 64;
+  a.grid = g_dev.grid;
+  a.logits = logits_dev;
+  a.x = x_dev;
+  a.tmp_g = (float *)wsp;
+  a.tmp_u = a.tmp_g + (size_t)pairs * f;
+  a.tmp_y = a.tmp_u + (size_t)pairs * f;
+  a.ids = ids_dev ? ids_dev : (int *)(a.tmp_y + (size_t)pairs * h);
+  a.w = w_dev ? w_dev : (float *)((int *)(a.tmp_y + (size_t)pairs * h) + pairs);
+  a.out = out_dev;
+  hipError_t e = gq::launch_moe(a, T, (hipStream_t)stream);
+  (void)hipFreeAsync(wsp, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(GQ_EHIP, "MoE launch failed: %s", hipGetErrorString(e));
+  return GQ_OK;
 }
 
 int gq_weight_free(gq_weight *w) {
@@ -337,10 +405,14 @@ int gq_set_iq3xxs_grid(const uint32_t *grid_host) {
   if (rc) return rc;
   std::lock_guard<std::mutex> lk(g_mu);
   if (grid_host) {
-    // magnitudes enter signed 8-bit dot products: each byte must be < 128
-    for (int i = 0; i < 256; i++)
-      if (grid_host[i] & 0x80808080u)
-        return fail(GQ_EINVAL, "IQ3_XXS grid entry %d has a magnitude byte >= 128", i);
+    // magnitudes enter signed 8-bit dot products, negated bytewise:
+    // each byte must be in 1..127 (ggml's codebook uses 4..62)
+    for (int i = 0; i < 256; i++) {
+      const uint32_t g = grid_host[i];
+      if ((g & 0x80808080u) || !(g & 0xffu) || !(g & 0xff00u) || !(g & 0xff0000u) ||
+          !(g & 0xff000000u))
+        return fail(GQ_EINVAL, "IQ3_XXS grid entry %d has a magnitude byte outside 1..127", i);
+    }
     memcpy(g_dev.grid_host, grid_host, 1024);
   }
   else default_grid(g_dev.grid_host);

@@ -39,6 +39,26 @@ struct MvArgs {
   MvSeg seg[MV_MAX_SEG];
 };
 
+// MoE expert FFN (router, grouped gate/up, down, combine).
+struct MoeArgs {
+  int fmt;
+  int n_experts, top_k, h, f;       // hidden h, expert intermediate f
+  const uint8_t *gate, *up, *down;  // stacked expert matrices (wave-tiled)
+  const uint16_t *gate_d, *up_d, *down_d;
+  int rt_h, rt_f;                   // rows per tile: gate/up (K = h), down (K = f)
+  int units_h, units_f, part_h, part_f;
+  const uint32_t *grid;
+  const float *logits;              // [T][n_experts]
+  const float *x;                   // [T][h]
+  int *ids;                         // [T][top_k]
+  float *w;                         // [T][top_k]
+  float *tmp_g, *tmp_u;             // [T*top_k][f]
+  float *tmp_y;                     // [T*top_k][h]
+  float *out;                       // [T][h]
+};
+
+hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st);
+
 size_t matvec_lds_bytes(int dtype, int units, int part_floats);
 hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st);
 

@@ -191,8 +191,14 @@ __device__ __forceinline__ float unit_q80(const uint4 *ch, int u, const Smem &S)
 
 // ------------------------------------------------------------- IQ3_XXS
 // ch[0..3] = 64 grid indices, ch[4..5] = 8 sign/scale words; d separate.
-// Signs are applied by splitting each group into its positive and negative
-// magnitudes (two dot products), so no byte negation can carry.
+// A sign is applied by two's-complement negation of the magnitude byte:
+// (g ^ 0xff) + 1 per byte, which cannot carry because magnitudes are in
+// 1..127 (enforced when a codebook is installed).
+__device__ __forceinline__ uint32_t neg_bytes(uint32_t g, uint32_t nib) {
+  const uint32_t m = ((nib * 0x00204081u) & 0x01010101u) * 0xFFu;  // 0xff per negative byte
+  return (g ^ m) + (m & 0x01010101u);
+}
+
 __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u, const Smem &S) {
   const float d = h2f(dbits);
   float acc = 0.f;
@@ -200,22 +206,17 @@ __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u
   for (int ib = 0; ib < 8; ib++) {
     const uint32_t aux = dw(ch + 4, ib);
     const uint32_t i0 = dw(ch, 2 * ib), i1 = dw(ch, 2 * ib + 1);
-    uint32_t pos[8], neg[8];
+    uint32_t q[8];
 #pragma unroll
     for (int l = 0; l < 4; l++) {
       const uint32_t sg = ksign7((aux >> (7 * l)) & 127u);
       const uint32_t word = l < 2 ? i0 : i1;
       const uint32_t g1 = S.grid[(word >> (16 * (l & 1))) & 0xff];
       const uint32_t g2 = S.grid[(word >> (16 * (l & 1) + 8)) & 0xff];
-      const uint32_t m1 = (((sg & 15u) * 0x00204081u) & 0x01010101u) * 0xFFu;
-      const uint32_t m2 = (((sg >> 4) * 0x00204081u) & 0x01010101u) * 0xFFu;
-      pos[2 * l] = g1 & ~m1;
-      neg[2 * l] = g1 & m1;
-      pos[2 * l + 1] = g2 & ~m2;
-      neg[2 * l + 1] = g2 & m2;
+      q[2 * l] = neg_bytes(g1, sg & 15u);
+      q[2 * l + 1] = neg_bytes(g2, sg >> 4);
     }
-    const int off = u * LIMB_STRIDE + 32 * ib;
-    const float s = limbdot<8>(pos, S, off) - limbdot<8>(neg, S, off);
+    const float s = limbdot<8>(q, S, u * LIMB_STRIDE + 32 * ib);
     const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
     acc = fmaf(db * aux_at(S, u, 2 * ib).x, s, acc);
   }
@@ -326,51 +327,71 @@ __device__ __forceinline__ float unit_dot(const Unit<FMT> &U, int u, const Smem 
   else return unit_iq3(U.ch, U.d, u, S);
 }
 
-// One wave = one tile of RT rows.  Blocks of 4 waves share the staged x.
-template <int FMT> struct Occ { static constexpr int W = 3; };
-template <> struct Occ<T_Q4_K> { static constexpr int W = 4; };
-template <> struct Occ<T_IQ3_XXS> { static constexpr int W = 4; };
+// One wave's job: tile t (RT rows) of one weight matrix.
+struct WaveJob {
+  const uint8_t *body;
+  const uint16_t *d;
+  float *y;
+  int rows, rt, t;
+  bool valid;
+};
 
-template <int FMT, bool K4>
-__global__ __launch_bounds__(256)
-void k_matvec(MvArgs a) {
-  extern __shared__ __align__(16) char smem_raw[];
+// x sources: load 16 consecutive x values (zero past k) for staging.
+template <bool K4>
+struct XPlain {
+  const float *x;
+  int k;
+  __device__ __forceinline__ void load(int e0, float (&xv)[16]) const { load_x16<K4>(x, k, e0, xv); }
+};
+
+// MoE down projection input: silu(g) * u of the gate/up outputs
+// (the SwiGLU of ffn_gate_up, src/model/llama/cpu_path.rs:225-227).
+struct XSwiGLU {
+  const float *g, *u;
+  int k;
+  __device__ __forceinline__ void load(int e0, float (&xv)[16]) const {
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int e = min(e0 + i, k - 1);
+      const float gv = g[e], uv = u[e];
+      const float sv = gv / (1.0f + expf(-gv)) * uv;
+      xv[i] = e0 + i < k ? sv : 0.f;
+    }
+  }
+};
+
+// The body shared by every matvec kernel: stage x (limbs) in LDS, stream
+// the job's tile with two units in flight per lane, reduce rows.  All four
+// waves of the block must share the x source (they share the staging).
+template <int FMT, class XS>
+__device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_floats,
+                                            const uint32_t *gsrc, const XS &xsrc, char *smem_raw) {
   Smem S;
-  smem_layout(a.units, a.part_floats, &S, smem_raw);
+  smem_layout(U, part_floats, &S, smem_raw);
   constexpr int C = Fmt<FMT>::C;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int gw = blockIdx.x * 4 + wave;
-  const bool valid = gw < a.total_tiles;
-  const int gwc = valid ? gw : a.total_tiles - 1;
-
-  // Segment of this wave (wave-uniform selects over scalar arguments).
-  MvSeg sg = a.seg[0];
-#pragma unroll
-  for (int i = 1; i < MV_MAX_SEG; i++)
-    if (i < a.nseg && gwc >= a.seg[i].tile_begin) sg = a.seg[i];
-  const int t = gwc - sg.tile_begin;
-  const int U = a.units;
-  const int rows_here = min(sg.rt, sg.rows - t * sg.rt);
+  const int t = job.t;
+  const int rows_here = min(job.rt, job.rows - t * job.rt);
   const int uit = rows_here * U;
   const int iters = (uit + 63) >> 6;
   const int nv_last = uit - 64 * (iters - 1);
-  const long tile_base = (long)t * sg.rt * U * C * 16;
-  const long dbase = (long)t * sg.rt * U;
+  const long tile_base = (long)t * job.rt * U * C * 16;
+  const long dbase = (long)t * job.rt * U;
   auto unit_ptr = [&](int it, long &cstride, const uint16_t *&dp) -> const uint8_t * {
     const bool last = it == iters - 1;
     const int l = last ? min(lane, nv_last - 1) : lane;
     cstride = last ? 16L * nv_last : 1024L;
-    dp = sg.d + dbase + 64 * it + l;
-    return sg.body + tile_base + (long)it * C * 1024 + 16 * l;
+    dp = job.d + dbase + 64 * it + l;
+    return job.body + tile_base + (long)it * C * 1024 + 16 * l;
   };
 
   // x of the first pass, then the first weight unit, then the LDS stores:
   // the wait before the stores leaves the weight loads in flight.
   const int kpad = U * 256;
   float xv[16];
-  load_x16<K4>(a.x, a.k, 16 * tid, xv);
+  xsrc.load(16 * tid, xv);
   uint32_t gword = 0;
-  if constexpr (FMT == T_IQ3_XXS) gword = a.grid[tid];
+  if constexpr (FMT == T_IQ3_XXS) gword = gsrc[tid];
   __builtin_amdgcn_sched_barrier(0);
   Unit<FMT> A, B;
   {
@@ -382,13 +403,13 @@ void k_matvec(MvArgs a) {
   __builtin_amdgcn_sched_barrier(0);
   stage_x<FMT == T_Q6_K>(kpad, 0, xv, S);
   for (int p = 1; 4096 * p < kpad; p++) {
-    load_x16<K4>(a.x, a.k, 4096 * p + 16 * tid, xv);
+    xsrc.load(4096 * p + 16 * tid, xv);
     stage_x<FMT == T_Q6_K>(kpad, p, xv, S);
   }
   if constexpr (FMT == T_IQ3_XXS) S.grid[tid] = gword;
   __syncthreads();
 
-  float *part = S.part + wave * a.part_floats;
+  float *part = S.part + wave * part_floats;
   auto load_it = [&](Unit<FMT> &dst, int it) {
     long cs;
     const uint16_t *dp;
@@ -419,13 +440,125 @@ void k_matvec(MvArgs a) {
   __syncthreads();
 
   // Row sums: 64/RT lanes per row, fixed order.
-  const int lpr = 64 / sg.rt;
+  const int lpr = 64 / job.rt;
   const int row = lane / lpr, sub = lane % lpr;
   float v = 0.f;
   if (row < rows_here)
     for (int c = sub; c < U; c += lpr) v += part[row * U + c];
   for (int off = lpr >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  if (valid && sub == 0 && row < rows_here) sg.y[t * sg.rt + row] = v;
+  if (job.valid && sub == 0 && row < rows_here) job.y[t * job.rt + row] = v;
+}
+
+// Plain / multi-segment matvec: one wave per tile over the segments.
+template <int FMT, bool K4>
+__global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
+  extern __shared__ __align__(16) char smem_raw[];
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool valid = gw < a.total_tiles;
+  const int gwc = valid ? gw : a.total_tiles - 1;
+  // Segment of this wave (wave-uniform selects over scalar arguments).
+  MvSeg sg = a.seg[0];
+#pragma unroll
+  for (int i = 1; i < MV_MAX_SEG; i++)
+    if (i < a.nseg && gwc >= a.seg[i].tile_begin) sg = a.seg[i];
+  const WaveJob job{sg.body, sg.d, sg.y, sg.rows, sg.rt, gwc - sg.tile_begin, valid};
+  matvec_wave<FMT>(job, a.units, a.part_floats, a.grid, XPlain<K4>{a.x, a.k}, smem_raw);
+}
+
+// ------------------------------------------------------------------- MoE
+// Pair p = (token p / top_k, slot p % top_k) routed to expert ids[p].
+// Stage 1: gate_e . x_t and up_e . x_t for every pair (blockIdx.y = p,
+// waves over the 2 * F / rt tiles of the two expert matrices).
+template <int FMT, bool K4>
+__global__ __launch_bounds__(256) void k_moe_gate_up(MoeArgs a) {
+  extern __shared__ __align__(16) char smem_raw[];
+  const int p = blockIdx.y;
+  const int e = a.ids[p];
+  const int tok = p / a.top_k;
+  const int tiles = a.f / a.rt_h;  // tiles per expert matrix
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool valid = gw < 2 * tiles;
+  const int gwc = valid ? gw : 2 * tiles - 1;
+  const bool is_up = gwc >= tiles;
+  const int lt = is_up ? gwc - tiles : gwc;
+  const WaveJob job{is_up ? a.up : a.gate, is_up ? a.up_d : a.gate_d,
+                    (is_up ? a.tmp_u : a.tmp_g) + (long)p * a.f - (long)e * a.f,
+                    a.n_experts * a.f, a.rt_h, e * tiles + lt, valid};
+  matvec_wave<FMT>(job, a.units_h, a.part_h, a.grid, XPlain<K4>{a.x + (long)tok * a.h, a.h},
+                   smem_raw);
+}
+
+// Stage 2: down_e . (silu(g) * u) for every pair.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
+  extern __shared__ __align__(16) char smem_raw[];
+  const int p = blockIdx.y;
+  const int e = a.ids[p];
+  const int tiles = a.h / a.rt_f;
+  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool valid = gw < tiles;
+  const int gwc = valid ? gw : tiles - 1;
+  const WaveJob job{a.down, a.down_d, a.tmp_y + (long)p * a.h - (long)e * a.h,
+                    a.n_experts * a.h, a.rt_f, e * tiles + gwc, valid};
+  matvec_wave<FMT>(job, a.units_f, a.part_f, a.grid,
+                   XSwiGLU{a.tmp_g + (long)p * a.f, a.tmp_u + (long)p * a.f, a.f}, smem_raw);
+}
+
+// Router: per token, top-k of the logits (ties: lower index) and their
+// softmax probabilities over all experts.  One 256-thread block per token;
+// the logits are staged in LDS and every expert's rank (the number of
+// experts that beat it) is counted in parallel: rank < k gives its slot.
+__global__ __launch_bounds__(256) void k_moe_route(const float *logits, int n_experts, int top_k,
+                                                   int *ids, float *w) {
+  __shared__ float lv[4096];
+  __shared__ float red[256];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  const float *l = logits + (long)t * n_experts;
+  float mx = -INFINITY;
+  for (int e = tid; e < n_experts; e += 256) {
+    lv[e] = l[e];
+    mx = fmaxf(mx, lv[e]);
+  }
+  red[tid] = mx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  mx = red[0];
+  __syncthreads();
+  float sum = 0.f;
+  for (int e = tid; e < n_experts; e += 256) sum += expf(lv[e] - mx);
+  red[tid] = sum;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) red[tid] += red[tid + s];
+    __syncthreads();
+  }
+  sum = red[0];
+  for (int e = tid; e < n_experts; e += 256) {
+    const float me = lv[e];
+    int rank = 0;
+    for (int o = 0; o < n_experts; o++) {
+      const float ov = lv[o];
+      rank += (ov > me) || (ov == me && o < e);
+    }
+    if (rank < top_k) {
+      ids[t * top_k + rank] = e;
+      w[t * top_k + rank] = expf(me - mx) / sum;
+    }
+  }
+}
+
+// out[t][i] = sum_s w[t][s] * y[t*k+s][i], slots in order.
+__global__ void k_moe_combine(const float *tmp_y, const float *w, int T, int top_k, int h,
+                              float *out) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)T * h) return;
+  const int t = (int)(i / h), c = (int)(i % h);
+  float acc = 0.f;
+  for (int s = 0; s < top_k; s++) acc += w[t * top_k + s] * tmp_y[((long)t * top_k + s) * h + c];
+  out[i] = acc;
 }
 
 // ------------------------------------------------------------- launch
@@ -468,6 +601,36 @@ static hipError_t launch_t(const MvArgs &a, hipStream_t st) {
 template <int FMT>
 static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
   return a.k % 4 == 0 ? launch_t<FMT, true>(a, st) : launch_t<FMT, false>(a, st);
+}
+
+hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st) {
+  if (a.fmt != T_IQ3_XXS && a.fmt != T_Q4_K && a.fmt != T_Q6_K && a.fmt != T_Q8_0 &&
+      a.fmt != T_Q5_K)
+    return hipErrorInvalidValue;
+  const int pairs = T * a.top_k;
+  hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(256), 0, st, a.logits, a.n_experts, a.top_k,
+                     a.ids, a.w);
+  const size_t lds1 = matvec_lds_bytes(a.fmt, a.units_h, a.part_h);
+  const size_t lds2 = matvec_lds_bytes(a.fmt, a.units_f, a.part_f);
+  const dim3 g1((2 * (a.f / a.rt_h) + 3) / 4, pairs), g2(((a.h / a.rt_f) + 3) / 4, pairs);
+#define GQ_MOE_LAUNCH(F)                                                                     \
+  if (a.fmt == F) {                                                                          \
+    if (a.h % 4 == 0)                                                                        \
+      hipLaunchKernelGGL((k_moe_gate_up<F, true>), g1, dim3(256), lds1, st, a);              \
+    else                                                                                     \
+      hipLaunchKernelGGL((k_moe_gate_up<F, false>), g1, dim3(256), lds1, st, a);             \
+    hipLaunchKernelGGL((k_moe_down<F>), g2, dim3(256), lds2, st, a);                         \
+  }
+  GQ_MOE_LAUNCH(T_IQ3_XXS)
+  GQ_MOE_LAUNCH(T_Q4_K)
+  GQ_MOE_LAUNCH(T_Q5_K)
+  GQ_MOE_LAUNCH(T_Q6_K)
+  GQ_MOE_LAUNCH(T_Q8_0)
+#undef GQ_MOE_LAUNCH
+  const long tot = (long)T * a.h;
+  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
+                     a.tmp_y, a.w, T, a.top_k, a.h, a.out);
+  return hipGetLastError();
 }
 
 hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st) {

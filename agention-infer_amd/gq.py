@@ -52,6 +52,8 @@ SIGNATURES = {
     "gq_set_iq3xxs_grid": (_I, [_P]),
     "gq_get_iq3xxs_grid": (_I, [_P]),
     "gq_sync": (_I, [_P]),
+    "gq_upload_experts": (_I, [_I, _P, _SZ, _I, _I, _I, ctypes.POINTER(_P)]),
+    "gq_moe_ffn": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _P]),
 }
 
 
@@ -213,6 +215,27 @@ class HipBackend:
         q = torch.empty(n, dtype=torch.int8, device=x_dev.device)
         _check(lib().gq_quantize_q8_32(_ptr(x_dev), n, _ptr(scale), _ptr(q), _stream(stream)))
         return scale, q
+
+    def upload_experts(self, dtype, w, in_dim, rows_per_expert, n_experts):
+        """A stacked expert tensor [n_experts][rows_per_expert][in_dim]."""
+        w = np.ascontiguousarray(w, dtype=np.uint8)
+        h = ctypes.c_void_p()
+        _check(lib().gq_upload_experts(dtype, _ptr(w), w.nbytes, in_dim, rows_per_expert,
+                                       n_experts, ctypes.byref(h)))
+        return GpuWeightHandle(h.value, dtype, in_dim, rows_per_expert * n_experts)
+
+    def moe_ffn(self, gate, up, down, n_experts, logits_dev, x_dev, top_k, out_dev=None,
+                want_routing=False, stream=None):
+        """MoE expert FFN for T tokens; returns out [T][h] (and ids, w)."""
+        import torch
+        T, h = x_dev.shape
+        if out_dev is None:
+            out_dev = torch.empty((T, h), dtype=torch.float32, device=x_dev.device)
+        ids = torch.empty((T, top_k), dtype=torch.int32, device=x_dev.device) if want_routing else None
+        w = torch.empty((T, top_k), dtype=torch.float32, device=x_dev.device) if want_routing else None
+        _check(lib().gq_moe_ffn(gate._h, up._h, down._h, n_experts, _ptr(logits_dev), T, top_k,
+                                _ptr(x_dev), _ptr(out_dev), _ptr(ids), _ptr(w), _stream(stream)))
+        return (out_dev, ids, w) if want_routing else out_dev
 
     def set_iq3xxs_grid(self, grid=None):
         if grid is None:

@@ -117,6 +117,25 @@ int gq_quantize_q8_32(const float *x_dev, int n, uint16_t *scale_dev, int8_t *q_
 int gq_set_iq3xxs_grid(const uint32_t *grid_host);
 int gq_get_iq3xxs_grid(uint32_t *grid_host);
 
+/* A stacked expert tensor as GGUF stores it (ffn_{gate,up,down}_exps,
+ * [n_experts][rows_per_expert][in_dim], docs/08-moe-routing.md:36-46):
+ * like gq_upload, with tiles that never straddle two experts. */
+int gq_upload_experts(int dtype, const void *w_host, size_t nbytes, int in_dim,
+                      int rows_per_expert, int n_experts, gq_weight **out);
+
+/* MoE FFN for T tokens (docs/08-moe-routing.md:24-30; the reference has no
+ * MoE forward pass, docs/roadmap/00-parity-roadmap.md:40):
+ *   ids[t], w[t] = top_k of softmax(logits[t]) (ties: lower expert index;
+ *                  weights are the full-softmax probabilities),
+ *   out[t] = sum_s w[t][s] * down_e(silu(gate_e x_t) * up_e x_t),
+ * SwiGLU as ffn_gate_up (src/model/llama/cpu_path.rs:200-232).  gate/up:
+ * [n_experts][f][h], down: [n_experts][h][f], uploaded with
+ * gq_upload_experts.  logits_dev [T][n_experts], x_dev/out_dev [T][h];
+ * ids_dev/w_dev ([T][top_k]) receive the routing if non-NULL. */
+int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, int n_experts,
+               const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
+               int *ids_dev, float *w_dev, void *stream);
+
 /* Wait for all work on `stream`. */
 int gq_sync(void *stream);
 

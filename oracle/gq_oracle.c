@@ -667,6 +667,58 @@ int gqo_matmul_batch_into(int dtype, const uint8_t *w, size_t nbytes, const floa
     return rc;
 }
 
+/* ------------------------------------------------------------------ MoE */
+
+void gqo_moe_route(const float *logits, int T, int E, int k, int *ids, float *w) {
+    for (int t = 0; t < T; t++) {
+        const float *l = logits + (size_t)t * E;
+        float mx = -INFINITY;
+        for (int e = 0; e < E; e++) mx = l[e] > mx ? l[e] : mx;
+        float sum = 0.0f;
+        for (int e = 0; e < E; e++) sum += expf(l[e] - mx);
+        unsigned char taken[4096] = {0};
+        for (int s = 0; s < k; s++) {
+            int best = -1;
+            for (int e = 0; e < E; e++)
+                if (!taken[e] && (best < 0 || l[e] > l[best])) best = e;
+            taken[best] = 1;
+            ids[t * k + s] = best;
+            w[t * k + s] = expf(l[best] - mx) / sum;
+        }
+    }
+}
+
+static float silu(float g) { return g / (1.0f + expf(-g)); }
+
+int gqo_moe_ffn(int dtype, const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
+                int H, int F, const float *x, int T, int k, const int *ids, const float *w,
+                float *out, int nthreads) {
+    const size_t rb_h = gqo_type_size(dtype, (size_t)H), rb_f = gqo_type_size(dtype, (size_t)F);
+    float *g = (float *)malloc(sizeof(float) * F), *u = (float *)malloc(sizeof(float) * F);
+    float *h = (float *)malloc(sizeof(float) * F), *y = (float *)malloc(sizeof(float) * H);
+    int rc = 0;
+    for (int t = 0; t < T && !rc; t++) {
+        float *o = out + (size_t)t * H;
+        for (int i = 0; i < H; i++) o[i] = 0.0f;
+        for (int s = 0; s < k && !rc; s++) {
+            const int e = ids[t * k + s];
+            if (e < 0 || e >= E) { rc = GQO_ERANGE; break; }
+            const uint8_t *ge = gate + (size_t)e * F * rb_h, *ue = up + (size_t)e * F * rb_h;
+            const uint8_t *de = down + (size_t)e * H * rb_f;
+            rc = gqo_matmul_into(dtype, ge, (size_t)F * rb_h, x + (size_t)t * H, H, g, F, nthreads);
+            if (!rc) rc = gqo_matmul_into(dtype, ue, (size_t)F * rb_h, x + (size_t)t * H, H, u, F, nthreads);
+            if (rc) break;
+            for (int i = 0; i < F; i++) h[i] = silu(g[i]) * u[i];
+            rc = gqo_matmul_into(dtype, de, (size_t)H * rb_f, h, F, y, H, nthreads);
+            if (rc) break;
+            const float ws = w[t * k + s];
+            for (int i = 0; i < H; i++) o[i] += ws * y[i];
+        }
+    }
+    free(g); free(u); free(h); free(y);
+    return rc;
+}
+
 /* sampler.rs:120-131 */
 size_t gqo_argmax(const float *xs, size_t n) {
     size_t best = 0;

@@ -88,6 +88,21 @@ int gqo_matmul_batch_into(int dtype, const uint8_t *w, size_t nbytes, const floa
 int gqo_matmul_batch_rows(int dtype, const uint8_t *w, size_t nbytes, const float *x,
                           size_t in_dim, size_t batch, size_t r0, size_t r1, float *rowmajor);
 
+/* MoE routing (docs/08-moe-routing.md:24-30: probs = softmax(scores),
+ * top_k_indices = argtop_k(probs, k)): for each of T tokens, ids[t][k] are
+ * the k largest logits (ties: lower expert index first) and w[t][k] their
+ * softmax probabilities over all E experts (not renormalised). */
+void gqo_moe_route(const float *logits, int T, int E, int k, int *ids, float *w);
+
+/* MoE FFN (docs/08-moe-routing.md:24-30) with the dense SwiGLU of
+ * ffn_gate_up (model/llama/cpu_path.rs:200-232):
+ *   out[t] = sum_s w[t][s] * down_e(silu(gate_e x_t) * up_e x_t),  e = ids[t][s].
+ * gate/up: E stacked [F][H] matrices, down: E stacked [H][F] matrices, all
+ * of `dtype`.  Slots are accumulated in order s = 0..k-1. */
+int gqo_moe_ffn(int dtype, const uint8_t *gate, const uint8_t *up, const uint8_t *down, int E,
+                int H, int F, const float *x, int T, int k, const int *ids, const float *w,
+                float *out, int nthreads);
+
 /* argmax, first maximum wins (sampler.rs:120-131). */
 size_t gqo_argmax(const float *xs, size_t n);
 

@@ -44,6 +44,8 @@ def lib():
             "gqo_matmul_dequant": (_I, [_I, _P, _SZ, _P, _SZ, _P, _SZ]),
             "gqo_matmul_batch_into": (_I, [_I, _P, _SZ, _P, _SZ, _SZ, _P, _SZ, _I]),
             "gqo_argmax": (_SZ, [_P, _SZ]),
+            "gqo_moe_route": (None, [_P, _I, _I, _I, _P, _P]),
+            "gqo_moe_ffn": (_I, [_I, _P, _P, _P, _I, _I, _I, _P, _I, _I, _P, _P, _P, _I]),
         }
         for n, (r, a) in sig.items():
             f = getattr(L, n)
@@ -172,6 +174,27 @@ def matmul_batch_into(dtype, w, X, out_dim, nthreads=0):
     out = np.zeros((batch, out_dim), np.float32)
     _chk(lib().gqo_matmul_batch_into(dtype, _p(w), w.nbytes, _p(X), in_dim, batch, _p(out),
                                      out_dim, nthreads))
+    return out
+
+
+def moe_route(logits, k):
+    logits = np.ascontiguousarray(logits, np.float32)
+    T, E = logits.shape
+    ids = np.zeros((T, k), np.int32)
+    w = np.zeros((T, k), np.float32)
+    lib().gqo_moe_route(_p(logits), T, E, k, _p(ids), _p(w))
+    return ids, w
+
+
+def moe_ffn(dtype, gate, up, down, E, H, F, x, ids, w, nthreads=0):
+    gate, up, down = (np.ascontiguousarray(a, np.uint8) for a in (gate, up, down))
+    x = np.ascontiguousarray(x, np.float32)
+    ids = np.ascontiguousarray(ids, np.int32)
+    w = np.ascontiguousarray(w, np.float32)
+    T, k = ids.shape
+    out = np.zeros((T, H), np.float32)
+    _chk(lib().gqo_moe_ffn(dtype, _p(gate), _p(up), _p(down), E, H, F, _p(x), T, k, _p(ids),
+                           _p(w), _p(out), nthreads))
     return out
 
 

@@ -189,7 +189,7 @@ def test_iq3_custom_grid(backend, orc):
     import torch
     say("iq3 custom grid")
     grid = (np.arange(256, dtype=np.uint64) * 2654435761 % (1 << 32)).astype(np.uint32)
-    grid = (grid & 0x3F3F3F3F).astype(np.uint32)
+    grid = ((grid & 0x3F3F3F3F) | 0x01010101).astype(np.uint32)  # magnitudes 1..63
     backend.set_iq3xxs_grid(grid)
     orc.set_iq3xxs_grid(grid)
     try:
@@ -205,6 +205,15 @@ def test_iq3_custom_grid(backend, orc):
         backend.set_iq3xxs_grid(None)
         orc.set_iq3xxs_grid(None)
     assert np.array_equal(backend.get_iq3xxs_grid(), orc.get_iq3xxs_grid())
+    import gq
+    bad = grid.copy()
+    bad[3] &= 0xFFFFFF00  # a zero magnitude
+    with pytest.raises(gq.GqError, match="1..127"):
+        backend.set_iq3xxs_grid(bad)
+    bad = grid.copy()
+    bad[5] |= 0x80
+    with pytest.raises(gq.GqError, match="1..127"):
+        backend.set_iq3xxs_grid(bad)
 
 
 def test_quantize_q8_32_bit_exact(backend, orc):

@@ -1,0 +1,90 @@
+"""GPU parity for the IQ3_XXS MoE expert FFN (gq_moe_ffn) against the CPU
+oracle (routing bit-identical, output max|err| <= 1e-4 * max|out_ref|).
+
+IQ3_XXS arithmetic is "parity unpinned" against the reference (it has no
+IQ3_XXS implementation); both sides use the same codebook.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import gq_synth as syn
+
+pytestmark = pytest.mark.gpu
+IQ3 = 18
+TOL = 1e-4
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def make(E, H, F, seed):
+    gate = syn.make_blocks(IQ3, E * F, H, seed=seed)
+    up = syn.make_blocks(IQ3, E * F, H, seed=seed + 1)
+    down = syn.make_blocks(IQ3, E * H, F, seed=seed + 2)
+    return gate, up, down
+
+
+def run(backend, orc, E, H, F, T, k, seed, check_tokens=None, weights=None):
+    import torch
+    gate, up, down = weights if weights else make(E, H, F, seed)
+    hg = backend.upload_experts(IQ3, gate, H, F, E)
+    hu = backend.upload_experts(IQ3, up, H, F, E)
+    hd = backend.upload_experts(IQ3, down, F, H, E)
+    rng = np.random.default_rng(seed + 10)
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    x = syn.make_x(H, seed=seed + 11, batch=T)
+    out, ids, w = backend.moe_ffn(hg, hu, hd, E, torch.from_numpy(logits).cuda(),
+                                  torch.from_numpy(x).cuda(), k, want_routing=True)
+    torch.cuda.synchronize()
+    out, ids, w = out.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy()
+    rids, rw = orc.moe_route(logits, k)
+    assert np.array_equal(ids, rids), "routing differs"
+    assert np.allclose(w, rw, rtol=2e-6, atol=0)
+    toks = range(T) if check_tokens is None else check_tokens
+    sel = list(toks)
+    ref = orc.moe_ffn(IQ3, gate, up, down, E, H, F, x[sel], rids[sel], rw[sel])
+    got = out[sel]
+    err = float(np.max(np.abs(got.astype(np.float64) - ref)))
+    bound = TOL * float(np.max(np.abs(ref)))
+    say(f"moe E={E} H={H} F={F} T={T} k={k}: max|err| {err:.3g} bound {bound:.3g}")
+    assert err <= bound
+    return ids
+
+
+@pytest.mark.parametrize("E,H,F,T,k", [(16, 512, 256, 3, 4), (8, 256, 768, 5, 2), (4, 1024, 512, 1, 4)])
+def test_moe_small(backend, orc, E, H, F, T, k):
+    say(f"moe small E={E} H={H} F={F} T={T} k={k}")
+    run(backend, orc, E, H, F, T, k, seed=E + H + T)
+
+
+def test_moe_full_config(backend, orc):
+    """config 4: 256 experts, hidden 3072, expert intermediate 1536, top-8,
+    T = 1, 4, 16 (T = 16 checked on 3 of its tokens; routing on all)."""
+    E, H, F, k = 256, 3072, 1536, 8
+    say("moe full config: generating 1.39 GB of IQ3_XXS experts")
+    weights = make(E, H, F, seed=100)
+    for T, toks in ((1, None), (4, None), (16, [0, 7, 15])):
+        say(f"moe full T={T}")
+        run(backend, orc, E, H, F, T, k, seed=200 + T, check_tokens=toks, weights=weights)
+
+
+def test_moe_errors(backend):
+    import gq
+    import torch
+    gate, up, down = make(4, 256, 256, seed=1)
+    hg = backend.upload_experts(IQ3, gate, 256, 256, 4)
+    hu = backend.upload_experts(IQ3, up, 256, 256, 4)
+    hd = backend.upload_experts(IQ3, down, 256, 256, 4)
+    x = torch.zeros((2, 256), device="cuda")
+    lg = torch.zeros((2, 4), device="cuda")
+    with pytest.raises(gq.GqError):
+        backend.moe_ffn(hg, hu, hd, 4, lg, x, 5)       # top_k > experts
+    with pytest.raises(gq.GqError):
+        backend.moe_ffn(hg, hu, hd, 3, lg, x, 2)       # wrong expert count
+    hq = backend.upload_experts(12, syn.make_blocks(12, 4 * 256, 256, seed=2), 256, 256, 4)
+    with pytest.raises(gq.GqError):
+        backend.moe_ffn(hq, hu, hd, 4, lg, x, 2)       # mixed dtypes

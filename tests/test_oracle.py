@@ -307,3 +307,42 @@ def test_argmax_first_max_wins(orc):
     # sampler.rs:120-131
     assert orc.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
     assert orc.argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
+
+
+# -------------------------------------------------------------------- MoE
+def test_moe_route_vs_numpy(orc):
+    rng = np.random.default_rng(5)
+    logits = rng.standard_normal((7, 256), dtype=np.float32)
+    logits[3, 10] = logits[3, 20] = 9.0  # a tie: lower index first
+    ids, w = orc.moe_route(logits, 8)
+    for t in range(7):
+        order = sorted(range(256), key=lambda e: (-logits[t, e], e))[:8]
+        assert list(ids[t]) == order
+        p = np.exp(logits[t].astype(np.float64) - logits[t].max())
+        p /= p.sum()
+        assert np.allclose(w[t], p[order], rtol=1e-5)
+    assert ids[3, 0] == 10 and ids[3, 1] == 20
+
+
+def test_moe_ffn_vs_numpy(orc):
+    E, H, F, T, k = 6, 256, 512, 3, 2
+    gate = syn.make_blocks(18, E * F, H, seed=1)
+    up = syn.make_blocks(18, E * F, H, seed=2)
+    down = syn.make_blocks(18, E * H, F, seed=3)
+    x = syn.make_x(H, seed=4, batch=T)
+    logits = np.random.default_rng(6).standard_normal((T, E), dtype=np.float32)
+    ids, w = orc.moe_route(logits, k)
+    out = orc.moe_ffn(18, gate, up, down, E, H, F, x, ids, w, nthreads=4)
+    grid = orc.get_iq3xxs_grid()
+    Wg = np.stack([npref.dequant_iq3_xxs(gate[r], H, grid) for r in range(E * F)]).astype(np.float64)
+    Wu = np.stack([npref.dequant_iq3_xxs(up[r], H, grid) for r in range(E * F)]).astype(np.float64)
+    Wd = np.stack([npref.dequant_iq3_xxs(down[r], F, grid) for r in range(E * H)]).astype(np.float64)
+    for t in range(T):
+        ref = np.zeros(H)
+        for s in range(k):
+            e = ids[t, s]
+            g = Wg[e * F:(e + 1) * F] @ x[t]
+            u = Wu[e * F:(e + 1) * F] @ x[t]
+            hmid = g / (1 + np.exp(-g)) * u
+            ref += w[t, s] * (Wd[e * H:(e + 1) * H] @ hmid)
+        assert np.max(np.abs(out[t] - ref)) <= 1e-4 * np.max(np.abs(ref))
