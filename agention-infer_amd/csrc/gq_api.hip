@@ -13,6 +13,7 @@
 #include <mutex>
 #include <string>
 #include <algorithm>
+#include <vector>
 
 #include "../../include/gq.h"
 #include "gq_device.h"
@@ -189,6 +190,43 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
 
 }  // namespace
 
+namespace gq {
+// Launch y_i = W_i . x for weights sharing dtype and in_dim (4 per launch).
+// With xu != nullptr the input is silu(xg) * xu instead of x.
+hipError_t matvec_launch(const gq_weight *const *ws, int count, const float *x, const float *xg,
+                         const float *xu, float *const *ys, hipStream_t st) {
+  const gq_weight *w0 = ws[0];
+  for (int base = 0; base < count; base += MV_MAX_SEG) {
+    MvArgs a{};
+    a.x = x;
+    a.xg = xg;
+    a.xu = xu;
+    a.grid = g_dev.grid;
+    a.k = w0->L.k;
+    a.units = w0->L.units;
+    a.chunks = w0->L.chunks;
+    int tiles = 0, ns = 0, part = 64;
+    for (int i = base; i < count && i < base + MV_MAX_SEG; i++) {
+      const gq_weight *w = ws[i];
+      if (w->L.rows == 0) continue;
+      a.seg[ns++] = MvSeg{w->body, w->d, ys[i], w->L.rows, w->L.rt, tiles};
+      tiles += num_tiles(w->L);
+      const int uit = w->L.rt * w->L.units;
+      part = std::max(part, (uit + 63) / 64 * 64);
+    }
+    if (ns == 0) continue;
+    a.nseg = ns;
+    a.total_tiles = tiles;
+    a.part_floats = part;
+    hipError_t e = launch_matvec(a, w0->L.dtype, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+const uint32_t *device_grid() { return g_dev.grid; }
+}  // namespace gq
+
 extern "C" {
 
 int gq_init(int device) {
@@ -306,30 +344,8 @@ int gq_matvec_multi(const gq_weight *const *ws, int count, const float *x_dev,
     if (ws[i]->L.rows > 0 && !y_dev[i]) return fail(GQ_EINVAL, "null output %d", i);
   }
   if (!x_dev) return fail(GQ_EINVAL, "null x");
-  const gq_weight *w0 = ws[0];
-  for (int base = 0; base < count; base += gq::MV_MAX_SEG) {
-    gq::MvArgs a{};
-    a.x = x_dev;
-    a.grid = g_dev.grid;
-    a.k = w0->L.k;
-    a.units = w0->L.units;
-    a.chunks = w0->L.chunks;
-    int tiles = 0, ns = 0, part = 64;
-    for (int i = base; i < count && ns < gq::MV_MAX_SEG; i++) {
-      const gq_weight *w = ws[i];
-      if (w->L.rows == 0) continue;
-      a.seg[ns++] = gq::MvSeg{w->body, w->d, y_dev[i], w->L.rows, w->L.rt, tiles};
-      tiles += gq::num_tiles(w->L);
-      const int uit = w->L.rt * w->L.units;
-      part = std::max(part, (uit + 63) / 64 * 64);
-    }
-    if (ns == 0) continue;
-    a.nseg = ns;
-    a.total_tiles = tiles;
-    a.part_floats = part;
-    hipError_t e = gq::launch_matvec(a, w0->L.dtype, (hipStream_t)stream);
-    if (e != hipSuccess) return fail(GQ_EHIP, "matvec launch failed: %s", hipGetErrorString(e));
-  }
+  hipError_t e = gq::matvec_launch(ws, count, x_dev, nullptr, nullptr, y_dev, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(GQ_EHIP, "matvec launch failed: %s", hipGetErrorString(e));
   return GQ_OK;
 }
 
@@ -446,6 +462,199 @@ int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mod
                                  (hipStream_t)stream);
   if (wsp) (void)hipFreeAsync(wsp, (hipStream_t)stream);
   if (e != hipSuccess) return fail(GQ_EHIP, "gemm launch failed: %s", hipGetErrorString(e));
+  return GQ_OK;
+}
+
+// ------------------------------------------------------------ decode model
+}  // extern "C"
+
+struct gq_model {
+  gq::DecodeLaunch L;
+  std::vector<const gq_weight *> wq, wk, wv, wo, wg, wu, wd;
+  std::vector<const float *> an, fn;
+  std::vector<void *> owned;  // device allocations
+  hipGraphExec_t graph = nullptr;
+  hipStream_t graph_stream = nullptr;
+  ~gq_model() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    for (void *p : owned) (void)hipFree(p);
+  }
+};
+
+namespace {
+template <typename T>
+int dalloc(gq_model *m, T **p, size_t count) {
+  void *q = nullptr;
+  if (hipMalloc(&q, count * sizeof(T) + 256) != hipSuccess)
+    return fail(GQ_ENOMEM, "hipMalloc of %zu bytes failed", count * sizeof(T));
+  m->owned.push_back(q);
+  *p = (T *)q;
+  return GQ_OK;
+}
+
+int check_w(const gq_weight *w, int rows, int k, const char *what, int layer) {
+  if (!w) return fail(GQ_EINVAL, "layer %d: null %s", layer, what);
+  if (w->L.rows != rows || w->L.k != k)
+    return fail(GQ_EINVAL, "layer %d: %s is %dx%d, expected %dx%d", layer, what, w->L.rows,
+                w->L.k, rows, k);
+  return check_matvec(w);
+}
+}  // namespace
+
+extern "C" {
+
+int gq_model_create(const gq_model_desc *d, gq_model **out) {
+  if (!d || !out) return fail(GQ_EINVAL, "null model descriptor");
+  *out = nullptr;
+  int rc = ensure_init();
+  if (rc) return rc;
+  const int H = d->hidden, hd = d->head_dim, nh = d->n_heads, nkv = d->n_kv_heads;
+  if (d->n_layers <= 0 || H <= 0 || hd <= 0 || hd > 128 || hd % 8 || nh <= 0 || nkv <= 0 ||
+      nh % nkv || d->ffn <= 0 || d->vocab <= 0 || d->ctx <= 0)
+    return fail(GQ_EINVAL, "bad model shape (head_dim must be a multiple of 8, <= 128; "
+                           "n_heads a multiple of n_kv_heads)");
+  for (int l = 0; l < d->n_layers; l++) {
+    if ((rc = check_w(d->wq[l], nh * hd, H, "wq", l)) || (rc = check_w(d->wk[l], nkv * hd, H, "wk", l)) ||
+        (rc = check_w(d->wv[l], nkv * hd, H, "wv", l)) || (rc = check_w(d->wo[l], H, nh * hd, "wo", l)) ||
+        (rc = check_w(d->wgate[l], d->ffn, H, "ffn_gate", l)) ||
+        (rc = check_w(d->wup[l], d->ffn, H, "ffn_up", l)) ||
+        (rc = check_w(d->wdown[l], H, d->ffn, "ffn_down", l)))
+      return rc;
+    if (d->wq[l]->L.dtype != d->wk[l]->L.dtype || d->wq[l]->L.dtype != d->wv[l]->L.dtype ||
+        d->wgate[l]->L.dtype != d->wup[l]->L.dtype)
+      return fail(GQ_EINVAL, "layer %d: q/k/v and gate/up must share a dtype", l);
+  }
+  if ((rc = check_w(d->lm_head, d->vocab, H, "output", -1))) return rc;
+  gq_model *m = new gq_model();
+  auto &L = m->L;
+  L.n_layers = d->n_layers; L.hidden = H; L.n_heads = nh; L.n_kv_heads = nkv; L.head_dim = hd;
+  L.ffn = d->ffn; L.vocab = d->vocab; L.ctx = d->ctx; L.eps = d->eps; L.theta = d->theta;
+  L.att_chunks = (d->ctx + 255) / 256;
+  L.max_tokens = d->max_tokens > 0 ? d->max_tokens : 4096;
+  for (int l = 0; l < d->n_layers; l++) {
+    m->wq.push_back(d->wq[l]); m->wk.push_back(d->wk[l]); m->wv.push_back(d->wv[l]);
+    m->wo.push_back(d->wo[l]); m->wg.push_back(d->wgate[l]); m->wu.push_back(d->wup[l]);
+    m->wd.push_back(d->wdown[l]);
+  }
+  L.wq = m->wq.data(); L.wk = m->wk.data(); L.wv = m->wv.data(); L.wo = m->wo.data();
+  L.wgate = m->wg.data(); L.wup = m->wu.data(); L.wdown = m->wd.data(); L.lm_head = d->lm_head;
+  const size_t kvd = (size_t)nkv * hd;
+  float *norms = nullptr, *embd = nullptr;
+  rc = dalloc(m, &norms, (size_t)(2 * d->n_layers + 1) * H);
+  if (!rc) rc = dalloc(m, &embd, (size_t)d->vocab * H);
+  if (!rc) rc = dalloc(m, &L.kcache, (size_t)d->n_layers * d->ctx * kvd);
+  if (!rc) rc = dalloc(m, &L.vcache, (size_t)d->n_layers * d->ctx * kvd);
+  float *buf = nullptr;
+  const size_t nbuf = 2 * (size_t)H + (size_t)nh * hd * 2 + 2 * kvd + (size_t)H + 2 * (size_t)d->ffn +
+                      (size_t)d->vocab + (size_t)nh * L.att_chunks * (2 + hd) + 64;
+  if (!rc) rc = dalloc(m, &buf, nbuf);
+  if (!rc) rc = dalloc(m, &L.state, 1);
+  if (!rc) rc = dalloc(m, &L.tokens, (size_t)L.max_tokens);
+  if (rc) { delete m; return rc; }
+  size_t o = 0;
+  auto take = [&](size_t n) { float *p = buf + o; o += (n + 15) & ~(size_t)15; return p; };
+  L.x = take(H); L.xn = take(H); L.q = take((size_t)nh * hd); L.att = take((size_t)nh * hd);
+  L.k = take(kvd); L.v = take(kvd); L.proj = take(H); L.g = take(d->ffn); L.u = take(d->ffn);
+  L.logits = take(d->vocab); L.att_part = take((size_t)nh * L.att_chunks * (2 + hd));
+  hipError_t e = hipSuccess;
+  for (int l = 0; l < d->n_layers && e == hipSuccess; l++) {
+    e = hipMemcpy(norms + (size_t)(2 * l) * H, d->attn_norm[l], H * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+      e = hipMemcpy(norms + (size_t)(2 * l + 1) * H, d->ffn_norm[l], H * 4, hipMemcpyHostToDevice);
+    m->an.push_back(norms + (size_t)(2 * l) * H);
+    m->fn.push_back(norms + (size_t)(2 * l + 1) * H);
+  }
+  if (e == hipSuccess)
+    e = hipMemcpy(norms + (size_t)2 * d->n_layers * H, d->output_norm, H * 4, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(embd, d->embd, (size_t)d->vocab * H * 4, hipMemcpyHostToDevice);
+  if (e != hipSuccess) { delete m; return fail(GQ_EHIP, "model upload failed: %s", hipGetErrorString(e)); }
+  L.attn_norm = m->an.data(); L.ffn_norm = m->fn.data();
+  L.output_norm = norms + (size_t)2 * d->n_layers * H;
+  L.embd = embd;
+  *out = m;
+  return GQ_OK;
+}
+
+int gq_model_free(gq_model *m) {
+  delete m;
+  return GQ_OK;
+}
+
+static int kv_copy(gq_model *m, int layer, uint16_t *k, uint16_t *v, int n_pos, bool up) {
+  if (!m || layer < 0 || layer >= m->L.n_layers || n_pos < 0 || n_pos > m->L.ctx)
+    return fail(GQ_EINVAL, "bad KV range (layer %d, %d positions)", layer, n_pos);
+  const size_t kvd = (size_t)m->L.n_kv_heads * m->L.head_dim;
+  const size_t off = (size_t)layer * m->L.ctx * kvd, bytes = (size_t)n_pos * kvd * 2;
+  hipError_t e = up ? hipMemcpy(m->L.kcache + off, k, bytes, hipMemcpyHostToDevice)
+                    : hipMemcpy(k, m->L.kcache + off, bytes, hipMemcpyDeviceToHost);
+  if (e == hipSuccess)
+    e = up ? hipMemcpy(m->L.vcache + off, v, bytes, hipMemcpyHostToDevice)
+           : hipMemcpy(v, m->L.vcache + off, bytes, hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return fail(GQ_EHIP, "KV copy failed: %s", hipGetErrorString(e));
+  return GQ_OK;
+}
+
+int gq_model_kv_upload(gq_model *m, int layer, const uint16_t *k, const uint16_t *v, int n_pos) {
+  return kv_copy(m, layer, (uint16_t *)k, (uint16_t *)v, n_pos, true);
+}
+
+int gq_model_kv_download(gq_model *m, int layer, uint16_t *k, uint16_t *v, int n_pos) {
+  return kv_copy(m, layer, k, v, n_pos, false);
+}
+
+static int set_state(gq_model *m, int token, int pos, hipStream_t s) {
+  if (token < 0 || token >= m->L.vocab) return fail(GQ_EINVAL, "token %d out of range", token);
+  if (pos < 0 || pos >= m->L.ctx) return fail(GQ_EINVAL, "position %d outside the context", pos);
+  HIP_TRY(gq::launch_set_state(m->L.state, token, pos, s));
+  return GQ_OK;
+}
+
+int gq_model_decode(gq_model *m, int token, int pos, float *logits_host, int *next_token) {
+  if (!m) return fail(GQ_EINVAL, "null model");
+  int rc = set_state(m, token, pos, nullptr);
+  if (rc) return rc;
+  hipError_t e = gq::launch_decode_step(m->L, nullptr);
+  if (e != hipSuccess) return fail(GQ_EHIP, "decode launch failed: %s", hipGetErrorString(e));
+  if (logits_host)
+    HIP_TRY(hipMemcpy(logits_host, m->L.logits, (size_t)m->L.vocab * 4, hipMemcpyDeviceToHost));
+  gq::DecodeState st;
+  HIP_TRY(hipMemcpy(&st, m->L.state, sizeof st, hipMemcpyDeviceToHost));
+  if (next_token) *next_token = st.token;
+  return GQ_OK;
+}
+
+int gq_model_generate(gq_model *m, int token, int pos, int n_steps, int *tokens_host,
+                      void *stream) {
+  if (!m) return fail(GQ_EINVAL, "null model");
+  if (n_steps < 0 || n_steps > m->L.max_tokens || pos + n_steps > m->L.ctx)
+    return fail(GQ_EINVAL, "%d steps from position %d exceed the context or token buffer",
+                n_steps, pos);
+  hipStream_t s = (hipStream_t)stream;
+  int rc = set_state(m, token, pos, s);
+  if (rc) return rc;
+  if (!m->graph || m->graph_stream != s) {
+    // Capture one step (its kernels read token/position from device state).
+    if (m->graph) { (void)hipGraphExecDestroy(m->graph); m->graph = nullptr; }
+    hipStream_t cap = nullptr;
+    HIP_TRY(hipStreamCreateWithFlags(&cap, hipStreamNonBlocking));
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamBeginCapture(cap, hipStreamCaptureModeThreadLocal);
+    if (e == hipSuccess) {
+      hipError_t le = gq::launch_decode_step(m->L, cap);
+      e = hipStreamEndCapture(cap, &g);
+      if (le != hipSuccess) e = le;
+    }
+    if (e == hipSuccess) e = hipGraphInstantiate(&m->graph, g, nullptr, nullptr, 0);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamDestroy(cap);
+    if (e != hipSuccess) return fail(GQ_EHIP, "decode graph capture failed: %s", hipGetErrorString(e));
+    m->graph_stream = s;
+  }
+  for (int i = 0; i < n_steps; i++) HIP_TRY(hipGraphLaunch(m->graph, s));
+  if (tokens_host && n_steps > 0) {
+    HIP_TRY(hipMemcpyAsync(tokens_host, m->L.tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+  }
   return GQ_OK;
 }
 

@@ -31,6 +31,7 @@ struct MvSeg {
 
 struct MvArgs {
   const float *x;
+  const float *xg, *xu;  // if xu != nullptr, x = silu(xg) * xu (SwiGLU input)
   const uint32_t *grid;  // IQ3_XXS codebook (device)
   int k, units, chunks;
   int part_floats;       // LDS floats per wave for per-unit partial sums
@@ -61,6 +62,36 @@ hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st);
 
 size_t matvec_lds_bytes(int dtype, int units, int part_floats);
 hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st);
+
+// Decode step state in device memory (advanced by the argmax kernel).
+struct DecodeState {
+  int token, pos, step, pad;
+};
+
+// Everything one decode step launches with (host struct, device pointers).
+struct DecodeLaunch {
+  int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, ctx;
+  int att_chunks, max_tokens;
+  float eps, theta;
+  const gq_weight *const *wq, *const *wk, *const *wv, *const *wo;
+  const gq_weight *const *wgate, *const *wup, *const *wdown;
+  const gq_weight *lm_head;
+  const float *const *attn_norm, *const *ffn_norm;  // host arrays of device pointers
+  const float *output_norm, *embd;
+  uint16_t *kcache, *vcache;  // [layer][ctx][kv_dim] f16
+  float *x, *xn, *q, *k, *v, *att, *proj, *g, *u, *logits, *att_part;
+  DecodeState *state;
+  int *tokens;                // [max_tokens] generated tokens
+};
+
+hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s);
+hipError_t launch_set_state(DecodeState *st, int token, int pos, hipStream_t s);
+
+// Host-side launch of y_i = W_i . x (or silu(xg) * xu when xu != nullptr)
+// for weights sharing dtype and in_dim; no argument checks.
+hipError_t matvec_launch(const gq_weight *const *ws, int count, const float *x, const float *xg,
+                         const float *xu, float *const *ys, hipStream_t st);
+const uint32_t *device_grid();
 
 // Rows per tile for a matrix (chosen at upload).
 int choose_rt(int dtype, int rows, int units);

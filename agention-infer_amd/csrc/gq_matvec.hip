@@ -450,7 +450,7 @@ __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_
 }
 
 // Plain / multi-segment matvec: one wave per tile over the segments.
-template <int FMT, bool K4>
+template <int FMT, bool K4, bool SW>
 __global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
   extern __shared__ __align__(16) char smem_raw[];
   const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -462,7 +462,10 @@ __global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
   for (int i = 1; i < MV_MAX_SEG; i++)
     if (i < a.nseg && gwc >= a.seg[i].tile_begin) sg = a.seg[i];
   const WaveJob job{sg.body, sg.d, sg.y, sg.rows, sg.rt, gwc - sg.tile_begin, valid};
-  matvec_wave<FMT>(job, a.units, a.part_floats, a.grid, XPlain<K4>{a.x, a.k}, smem_raw);
+  if constexpr (SW)
+    matvec_wave<FMT>(job, a.units, a.part_floats, a.grid, XSwiGLU{a.xg, a.xu, a.k}, smem_raw);
+  else
+    matvec_wave<FMT>(job, a.units, a.part_floats, a.grid, XPlain<K4>{a.x, a.k}, smem_raw);
 }
 
 // ------------------------------------------------------------------- MoE
@@ -587,20 +590,21 @@ int choose_rt(int dtype, int rows, int units) {
   return best;
 }
 
-template <int FMT, bool K4>
+template <int FMT, bool K4, bool SW>
 static hipError_t launch_t(const MvArgs &a, hipStream_t st) {
   const size_t lds = matvec_lds_bytes(FMT, a.units, a.part_floats);
   if (lds > 64 * 1024)
-    (void)hipFuncSetAttribute((const void *)k_matvec<FMT, K4>,
+    (void)hipFuncSetAttribute((const void *)k_matvec<FMT, K4, SW>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   const int blocks = (a.total_tiles + 3) / 4;
-  hipLaunchKernelGGL((k_matvec<FMT, K4>), dim3(blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_matvec<FMT, K4, SW>), dim3(blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
 template <int FMT>
 static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
-  return a.k % 4 == 0 ? launch_t<FMT, true>(a, st) : launch_t<FMT, false>(a, st);
+  if (a.xu) return launch_t<FMT, false, true>(a, st);
+  return a.k % 4 == 0 ? launch_t<FMT, true, false>(a, st) : launch_t<FMT, false, false>(a, st);
 }
 
 hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st) {

@@ -53,6 +53,12 @@ SIGNATURES = {
     "gq_get_iq3xxs_grid": (_I, [_P]),
     "gq_sync": (_I, [_P]),
     "gq_upload_experts": (_I, [_I, _P, _SZ, _I, _I, _I, ctypes.POINTER(_P)]),
+    "gq_model_create": (_I, [_P, ctypes.POINTER(_P)]),
+    "gq_model_free": (_I, [_P]),
+    "gq_model_kv_upload": (_I, [_P, _I, _P, _P, _I]),
+    "gq_model_kv_download": (_I, [_P, _I, _P, _P, _I]),
+    "gq_model_decode": (_I, [_P, _I, _I, _P, ctypes.POINTER(_I)]),
+    "gq_model_generate": (_I, [_P, _I, _I, _I, _P, _P]),
     "gq_moe_ffn": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _P]),
 }
 
@@ -252,6 +258,85 @@ class HipBackend:
 
     def sync(self, stream=None):
         _check(lib().gq_sync(_stream(stream)))
+
+
+class _ModelDesc(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads",
+                                             "head_dim", "ffn", "vocab", "ctx", "max_tokens")] + \
+        [("eps", ctypes.c_float), ("theta", ctypes.c_float)] + \
+        [(n, ctypes.c_void_p) for n in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown",
+                                         "lm_head", "attn_norm", "ffn_norm", "output_norm",
+                                         "embd")]
+
+
+class DecodeModel:
+    """GPU-resident dense decoder (run_gpu_resident, gpu_resident.rs:427-697).
+
+    weights: dict with per-layer lists of GpuWeightHandle ("wq", "wk", "wv",
+    "wo", "wgate", "wup", "wdown"), "lm_head", host float32 arrays
+    "attn_norm"/"ffn_norm" ([n_layers][hidden]), "output_norm", "embd".
+    """
+
+    def __init__(self, cfg, weights):
+        self._keep = []
+        d = _ModelDesc()
+        for k in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab",
+                  "ctx"):
+            setattr(d, k, int(cfg[k]))
+        d.max_tokens = int(cfg.get("max_tokens", 4096))
+        d.eps, d.theta = float(cfg["eps"]), float(cfg["theta"])
+        L = cfg["n_layers"]
+        for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown"):
+            arr = (ctypes.c_void_p * L)(*[h._h.value for h in weights[k]])
+            self._keep.append(arr)
+            setattr(d, k, ctypes.cast(arr, ctypes.c_void_p))
+        d.lm_head = weights["lm_head"]._h.value
+        for k in ("attn_norm", "ffn_norm"):
+            rows = [np.ascontiguousarray(r, np.float32) for r in weights[k]]
+            self._keep.extend(rows)
+            arr = (ctypes.c_void_p * L)(*[r.ctypes.data for r in rows])
+            self._keep.append(arr)
+            setattr(d, k, ctypes.cast(arr, ctypes.c_void_p))
+        for k in ("output_norm", "embd"):
+            a = np.ascontiguousarray(weights[k], np.float32)
+            self._keep.append(a)
+            setattr(d, k, a.ctypes.data)
+        self._weights = weights  # handles must outlive the model
+        self.cfg = cfg
+        h = ctypes.c_void_p()
+        _check(lib().gq_model_create(ctypes.byref(d), ctypes.byref(h)))
+        self._h = h
+        self._keep = None  # the library copied norms and embedding
+
+    def __del__(self):
+        if getattr(self, "_h", None) is not None and _lib is not None:
+            _lib.gq_model_free(self._h)
+            self._h = None
+
+    def kv_upload(self, layer, k_f16, v_f16):
+        k = np.ascontiguousarray(k_f16, np.uint16)
+        v = np.ascontiguousarray(v_f16, np.uint16)
+        _check(lib().gq_model_kv_upload(self._h, layer, _ptr(k), _ptr(v), k.shape[0]))
+
+    def kv_download(self, layer, n_pos):
+        kvd = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
+        k = np.zeros((n_pos, kvd), np.uint16)
+        v = np.zeros((n_pos, kvd), np.uint16)
+        _check(lib().gq_model_kv_download(self._h, layer, _ptr(k), _ptr(v), n_pos))
+        return k, v
+
+    def decode(self, token, pos, want_logits=True):
+        """One step (Model::forward): returns (next_token, logits or None)."""
+        logits = np.zeros(self.cfg["vocab"], np.float32) if want_logits else None
+        nxt = ctypes.c_int()
+        _check(lib().gq_model_decode(self._h, token, pos, _ptr(logits), ctypes.byref(nxt)))
+        return nxt.value, logits
+
+    def generate(self, token, pos, n_steps, stream=None):
+        """n_steps greedy steps (one HIP graph replay each); returns the tokens."""
+        out = np.zeros(n_steps, np.int32)
+        _check(lib().gq_model_generate(self._h, token, pos, n_steps, _ptr(out), _stream(stream)))
+        return out
 
 
 def create_backend(preference="hip", device=0):

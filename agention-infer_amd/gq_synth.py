@@ -79,3 +79,62 @@ def make_x(n, seed=1, batch=None):
     rng = np.random.default_rng(seed)
     shape = (n,) if batch is None else (batch, n)
     return rng.standard_normal(shape, dtype=np.float32)
+
+
+# ------------------------------------------------------------ dense decoder
+QWEN25_7B = dict(n_layers=28, hidden=3584, n_heads=28, n_kv_heads=4, head_dim=128, ffn=18944,
+                 vocab=152064, eps=1e-6, theta=1e6, attn_type=Q4_K, gate_up_type=Q4_K,
+                 down_type=Q6_K, head_type=Q6_K)
+
+
+def make_decoder(cfg, seed=0):
+    """Random-init weights of a dense decoder in ggml block order (the
+    Q4_K_M layout of the benchmark: Q4_K attention/gate/up, Q6_K down/head),
+    RMSNorm weights ~ N(1, 0.1), f32 embedding ~ N(0, 1)."""
+    rng = np.random.default_rng(seed)
+    L, H, F = cfg["n_layers"], cfg["hidden"], cfg["ffn"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    w = {k: [] for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown", "attn_norm", "ffn_norm")}
+    s = seed * 1000
+    for l in range(L):
+        s += 10
+        w["wq"].append(make_blocks(cfg["attn_type"], qd, H, seed=s + 1))
+        w["wk"].append(make_blocks(cfg["attn_type"], kvd, H, seed=s + 2))
+        w["wv"].append(make_blocks(cfg["attn_type"], kvd, H, seed=s + 3))
+        w["wo"].append(make_blocks(cfg["attn_type"], H, qd, seed=s + 4))
+        w["wgate"].append(make_blocks(cfg["gate_up_type"], F, H, seed=s + 5))
+        w["wup"].append(make_blocks(cfg["gate_up_type"], F, H, seed=s + 6))
+        w["wdown"].append(make_blocks(cfg["down_type"], H, F, seed=s + 7))
+        w["attn_norm"].append((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+        w["ffn_norm"].append((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))
+    w["lm_head"] = make_blocks(cfg["head_type"], cfg["vocab"], H, seed=s + 100)
+    w["output_norm"] = (1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32)
+    w["embd"] = rng.standard_normal((cfg["vocab"], H), dtype=np.float32)
+    return w
+
+
+def make_kv(cfg, n_pos, seed=0):
+    """Prefilled f16 KV cache ~ N(0, 1): [n_layers][n_pos][kv_dim] bits."""
+    rng = np.random.default_rng(seed)
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    shape = (cfg["n_layers"], n_pos, kvd)
+    k = rng.standard_normal(shape, dtype=np.float32).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal(shape, dtype=np.float32).astype(np.float16).view(np.uint16)
+    return k, v
+
+
+def upload_decoder(backend, cfg, w):
+    """Upload every weight matrix once (pre_upload_gpu, gpu_resident.rs:69-229)."""
+    H, F = cfg["hidden"], cfg["ffn"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    dims = dict(wq=(qd, H), wk=(kvd, H), wv=(kvd, H), wo=(H, qd), wgate=(F, H), wup=(F, H),
+                wdown=(H, F))
+    types = dict(wq="attn_type", wk="attn_type", wv="attn_type", wo="attn_type",
+                 wgate="gate_up_type", wup="gate_up_type", wdown="down_type")
+    hw = {}
+    for k, (rows, cols) in dims.items():
+        hw[k] = [backend.upload_weight(cfg[types[k]], a, cols, rows) for a in w[k]]
+    hw["lm_head"] = backend.upload_weight(cfg["head_type"], w["lm_head"], H, cfg["vocab"])
+    for k in ("attn_norm", "ffn_norm", "output_norm", "embd"):
+        hw[k] = w[k]
+    return hw

@@ -136,6 +136,47 @@ int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down
                const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
                int *ids_dev, float *w_dev, void *stream);
 
+/* ---- GPU-resident decode of a dense Llama/Qwen2-style decoder ----------
+ * The reference's run_gpu_resident (src/model/llama/gpu_resident.rs:427-697)
+ * with the arithmetic of LlamaModel::run (src/model/llama/cpu_path.rs:
+ * 695-818): embedding row, per layer RMSNorm -> q/k/v -> RoPE (NEOX) ->
+ * f16 KV cache (KvDtype::F16) -> attention -> o -> residual -> RMSNorm ->
+ * SwiGLU FFN -> residual, final RMSNorm, output head, greedy argmax
+ * (sampler.rs:120-131).  Weight handles stay owned by the caller and must
+ * outlive the model; norms and the f32 embedding are copied to the device. */
+typedef struct gq_model gq_model;
+typedef struct {
+  int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, ctx, max_tokens;
+  float eps, theta;
+  const gq_weight *const *wq, *const *wk, *const *wv, *const *wo;  /* [n_layers] */
+  const gq_weight *const *wgate, *const *wup, *const *wdown;       /* [n_layers] */
+  const gq_weight *lm_head;
+  const float *const *attn_norm, *const *ffn_norm;  /* host [n_layers][hidden] */
+  const float *output_norm;                         /* host [hidden] */
+  const float *embd;                                /* host [vocab][hidden] */
+} gq_model_desc;
+
+int gq_model_create(const gq_model_desc *desc, gq_model **out);
+int gq_model_free(gq_model *m);
+
+/* Fill / read back KV cache rows [0, n_pos) of a layer (f16 bits,
+ * [n_pos][n_kv_heads * head_dim]), e.g. a prefilled context
+ * (KvCache::write_range, src/model/mod.rs:671-680). */
+int gq_model_kv_upload(gq_model *m, int layer, const uint16_t *k_host, const uint16_t *v_host,
+                       int n_pos);
+int gq_model_kv_download(gq_model *m, int layer, uint16_t *k_host, uint16_t *v_host, int n_pos);
+
+/* One decode step (Model::forward, src/model/llama/mod.rs:336-363): token at
+ * position pos; logits_host[vocab] (may be NULL) and the greedy next token. */
+int gq_model_decode(gq_model *m, int token, int pos, float *logits_host, int *next_token);
+
+/* n_steps greedy steps from (token, pos) (runner::greedy_run decode loop,
+ * src/runner.rs:67-135): each step is one replay of a captured HIP graph;
+ * the argmax feeds the next step on the device.  tokens_host[n_steps]
+ * receives the generated tokens (synchronous when non-NULL). */
+int gq_model_generate(gq_model *m, int token, int pos, int n_steps, int *tokens_host,
+                      void *stream);
+
 /* Wait for all work on `stream`. */
 int gq_sync(void *stream);
 

@@ -719,6 +719,153 @@ int gqo_moe_ffn(int dtype, const uint8_t *gate, const uint8_t *up, const uint8_t
     return rc;
 }
 
+/* --------------------------------------------------------------- decode */
+
+/* cpu_path.rs:67-74: sum of squares (sequential), rms = sqrt(ss/n + eps),
+ * out = w * x / rms */
+static void rms_norm(const float *x, const float *w, int n, float eps, float *out) {
+    float ss = 0.0f;
+    for (int i = 0; i < n; i++) ss += x[i] * x[i];
+    float rms = sqrtf(ss / (float)n + eps);
+    for (int i = 0; i < n; i++) out[i] = w[i] * x[i] / rms;
+}
+
+/* cpu_path.rs:99-133 (freq_scale = 1) */
+static void rope(float *q, float *k, int n_heads, int n_kv, int hd, float theta, int pos) {
+    int half = hd / 2;
+    float *sn = (float *)malloc(sizeof(float) * half), *cs = (float *)malloc(sizeof(float) * half);
+    for (int d = 0; d < half; d++) {
+        float freq = (float)pos * 1.0f / powf(theta, 2.0f * (float)d / (float)hd);
+        sn[d] = sinf(freq);
+        cs[d] = cosf(freq);
+    }
+    for (int pass = 0; pass < 2; pass++) {
+        float *v = pass ? k : q;
+        int nh = pass ? n_kv : n_heads;
+        for (int h = 0; h < nh; h++) {
+            float *p = v + (size_t)h * hd;
+            for (int d = 0; d < half; d++) {
+                float x0 = p[d], x1 = p[d + half];
+                p[d] = x0 * cs[d] - x1 * sn[d];
+                p[d + half] = x0 * sn[d] + x1 * cs[d];
+            }
+        }
+    }
+    free(sn);
+    free(cs);
+}
+
+/* gqo_f16_to_f32 tabulated over all 65536 patterns (same values). */
+static float g_f16_tab[65536];
+static pthread_once_t g_f16_once = PTHREAD_ONCE_INIT;
+static void f16_tab_init(void) {
+    for (uint32_t i = 0; i < 65536; i++) g_f16_tab[i] = gqo_f16_to_f32((uint16_t)i);
+}
+static const float *f16_table(void) {
+    pthread_once(&g_f16_once, f16_tab_init);
+    return g_f16_tab;
+}
+
+typedef struct {
+    const float *q, *kall, *vall;
+    float *att;
+    int n, hd, kvd, group, h0, h1;
+} attn_job;
+
+static void *attn_worker(void *p) {
+    attn_job *j = (attn_job *)p;
+    const int hd = j->hd, kvd = j->kvd, n = j->n;
+    float *sc = (float *)malloc(sizeof(float) * n);
+    const float sq = sqrtf((float)hd);
+    for (int h = j->h0; h < j->h1; h++) {
+        const int kh = h / j->group;
+        const float *qh = j->q + (size_t)h * hd;
+        for (int t = 0; t < n; t++) {
+            const float *kt = j->kall + (size_t)t * kvd + (size_t)kh * hd;
+            float dot = 0.0f;
+            for (int d = 0; d < hd; d++) dot += qh[d] * kt[d];
+            sc[t] = dot / sq;
+        }
+        float mx = -INFINITY;
+        for (int t = 0; t < n; t++) mx = sc[t] > mx ? sc[t] : mx;
+        for (int t = 0; t < n; t++) sc[t] = expf(sc[t] - mx);
+        float sum = 0.0f;
+        for (int t = 0; t < n; t++) sum += sc[t];
+        for (int t = 0; t < n; t++) sc[t] /= sum;
+        for (int t = 0; t < n; t++) {
+            const float *vt = j->vall + (size_t)t * kvd + (size_t)kh * hd;
+            for (int d = 0; d < hd; d++) j->att[h * hd + d] += sc[t] * vt[d];
+        }
+    }
+    free(sc);
+    return NULL;
+}
+
+int gqo_decode_step(const gqo_model *m, int token, int pos, float *logits, int nthreads) {
+    const int H = m->hidden, hd = m->head_dim, nh = m->n_heads, nkv = m->n_kv_heads;
+    const int kvd = nkv * hd, F = m->ffn, group = nh / nkv, n = pos + 1;
+    float *x = (float *)malloc(sizeof(float) * H), *xn = (float *)malloc(sizeof(float) * H);
+    float *q = (float *)malloc(sizeof(float) * nh * hd), *k = (float *)malloc(sizeof(float) * kvd);
+    float *v = (float *)malloc(sizeof(float) * kvd), *att = (float *)malloc(sizeof(float) * nh * hd);
+    float *proj = (float *)malloc(sizeof(float) * H), *act = (float *)malloc(sizeof(float) * F);
+    float *g = (float *)malloc(sizeof(float) * F), *u = (float *)malloc(sizeof(float) * F);
+    float *kall = (float *)malloc(sizeof(float) * (size_t)n * kvd);
+    float *vall = (float *)malloc(sizeof(float) * (size_t)n * kvd);
+    int rc = 0;
+    memcpy(x, m->embd + (size_t)token * H, sizeof(float) * H);
+    const size_t rb_a = gqo_type_size(m->attn_type, H), rb_g = gqo_type_size(m->gate_up_type, H);
+    const size_t rb_d = gqo_type_size(m->down_type, F);
+    for (int L = 0; L < m->n_layers && !rc; L++) {
+        rms_norm(x, m->attn_norm[L], H, m->eps, xn);
+        rc |= gqo_matmul_into(m->attn_type, m->wq[L], rb_a * nh * hd, xn, H, q, nh * hd, nthreads);
+        rc |= gqo_matmul_into(m->attn_type, m->wk[L], rb_a * kvd, xn, H, k, kvd, nthreads);
+        rc |= gqo_matmul_into(m->attn_type, m->wv[L], rb_a * kvd, xn, H, v, kvd, nthreads);
+        rope(q, k, nh, nkv, hd, m->theta, pos);
+        uint16_t *kc = m->kcache[L], *vc = m->vcache[L];
+        for (int i = 0; i < kvd; i++) {
+            kc[(size_t)pos * kvd + i] = gqo_f32_to_f16(k[i]);
+            vc[(size_t)pos * kvd + i] = gqo_f32_to_f16(v[i]);
+        }
+        const float *tab = f16_table();
+        for (size_t i = 0; i < (size_t)n * kvd; i++) {
+            kall[i] = tab[kc[i]];
+            vall[i] = tab[vc[i]];
+        }
+        /* attention_into (cpu_path.rs:141-194); heads are independent and
+         * are computed on separate threads (same arithmetic per head). */
+        for (int i = 0; i < nh * hd; i++) att[i] = 0.0f;
+        attn_job aj = {q, kall, vall, att, n, hd, kvd, group, 0, 0};
+        int nt = hw_threads(nthreads);
+        if (nt > nh) nt = nh;
+        pthread_t th[256];
+        attn_job jobs[256];
+        int per = (nh + nt - 1) / nt;
+        for (int t = 0; t < nt; t++) {
+            jobs[t] = aj;
+            jobs[t].h0 = t * per < nh ? t * per : nh;
+            jobs[t].h1 = (t + 1) * per < nh ? (t + 1) * per : nh;
+            pthread_create(&th[t], NULL, attn_worker, &jobs[t]);
+        }
+        for (int t = 0; t < nt; t++) pthread_join(th[t], NULL);
+        rc |= gqo_matmul_into(m->attn_type, m->wo[L], rb_a * H, att, nh * hd, proj, H, nthreads);
+        for (int i = 0; i < H; i++) x[i] += proj[i];
+        rms_norm(x, m->ffn_norm[L], H, m->eps, xn);
+        rc |= gqo_matmul_into(m->gate_up_type, m->wgate[L], rb_g * F, xn, H, g, F, nthreads);
+        rc |= gqo_matmul_into(m->gate_up_type, m->wup[L], rb_g * F, xn, H, u, F, nthreads);
+        for (int i = 0; i < F; i++) act[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+        rc |= gqo_matmul_into(m->down_type, m->wdown[L], rb_d * H, act, F, proj, H, nthreads);
+        for (int i = 0; i < H; i++) x[i] += proj[i];
+    }
+    if (!rc) {
+        rms_norm(x, m->output_norm, H, m->eps, xn);
+        rc = gqo_matmul_into(m->head_type, m->lm_head, gqo_type_size(m->head_type, H) * m->vocab,
+                             xn, H, logits, m->vocab, nthreads);
+    }
+    free(x); free(xn); free(q); free(k); free(v); free(att); free(proj); free(act);
+    free(g); free(u); free(kall); free(vall);
+    return rc;
+}
+
 /* sampler.rs:120-131 */
 size_t gqo_argmax(const float *xs, size_t n) {
     size_t best = 0;

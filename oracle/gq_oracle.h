@@ -103,6 +103,32 @@ int gqo_moe_ffn(int dtype, const uint8_t *gate, const uint8_t *up, const uint8_t
                 int H, int F, const float *x, int T, int k, const int *ids, const float *w,
                 float *out, int nthreads);
 
+/* A dense Llama/Qwen2-style decoder (the Attention mixer of LlamaModel) for
+ * the decode restatement.  Weights are ggml bytes (rows of type_size(K));
+ * norms and the embedding are f32; the KV cache is f16 bits
+ * [layer][ctx][n_kv_heads * head_dim] (KvDtype::F16, model/mod.rs:567-603). */
+typedef struct {
+    int n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, ctx;
+    float eps, theta;
+    int attn_type, gate_up_type, down_type, head_type;
+    const float *embd;                /* [vocab][hidden] */
+    const float *output_norm;         /* [hidden] */
+    const uint8_t *lm_head;
+    const float *const *attn_norm;    /* [n_layers] -> [hidden] */
+    const float *const *ffn_norm;
+    const uint8_t *const *wq, *const *wk, *const *wv, *const *wo;
+    const uint8_t *const *wgate, *const *wup, *const *wdown;
+    uint16_t *const *kcache, *const *vcache;
+} gqo_model;
+
+/* LlamaModel::run (model/llama/cpu_path.rs:695-818) for the Attention
+ * mixer: embedding row, per layer rms_norm_into (:67-74) -> q/k/v matmuls ->
+ * rope (:99-133, NEOX pairs d <-> d + head_dim/2) -> KvCache::write /
+ * read_up_to (model/mod.rs:657-702, f16) -> attention_into (:141-194) -> wo
+ * -> residual -> rms_norm -> ffn_gate_up (:200-232) -> down -> residual;
+ * final norm and lm head.  logits[vocab]. */
+int gqo_decode_step(const gqo_model *m, int token, int pos, float *logits, int nthreads);
+
 /* argmax, first maximum wins (sampler.rs:120-131). */
 size_t gqo_argmax(const float *xs, size_t n);
 

@@ -45,6 +45,7 @@ def lib():
             "gqo_matmul_batch_into": (_I, [_I, _P, _SZ, _P, _SZ, _SZ, _P, _SZ, _I]),
             "gqo_argmax": (_SZ, [_P, _SZ]),
             "gqo_moe_route": (None, [_P, _I, _I, _I, _P, _P]),
+            "gqo_decode_step": (_I, [_P, _I, _I, _P, _I]),
             "gqo_moe_ffn": (_I, [_I, _P, _P, _P, _I, _I, _I, _P, _I, _I, _P, _P, _P, _I]),
         }
         for n, (r, a) in sig.items():
@@ -196,6 +197,61 @@ def moe_ffn(dtype, gate, up, down, E, H, F, x, ids, w, nthreads=0):
     _chk(lib().gqo_moe_ffn(dtype, _p(gate), _p(up), _p(down), E, H, F, _p(x), T, k, _p(ids),
                            _p(w), _p(out), nthreads))
     return out
+
+
+class _Model(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("n_layers", "hidden", "n_heads", "n_kv_heads",
+                                             "head_dim", "ffn", "vocab", "ctx")] + \
+        [("eps", ctypes.c_float), ("theta", ctypes.c_float)] + \
+        [(n, ctypes.c_int) for n in ("attn_type", "gate_up_type", "down_type", "head_type")] + \
+        [(n, ctypes.c_void_p) for n in ("embd", "output_norm", "lm_head", "attn_norm",
+                                         "ffn_norm", "wq", "wk", "wv", "wo", "wgate", "wup",
+                                         "wdown", "kcache", "vcache")]
+
+
+class DecoderModel:
+    """LlamaModel::run restated on the CPU (gqo_decode_step) with its own f16
+    KV cache [layer][ctx][kv_dim]."""
+
+    def __init__(self, cfg, w, kv_init=None):
+        self.cfg = cfg
+        self.keep = []
+        m = _Model()
+        for k in ("n_layers", "hidden", "n_heads", "n_kv_heads", "head_dim", "ffn", "vocab", "ctx"):
+            setattr(m, k, int(cfg[k]))
+        m.eps, m.theta = float(cfg["eps"]), float(cfg["theta"])
+        m.attn_type, m.gate_up_type = cfg["attn_type"], cfg["gate_up_type"]
+        m.down_type, m.head_type = cfg["down_type"], cfg["head_type"]
+
+        def ptr_array(arrs):
+            arrs = [np.ascontiguousarray(a) for a in arrs]
+            self.keep.extend(arrs)
+            pa = (ctypes.c_void_p * len(arrs))(*[a.ctypes.data for a in arrs])
+            self.keep.append(pa)
+            return ctypes.cast(pa, ctypes.c_void_p)
+
+        for k in ("embd", "output_norm", "lm_head"):
+            a = np.ascontiguousarray(w[k])
+            self.keep.append(a)
+            setattr(m, k, a.ctypes.data)
+        for k in ("attn_norm", "ffn_norm", "wq", "wk", "wv", "wo", "wgate", "wup", "wdown"):
+            setattr(m, k, ptr_array(w[k]))
+        L, ctx = cfg["n_layers"], cfg["ctx"]
+        kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+        self.kc = np.zeros((L, ctx, kvd), np.uint16)
+        self.vc = np.zeros((L, ctx, kvd), np.uint16)
+        if kv_init is not None:
+            kk, vv = kv_init
+            self.kc[:, :kk.shape[1]] = kk
+            self.vc[:, :vv.shape[1]] = vv
+        m.kcache = ptr_array([self.kc[l] for l in range(L)])
+        m.vcache = ptr_array([self.vc[l] for l in range(L)])
+        self.m = m
+
+    def step(self, token, pos, nthreads=0):
+        logits = np.zeros(self.cfg["vocab"], np.float32)
+        _chk(lib().gqo_decode_step(ctypes.byref(self.m), token, pos, _p(logits), nthreads))
+        return logits
 
 
 def argmax(xs):
