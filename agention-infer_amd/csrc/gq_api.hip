@@ -193,14 +193,28 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
 namespace gq {
 // Launch y_i = W_i . x for weights sharing dtype and in_dim (4 per launch).
 // With xu != nullptr the input is silu(xg) * xu instead of x.
-hipError_t matvec_launch(const gq_weight *const *ws, int count, const float *x, const float *xg,
-                         const float *xu, float *const *ys, hipStream_t st) {
+hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, float *const *ys,
+                         hipStream_t st, bool pair) {
   const gq_weight *w0 = ws[0];
+  if (pair) {  // {gate, up}: one segment of gate tiles, up as the second matrix
+    if (count != 2) return hipErrorInvalidValue;
+    MvArgs a{};
+    a.in = in;
+    a.grid = g_dev.grid;
+    a.k = w0->L.k;
+    a.units = w0->L.units;
+    a.chunks = w0->L.chunks;
+    a.pair = 1;
+    a.nseg = 2;
+    a.seg[0] = MvSeg{w0->body, w0->d, ys[0], w0->L.rows, w0->L.rt, 0};
+    a.seg[1] = MvSeg{ws[1]->body, ws[1]->d, nullptr, ws[1]->L.rows, ws[1]->L.rt, 0};
+    a.total_tiles = num_tiles(w0->L);
+    a.part_floats = 2 * ((w0->L.rt * w0->L.units + 63) / 64 * 64);
+    return a.total_tiles ? launch_matvec(a, w0->L.dtype, st) : hipSuccess;
+  }
   for (int base = 0; base < count; base += MV_MAX_SEG) {
     MvArgs a{};
-    a.x = x;
-    a.xg = xg;
-    a.xu = xu;
+    a.in = in;
     a.grid = g_dev.grid;
     a.k = w0->L.k;
     a.units = w0->L.units;
@@ -344,7 +358,9 @@ int gq_matvec_multi(const gq_weight *const *ws, int count, const float *x_dev,
     if (ws[i]->L.rows > 0 && !y_dev[i]) return fail(GQ_EINVAL, "null output %d", i);
   }
   if (!x_dev) return fail(GQ_EINVAL, "null x");
-  hipError_t e = gq::matvec_launch(ws, count, x_dev, nullptr, nullptr, y_dev, (hipStream_t)stream);
+  gq::MvIn in;
+  in.x = x_dev;
+  hipError_t e = gq::matvec_launch(ws, count, in, y_dev, (hipStream_t)stream);
   if (e != hipSuccess) return fail(GQ_EHIP, "matvec launch failed: %s", hipGetErrorString(e));
   return GQ_OK;
 }
@@ -509,10 +525,12 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   int rc = ensure_init();
   if (rc) return rc;
   const int H = d->hidden, hd = d->head_dim, nh = d->n_heads, nkv = d->n_kv_heads;
-  if (d->n_layers <= 0 || H <= 0 || hd <= 0 || hd > 128 || hd % 8 || nh <= 0 || nkv <= 0 ||
-      nh % nkv || d->ffn <= 0 || d->vocab <= 0 || d->ctx <= 0)
-    return fail(GQ_EINVAL, "bad model shape (head_dim must be a multiple of 8, <= 128; "
-                           "n_heads a multiple of n_kv_heads)");
+  if (d->n_layers <= 0 || H <= 0 || H % 4 || (hd != 64 && hd != 128) || nh <= 0 || nkv <= 0 ||
+      nh % nkv || nh / nkv > 8 || d->ffn <= 0 || d->vocab <= 0 || d->ctx <= 0 ||
+      d->ctx > 256 * gq::ATT_CHUNK)
+    return fail(GQ_EINVAL, "bad model shape (hidden a multiple of 4, head_dim 64 or 128, "
+                           "n_heads a multiple of n_kv_heads with at most 8 query heads per KV "
+                           "head, ctx <= %d)", 256 * gq::ATT_CHUNK);
   for (int l = 0; l < d->n_layers; l++) {
     if ((rc = check_w(d->wq[l], nh * hd, H, "wq", l)) || (rc = check_w(d->wk[l], nkv * hd, H, "wk", l)) ||
         (rc = check_w(d->wv[l], nkv * hd, H, "wv", l)) || (rc = check_w(d->wo[l], H, nh * hd, "wo", l)) ||
@@ -523,13 +541,18 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
     if (d->wq[l]->L.dtype != d->wk[l]->L.dtype || d->wq[l]->L.dtype != d->wv[l]->L.dtype ||
         d->wgate[l]->L.dtype != d->wup[l]->L.dtype)
       return fail(GQ_EINVAL, "layer %d: q/k/v and gate/up must share a dtype", l);
+    const gq_weight *g = d->wgate[l];
+    if (d->wup[l]->L.rt != g->L.rt ||
+        gq::matvec_lds_bytes(g->L.dtype, g->L.units, 2 * ((g->L.rt * g->L.units + 63) / 64 * 64)) >
+            160 * 1024)
+      return fail(GQ_EINVAL, "layer %d: ffn_gate/ffn_up layouts do not pair", l);
   }
   if ((rc = check_w(d->lm_head, d->vocab, H, "output", -1))) return rc;
   gq_model *m = new gq_model();
   auto &L = m->L;
   L.n_layers = d->n_layers; L.hidden = H; L.n_heads = nh; L.n_kv_heads = nkv; L.head_dim = hd;
   L.ffn = d->ffn; L.vocab = d->vocab; L.ctx = d->ctx; L.eps = d->eps; L.theta = d->theta;
-  L.att_chunks = (d->ctx + 255) / 256;
+  L.att_chunks = (d->ctx + gq::ATT_CHUNK - 1) / gq::ATT_CHUNK;
   L.max_tokens = d->max_tokens > 0 ? d->max_tokens : 4096;
   for (int l = 0; l < d->n_layers; l++) {
     m->wq.push_back(d->wq[l]); m->wk.push_back(d->wk[l]); m->wv.push_back(d->wv[l]);
@@ -545,17 +568,25 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   if (!rc) rc = dalloc(m, &L.kcache, (size_t)d->n_layers * d->ctx * kvd);
   if (!rc) rc = dalloc(m, &L.vcache, (size_t)d->n_layers * d->ctx * kvd);
   float *buf = nullptr;
-  const size_t nbuf = 2 * (size_t)H + (size_t)nh * hd * 2 + 2 * kvd + (size_t)H + 2 * (size_t)d->ffn +
-                      (size_t)d->vocab + (size_t)nh * L.att_chunks * (2 + hd) + 64;
+  const int nb_amax = (d->vocab + gq::ARGMAX_SPAN - 1) / gq::ARGMAX_SPAN;
+  const size_t nbuf = 3 * ((size_t)H + 16) + 2 * ((size_t)nh * hd + 16) + 2 * (kvd + 16) +
+                      ((size_t)d->ffn + 16) + ((size_t)d->vocab + 16) +
+                      ((size_t)nh * L.att_chunks * (2 + hd) + 16) + (nb_amax + 16);
+  int *ibuf = nullptr;
+  const size_t nibuf = (size_t)nkv + 1 + nb_amax;
   if (!rc) rc = dalloc(m, &buf, nbuf);
+  if (!rc) rc = dalloc(m, &ibuf, nibuf);
   if (!rc) rc = dalloc(m, &L.state, 1);
   if (!rc) rc = dalloc(m, &L.tokens, (size_t)L.max_tokens);
   if (rc) { delete m; return rc; }
   size_t o = 0;
   auto take = [&](size_t n) { float *p = buf + o; o += (n + 15) & ~(size_t)15; return p; };
-  L.x = take(H); L.xn = take(H); L.q = take((size_t)nh * hd); L.att = take((size_t)nh * hd);
-  L.k = take(kvd); L.v = take(kvd); L.proj = take(H); L.g = take(d->ffn); L.u = take(d->ffn);
+  L.xa = take(H); L.xb = take(H); L.proj = take(H);
+  L.q = take((size_t)nh * hd); L.att = take((size_t)nh * hd);
+  L.k = take(kvd); L.v = take(kvd); L.h = take(d->ffn);
   L.logits = take(d->vocab); L.att_part = take((size_t)nh * L.att_chunks * (2 + hd));
+  L.amax_v = take(nb_amax);
+  L.att_count = ibuf; L.amax_count = ibuf + nkv; L.amax_i = ibuf + nkv + 1;
   hipError_t e = hipSuccess;
   for (int l = 0; l < d->n_layers && e == hipSuccess; l++) {
     e = hipMemcpy(norms + (size_t)(2 * l) * H, d->attn_norm[l], H * 4, hipMemcpyHostToDevice);
@@ -567,6 +598,9 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   if (e == hipSuccess)
     e = hipMemcpy(norms + (size_t)2 * d->n_layers * H, d->output_norm, H * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(embd, d->embd, (size_t)d->vocab * H * 4, hipMemcpyHostToDevice);
+  // counters of the last-block merges start (and end every launch) at zero
+  if (e == hipSuccess) e = hipMemset(ibuf, 0, nibuf * sizeof(int));
+  if (e == hipSuccess) e = hipMemset(buf, 0, nbuf * sizeof(float));
   if (e != hipSuccess) { delete m; return fail(GQ_EHIP, "model upload failed: %s", hipGetErrorString(e)); }
   L.attn_norm = m->an.data(); L.ffn_norm = m->fn.data();
   L.output_norm = norms + (size_t)2 * d->n_layers * H;

@@ -1,222 +1,395 @@
 // gq_decode.hip -- the non-matmul kernels of a GPU-resident decode step for
-// a dense Llama/Qwen2-style decoder (the reference's run_gpu_resident,
-// src/model/llama/gpu_resident.rs:427-697, restating the arithmetic of
-// LlamaModel::run, src/model/llama/cpu_path.rs:695-818).
+// a dense Llama/Qwen2-style decoder and the step's launch sequence (the
+// reference's run_gpu_resident, src/model/llama/gpu_resident.rs:427-697,
+// restating the arithmetic of LlamaModel::run, src/model/llama/
+// cpu_path.rs:695-818).
+//
+// One step is 5 launches per layer plus 2:
+//   qkv matvec   input RMSNorm(x + proj) (residual add fused; block 0 stores
+//                the new residual stream; layer 0 reads the embedding row)
+//   attention    RoPE of q and of the new k, f16 KV row store, scores,
+//                softmax and the weighted V sum for all query heads of one
+//                KV head over a chunk of positions; the last chunk block of
+//                a KV head combines the chunks
+//   o matvec
+//   gate/up      one matvec over both matrices with input RMSNorm(x + o)
+//                and output silu(gate) * up
+//   down matvec
+// then the output head (input RMSNorm(x + proj)) and the greedy argmax.
 //
 // Step state (token, position, step counter) lives in device memory so that
 // a captured HIP graph of one step can be replayed for every greedy step:
-// the argmax kernel writes the next token and advances the position.
+// the argmax writes the next token and advances the position.  The chunk
+// counters used by the last-block merges return to zero at the end of
+// every launch, so a replay starts from the same state.
 #include "gq_device.h"
 #include "gq_internal.h"
 
 namespace gq {
 
-// Block-wide sum for 1024 threads (16 waves).
-__device__ __forceinline__ float block_sum_1024(float v, float *red) {
+
+// ----------------------------------------------------------- attention
+// Block (kv head kh, chunk c): positions [c*CH, min((c+1)*CH, n)) for the
+// `group` query heads kh*group .. kh*group+group-1 (GQA: each K/V row is
+// read once for all of them), ATT_WAVES waves of 32 positions each.
+//   scores  s[g][t] = (q_g . k_t) / sqrt(hd)        (attention_into,
+//   softmax m_g = max s, p = exp(s - m_g), l_g = sum p   cpu_path.rs:141-194)
+//   values  o[g][d] = sum_t p[g][t] v_t[d]
+// Scores run on v_mfma_f32_16x16x32_f16 (rows = query heads, columns =
+// positions, depth = head dims): K rows are f16 already and go straight
+// from HBM into the B operands; q is scaled by a power of two and split
+// into f16 hi + lo parts, so each product is exact in fp32 and q is carried
+// to ~22 bits.  The V sum runs on fp32 FMAs, a lane owning HD/64 dims of
+// every row of its wave (no cross-lane reduction), then across waves.
+// The partial (m, l, o) of each (head, chunk) goes to `part`; the last
+// block of a KV head to finish (chunk counter) merges the chunks:
+//   att[h] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+// The block holding position pos = n - 1 also rotates the new k, rounds k
+// and v to f16 (KvDtype::F16::pack) and stores them in the cache; it uses
+// the rounded values for position pos itself.
+constexpr int ATT_MAXG = 8;      // query heads per KV head
+constexpr int ATT_MAXCH = 256;   // chunks (ctx <= 256 * ATT_CHUNK)
+constexpr int ATT_WAVES = 8;
+constexpr int ATT_THREADS = 64 * ATT_WAVES;
+static_assert(ATT_WAVES == ATT_MAXG, "one wave per query head in the softmax");
+static_assert(ATT_CHUNK == 32 * ATT_WAVES, "32 positions per wave");
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4a_t __attribute__((ext_vector_type(4)));
+
+template <int HD>
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
+    const float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc,
+    const DecodeState *st, int group, int kvd, float theta, float *part, int *count, float *att) {
+  constexpr int CH = ATT_CHUNK;
+  constexpr int NW = ATT_WAVES;
+  constexpr int PW = CH / NW;  // positions per wave
+  constexpr int NT = PW / 16;  // 16-position MFMA tiles per wave
+  constexpr int KS = HD / 32;  // MFMA depth steps
+  constexpr int DPL = HD / 64; // value dims per lane
+  constexpr int HALF = HD / 2;
+  __shared__ float sp[ATT_MAXG][CH];
+  __shared__ float ored[NW][ATT_MAXG][HD];  // reused for the merge factors
+  __shared__ float qsh[ATT_MAXG][HD];
+  __shared__ float rs[HALF], rc[HALF];
+  __shared__ __align__(16) uint16_t knew[HD];
+  __shared__ __align__(16) uint16_t vnew[HD];
+  __shared__ float qmax_s[NW];
+  __shared__ int last_s;
+  static_assert(sizeof(ored) >= 2 * sizeof(float) * ATT_MAXG * ATT_MAXCH, "merge factors fit");
+
+  const int kh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int pos = st->pos, n = pos + 1, t0 = c * CH;
+  if (t0 >= n) return;
+  const int nch = (n + CH - 1) / CH;
+  const int nchunk_grid = gridDim.y;
+  const int tw = t0 + wave * PW;  // first position of this wave
+
+  // K rows as MFMA B operands (row tw + 16*tt + lane%16, dims
+  // 8*(lane/16) + 32*ks), V dims DPL*lane of the wave's rows; clamped to
+  // n - 1 (unused past n).
+  uint4 kb[NT][KS];
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-  if (l == 0) red[w] = v;
-  __syncthreads();
-  float s = 0.f;
-  if (threadIdx.x < 64) {
-    s = threadIdx.x < 16 ? red[threadIdx.x] : 0.f;
+  for (int tt = 0; tt < NT; tt++) {
+    const int t = min(tw + 16 * tt + (lane & 15), n - 1);
 #pragma unroll
-    for (int off = 8; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-    if (threadIdx.x == 0) red[16] = s;
+    for (int ks = 0; ks < KS; ks++)
+      kb[tt][ks] = ldw4(kc + (long)t * kvd + (long)kh * HD + 8 * (lane >> 4) + 32 * ks);
   }
-  __syncthreads();
-  s = red[16];
-  __syncthreads();
-  return s;
-}
-
-// x = embd[token]  (the embedding row lookup, cpu_path.rs:705-707).
-__global__ void k_embed(const float *embd, const DecodeState *st, float *x, int h) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < h) x[i] = embd[(long)st->token * h + i];
-}
-
-// Optional residual add (x += r), then out = w * x / rms(x)
-// (rms_norm_into, cpu_path.rs:67-74).  One 1024-thread block.
-__global__ __launch_bounds__(1024) void k_add_rmsnorm(float *x, const float *r, const float *w,
-                                                      float *out, int h, float eps) {
-  __shared__ float red[17];
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < h; i += 1024) {
-    float v = x[i];
-    if (r) {
-      v += r[i];
-      x[i] = v;
-    }
-    ss += v * v;
-  }
-  ss = block_sum_1024(ss, red);
-  const float rms = sqrtf(ss / (float)h + eps);
-  for (int i = threadIdx.x; i < h; i += 1024) out[i] = w[i] * x[i] / rms;
-}
-
-// RoPE on q and k at the current position (NEOX pairs d <-> d + hd/2,
-// freq = pos / theta^(2d/hd), cpu_path.rs:99-133), then k and v stored as
-// f16 (round to nearest even, KvDtype::F16::pack) into the cache row.
-// Grid: n_heads + n_kv_heads blocks of hd/2 threads.
-__global__ void k_rope_kv(float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc,
-                          const DecodeState *st, int n_heads, int n_kv, int hd, float theta) {
-  const int hb = blockIdx.x, d = threadIdx.x, half = hd / 2;
-  const int pos = st->pos;
-  const float freq = (float)pos * 1.0f / powf(theta, 2.0f * (float)d / (float)hd);
-  const float sn = sinf(freq), cs = cosf(freq);
-  if (hb < n_heads) {
-    float *p = q + (long)hb * hd;
-    const float x0 = p[d], x1 = p[d + half];
-    p[d] = x0 * cs - x1 * sn;
-    p[d + half] = x0 * sn + x1 * cs;
-  } else {
-    const int h = hb - n_heads;
-    const long kvd = (long)n_kv * hd;
-    const float *pk = k + (long)h * hd;
-    const float x0 = pk[d], x1 = pk[d + half];
-    const float y0 = x0 * cs - x1 * sn, y1 = x0 * sn + x1 * cs;
-    uint16_t *kr = kc + (long)pos * kvd + (long)h * hd;
-    uint16_t *vr = vc + (long)pos * kvd + (long)h * hd;
-    kr[d] = __half_as_ushort(__float2half_rn(y0));
-    kr[d + half] = __half_as_ushort(__float2half_rn(y1));
-    vr[d] = __half_as_ushort(__float2half_rn(v[(long)h * hd + d]));
-    vr[d + half] = __half_as_ushort(__float2half_rn(v[(long)h * hd + d + half]));
-  }
-}
-
-// Attention, split over position chunks (flash-decode): block (h, c) scores
-// positions [c*ATT_CHUNK, ...) of head h against its KV head h / group,
-// writing m = max score, l = sum exp(s - m), o = sum exp(s - m) v.
-// Scores are q.k / sqrt(hd) as attention_into (cpu_path.rs:141-194).
-constexpr int ATT_CHUNK = 256;
-
-__global__ __launch_bounds__(256) void k_attn_partial(const float *q, const uint16_t *kc,
-                                                      const uint16_t *vc, const DecodeState *st,
-                                                      int n_heads, int group, int hd, int kvd,
-                                                      float *part) {
-  __shared__ float qs[256];
-  __shared__ float sc[ATT_CHUNK];
-  __shared__ float red[8];
-  __shared__ float ohalf[2][256];
-  const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
-  const int n = st->pos + 1;
-  const int t0 = c * ATT_CHUNK;
-  const int kh = h / group;
-  float *out = part + ((long)h * gridDim.y + c) * (2 + hd);
-  if (t0 >= n) {  // chunk past the current length: neutral partial
-    if (tid == 0) {
-      out[0] = -INFINITY;
-      out[1] = 0.f;
-    }
-    if (tid < hd) out[2 + tid] = 0.f;
-    return;
-  }
-  if (tid < hd) qs[tid] = q[(long)h * hd + tid];
-  __syncthreads();
-  const int t = t0 + tid;
-  float s = -INFINITY;
-  if (t < n) {
-    const uint16_t *kr = kc + (long)t * kvd + (long)kh * hd;
-    float dot = 0.f;
-    for (int d = 0; d < hd; d += 8) {
-      const uint4 raw = *(const uint4 *)(kr + d);
-      const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+  uint32_t vr[PW];
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        dot += qs[d + 2 * j] * h2f(w4[j]);
-        dot += qs[d + 2 * j + 1] * h2f(w4[j] >> 16);
+  for (int j = 0; j < PW; j++) {
+    const uint16_t *p = vc + (long)min(tw + j, n - 1) * kvd + (long)kh * HD + DPL * lane;
+    vr[j] = DPL == 2 ? ldw1(p) : (uint32_t)ldh(p);
+  }
+
+  // RoPE table for pair index i (cpu_path.rs:99-133, NEOX pairs d <-> d + hd/2).
+  if (tid < HALF) {
+    const float ang = (float)pos * 1.0f / powf(theta, 2.0f * (float)tid / (float)HD);
+    rs[tid] = sinf(ang);
+    rc[tid] = cosf(ang);
+  }
+  __syncthreads();
+  // New K/V row of this KV head: rotate k, round both to f16, store.
+  if (pos < t0 + CH && tid < HD) {
+    const int d = tid, i = d % HALF;
+    const float *pk = k + (long)kh * HD;
+    const float own = pk[d], par = pk[(d + HALF) % HD];
+    const float rot = d < HALF ? own * rc[i] - par * rs[i] : par * rs[i] + own * rc[i];
+    const uint16_t kbits = __half_as_ushort(__float2half_rn(rot));
+    const uint16_t vbits = __half_as_ushort(__float2half_rn(v[(long)kh * HD + d]));
+    knew[d] = kbits;
+    vnew[d] = vbits;
+    kc[(long)pos * kvd + (long)kh * HD + d] = kbits;
+    vc[(long)pos * kvd + (long)kh * HD + d] = vbits;
+  }
+  // Rotated q of the group's heads, and its max |q|.
+  float qm = 0.f;
+  for (int o = tid; o < group * HD; o += ATT_THREADS) {
+    const int g = o / HD, d = o % HD, i = d % HALF;
+    const float *qh = q + (long)(kh * group + g) * HD;
+    const float own = qh[d], par = qh[(d + HALF) % HD];
+    const float rot = d < HALF ? own * rc[i] - par * rs[i] : par * rs[i] + own * rc[i];
+    qsh[g][d] = rot;
+    qm = fmaxf(qm, fabsf(rot));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) qm = fmaxf(qm, __shfl_xor(qm, off, 64));
+  if (lane == 0) qmax_s[wave] = qm;
+  __syncthreads();
+  qm = qmax_s[0];
+#pragma unroll
+  for (int w = 1; w < NW; w++) qm = fmaxf(qm, qmax_s[w]);
+
+  // A operands: q * 2^e (max in [512, 1024)) as f16 hi + lo.
+  int ex = 0;
+  (void)frexpf(qm, &ex);
+  const float qscale = qm > 0.f ? ldexpf(1.0f, 10 - ex) : 1.0f;
+  f16x8_t ahi[KS], alo[KS];
+  {
+    const int m = lane & 15;
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const float x = m < group ? qsh[m][8 * (lane >> 4) + 32 * ks + j] * qscale : 0.f;
+        const _Float16 h = (_Float16)x;
+        ahi[ks][j] = h;
+        alo[ks][j] = (_Float16)(x - (float)h);
       }
     }
-    s = dot / sqrtf((float)hd);
   }
-  // block max
-  float m = s;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-  if ((tid & 63) == 0) red[tid >> 6] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float p = t < n ? expf(s - m) : 0.f;
-  sc[tid] = p;
-  float l = p;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off, 64);
-  __syncthreads();
-  if ((tid & 63) == 0) red[4 + (tid >> 6)] = l;
-  __syncthreads();
-  l = red[4] + red[5] + red[6] + red[7];
-  // o[d] = sum_t p_t v_t[d]: threads (d, half) take alternate positions
-  const int d = tid % 128, hv = tid / 128;
-  const int tn = min(ATT_CHUNK, n - t0);
-  float o = 0.f;
-  if (d < hd)
-    for (int j = hv; j < tn; j += 2)
-      o += sc[j] * h2f(vc[(long)(t0 + j) * kvd + (long)kh * hd + d]);
-  ohalf[hv][d] = o;
-  __syncthreads();
-  if (tid < hd) out[2 + tid] = ohalf[0][tid] + ohalf[1][tid];
-  if (tid == 0) {
-    out[0] = m;
-    out[1] = l;
-  }
-}
 
-// Combine the chunks of each head: out = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
-__global__ void k_attn_combine(const float *part, int nchunks, int hd, float *att) {
-  const int h = blockIdx.x, d = threadIdx.x;
-  const float *ph = part + (long)h * nchunks * (2 + hd);
-  float M = -INFINITY;
-  for (int c = 0; c < nchunks; c++) M = fmaxf(M, ph[c * (2 + hd)]);
-  float L = 0.f, o = 0.f;
-  for (int c = 0; c < nchunks; c++) {
-    const float *pc = ph + c * (2 + hd);
-    if (pc[0] == -INFINITY) continue;
-    const float f = expf(pc[0] - M);
-    L += pc[1] * f;
-    o += pc[2 + d] * f;
-  }
-  if (d < hd) att[(long)h * hd + d] = o / L;
-}
-
-// Greedy argmax (first maximum wins, sampler.rs:120-131); records the token,
-// makes it the next input and advances the position.  One 1024-thread block.
-__global__ __launch_bounds__(1024) void k_argmax_next(const float *logits, int n, DecodeState *st,
-                                                      int *tokens, int max_tokens) {
-  __shared__ float bv_s[16];
-  __shared__ int bi_s[16];
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < n; i += 1024) {
-    const float v = logits[i];
-    if (v > bv) {  // i increases per thread: strict > keeps the first
-      bv = v;
-      bi = i;
+  // Scores: lane holds S[head 4*(lane/16) + i][position lane%16] per tile.
+  {
+    const float rsq = sqrtf((float)HD);
+    const float inv_scale = 1.0f / qscale;  // a power of two: exact
+    uint4 kn[KS];  // the new row's fragments (read whether used or not)
+#pragma unroll
+    for (int ks = 0; ks < KS; ks++) kn[ks] = *(const uint4 *)(knew + 8 * (lane >> 4) + 32 * ks);
+#pragma unroll
+    for (int tt = 0; tt < NT; tt++) {
+      const int tcol = tw + 16 * tt + (lane & 15);
+      const bool isnew = tcol == pos;
+      f32x4a_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) {
+        const uint4 raw = make_uint4(isnew ? kn[ks].x : kb[tt][ks].x, isnew ? kn[ks].y : kb[tt][ks].y,
+                                     isnew ? kn[ks].z : kb[tt][ks].z, isnew ? kn[ks].w : kb[tt][ks].w);
+        f16x8_t bk;
+        __builtin_memcpy(&bk, &raw, 16);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int g = 4 * (lane >> 4) + i;
+        if (g < group) sp[g][tcol - t0] = tcol < n ? acc[i] * inv_scale / rsq : -INFINITY;
+      }
     }
   }
+  __syncthreads();
+
+  // Softmax statistics: wave g handles head g.
+  float mh = -INFINITY, lh = 0.f;
+  if (wave < group) {
+    float vals[CH / 64];
+#pragma unroll
+    for (int i = 0; i < CH / 64; i++) {
+      vals[i] = sp[wave][lane + 64 * i];
+      mh = fmaxf(mh, vals[i]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mh = fmaxf(mh, __shfl_xor(mh, off, 64));
+#pragma unroll
+    for (int i = 0; i < CH / 64; i++) {
+      const float p = expf(vals[i] - mh);  // exp(-inf) = 0 past n
+      sp[wave][lane + 64 * i] = p;
+      lh += p;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) lh += __shfl_xor(lh, off, 64);
+  }
+  __syncthreads();
+
+  // Values: lane owns dims DPL*lane .. +DPL of the wave's PW rows.
+  {
+    float acc[ATT_MAXG][DPL];
+#pragma unroll
+    for (int g = 0; g < ATT_MAXG; g++)
+#pragma unroll
+      for (int e = 0; e < DPL; e++) acc[g][e] = 0.f;
+    const uint32_t vn = DPL == 2 ? *(const uint32_t *)(vnew + DPL * lane) : (uint32_t)vnew[lane];
+#pragma unroll
+    for (int j = 0; j < PW; j++) {
+      const int tl = wave * PW + j;
+      const uint32_t raw = t0 + tl == pos ? vn : vr[j];
+      float vf[DPL];
+#pragma unroll
+      for (int e = 0; e < DPL; e++) vf[e] = h2f(raw >> (16 * e));
+#pragma unroll
+      for (int g = 0; g < ATT_MAXG; g++) {
+        if (g < group) {
+          const float p = sp[g][tl];
+#pragma unroll
+          for (int e = 0; e < DPL; e++) acc[g][e] += p * vf[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < ATT_MAXG; g++)
+      if (g < group)
+#pragma unroll
+        for (int e = 0; e < DPL; e++) ored[wave][g][DPL * lane + e] = acc[g][e];
+  }
+  __syncthreads();
+  for (int o = tid; o < group * HD; o += ATT_THREADS) {
+    const int g = o / HD, d = o % HD;
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) s += ored[w][g][d];
+    part[((long)(kh * group + g) * nchunk_grid + c) * (2 + HD) + 2 + d] = s;
+  }
+  if (lane == 0 && wave < group) {
+    float *pm = part + ((long)(kh * group + wave) * nchunk_grid + c) * (2 + HD);
+    pm[0] = mh;
+    pm[1] = lh;
+  }
+
+  // The last block of this KV head merges the chunks.  One thread per
+  // block fences (an agent-scope release writes back this XCD's L2; the
+  // barrier before it orders the whole block's stores), and the last
+  // block's acquire fence invalidates its caches before it reads the other
+  // blocks' partials.
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    const bool last = atomicAdd(count + kh, 1) == nch - 1;
+    if (last) __threadfence();
+    last_s = last;
+  }
+  __syncthreads();
+  if (!last_s) return;
+  float (*fac)[ATT_MAXCH] = (float (*)[ATT_MAXCH])&ored[0][0][0];
+  float (*fl)[ATT_MAXCH] = fac + ATT_MAXG;
+  const int nch16 = (nch + 15) & ~15;
+  for (int i = tid; i < group * nch16; i += ATT_THREADS) {
+    const int g = i / nch16, cc = i % nch16;
+    float m = -INFINITY, l = 0.f;
+    if (cc < nch) {
+      const float *pm = part + ((long)(kh * group + g) * nchunk_grid + cc) * (2 + HD);
+      m = pm[0];
+      l = pm[1];
+    }
+    fac[g][cc] = m;
+    fl[g][cc] = l;
+  }
+  __syncthreads();
+  if (tid < group) {  // fac[g][c] = e^(m_c - M) / L (0 for c >= nch)
+    float M = -INFINITY;
+    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, fac[tid][cc]);
+    float L = 0.f;
+    for (int cc = 0; cc < nch; cc++) {
+      const float e = expf(fac[tid][cc] - M);
+      fac[tid][cc] = e;
+      L += fl[tid][cc] * e;
+    }
+    const float inv = 1.0f / L;
+    for (int cc = 0; cc < nch16; cc++) fac[tid][cc] = cc < nch ? fac[tid][cc] * inv : 0.f;
+  }
+  __syncthreads();
+  for (int o = tid; o < group * HD; o += ATT_THREADS) {
+    const int g = o / HD, d = o % HD;
+    const float *po = part + (long)(kh * group + g) * nchunk_grid * (2 + HD) + 2 + d;
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < nch; cb += 16) {
+      float vals[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) vals[j] = cb + j < nch ? po[(long)(cb + j) * (2 + HD)] : 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; j++) s4[j & 3] += vals[j] * fac[g][cb + j];
+    }
+    att[(long)(kh * group + g) * HD + d] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  }
+  if (tid == 0) count[kh] = 0;
+}
+
+// -------------------------------------------------------------- argmax
+// Greedy argmax (first maximum wins, sampler.rs:120-131).  Block b takes
+// logits [b*SPAN, (b+1)*SPAN); the last block to finish reduces the block
+// results, records the token, makes it the next input and advances the
+// position.
+__device__ __forceinline__ void amax_merge(float &bv, int &bi, float ov, int oi) {
+  if (ov > bv || (ov == bv && oi < bi)) {
+    bv = ov;
+    bi = oi;
+  }
+}
+
+__device__ __forceinline__ void block_amax(float &bv, int &bi, float *sv, int *si) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     const float ov = __shfl_xor(bv, off, 64);
     const int oi = __shfl_xor(bi, off, 64);
-    if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+    amax_merge(bv, bi, ov, oi);
   }
   const int w = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
-    bv_s[w] = bv;
-    bi_s[w] = bi;
+    sv[w] = bv;
+    si[w] = bi;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float v = bv_s[0];
-    int idx = bi_s[0];
-    for (int j = 1; j < 16; j++)
-      if (bv_s[j] > v || (bv_s[j] == v && bi_s[j] < idx)) { v = bv_s[j]; idx = bi_s[j]; }
-    if (idx == 0x7fffffff) idx = 0;  // all -inf / NaN: index 0, as argmax's initial best
-    if (tokens && st->step < max_tokens) tokens[st->step] = idx;
-    st->token = idx;
-    st->pos += 1;
-    st->step += 1;
+  bv = sv[0];
+  bi = si[0];
+  for (int j = 1; j < 4; j++) amax_merge(bv, bi, sv[j], si[j]);
+}
+
+__global__ __launch_bounds__(256) void k_argmax(const float *logits, int n, float *pv, int *pi,
+                                                int *count, DecodeState *st, int *tokens,
+                                                int max_tokens) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  __shared__ int last_s;
+  const int tid = threadIdx.x;
+  const int base = blockIdx.x * ARGMAX_SPAN;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < ARGMAX_SPAN / 256; i++) {
+    const int e = base + tid + 256 * i;  // increasing per thread: strict > keeps the first
+    if (e < n) {
+      const float x = logits[e];
+      if (x > bv) {
+        bv = x;
+        bi = e;
+      }
+    }
+  }
+  block_amax(bv, bi, sv, si);
+  if (tid == 0) {
+    pv[blockIdx.x] = bv;
+    pi[blockIdx.x] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    __threadfence();
+    const bool last = atomicAdd(count, 1) == (int)gridDim.x - 1;
+    if (last) __threadfence();
+    last_s = last;
+  }
+  __syncthreads();
+  if (!last_s) return;
+  bv = -INFINITY;
+  bi = 0x7fffffff;
+  for (int b = tid; b < (int)gridDim.x; b += 256) amax_merge(bv, bi, pv[b], pi[b]);
+  block_amax(bv, bi, sv, si);
+  if (tid == 0) {
+    const int idx = bi == 0x7fffffff ? 0 : bi;  // no logit above -inf: index 0
+    const int step = st->step;
+    if (tokens && step < max_tokens) tokens[step] = idx;
+    *st = DecodeState{idx, st->pos + 1, step + 1, 0};
+    *count = 0;
   }
 }
 
@@ -232,44 +405,63 @@ hipError_t launch_set_state(DecodeState *st, int token, int pos, hipStream_t s) 
 }
 
 hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
-  const int H = m.hidden, hd = m.head_dim, nh = m.n_heads, nkv = m.n_kv_heads;
-  const int kvd = nkv * hd;
-  hipLaunchKernelGGL(k_embed, dim3((H + 255) / 256), dim3(256), 0, s, m.embd, m.state, m.x, H);
+  const int hd = m.head_dim, nh = m.n_heads, nkv = m.n_kv_heads;
+  const int kvd = nkv * hd, group = nh / nkv;
+  hipError_t e;
   for (int L = 0; L < m.n_layers; L++) {
-    // attention block (the previous layer's FFN residual is added here)
-    hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, s, m.x, L ? m.proj : nullptr,
-                       m.attn_norm[L], m.xn, H, m.eps);
+    // x_b = x_a + proj (layer 0: the embedding row); q, k, v of RMSNorm(x_b)
+    MvIn in;
+    in.src = MV_NORM;
+    in.x = L ? m.xa : m.embd;
+    in.tok = L ? nullptr : &m.state->token;
+    in.r = L ? m.proj : nullptr;
+    in.nw = m.attn_norm[L];
+    in.xo = m.xb;
+    in.eps = m.eps;
     const gq_weight *qkv[3] = {m.wq[L], m.wk[L], m.wv[L]};
     float *qkv_out[3] = {m.q, m.k, m.v};
-    hipError_t e = matvec_launch(qkv, 3, m.xn, nullptr, nullptr, qkv_out, s);
-    if (e != hipSuccess) return e;
+    if ((e = matvec_launch(qkv, 3, in, qkv_out, s)) != hipSuccess) return e;
     uint16_t *kc = m.kcache + (long)L * m.ctx * kvd, *vc = m.vcache + (long)L * m.ctx * kvd;
-    hipLaunchKernelGGL(k_rope_kv, dim3(nh + nkv), dim3(hd / 2), 0, s, m.q, m.k, m.v, kc, vc,
-                       m.state, nh, nkv, hd, m.theta);
-    hipLaunchKernelGGL(k_attn_partial, dim3(nh, m.att_chunks), dim3(256), 0, s, m.q, kc, vc,
-                       m.state, nh, nh / nkv, hd, kvd, m.att_part);
-    hipLaunchKernelGGL(k_attn_combine, dim3(nh), dim3(hd), 0, s, m.att_part, m.att_chunks, hd,
-                       m.att);
+    if (hd == 128)
+      hipLaunchKernelGGL(k_attn_gqa<128>, dim3(nkv, m.att_chunks), dim3(ATT_THREADS), 0, s, m.q, m.k, m.v,
+                         kc, vc, m.state, group, kvd, m.theta, m.att_part, m.att_count, m.att);
+    else
+      hipLaunchKernelGGL(k_attn_gqa<64>, dim3(nkv, m.att_chunks), dim3(ATT_THREADS), 0, s, m.q, m.k, m.v,
+                         kc, vc, m.state, group, kvd, m.theta, m.att_part, m.att_count, m.att);
+    MvIn ain;
+    ain.x = m.att;
     const gq_weight *wo[1] = {m.wo[L]};
     float *proj[1] = {m.proj};
-    if ((e = matvec_launch(wo, 1, m.att, nullptr, nullptr, proj, s)) != hipSuccess) return e;
-    // FFN block
-    hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, s, m.x, m.proj, m.ffn_norm[L],
-                       m.xn, H, m.eps);
+    if ((e = matvec_launch(wo, 1, ain, proj, s)) != hipSuccess) return e;
+    // x_a = x_b + o; h = silu(gate . n) * (up . n), n = RMSNorm(x_a)
+    MvIn fin;
+    fin.src = MV_NORM;
+    fin.x = m.xb;
+    fin.r = m.proj;
+    fin.nw = m.ffn_norm[L];
+    fin.xo = m.xa;
+    fin.eps = m.eps;
     const gq_weight *gu[2] = {m.wgate[L], m.wup[L]};
-    float *gu_out[2] = {m.g, m.u};
-    if ((e = matvec_launch(gu, 2, m.xn, nullptr, nullptr, gu_out, s)) != hipSuccess) return e;
+    float *hout[2] = {m.h, nullptr};
+    if ((e = matvec_launch(gu, 2, fin, hout, s, true)) != hipSuccess) return e;
+    MvIn din;
+    din.x = m.h;
     const gq_weight *wd[1] = {m.wdown[L]};
-    if ((e = matvec_launch(wd, 1, nullptr, m.g, m.u, proj, s)) != hipSuccess) return e;
+    if ((e = matvec_launch(wd, 1, din, proj, s)) != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(1024), 0, s, m.x, m.proj, m.output_norm, m.xn,
-                     H, m.eps);
+  // logits of RMSNorm(x_a + proj)
+  MvIn hin;
+  hin.src = MV_NORM;
+  hin.x = m.xa;
+  hin.r = m.proj;
+  hin.nw = m.output_norm;
+  hin.eps = m.eps;
   const gq_weight *hw[1] = {m.lm_head};
   float *lo[1] = {m.logits};
-  hipError_t e = matvec_launch(hw, 1, m.xn, nullptr, nullptr, lo, s);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_argmax_next, dim3(1), dim3(1024), 0, s, m.logits, m.vocab, m.state,
-                     m.tokens, m.max_tokens);
+  if ((e = matvec_launch(hw, 1, hin, lo, s)) != hipSuccess) return e;
+  const int nb = (m.vocab + ARGMAX_SPAN - 1) / ARGMAX_SPAN;
+  hipLaunchKernelGGL(k_argmax, dim3(nb), dim3(256), 0, s, m.logits, m.vocab, m.amax_v, m.amax_i,
+                     m.amax_count, m.state, m.tokens, m.max_tokens);
   return hipGetLastError();
 }
 

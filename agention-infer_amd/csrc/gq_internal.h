@@ -29,13 +29,31 @@ struct MvSeg {
   int tile_begin;  // first global tile (= wave) of this segment
 };
 
+// Where the matvec input vector comes from.
+enum MvSource {
+  MV_X = 0,       // x
+  MV_SWIGLU = 1,  // silu(xg) * xu
+  MV_NORM = 2,    // RMSNorm(x + r) * nw; block 0 stores x + r to xo
+};
+
+struct MvIn {
+  int src = MV_X;
+  const float *x = nullptr;   // MV_X / MV_NORM residual stream
+  const float *xg = nullptr, *xu = nullptr;
+  const float *r = nullptr;   // MV_NORM: residual added to x (may be null)
+  const float *nw = nullptr;  // MV_NORM: norm weight
+  float *xo = nullptr;        // MV_NORM: x + r written here (may be null)
+  const int *tok = nullptr;   // MV_NORM: if set, x is row *tok of the table x
+  float eps = 0.f;
+};
+
 struct MvArgs {
-  const float *x;
-  const float *xg, *xu;  // if xu != nullptr, x = silu(xg) * xu (SwiGLU input)
+  MvIn in;
   const uint32_t *grid;  // IQ3_XXS codebook (device)
   int k, units, chunks;
   int part_floats;       // LDS floats per wave for per-unit partial sums
   int total_tiles;
+  int pair;              // 1: seg[0] = gate, seg[1] = up (same shape); y0 = silu(g) * u
   int nseg;
   MvSeg seg[MV_MAX_SEG];
 };
@@ -79,18 +97,26 @@ struct DecodeLaunch {
   const float *const *attn_norm, *const *ffn_norm;  // host arrays of device pointers
   const float *output_norm, *embd;
   uint16_t *kcache, *vcache;  // [layer][ctx][kv_dim] f16
-  float *x, *xn, *q, *k, *v, *att, *proj, *g, *u, *logits, *att_part;
+  float *xa, *xb;             // residual stream, ping-pong
+  float *q, *k, *v, *att, *proj, *h, *logits, *att_part;
+  float *amax_v;              // per-block argmax partials
+  int *amax_i;
+  int *att_count;             // [n_kv_heads] chunk counters (zero between launches)
+  int *amax_count;            // argmax block counter (zero between launches)
   DecodeState *state;
   int *tokens;                // [max_tokens] generated tokens
 };
 
 hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s);
+constexpr int ATT_CHUNK = 256;   // positions per attention block
+constexpr int ARGMAX_SPAN = 4096;  // logits per argmax block
 hipError_t launch_set_state(DecodeState *st, int token, int pos, hipStream_t s);
 
-// Host-side launch of y_i = W_i . x (or silu(xg) * xu when xu != nullptr)
-// for weights sharing dtype and in_dim; no argument checks.
-hipError_t matvec_launch(const gq_weight *const *ws, int count, const float *x, const float *xg,
-                         const float *xu, float *const *ys, hipStream_t st);
+// Host-side launch of y_i = W_i . in for weights sharing dtype and in_dim;
+// no argument checks.  With pair, ws = {gate, up} and ys[0] receives
+// silu(gate . in) * (up . in).
+hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, float *const *ys,
+                         hipStream_t st, bool pair = false);
 const uint32_t *device_grid();
 
 // Rows per tile for a matrix (chosen at upload).

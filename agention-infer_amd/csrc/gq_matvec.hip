@@ -43,6 +43,7 @@ struct Smem {
   float2 *aux;            // AUX_STRIDE bytes per unit
   uint32_t *grid;         // IQ3_XXS codebook
   float *part;            // per-wave per-unit partial sums
+  float *red;             // 16 floats of block reduction scratch
 };
 
 __host__ __device__ inline size_t smem_layout(int units, int part_floats, Smem *s, char *base) {
@@ -52,7 +53,9 @@ __host__ __device__ inline size_t smem_layout(int units, int part_floats, Smem *
   const size_t o2 = take(limb), o1 = take(limb), o0 = take(limb);
   const size_t oaux = take((size_t)units * AUX_STRIDE), og = take(1024);
   const size_t op = take((size_t)4 * part_floats * 4);
+  const size_t ored = take(64);
   if (s) {
+    s->red = (float *)(base + ored);
     s->l2 = (uint8_t *)(base + o2);
     s->l1 = (uint8_t *)(base + o1);
     s->l0 = (uint8_t *)(base + o0);
@@ -327,45 +330,115 @@ __device__ __forceinline__ float unit_dot(const Unit<FMT> &U, int u, const Smem 
   else return unit_iq3(U.ch, U.d, u, S);
 }
 
-// One wave's job: tile t (RT rows) of one weight matrix.
+// x sources.  issue() starts the loads of 16 consecutive input values
+// (zero past k) into a Raw record, make() turns a Raw record into the 16
+// values to stage; pre_barrier()/scale() give a factor applied to every
+// row sum (1 except for the normalised source).
+template <bool K4>
+struct XPlain {
+  const float *x;
+  int k;
+  struct Raw { float v[16]; };
+  __device__ __forceinline__ void issue(int e0, Raw &r) const { load_x16<K4>(x, k, e0, r.v); }
+  __device__ __forceinline__ void make(const Raw &r, int, float (&xv)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) xv[i] = r.v[i];
+  }
+  __device__ __forceinline__ void pre_barrier(float *) const {}
+  __device__ __forceinline__ float scale(const float *) const { return 1.f; }
+};
+
+// silu(g) * u of the gate/up outputs (the SwiGLU of ffn_gate_up,
+// src/model/llama/cpu_path.rs:225-227); zero past k since silu(0) * 0 = 0.
+template <bool K4>
+struct XSwiGLU {
+  const float *g, *u;
+  int k;
+  struct Raw { float g[16], u[16]; };
+  __device__ __forceinline__ void issue(int e0, Raw &r) const {
+    load_x16<K4>(g, k, e0, r.g);
+    load_x16<K4>(u, k, e0, r.u);
+  }
+  __device__ __forceinline__ void make(const Raw &r, int, float (&xv)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) xv[i] = r.g[i] / (1.0f + expf(-r.g[i])) * r.u[i];
+  }
+  __device__ __forceinline__ void pre_barrier(float *) const {}
+  __device__ __forceinline__ float scale(const float *) const { return 1.f; }
+};
+
+// RMSNorm of the residual stream (rms_norm_into, cpu_path.rs:67-74) with the
+// residual add in front (x += proj, cpu_path.rs:780-782 and 806-808):
+// v = x + r, the staged input is nw * v, and since every row sum is linear
+// in the input, 1 / rms(v) multiplies the row sums instead of the inputs.
+// xo (block 0 only) receives v, the new residual stream.
+template <bool K4>
+struct XNorm {
+  const float *x, *r, *nw;
+  float *xo;
+  int k;
+  float eps;
+  float ss = 0.f;
+  struct Raw { float x[16], r[16], w[16]; };
+  __device__ __forceinline__ void issue(int e0, Raw &q) const {
+    load_x16<K4>(x, k, e0, q.x);
+    if (r) load_x16<K4>(r, k, e0, q.r);
+    load_x16<K4>(nw, k, e0, q.w);
+  }
+  __device__ __forceinline__ void make(const Raw &q, int e0, float (&xv)[16]) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      v[i] = r ? q.x[i] + q.r[i] : q.x[i];
+      ss += v[i] * v[i];
+      xv[i] = q.w[i] * v[i];
+    }
+    if (xo) {
+      if (K4) {
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          if (e0 + 4 * j < k)
+            *(float4 *)(xo + e0 + 4 * j) = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++)
+          if (e0 + i < k) xo[e0 + i] = v[i];
+      }
+    }
+  }
+  __device__ __forceinline__ void pre_barrier(float *red) const {
+    float t = ss;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off, 64);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
+  }
+  __device__ __forceinline__ float scale(const float *red) const {
+    const float t = (red[0] + red[1]) + (red[2] + red[3]);
+    return 1.0f / sqrtf(t / (float)k + eps);
+  }
+};
+
+// One wave's work: tile t of a matrix (and with NT = 2 the same tile of a
+// second matrix of the same shape, body2 / d2).
 struct WaveJob {
   const uint8_t *body;
   const uint16_t *d;
+  const uint8_t *body2;
+  const uint16_t *d2;
   float *y;
   int rows, rt, t;
   bool valid;
 };
 
-// x sources: load 16 consecutive x values (zero past k) for staging.
-template <bool K4>
-struct XPlain {
-  const float *x;
-  int k;
-  __device__ __forceinline__ void load(int e0, float (&xv)[16]) const { load_x16<K4>(x, k, e0, xv); }
-};
-
-// MoE down projection input: silu(g) * u of the gate/up outputs
-// (the SwiGLU of ffn_gate_up, src/model/llama/cpu_path.rs:225-227).
-struct XSwiGLU {
-  const float *g, *u;
-  int k;
-  __device__ __forceinline__ void load(int e0, float (&xv)[16]) const {
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const int e = min(e0 + i, k - 1);
-      const float gv = g[e], uv = u[e];
-      const float sv = gv / (1.0f + expf(-gv)) * uv;
-      xv[i] = e0 + i < k ? sv : 0.f;
-    }
-  }
-};
-
 // The body shared by every matvec kernel: stage x (limbs) in LDS, stream
-// the job's tile with two units in flight per lane, reduce rows.  All four
-// waves of the block must share the x source (they share the staging).
-template <int FMT, class XS>
+// the job's tile(s) with two units in flight per lane, reduce rows.  All
+// four waves of the block must share the x source (they share the
+// staging).  The raw loads of the first NP passes of 4096 inputs are
+// issued together, before the first weight unit; later passes follow one
+// by one.
+template <int FMT, int NP, int NT, class XS>
 __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_floats,
-                                            const uint32_t *gsrc, const XS &xsrc, char *smem_raw) {
+                                            const uint32_t *gsrc, XS &xsrc, char *smem_raw) {
   Smem S;
   smem_layout(U, part_floats, &S, smem_raw);
   constexpr int C = Fmt<FMT>::C;
@@ -375,21 +448,25 @@ __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_
   const int uit = rows_here * U;
   const int iters = (uit + 63) >> 6;
   const int nv_last = uit - 64 * (iters - 1);
+  const int total_it = NT * iters;
   const long tile_base = (long)t * job.rt * U * C * 16;
   const long dbase = (long)t * job.rt * U;
-  auto unit_ptr = [&](int it, long &cstride, const uint16_t *&dp) -> const uint8_t * {
+  auto unit_ptr = [&](int itg, long &cstride, const uint16_t *&dp) -> const uint8_t * {
+    const bool second = NT == 2 && itg >= iters;
+    const int it = second ? itg - iters : itg;
     const bool last = it == iters - 1;
     const int l = last ? min(lane, nv_last - 1) : lane;
     cstride = last ? 16L * nv_last : 1024L;
-    dp = job.d + dbase + 64 * it + l;
-    return job.body + tile_base + (long)it * C * 1024 + 16 * l;
+    dp = (second ? job.d2 : job.d) + dbase + 64 * it + l;
+    return (second ? job.body2 : job.body) + tile_base + (long)it * C * 1024 + 16 * l;
   };
 
-  // x of the first pass, then the first weight unit, then the LDS stores:
-  // the wait before the stores leaves the weight loads in flight.
   const int kpad = U * 256;
-  float xv[16];
-  xsrc.load(16 * tid, xv);
+  const int passes = (kpad + 4095) >> 12;
+  typename XS::Raw raw[NP];
+#pragma unroll
+  for (int p = 0; p < NP; p++)
+    if (p < passes) xsrc.issue(4096 * p + 16 * tid, raw[p]);
   uint32_t gword = 0;
   if constexpr (FMT == T_IQ3_XXS) gword = gsrc[tid];
   __builtin_amdgcn_sched_barrier(0);
@@ -401,36 +478,50 @@ __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_
     load_unit<FMT>(A, p, cs, dp);
   }
   __builtin_amdgcn_sched_barrier(0);
-  stage_x<FMT == T_Q6_K>(kpad, 0, xv, S);
-  for (int p = 1; 4096 * p < kpad; p++) {
-    xsrc.load(4096 * p + 16 * tid, xv);
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    if (p < passes) {
+      float xv[16];
+      xsrc.make(raw[p], 4096 * p + 16 * tid, xv);
+      stage_x<FMT == T_Q6_K>(kpad, p, xv, S);
+    }
+  }
+  for (int p = NP; p < passes; p++) {
+    typename XS::Raw r1;
+    xsrc.issue(4096 * p + 16 * tid, r1);
+    float xv[16];
+    xsrc.make(r1, 4096 * p + 16 * tid, xv);
     stage_x<FMT == T_Q6_K>(kpad, p, xv, S);
   }
   if constexpr (FMT == T_IQ3_XXS) S.grid[tid] = gword;
+  xsrc.pre_barrier(S.red);
   __syncthreads();
+  const float rscale = xsrc.scale(S.red);
 
   float *part = S.part + wave * part_floats;
-  auto load_it = [&](Unit<FMT> &dst, int it) {
+  auto load_it = [&](Unit<FMT> &dst, int itg) {
     long cs;
     const uint16_t *dp;
-    const uint8_t *p = unit_ptr(it, cs, dp);
+    const uint8_t *p = unit_ptr(itg, cs, dp);
     load_unit<FMT>(dst, p, cs, dp);
   };
-  auto consume = [&](const Unit<FMT> &src, int it) {
+  auto consume = [&](const Unit<FMT> &src, int itg) {
+    const bool second = NT == 2 && itg >= iters;
+    const int it = second ? itg - iters : itg;
     const int j = 64 * it + lane;
     const float v = unit_dot<FMT>(src, j % U, S);
-    if (j < uit) part[j] = v;
+    if (j < uit) part[(second ? 64 * iters : 0) + j] = v;
   };
   // Steady state: two units in flight per lane; the tail is peeled so that
   // no unit is ever loaded twice.
   int it = 0;
-  for (; it + 2 < iters; it += 2) {
+  for (; it + 2 < total_it; it += 2) {
     load_it(B, it + 1);
     consume(A, it);
     load_it(A, it + 2);
     consume(B, it + 1);
   }
-  if (it + 1 < iters) {
+  if (it + 1 < total_it) {
     load_it(B, it + 1);
     consume(A, it);
     consume(B, it + 1);
@@ -442,15 +533,27 @@ __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_
   // Row sums: 64/RT lanes per row, fixed order.
   const int lpr = 64 / job.rt;
   const int row = lane / lpr, sub = lane % lpr;
-  float v = 0.f;
-  if (row < rows_here)
-    for (int c = sub; c < U; c += lpr) v += part[row * U + c];
-  for (int off = lpr >> 1; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  if (job.valid && sub == 0 && row < rows_here) job.y[t * job.rt + row] = v;
+  float v[NT];
+#pragma unroll
+  for (int m = 0; m < NT; m++) {
+    const float *pm = part + m * 64 * iters;
+    float acc = 0.f;
+    if (row < rows_here)
+      for (int c = sub; c < U; c += lpr) acc += pm[row * U + c];
+    for (int off = lpr >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    v[m] = acc * rscale;
+  }
+  if (job.valid && sub == 0 && row < rows_here) {
+    float out = v[0];
+    if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
+    job.y[t * job.rt + row] = out;
+  }
 }
 
-// Plain / multi-segment matvec: one wave per tile over the segments.
-template <int FMT, bool K4, bool SW>
+// Plain / multi-segment matvec: one wave per tile over the segments.  With
+// NT = 2 (gate/up pair) there is one segment of tiles and seg[1] supplies
+// the second matrix.
+template <int FMT, bool K4, int SRC, int NP, int NT>
 __global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
   extern __shared__ __align__(16) char smem_raw[];
   const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -458,14 +561,24 @@ __global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
   const int gwc = valid ? gw : a.total_tiles - 1;
   // Segment of this wave (wave-uniform selects over scalar arguments).
   MvSeg sg = a.seg[0];
+  if constexpr (NT == 1) {
 #pragma unroll
-  for (int i = 1; i < MV_MAX_SEG; i++)
-    if (i < a.nseg && gwc >= a.seg[i].tile_begin) sg = a.seg[i];
-  const WaveJob job{sg.body, sg.d, sg.y, sg.rows, sg.rt, gwc - sg.tile_begin, valid};
-  if constexpr (SW)
-    matvec_wave<FMT>(job, a.units, a.part_floats, a.grid, XSwiGLU{a.xg, a.xu, a.k}, smem_raw);
-  else
-    matvec_wave<FMT>(job, a.units, a.part_floats, a.grid, XPlain<K4>{a.x, a.k}, smem_raw);
+    for (int i = 1; i < MV_MAX_SEG; i++)
+      if (i < a.nseg && gwc >= a.seg[i].tile_begin) sg = a.seg[i];
+  }
+  const WaveJob job{sg.body, sg.d, a.seg[1].body, a.seg[1].d, sg.y, sg.rows, sg.rt,
+                    gwc - sg.tile_begin, valid};
+  if constexpr (SRC == MV_NORM) {
+    const float *x = a.in.tok ? a.in.x + (long)(*a.in.tok) * a.k : a.in.x;
+    XNorm<K4> xs{x, a.in.r, a.in.nw, blockIdx.x == 0 ? a.in.xo : nullptr, a.k, a.in.eps};
+    matvec_wave<FMT, NP, NT>(job, a.units, a.part_floats, a.grid, xs, smem_raw);
+  } else if constexpr (SRC == MV_SWIGLU) {
+    XSwiGLU<K4> xs{a.in.xg, a.in.xu, a.k};
+    matvec_wave<FMT, NP, NT>(job, a.units, a.part_floats, a.grid, xs, smem_raw);
+  } else {
+    XPlain<K4> xs{a.in.x, a.k};
+    matvec_wave<FMT, NP, NT>(job, a.units, a.part_floats, a.grid, xs, smem_raw);
+  }
 }
 
 // ------------------------------------------------------------------- MoE
@@ -484,15 +597,15 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(MoeArgs a) {
   const int gwc = valid ? gw : 2 * tiles - 1;
   const bool is_up = gwc >= tiles;
   const int lt = is_up ? gwc - tiles : gwc;
-  const WaveJob job{is_up ? a.up : a.gate, is_up ? a.up_d : a.gate_d,
+  const WaveJob job{is_up ? a.up : a.gate, is_up ? a.up_d : a.gate_d, nullptr, nullptr,
                     (is_up ? a.tmp_u : a.tmp_g) + (long)p * a.f - (long)e * a.f,
                     a.n_experts * a.f, a.rt_h, e * tiles + lt, valid};
-  matvec_wave<FMT>(job, a.units_h, a.part_h, a.grid, XPlain<K4>{a.x + (long)tok * a.h, a.h},
-                   smem_raw);
+  XPlain<K4> xs{a.x + (long)tok * a.h, a.h};
+  matvec_wave<FMT, 1, 1>(job, a.units_h, a.part_h, a.grid, xs, smem_raw);
 }
 
 // Stage 2: down_e . (silu(g) * u) for every pair.
-template <int FMT>
+template <int FMT, bool K4>
 __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
   extern __shared__ __align__(16) char smem_raw[];
   const int p = blockIdx.y;
@@ -501,10 +614,10 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
   const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
   const bool valid = gw < tiles;
   const int gwc = valid ? gw : tiles - 1;
-  const WaveJob job{a.down, a.down_d, a.tmp_y + (long)p * a.h - (long)e * a.h,
+  const WaveJob job{a.down, a.down_d, nullptr, nullptr, a.tmp_y + (long)p * a.h - (long)e * a.h,
                     a.n_experts * a.h, a.rt_f, e * tiles + gwc, valid};
-  matvec_wave<FMT>(job, a.units_f, a.part_f, a.grid,
-                   XSwiGLU{a.tmp_g + (long)p * a.f, a.tmp_u + (long)p * a.f, a.f}, smem_raw);
+  XSwiGLU<K4> xs{a.tmp_g + (long)p * a.f, a.tmp_u + (long)p * a.f, a.f};
+  matvec_wave<FMT, 1, 1>(job, a.units_f, a.part_f, a.grid, xs, smem_raw);
 }
 
 // Router: per token, top-k of the logits (ties: lower index) and their
@@ -590,21 +703,39 @@ int choose_rt(int dtype, int rows, int units) {
   return best;
 }
 
-template <int FMT, bool K4, bool SW>
+template <int FMT, bool K4, int SRC, int NP, int NT>
 static hipError_t launch_t(const MvArgs &a, hipStream_t st) {
   const size_t lds = matvec_lds_bytes(FMT, a.units, a.part_floats);
   if (lds > 64 * 1024)
-    (void)hipFuncSetAttribute((const void *)k_matvec<FMT, K4, SW>,
+    (void)hipFuncSetAttribute((const void *)k_matvec<FMT, K4, SRC, NP, NT>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   const int blocks = (a.total_tiles + 3) / 4;
-  hipLaunchKernelGGL((k_matvec<FMT, K4, SW>), dim3(blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_matvec<FMT, K4, SRC, NP, NT>), dim3(blocks), dim3(256), lds, st, a);
   return hipGetLastError();
 }
 
+// Instances: plain x with 1, 4 or 8 staging passes in flight together;
+// the normalised source (k % 4 == 0, one pass in flight) alone or for a
+// gate/up pair; the SwiGLU source with one pass in flight.
 template <int FMT>
 static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
-  if (a.xu) return launch_t<FMT, false, true>(a, st);
-  return a.k % 4 == 0 ? launch_t<FMT, true, false>(a, st) : launch_t<FMT, false, false>(a, st);
+  const int passes = (a.units + 15) / 16;
+  const bool k4 = a.k % 4 == 0;
+  switch (a.in.src) {
+  case MV_NORM:
+    if (!k4) return hipErrorInvalidValue;
+    return a.pair ? launch_t<FMT, true, MV_NORM, 1, 2>(a, st) : launch_t<FMT, true, MV_NORM, 1, 1>(a, st);
+  case MV_SWIGLU:
+    if (a.pair) return hipErrorInvalidValue;
+    return k4 ? launch_t<FMT, true, MV_SWIGLU, 1, 1>(a, st) : launch_t<FMT, false, MV_SWIGLU, 1, 1>(a, st);
+  default:
+    if (a.pair) return hipErrorInvalidValue;
+    if (passes == 1)
+      return k4 ? launch_t<FMT, true, MV_X, 1, 1>(a, st) : launch_t<FMT, false, MV_X, 1, 1>(a, st);
+    if (passes <= 4)
+      return k4 ? launch_t<FMT, true, MV_X, 4, 1>(a, st) : launch_t<FMT, false, MV_X, 4, 1>(a, st);
+    return k4 ? launch_t<FMT, true, MV_X, 8, 1>(a, st) : launch_t<FMT, false, MV_X, 8, 1>(a, st);
+  }
 }
 
 hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st) {
@@ -623,7 +754,10 @@ hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st) {
       hipLaunchKernelGGL((k_moe_gate_up<F, true>), g1, dim3(256), lds1, st, a);              \
     else                                                                                     \
       hipLaunchKernelGGL((k_moe_gate_up<F, false>), g1, dim3(256), lds1, st, a);             \
-    hipLaunchKernelGGL((k_moe_down<F>), g2, dim3(256), lds2, st, a);                         \
+    if (a.f % 4 == 0)                                                                        \
+      hipLaunchKernelGGL((k_moe_down<F, true>), g2, dim3(256), lds2, st, a);                 \
+    else                                                                                     \
+      hipLaunchKernelGGL((k_moe_down<F, false>), g2, dim3(256), lds2, st, a);                \
   }
   GQ_MOE_LAUNCH(T_IQ3_XXS)
   GQ_MOE_LAUNCH(T_Q4_K)
