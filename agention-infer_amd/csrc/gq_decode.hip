@@ -76,7 +76,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   __shared__ __align__(16) uint16_t vnew[HD];
   __shared__ float qmax_s[NW];
   __shared__ int last_s;
-  static_assert(sizeof(ored) >= 2 * sizeof(float) * ATT_MAXG * ATT_MAXCH, "merge factors fit");
+  static_assert(sizeof(ored) >= sizeof(float) * ATT_MAXG * ATT_MAXCH, "merge factors fit");
 
   const int kh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -215,33 +215,37 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
 
   // Values: lane owns dims DPL*lane .. +DPL of the wave's PW rows.
   {
-    float acc[ATT_MAXG][DPL];
-#pragma unroll
-    for (int g = 0; g < ATT_MAXG; g++)
-#pragma unroll
-      for (int e = 0; e < DPL; e++) acc[g][e] = 0.f;
     const uint32_t vn = DPL == 2 ? *(const uint32_t *)(vnew + DPL * lane) : (uint32_t)vnew[lane];
+    float vf[PW][DPL];
 #pragma unroll
     for (int j = 0; j < PW; j++) {
-      const int tl = wave * PW + j;
-      const uint32_t raw = t0 + tl == pos ? vn : vr[j];
-      float vf[DPL];
+      const uint32_t raw = tw + j == pos ? vn : vr[j];
 #pragma unroll
-      for (int e = 0; e < DPL; e++) vf[e] = h2f(raw >> (16 * e));
-#pragma unroll
-      for (int g = 0; g < ATT_MAXG; g++) {
-        if (g < group) {
-          const float p = sp[g][tl];
-#pragma unroll
-          for (int e = 0; e < DPL; e++) acc[g][e] += p * vf[e];
-        }
-      }
+      for (int e = 0; e < DPL; e++) vf[j][e] = h2f(raw >> (16 * e));
     }
 #pragma unroll
-    for (int g = 0; g < ATT_MAXG; g++)
-      if (g < group)
+    for (int g = 0; g < ATT_MAXG; g++) {
+      if (g < group) {
+        float pr[PW];
 #pragma unroll
-        for (int e = 0; e < DPL; e++) ored[wave][g][DPL * lane + e] = acc[g][e];
+        for (int j = 0; j < PW; j += 4) {
+          const float4 p4 = *(const float4 *)&sp[g][wave * PW + j];
+          pr[j] = p4.x;
+          pr[j + 1] = p4.y;
+          pr[j + 2] = p4.z;
+          pr[j + 3] = p4.w;
+        }
+        float acc[DPL];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+#pragma unroll
+        for (int j = 0; j < PW; j++)
+#pragma unroll
+          for (int e = 0; e < DPL; e++) acc[e] += pr[j] * vf[j][e];
+#pragma unroll
+        for (int e = 0; e < DPL; e++) ored[wave][g][DPL * lane + e] = acc[e];
+      }
+    }
   }
   __syncthreads();
   for (int o = tid; o < group * HD; o += ATT_THREADS) {
@@ -272,31 +276,31 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   __syncthreads();
   if (!last_s) return;
   float (*fac)[ATT_MAXCH] = (float (*)[ATT_MAXCH])&ored[0][0][0];
-  float (*fl)[ATT_MAXCH] = fac + ATT_MAXG;
-  const int nch16 = (nch + 15) & ~15;
-  for (int i = tid; i < group * nch16; i += ATT_THREADS) {
-    const int g = i / nch16, cc = i % nch16;
-    float m = -INFINITY, l = 0.f;
-    if (cc < nch) {
-      const float *pm = part + ((long)(kh * group + g) * nchunk_grid + cc) * (2 + HD);
-      m = pm[0];
-      l = pm[1];
-    }
-    fac[g][cc] = m;
-    fl[g][cc] = l;
-  }
-  __syncthreads();
-  if (tid < group) {  // fac[g][c] = e^(m_c - M) / L (0 for c >= nch)
+  // fac[g][c] = e^(m_c - M) / L, wave g for head g (0 for c >= nch).
+  if (wave < group) {
+    const float *pm = part + (long)(kh * group + wave) * nchunk_grid * (2 + HD);
+    float m[ATT_MAXCH / 64], l[ATT_MAXCH / 64];
     float M = -INFINITY;
-    for (int cc = 0; cc < nch; cc++) M = fmaxf(M, fac[tid][cc]);
-    float L = 0.f;
-    for (int cc = 0; cc < nch; cc++) {
-      const float e = expf(fac[tid][cc] - M);
-      fac[tid][cc] = e;
-      L += fl[tid][cc] * e;
+#pragma unroll
+    for (int i = 0; i < ATT_MAXCH / 64; i++) {
+      const int cc = lane + 64 * i;
+      m[i] = cc < nch ? pm[(long)cc * (2 + HD)] : -INFINITY;
+      l[i] = cc < nch ? pm[(long)cc * (2 + HD) + 1] : 0.f;
+      M = fmaxf(M, m[i]);
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
+    float L = 0.f;
+#pragma unroll
+    for (int i = 0; i < ATT_MAXCH / 64; i++) {
+      m[i] = lane + 64 * i < nch ? expf(m[i] - M) : 0.f;
+      L += l[i] * m[i];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
     const float inv = 1.0f / L;
-    for (int cc = 0; cc < nch16; cc++) fac[tid][cc] = cc < nch ? fac[tid][cc] * inv : 0.f;
+#pragma unroll
+    for (int i = 0; i < ATT_MAXCH / 64; i++) fac[wave][lane + 64 * i] = m[i] * inv;
   }
   __syncthreads();
   for (int o = tid; o < group * HD; o += ATT_THREADS) {

@@ -301,6 +301,7 @@ __device__ __forceinline__ void load_x16(const float *x, int k, int e0, float (&
 
 // ------------------------------------------------------------- kernel
 template <int FMT> struct Fmt;
+// C: 16-byte chunks per unit.
 template <> struct Fmt<T_Q4_K> { static constexpr int C = 9; static constexpr bool HAS_D = false; };
 template <> struct Fmt<T_Q5_K> { static constexpr int C = 11; static constexpr bool HAS_D = false; };
 template <> struct Fmt<T_Q6_K> { static constexpr int C = 13; static constexpr bool HAS_D = true; };
@@ -431,11 +432,13 @@ struct WaveJob {
 };
 
 // The body shared by every matvec kernel: stage x (limbs) in LDS, stream
-// the job's tile(s) with two units in flight per lane, reduce rows.  All
+// the job's tile(s) with two units per lane in flight, reduce rows.  All
 // four waves of the block must share the x source (they share the
 // staging).  The raw loads of the first NP passes of 4096 inputs are
-// issued together, before the first weight unit; later passes follow one
-// by one.
+// issued together, then the first weight unit, which stays in flight
+// while x is converted; later passes follow one by one.  (Issuing more
+// weight units before the staging keeps more registers live through it
+// and costs more in occupancy than it gains.)
 template <int FMT, int NP, int NT, class XS>
 __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_floats,
                                             const uint32_t *gsrc, XS &xsrc, char *smem_raw) {
