@@ -74,6 +74,142 @@ def cpu_baseline(mats, host, xs, nthreads, budget_s=15.0):
                       f"through oracle matmul_into, {el:.1f} s"}
 
 
+DECODE_PREFILL, DECODE_STEPS = 4096, 128
+MFMA_PEAK_TFLOPS = {"bf16": 2500.0, "int8": 5000.0}  # dense, no sparsity
+
+
+def _timed(torch, fn, reps):
+    """Average ms of fn() over reps runs, events on the current stream."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def gemm_leg(be, gq, syn, torch, cpu):
+    """Q4_K 18944x3584 weights times 512 tokens of
+    3584 activations, bf16 dequant-to-LDS MFMA and per-32 Q8 int8 MFMA."""
+    rows, k, n = FFN, HID, 512
+    w = syn.make_blocks(Q4_K, rows, k, seed=31)
+    h = be.upload_weight(Q4_K, w, k, rows)
+    X = torch.from_numpy(syn.make_x(k, seed=32, batch=n)).cuda()
+    Y = torch.empty(n, rows, device="cuda")
+    flops = 2.0 * rows * k * n
+    out = {"shape": f"W {rows}x{k} Q4_K, X {n}x{k}", "flop": flops}
+    for mode, name in ((gq.GQ_GEMM_BF16, "bf16"), (gq.GQ_GEMM_INT8, "int8")):
+        for _ in range(3):
+            h.launch_only_batch(X, mode=mode, Y_dev=Y)
+        torch.cuda.synchronize()
+        ms = _timed(torch, lambda: h.launch_only_batch(X, mode=mode, Y_dev=Y), 20)
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                     "peak": MFMA_PEAK_TFLOPS[name], "frac": round(tf / MFMA_PEAK_TFLOPS[name], 4)}
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        nthreads = min(len(os.sched_getaffinity(0)), 16)
+        xs = X[:32].cpu().numpy()
+        t0 = time.perf_counter()
+        oracle.matmul_batch_into(Q4_K, w, xs, rows, nthreads)
+        el = time.perf_counter() - t0
+        out["cpu_gflops"] = round(2.0 * rows * k * 32 / el / 1e9, 2)
+        out["cpu_sample"] = f"oracle matmul_batch_into, 32 of the 512 tokens, {nthreads} threads"
+    return out
+
+
+def moe_leg(be, gq, syn, torch, cpu):
+    """256 IQ3_XXS experts (gate/up 1536x3072, down
+    3072x1536), top-8 routing from N(0,1) logits, T = 1, 4, 16 tokens.
+    GB/s counts the weight bytes of the distinct experts a call touches."""
+    E, H, F, K = 256, 3072, 1536, 8
+    IQ3 = 18
+    gw = syn.make_blocks(IQ3, E * F, H, seed=41)
+    uw = syn.make_blocks(IQ3, E * F, H, seed=42)
+    dw = syn.make_blocks(IQ3, E * H, F, seed=43)
+    g = be.upload_experts(IQ3, gw, H, F, E)
+    u = be.upload_experts(IQ3, uw, H, F, E)
+    d = be.upload_experts(IQ3, dw, F, H, E)
+    per_expert = 2 * gq.type_size(IQ3, H) * F + gq.type_size(IQ3, F) * H
+    out = {"shape": f"{E} experts, h {H}, f {F}, top-{K}", "per_expert_bytes": per_expert}
+    for T in (1, 4, 16):
+        lg = torch.from_numpy(syn.make_x(E, seed=50 + T, batch=T)).cuda()
+        x = torch.from_numpy(syn.make_x(H, seed=60 + T, batch=T)).cuda()
+        y, ids, _ = be.moe_ffn(g, u, d, E, lg, x, K, want_routing=True)
+        uniq = len(set(ids.cpu().numpy().reshape(-1).tolist()))
+        torch.cuda.synchronize()
+        ms = _timed(torch, lambda: be.moe_ffn(g, u, d, E, lg, x, K, out_dev=y), 20)
+        out[f"T{T}"] = {"us": round(ms * 1e3, 1), "unique_experts": uniq,
+                        "GB/s": round(uniq * per_expert / (ms * 1e-3) / 1e9, 1)}
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        nthreads = min(len(os.sched_getaffinity(0)), 16)
+        lg1 = syn.make_x(E, seed=51, batch=1)
+        x1 = syn.make_x(H, seed=61, batch=1)
+        ids, wts = oracle.moe_route(lg1, K)
+        t0 = time.perf_counter()
+        reps = 5
+        for _ in range(reps):
+            oracle.moe_ffn(IQ3, gw, uw, dw, E, H, F, x1, ids, wts, nthreads)
+        el = (time.perf_counter() - t0) / reps
+        out["cpu_T1_us"] = round(el * 1e6, 1)
+        out["cpu_sample"] = f"oracle moe_ffn, T=1, {reps} calls, {nthreads} threads"
+    return out
+
+
+def decode_leg(be, gq, syn, torch, cpu_steps):
+    """GPU-resident 7B-shape Q4_K_M decode (28 layers,
+    f16 KV prefilled to 4096 positions, 128 greedy steps, one HIP graph
+    replay per step).  Returns the figures and the oracle's host-side
+    decode rate on a bounded sample (cpu_steps steps, same model)."""
+    cfg = dict(syn.QWEN25_7B, ctx=DECODE_PREFILL + DECODE_STEPS + 16)
+    w = syn.make_decoder(cfg, seed=11)
+    kv = syn.make_kv(cfg, DECODE_PREFILL, seed=12)
+    hw = syn.upload_decoder(be, cfg, w)
+    m = gq.DecodeModel(dict(cfg, max_tokens=DECODE_STEPS), hw)
+    for layer in range(cfg["n_layers"]):
+        m.kv_upload(layer, kv[0][layer], kv[1][layer])
+    stream = torch.cuda.current_stream()
+    m.generate(1234, DECODE_PREFILL, 8, stream=stream.cuda_stream)  # capture + warm
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    m.generate(1234, DECODE_PREFILL, DECODE_STEPS, stream=stream.cuda_stream)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_tok = e0.elapsed_time(e1) / DECODE_STEPS
+    tokens = m.generate(1234, DECODE_PREFILL, DECODE_STEPS, stream=stream.cuda_stream)
+    wbytes = sum(gq_w.nbytes() for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
+                 for gq_w in hw[k]) + hw["lm_head"].nbytes()
+    kv_bytes = 2 * cfg["n_layers"] * (DECODE_PREFILL + DECODE_STEPS // 2) * \
+        cfg["n_kv_heads"] * cfg["head_dim"] * 2
+    step_bytes = wbytes + kv_bytes
+    out = {"tok_s": round(1e3 / ms_tok, 1), "ms_per_token": round(ms_tok, 4),
+           "steps": DECODE_STEPS, "prefill_positions": DECODE_PREFILL,
+           "hbm_GB_s": round(step_bytes / (ms_tok * 1e-3) / 1e9, 1),
+           "bytes_per_step": step_bytes,
+           "first_tokens": [int(t) for t in tokens[:4]],
+           "model": "Qwen2.5-7B-shaped Q4_K_M (random init), 28 layers, hidden 3584, "
+                    "28/4 heads, ffn 18944, vocab 152064"}
+    if cpu_steps > 0:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        om = oracle.DecoderModel(cfg, w, kv)
+        om.step(1234, DECODE_PREFILL)  # warm
+        t0 = time.perf_counter()
+        tok = 1234
+        for i in range(cpu_steps):
+            tok = oracle.argmax(om.step(tok, DECODE_PREFILL + i))
+        el = time.perf_counter() - t0
+        out["cpu_tok_s"] = round(cpu_steps / el, 3)
+        out["cpu_sample"] = f"{cpu_steps} oracle decode steps (gqo_decode_step, all host threads)"
+    del m
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -81,6 +217,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-decode", action="store_true", help="skip the 7B decode leg")
+    ap.add_argument("--only", choices=["decode", "gemm", "moe"],
+                    help="run only this leg and print its figures (for profiling)")
+    ap.add_argument("--cpu-decode-steps", type=int, default=3)
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
@@ -97,6 +237,14 @@ def main():
 
     be = gq.create_backend("hip", 0)
     stream = torch.cuda.current_stream()
+    if args.only == "decode":
+        print(json.dumps({"decode": decode_leg(be, gq, syn, torch, 0 if args.no_cpu else
+                                               args.cpu_decode_steps)}), flush=True)
+        return
+    if args.only in ("gemm", "moe"):
+        leg = gemm_leg if args.only == "gemm" else moe_leg
+        print(json.dumps({args.only: leg(be, gq, syn, torch, not args.no_cpu)}), flush=True)
+        return
 
     host, xs, mats, copies = {}, {}, [], {}
     for i, (name, dtype, out_dim, in_dim) in enumerate(MATS):
@@ -219,6 +367,12 @@ def main():
     if not args.no_cpu:
         nthreads = min(len(os.sched_getaffinity(0)), 16)
         out["cpu_baseline"] = cpu_baseline(mats, host, xs, nthreads, args.cpu_seconds)
+    out["gemm"] = gemm_leg(be, gq, syn, torch, not args.no_cpu)
+    out["moe"] = moe_leg(be, gq, syn, torch, not args.no_cpu)
+    if not args.no_decode:
+        del copies, host
+        torch.cuda.empty_cache()
+        out["decode"] = decode_leg(be, gq, syn, torch, 0 if args.no_cpu else args.cpu_decode_steps)
     print(json.dumps(out), flush=True)
 
 

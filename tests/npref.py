@@ -154,3 +154,56 @@ def quantize_row_q8_k(x):
             d[b] = np.float32(1.0) / iscale
     bs = qs.reshape(nb, 16, 16).astype(np.int16).sum(axis=2).reshape(-1)
     return d, qs.reshape(-1), bs.astype(np.int16)
+
+
+def decode_step(cfg, w, kc, vc, token, pos):
+    """One decode step of a dense Llama/Qwen2 decoder in float64, written
+    from the model's definition (RMSNorm, NEOX RoPE with theta^(2i/hd),
+    causal softmax attention with grouped KV heads, SwiGLU FFN, residual
+    adds), with the weights dequantized by the numpy block decoders above.
+    kc / vc: float16 bit arrays [n_layers][ctx][kv_dim], updated at pos
+    with k / v rounded to f16.  Returns the logits (float64)."""
+    H, hd = cfg["hidden"], cfg["head_dim"]
+    nh, nkv, F = cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"]
+    half, group = hd // 2, nh // nkv
+
+    def mat(dtype, blob, rows, cols):
+        return np.stack([dequant(dtype, blob[r], cols) for r in range(rows)]).astype(np.float64)
+
+    def norm(x, g):
+        return g * x / np.sqrt(np.mean(x * x) + cfg["eps"])
+
+    i = np.arange(half)
+    ang = pos / np.power(float(cfg["theta"]), 2.0 * i / hd)
+    cs, sn = np.cos(ang), np.sin(ang)
+
+    def rope(v):  # v [heads, hd]
+        a, b = v[:, :half].copy(), v[:, half:].copy()
+        return np.concatenate([a * cs - b * sn, a * sn + b * cs], axis=1)
+
+    x = w["embd"][token].astype(np.float64)
+    for L in range(cfg["n_layers"]):
+        xn = norm(x, w["attn_norm"][L].astype(np.float64))
+        q = mat(cfg["attn_type"], w["wq"][L], nh * hd, H) @ xn
+        k = mat(cfg["attn_type"], w["wk"][L], nkv * hd, H) @ xn
+        v = mat(cfg["attn_type"], w["wv"][L], nkv * hd, H) @ xn
+        q = rope(q.reshape(nh, hd))
+        k = rope(k.reshape(nkv, hd)).reshape(-1)
+        kc[L, pos] = k.astype(np.float16).view(np.uint16)
+        vc[L, pos] = v.astype(np.float16).view(np.uint16)
+        K = kc[L, :pos + 1].view(np.float16).astype(np.float64).reshape(pos + 1, nkv, hd)
+        V = vc[L, :pos + 1].view(np.float16).astype(np.float64).reshape(pos + 1, nkv, hd)
+        att = np.empty((nh, hd))
+        for h in range(nh):
+            s = K[:, h // group, :] @ q[h] / np.sqrt(hd)
+            p = np.exp(s - s.max())
+            att[h] = (p / p.sum()) @ V[:, h // group, :]
+        x = x + mat(cfg["attn_type"], w["wo"][L], H, nh * hd) @ att.reshape(-1)
+        xn = norm(x, w["ffn_norm"][L].astype(np.float64))
+        g = mat(cfg["gate_up_type"], w["wgate"][L], F, H) @ xn
+        u = mat(cfg["gate_up_type"], w["wup"][L], F, H) @ xn
+        with np.errstate(over="ignore"):  # exp(-g) = inf gives silu(g) = -0
+            act = g / (1.0 + np.exp(-g)) * u
+        x = x + mat(cfg["down_type"], w["wdown"][L], H, F) @ act
+    xn = norm(x, w["output_norm"].astype(np.float64))
+    return mat(cfg["head_type"], w["lm_head"], cfg["vocab"], H) @ xn

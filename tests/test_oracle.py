@@ -346,3 +346,47 @@ def test_moe_ffn_vs_numpy(orc):
             hmid = g / (1 + np.exp(-g)) * u
             ref += w[t, s] * (Wd[e * H:(e + 1) * H] @ hmid)
         assert np.max(np.abs(out[t] - ref)) <= 1e-4 * np.max(np.abs(ref))
+
+
+TINY_MODEL = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512,
+                  vocab=300, ctx=24, eps=1e-6, theta=1e6, attn_type=Q4_K, gate_up_type=Q4_K,
+                  down_type=Q6_K, head_type=Q6_K)
+
+
+def test_decode_step_vs_numpy(orc):
+    """gqo_decode_step (cpu_path.rs:695-818) against an independent float64
+    restatement: same logits to fp32 accumulation error, same KV rows up to
+    one f16 rounding step.  An embedding scaled by 1e4 keeps every term of
+    the residual stream visible in the logits."""
+    cfg = TINY_MODEL
+    w = syn.make_decoder(cfg, 21, embd_scale=1e4)
+    kv = syn.make_kv(cfg, 16, 22)
+    om = orc.DecoderModel(cfg, w, kv)
+    kc = np.zeros_like(om.kc)
+    vc = np.zeros_like(om.vc)
+    kc[:, :16], vc[:, :16] = kv
+    for pos, tok in ((16, 7), (17, 250), (18, 0)):
+        got = om.step(tok, pos)
+        ref = npref.decode_step(cfg, w, kc, vc, tok, pos)
+        assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max(), pos
+        assert orc.argmax(got) == int(np.argmax(ref))
+    for arr_o, arr_r in ((om.kc, kc), (om.vc, vc)):
+        a = arr_o[:, :19].view(np.float16).astype(np.float64)
+        b = arr_r[:, :19].view(np.float16).astype(np.float64)
+        assert np.allclose(a, b, rtol=2e-3, atol=1e-3)
+
+
+def test_decode_step_first_position(orc):
+    """At position 0 RoPE is the identity and attention over one position
+    returns v itself: the oracle's step equals the numpy step there too."""
+    cfg = dict(TINY_MODEL, n_layers=1)
+    w = syn.make_decoder(cfg, 23, embd_scale=1e4)
+    om = orc.DecoderModel(cfg, w)
+    kc = np.zeros_like(om.kc)
+    vc = np.zeros_like(om.vc)
+    got = om.step(3, 0)
+    ref = npref.decode_step(cfg, w, kc, vc, 3, 0)
+    assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max()
+    a = om.vc[0, 0].view(np.float16).astype(np.float64)
+    b = vc[0, 0].view(np.float16).astype(np.float64)
+    assert np.allclose(a, b, rtol=2e-3, atol=1e-3)
