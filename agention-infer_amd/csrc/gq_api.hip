@@ -601,6 +601,8 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   // counters of the last-block merges start (and end every launch) at zero
   if (e == hipSuccess) e = hipMemset(ibuf, 0, nibuf * sizeof(int));
   if (e == hipSuccess) e = hipMemset(buf, 0, nbuf * sizeof(float));
+  if (e == hipSuccess) e = hipMemset(L.kcache, 0, (size_t)d->n_layers * d->ctx * kvd * 2);
+  if (e == hipSuccess) e = hipMemset(L.vcache, 0, (size_t)d->n_layers * d->ctx * kvd * 2);
   if (e != hipSuccess) { delete m; return fail(GQ_EHIP, "model upload failed: %s", hipGetErrorString(e)); }
   L.attn_norm = m->an.data(); L.ffn_norm = m->fn.data();
   L.output_norm = norms + (size_t)2 * d->n_layers * H;

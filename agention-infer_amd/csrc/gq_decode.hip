@@ -219,7 +219,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     float vf[PW][DPL];
 #pragma unroll
     for (int j = 0; j < PW; j++) {
-      const uint32_t raw = tw + j == pos ? vn : vr[j];
+      // Rows past pos were clamped to row pos, which this launch is still
+      // writing: their p is 0, but 0 * (stale NaN/inf) is not, so they
+      // read as 0; row pos itself is the freshly rounded one.
+      const uint32_t raw = tw + j == pos ? vn : (tw + j > pos ? 0u : vr[j]);
 #pragma unroll
       for (int e = 0; e < DPL; e++) vf[j][e] = h2f(raw >> (16 * e));
     }

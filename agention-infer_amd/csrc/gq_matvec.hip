@@ -227,11 +227,11 @@ __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u
 }
 
 // ------------------------------------------------------------- staging
-// Thread t converts elements [4096p + 16t, +16) of x; 32-runs are thread
-// pairs (2m, 2m+1).  All threads execute the shuffles.
+// A thread converts elements [e0, e0 + 16) of x; 32-runs are the thread
+// pairs (2m, 2m+1), whose e0 differ by 16.  All threads execute the
+// shuffles.
 template <bool Q6>
-__device__ __forceinline__ void stage_x(int kpad, int p, const float (&xv)[16], const Smem &S) {
-  const int e0 = 4096 * p + 16 * (int)threadIdx.x;
+__device__ __forceinline__ void stage_x(int kpad, int e0, const float (&xv)[16], const Smem &S) {
   float amax = 0.f, sum = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; i++) {
@@ -242,26 +242,25 @@ __device__ __forceinline__ void stage_x(int kpad, int p, const float (&xv)[16], 
   const float sum32 = sum + __shfl_xor(sum, 1, 64);
   if (e0 >= kpad) return;
   const float inv = amax > 0.f ? LIMB_RANGE / amax : 0.f;
+  // Signed base-256 digits of X (each in [-128, 127], unique): since
+  // |X| <= 127 * 2^16, X + 0x808080 lies in [0, 2^24) and its bytes are
+  // digit + 128, so the bytes of (X + 0x808080) ^ 0x808080 are the digits.
   uint32_t w2[4], w1[4], w0[4];
   int xs = 0;
 #pragma unroll
   for (int q = 0; q < 4; q++) {
-    uint32_t b2 = 0, b1 = 0, b0 = 0;
+    uint32_t V[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
       const int X = (int)rintf(xv[4 * q + r] * inv);
       xs += X;
-      const int x0 = (int)(int8_t)(X & 0xff);
-      const int X1 = (X - x0) >> 8;
-      const int x1 = (int)(int8_t)(X1 & 0xff);
-      const int x2 = (X1 - x1) >> 8;
-      b0 |= (uint32_t)(x0 & 0xff) << (8 * r);
-      b1 |= (uint32_t)(x1 & 0xff) << (8 * r);
-      b2 |= (uint32_t)(x2 & 0xff) << (8 * r);
+      V[r] = ((uint32_t)X + 0x808080u) ^ 0x808080u;
     }
-    w2[q] = b2;
-    w1[q] = b1;
-    w0[q] = b0;
+    w0[q] = (V[0] & 0xffu) | ((V[1] & 0xffu) << 8) | ((V[2] & 0xffu) << 16) | (V[3] << 24);
+    w1[q] = ((V[0] >> 8) & 0xffu) | (V[1] & 0xff00u) | ((V[2] & 0xff00u) << 8) |
+            ((V[3] >> 8) << 24);
+    w2[q] = ((V[0] >> 16) & 0xffu) | ((V[1] >> 8) & 0xff00u) | (V[2] & 0xff0000u) |
+            ((V[3] >> 16) << 24);
   }
   const int lo = (e0 >> 8) * LIMB_STRIDE + (e0 & 255);
   *(uint4 *)(S.l2 + lo) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
@@ -466,10 +465,11 @@ __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_
 
   const int kpad = U * 256;
   const int passes = (kpad + 4095) >> 12;
+  auto pass_e0 = [&](int p) { return 4096 * p + 16 * tid; };
   typename XS::Raw raw[NP];
 #pragma unroll
   for (int p = 0; p < NP; p++)
-    if (p < passes) xsrc.issue(4096 * p + 16 * tid, raw[p]);
+    if (p < passes) xsrc.issue(pass_e0(p), raw[p]);
   uint32_t gword = 0;
   if constexpr (FMT == T_IQ3_XXS) gword = gsrc[tid];
   __builtin_amdgcn_sched_barrier(0);
@@ -485,16 +485,18 @@ __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_
   for (int p = 0; p < NP; p++) {
     if (p < passes) {
       float xv[16];
-      xsrc.make(raw[p], 4096 * p + 16 * tid, xv);
-      stage_x<FMT == T_Q6_K>(kpad, p, xv, S);
+      const int e0 = pass_e0(p);
+      xsrc.make(raw[p], e0, xv);
+      stage_x<FMT == T_Q6_K>(kpad, e0, xv, S);
     }
   }
   for (int p = NP; p < passes; p++) {
     typename XS::Raw r1;
-    xsrc.issue(4096 * p + 16 * tid, r1);
+    const int e0 = pass_e0(p);
+    xsrc.issue(e0, r1);
     float xv[16];
-    xsrc.make(r1, 4096 * p + 16 * tid, xv);
-    stage_x<FMT == T_Q6_K>(kpad, p, xv, S);
+    xsrc.make(r1, e0, xv);
+    stage_x<FMT == T_Q6_K>(kpad, e0, xv, S);
   }
   if constexpr (FMT == T_IQ3_XXS) S.grid[tid] = gword;
   xsrc.pre_barrier(S.red);
