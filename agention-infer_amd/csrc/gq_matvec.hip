@@ -517,21 +517,16 @@ __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_
     const float v = unit_dot<FMT>(src, j % U, S);
     if (j < uit) part[(second ? 64 * iters : 0) + j] = v;
   };
-  // Steady state: two units in flight per lane; the tail is peeled so that
-  // no unit is ever loaded twice.
-  int it = 0;
-  for (; it + 2 < total_it; it += 2) {
-    load_it(B, it + 1);
+  // Two units in flight per lane; the wave-uniform conditions keep the
+  // last iterations from loading a unit twice with only two inlined copies
+  // of the unit arithmetic (kernel code size is launch latency: every
+  // launch of a decode step starts with a cold instruction cache).
+  for (int it = 0; it < total_it; it += 2) {
+    const bool hb = it + 1 < total_it;
+    if (hb) load_it(B, it + 1);
     consume(A, it);
-    load_it(A, it + 2);
-    consume(B, it + 1);
-  }
-  if (it + 1 < total_it) {
-    load_it(B, it + 1);
-    consume(A, it);
-    consume(B, it + 1);
-  } else {
-    consume(A, it);
+    if (it + 2 < total_it) load_it(A, it + 2);
+    if (hb) consume(B, it + 1);
   }
   __syncthreads();
 
