@@ -332,6 +332,7 @@ int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down
 int gq_weight_free(gq_weight *w) {
   if (!w) return GQ_OK;
   if (w->body) (void)hipFree(w->body);
+  if (w->gemm_raw) (void)hipFree(w->gemm_raw);
   delete w;
   return GQ_OK;
 }
@@ -472,6 +473,22 @@ int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mod
   if (ws == (size_t)-1)
     return fail(GQ_EDTYPE, "gq_gemm: %s weights with in_dim %d not supported in this mode",
                 type_name(w->L.dtype), w->L.k);
+  if (mode == GQ_GEMM_BF16 && !w->gemm_raw) {
+    // The bf16 GEMM streams whole 144-byte units of each row, which the
+    // tiled matvec layout scatters; keep a ggml-order copy (made once).
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!w->gemm_raw) {
+      uint8_t *raw = nullptr;
+      if (hipMalloc(&raw, w->ggml_bytes) != hipSuccess)
+        return fail(GQ_ENOMEM, "hipMalloc of %zu bytes (GEMM weight copy) failed", w->ggml_bytes);
+      hipError_t e = gq::launch_unrepack_q4k(w->L, w->body, raw, (hipStream_t)stream);
+      if (e != hipSuccess) {
+        (void)hipFree(raw);
+        return fail(GQ_EHIP, "GEMM weight copy failed: %s", hipGetErrorString(e));
+      }
+      const_cast<gq_weight *>(w)->gemm_raw = raw;
+    }
+  }
   void *wsp = nullptr;
   if (ws) HIP_TRY(hipMallocAsync(&wsp, ws, (hipStream_t)stream));
   hipError_t e = gq::launch_gemm(w, X_dev, n, Y_dev, mode, wsp, ws, g_dev.num_cus,

@@ -19,11 +19,9 @@
 //                dot); its result is scaled by (d*sc)*xs and the min term
 //                dmin*m*xs*sum(q) is subtracted in fp32.
 //
-// Tiling: a block computes BM=160 weight rows x BN=256 tokens with 4
-// waves (2 x 2, 80 x 128 each = 5 x 8 MFMA tiles of 16 x 16).  18944 rows
+// Tiling: a block computes BM=160 weight rows x BN=256 tokens.  18944 rows
 // x 512 tokens -> 119 x 2 = 238 blocks: one round on 256 CUs.  K advances
-// 64 elements (one Q4_K group) per stage; LDS tiles are double-buffered and
-// the next stage's global loads are issued before the current stage's MFMAs.
+// 64 elements (one Q4_K group) per stage.
 #include "gq_device.h"
 #include "gq_internal.h"
 #include "../../include/gq.h"
@@ -46,13 +44,28 @@ __device__ __forceinline__ uint32_t f2bf(float f) {
 }
 
 // ----------------------------------------------------------- prepasses
-// X fp32 [n][k] -> bf16 [n][kpad] (zero padded).
-__global__ void k_x_to_bf16(const float *X, int n, int k, int kpad, uint16_t *out) {
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long total = (long)n * kpad;
-  if (i >= total) return;
-  const int t = (int)(i / kpad), c = (int)(i % kpad);
-  out[i] = c < k ? (uint16_t)f2bf(X[(long)t * k + c]) : 0;
+// X fp32 [n][k] -> bf16 in MFMA B-operand fragments: fragment (token tile
+// nt, k-step ks) of 16 tokens x 32 k is 64 lane slots of 8 bf16 (lane l:
+// token 16nt + l%16, k 32ks + 8(l/16)), fragments ordered [nt][ks], so the
+// GEMM loads each one as 1 KiB of contiguous memory.  Tokens are padded
+// with zeros to npad, k to kpad.  One thread per slot.
+__global__ void k_x_to_bf16_frag(const float *X, int n, int npad, int k, int kpad, uint16_t *out) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;  // slot
+  const int ksteps = kpad / 32;
+  if (i >= (long)(npad / 16) * ksteps * 64) return;
+  const int l = (int)(i & 63);
+  const long f = i >> 6;
+  const int nt = (int)(f / ksteps), ks = (int)(f % ksteps);
+  const int t = 16 * nt + (l & 15), c0 = 32 * ks + 8 * (l >> 4);
+  uint32_t o[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const int c = c0 + 2 * e;
+    const float a = t < n && c < k ? X[(long)t * k + c] : 0.f;
+    const float b = t < n && c + 1 < k ? X[(long)t * k + c + 1] : 0.f;
+    o[e] = f2bf(a) | (f2bf(b) << 16);
+  }
+  *(uint4 *)(out + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
 // X fp32 [n][k] -> per-32 Q8 (KvDtype::Q8_0::pack): q [n][kpad] int8,
@@ -127,13 +140,79 @@ __device__ __forceinline__ void store_w_i8(const WRegs &w, int j, uint8_t *dst, 
 }
 
 // ----------------------------------------------------------- bf16 kernel
-// 512 threads = 8 waves as 2 (rows) x 4 (tokens); wave tile 80 x 64.
-// Per 64-wide K stage, threads 0..319 each dequantize one 32-element
-// sub-block of one row (row t/2, low nibbles for even t, high for odd);
-// all 512 threads stage the X tile.  Two waves per SIMD let one wave's
-// dequant VALU run beside the other's MFMAs.
-constexpr int LDA = BK + 8;  // bf16 elements per LDS row (16 B pad)
-constexpr int WN2 = 64, TN2 = WN2 / 16;
+// Producer / consumer: 512 threads.  Waves 0-3 only multiply: each owns an
+// 80-row x 128-token tile (5 x 8 MFMA tiles) of the 160 x 256 block tile.
+// Waves 4-7 only move and dequantize data, straight from memory to LDS
+// (global_load_lds_dwordx4, no registers):
+//   * waves 4-5 fetch the raw Q4_K units of the block's 160 rows (ggml
+//     order, 144 B per row per 256 k), one unit (4 stages of 64 k) ahead;
+//   * waves 6-7 fetch the X tile (256 tokens x 64 bf16) one stage ahead;
+//   * all four dequantize the next stage's W tile (d*sc*q - dmin*m, bf16).
+// LDS tiles are fragment-major: MFMA operand (ks, t) -- 16 rows or tokens x
+// 32 k -- is 64 lane slots of 16 B (lane l: row / token 16t + l%16, k
+// 32ks + 8(l/16) .. +8), so every operand read is a conflict-free 128-bit
+// load of consecutive slots and every X load writes a whole fragment.
+// Rings (2 slots each): dequantized W, X, raw W units (152 KiB).  One
+// barrier per stage.  A wave's waits count only its own loads, so the two
+// kinds of loads are issued by different waves.
+constexpr int AT = BM / 16, BT = BN / 16;     // 10 row tiles, 16 token tiles
+constexpr int A_FR = 2 * AT, B_FR = 2 * BT;   // fragments per stage
+constexpr int FR16 = 512;                     // bf16 per 1 KiB fragment
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// s_waitcnt vmcnt(N), leaving the other counters alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+__device__ __forceinline__ void dma16(const void *g, void *lds) {
+  __builtin_amdgcn_global_load_lds(g, (lds_void_t *)lds, 16, 0, 0);
+}
+
+// LDS reads written as asm and waited for inside: the compiler, seeing
+// loads straight to LDS still outstanding, would otherwise wait for all of
+// them (vmcnt(0)) before any LDS read; the callers wait for exactly the
+// loads they read.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void lds_read2(const uint4 *p0, const uint4 *p1, uint4 &a, uint4 &b) {
+  const uint32_t a0 = (uint32_t)(uintptr_t)(lds_void_t *)p0;
+  const uint32_t a1 = (uint32_t)(uintptr_t)(lds_void_t *)p1;
+  u32x4_t x, y;
+  asm volatile(
+      "ds_read_b128 %0, %2\n\t"
+      "ds_read_b128 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x), "=&v"(y)
+      : "v"(a0), "v"(a1)
+      : "memory");
+  a = make_uint4(x[0], x[1], x[2], x[3]);
+  b = make_uint4(y[0], y[1], y[2], y[3]);
+}
+
+// Six 16-byte LDS reads, one wait.
+__device__ __forceinline__ void lds_read6(const uint32_t (&ad)[6], uint4 (&v)[6]) {
+  u32x4_t x0, x1, x2, x3, x4, x5;
+  asm volatile(
+      "ds_read_b128 %0, %6\n\t"
+      "ds_read_b128 %1, %7\n\t"
+      "ds_read_b128 %2, %8\n\t"
+      "ds_read_b128 %3, %9\n\t"
+      "ds_read_b128 %4, %10\n\t"
+      "ds_read_b128 %5, %11\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(x4), "=&v"(x5)
+      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5])
+      : "memory");
+  v[0] = make_uint4(x0[0], x0[1], x0[2], x0[3]);
+  v[1] = make_uint4(x1[0], x1[1], x1[2], x1[3]);
+  v[2] = make_uint4(x2[0], x2[1], x2[2], x2[3]);
+  v[3] = make_uint4(x3[0], x3[1], x3[2], x3[3]);
+  v[4] = make_uint4(x4[0], x4[1], x4[2], x4[3]);
+  v[5] = make_uint4(x5[0], x5[1], x5[2], x5[3]);
+}
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
@@ -142,100 +221,161 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// 32 values of sub-block 2j+hi of a row: (d*sc)*q - dmin*m, as bf16.
-__device__ __forceinline__ void dequant_sub_bf16(const WRegs &w, int j, int hi, uint16_t *dst) {
-  uint32_t sc, m;
-  scale_min_k4(2 * j + hi, w.hd.y, w.hd.z, w.hd.w, sc, m);
-  const float d = h2f(w.hd.x), dmin = h2f(w.hd.x >> 16);
-  const float ds = d * (float)sc, mm = dmin * (float)m;
-  const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
-  uint32_t o[16];
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const uint32_t q = hi ? (qw[i] >> 4) & 0x0F0F0F0Fu : qw[i] & 0x0F0F0F0Fu;
-    const float e0 = ds * ub<0>(q) - mm, e1 = ds * ub<1>(q) - mm;
-    const float e2 = ds * ub<2>(q) - mm, e3 = ds * ub<3>(q) - mm;
-    o[2 * i] = w.ok ? pack_bf16(e0, e1) : 0u;
-    o[2 * i + 1] = w.ok ? pack_bf16(e2, e3) : 0u;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-    *(uint4 *)(dst + 8 * i) = make_uint4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
-}
+// Raw (ggml-order) Q4_K bytes for the GEMM: a row's 144-byte units are
+// contiguous, so a producer fetches whole units (2.25 cache lines) instead
+// of the scattered 16-byte chunks of the tiled matvec layout.
+constexpr int UB = 144;                        // bytes per Q4_K unit
+constexpr int WU_SLOT = 24 * 1024;             // one unit of BM rows (23040 B) + pad
+constexpr int W_INSTR = WU_SLOT / 1024;        // 24 loads of 64 x 16 B per unit
 
-__global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *body,
+__global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw, long row_bytes,
                                                    const uint16_t *Xb, int n, int kpad,
                                                    float *Y) {
-  __shared__ __align__(16) uint16_t As[2][BM * LDA];
-  __shared__ __align__(16) uint16_t Bs[2][BN * LDA];
+  __shared__ __align__(16) uint16_t As[2][A_FR * FR16];
+  __shared__ __align__(16) uint16_t Xs[2][B_FR * FR16];
+  __shared__ __align__(16) uint8_t Wu[2][WU_SLOT];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
   const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
-  const int stages = kpad / BK;
-  const bool wtask = tid < 2 * BM;
-  const int wrow = tid >> 1, whi = tid & 1;
+  const int stages = kpad / BK, last = stages - 1, lastu = L.units - 1;
+  const bool mma = wave < 4;
 
-  auto load_x = [&](int kt, uint4 (&xr)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int c = tid + 512 * i, tok = c >> 3, part = c & 7;
-      const int tn = min(n0 + tok, n - 1);
-      xr[i] = *(const uint4 *)(Xb + (long)tn * kpad + kt * BK + 8 * part);
-      if (n0 + tok >= n) xr[i] = make_uint4(0, 0, 0, 0);
-    }
-  };
-  auto store_x = [&](int buf, const uint4 (&xr)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int c = tid + 512 * i, tok = c >> 3, part = c & 7;
-      *(uint4 *)(&Bs[buf][tok * LDA + 8 * part]) = xr[i];
-    }
-  };
-
-  f32x4_t acc[TM][TN2];
+  // ---- consumer state
+  const int wm = wave & 1, wn = (wave >> 1) & 1;
+  f32x4_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < TN2; j++) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TN; j++) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  WRegs wr;
-  uint4 xr[4];
-  if (wtask) wr = load_w(L, body, m0 + wrow, 0, 0);
-  load_x(0, xr);
-  if (wtask) dequant_sub_bf16(wr, 0, whi, &As[0][wrow * LDA + 32 * whi]);
-  store_x(0, xr);
-  __syncthreads();
-
-  for (int kt = 0; kt < stages; kt++) {
-    const int buf = kt & 1;
-    // Straight-line stage body (no branch around the next stage's loads and
-    // dequant) so the scheduler can interleave the dequant VALU work with
-    // this stage's MFMAs; past the last stage it reloads the last stage into
-    // the unused buffer.
-    const int kn = min(kt + 1, stages - 1);
-    if (wtask) wr = load_w(L, body, m0 + wrow, kn >> 2, kn & 3);
-    load_x(kn, xr);
+  // ---- producers: waves 4-5 fetch raw W units, waves 6-7 fetch X tiles;
+  // all four dequantize (640 tasks of 16 elements per stage).
+  const int pw = (wave - 4) & 3, pt = tid & 255;
+  const bool wfetch = pw < 2;
+  // raw W: this wave's 12 loads cover 16-byte slots (12pw + q)*64 + lane of
+  // the unit image [row][144 B]; slots past BM rows land in the pad.
+  // (Addresses are recomputed per unit: kept in registers they would
+  // compete with the multiply waves' accumulators.)
+  // X: this wave's 16 loads are fragments f = 16(pw-2) + q of the stage:
+  // k-step f/16, token tile f%16 (1 KiB each in the prepass's order).
+  const int ksteps = kpad / 32;
+  const uint16_t *xsrc = Xb + ((long)(n0 / 16) * ksteps * 64 + lane) * 8;
+  auto load_w_unit = [&](int u) {  // unit u (clamped) into slot u & 1
+    const int uc = min(u, lastu);
+#pragma unroll 4
+    for (int q = 0; q < 12; q++) {
+      const int sl = min((12 * (pw & 1) + q) * 64 + lane, BM * 9 - 1);
+      const int row = min(m0 + sl / 9, L.rows - 1);
+      dma16(raw + (long)row * row_bytes + (long)uc * UB + 16 * (sl % 9),
+            &Wu[u & 1][(12 * (pw & 1) + q) * 1024]);
+    }
+  };
+  auto load_x = [&](int s) {  // X tile of stage s (clamped) into slot s & 1
+    const int sc = min(s, last);
+#pragma unroll 4
+    for (int q = 0; q < 16; q++) {
+      const int f = 16 * (pw & 1) + q, nt = f & 15, ks = f >> 4;
+      dma16(xsrc + ((long)nt * ksteps + 2 * sc + ks) * 512, &Xs[s & 1][f * FR16]);
+    }
+  };
+  auto dequant = [&](int s) {  // W tile of stage s into As[s & 1]
+    const int u = s >> 2, j = s & 3;
+    const uint8_t *wu = Wu[u & 1];
+    // Tasks pt, pt + 256, pt + 512 (< 640): row r, half h, 16-element
+    // quarter qq.  All LDS reads first (one wait: latency under the
+    // multiply waves' LDS traffic is long), then the arithmetic.
+    uint32_t ad[6];
+    int tk[3];
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      const int kk = 32 * ks + 8 * (lane >> 4);
-      bf16x8_t a[TM];
+    for (int round = 0; round < 3; round++) {
+      tk[round] = min(pt + 256 * round, 4 * BM - 1);
+      const int r = tk[round] >> 2, qq = tk[round] & 1;
+      ad[2 * round] = (uint32_t)(uintptr_t)(lds_void_t *)(wu + r * UB);
+      ad[2 * round + 1] = (uint32_t)(uintptr_t)(lds_void_t *)(wu + r * UB + 16 + 32 * j + 16 * qq);
+    }
+    uint4 v[6];
+    lds_read6(ad, v);
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const uint4 v = *(const uint4 *)(&As[buf][(WM * wm + 16 * i + (lane & 15)) * LDA + kk]);
-        a[i] = __builtin_bit_cast(bf16x8_t, v);
-      }
+    for (int round = 0; round < 3; round++) {
+      if (round < 2 || pt + 512 < 4 * BM) {
+        const int task = tk[round];
+        const int r = task >> 2, h = (task >> 1) & 1, qq = task & 1;
+        const uint4 hd = v[2 * round], qs = v[2 * round + 1];
+        const bool ok = m0 + r < L.rows;
+        uint32_t sc, mn;
+        scale_min_k4(2 * j + h, hd.y, hd.z, hd.w, sc, mn);
+        const float ds = h2f(hd.x) * (float)sc, mm = h2f(hd.x >> 16) * (float)mn;
+        const uint32_t qw[4] = {qs.x, qs.y, qs.z, qs.w};
+        uint32_t o[8];
 #pragma unroll
-      for (int j = 0; j < TN2; j++) {
-        const uint4 v = *(const uint4 *)(&Bs[buf][(WN2 * wn + 16 * j + (lane & 15)) * LDA + kk]);
-        const bf16x8_t b = __builtin_bit_cast(bf16x8_t, v);
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[i][j], 0, 0, 0);
+        for (int i = 0; i < 4; i++) {
+          const uint32_t q = h ? (qw[i] >> 4) & 0x0F0F0F0Fu : qw[i] & 0x0F0F0F0Fu;
+          o[2 * i] = ok ? pack_bf16(ds * ub<0>(q) - mm, ds * ub<1>(q) - mm) : 0u;
+          o[2 * i + 1] = ok ? pack_bf16(ds * ub<2>(q) - mm, ds * ub<3>(q) - mm) : 0u;
+        }
+        // k 32h + 16qq .. +16 = lane slots 2qq, 2qq+1 of k-step h
+        uint16_t *dst = &As[s & 1][((h * AT + (r >> 4)) * 64 + (r & 15) + 32 * qq) * 8];
+        *(uint4 *)dst = make_uint4(o[0], o[1], o[2], o[3]);
+        *(uint4 *)(dst + 128) = make_uint4(o[4], o[5], o[6], o[7]);
       }
     }
-    if (wtask) dequant_sub_bf16(wr, kn & 3, whi, &As[buf ^ 1][wrow * LDA + 32 * whi]);
-    store_x(buf ^ 1, xr);
-    __syncthreads();
+  };
+
+  // ---- prologue.  A W unit is read by all producer waves but only the W
+  // waves can wait for its loads, so it is waited for one stage before its
+  // first use and published by that stage's barrier.
+  if (!mma) {
+    if (wfetch) {
+      load_w_unit(0);
+      wait_vm<0>();
+      load_w_unit(1);
+    } else {
+      load_x(0);
+      wait_vm<0>();
+    }
+  }
+  __builtin_amdgcn_s_barrier();  // unit 0 and X tile 0 in LDS
+  if (!mma) {
+    dequant(0);
+    wait_lgkm0();
+  }
+  __builtin_amdgcn_s_barrier();  // W tile 0 in LDS
+
+  for (int kt = 0; kt < stages; kt++) {
+    if (mma) {
+      const uint16_t *A = As[kt & 1], *B = Xs[kt & 1];
+#pragma unroll
+      for (int ks = 0; ks < 2; ks++) {
+        bf16x8_t a[TM];
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+          a[i] = *(const bf16x8_t *)(A + ((ks * AT + TM * wm + i) * 64 + lane) * 8);
+#pragma unroll
+        for (int jn = 0; jn < TN; jn++) {
+          const bf16x8_t b = *(const bf16x8_t *)(B + ((ks * BT + TN * wn + jn) * 64 + lane) * 8);
+#pragma unroll
+          for (int i = 0; i < TM; i++)
+            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[i][jn], 0, 0, 0);
+        }
+      }
+    } else if (wfetch) {
+      // Unit v is requested at stage 4v - 5, waited for at stage 4v - 2
+      // (the W waves' only outstanding loads) and published by that
+      // stage's barrier; stage 4v, its first, is dequantized at 4v - 1.
+      if ((kt & 3) == 2) wait_vm<0>();
+      dequant(kt + 1);
+      if ((kt & 3) == 3) load_w_unit((kt + 5) >> 2);
+      wait_lgkm0();
+    } else {
+      load_x(kt + 1);
+      dequant(kt + 1);
+      wait_vm<0>();
+      wait_lgkm0();
+    }
+    __builtin_amdgcn_s_barrier();
+  }
+  if (!mma) {
+    wait_vm<0>();  // drain the clamped reloads before the block ends
+    return;
   }
 
   // D layout: lane holds rows 4*(lane/16)+r (weight rows) of column lane%16 (token).
@@ -243,8 +383,8 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *body
   for (int i = 0; i < TM; i++) {
     const int m = m0 + WM * wm + 16 * i + 4 * (lane >> 4);
 #pragma unroll
-    for (int j = 0; j < TN2; j++) {
-      const int t = n0 + WN2 * wn + 16 * j + (lane & 15);
+    for (int j = 0; j < TN; j++) {
+      const int t = n0 + WN * wn + 16 * j + (lane & 15);
       if (t >= n) continue;
       float *yp = Y + (long)t * L.rows + m;
       if (m + 3 < L.rows && (L.rows & 3) == 0) {
@@ -389,9 +529,30 @@ __global__ __launch_bounds__(256) void k_gemm_i8(Layout L, const uint8_t *body, 
 size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode) {
   if (w->L.dtype != T_Q4_K) return (size_t)-1;
   const size_t kpad = (size_t)w->L.units * 256;
-  if (mode == GQ_GEMM_BF16) return (size_t)n * kpad * 2 + 256;
+  if (mode == GQ_GEMM_BF16) return (size_t)((n + BN - 1) / BN * BN) * kpad * 2 + 256;
   // int8: q [n][kpad] + scale f32 [n][kpad/32] + qsum int [n][kpad/32]
   return (size_t)n * kpad + (size_t)n * (kpad / 32) * 8 + 512;
+}
+
+// ggml-order copy of a Q4_K tiled body: chunk c of unit u of a row holds
+// the unit's bytes 16c .. 16c+15.
+__global__ void k_unrepack_q4k(Layout L, const uint8_t *body, long row_bytes, uint8_t *raw) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)L.rows * L.units * 9) return;
+  const int c = (int)(i % 9);
+  const long ru = i / 9;
+  const int r = (int)(ru / L.units), u = (int)(ru % L.units);
+  const int t = r / L.rt, j = (r % L.rt) * L.units + u;
+  *(uint4 *)(raw + (long)r * row_bytes + (long)u * UB + 16 * c) =
+      *(const uint4 *)(body + chunk_offset(L, t, j, c));
+}
+
+hipError_t launch_unrepack_q4k(const Layout &L, const uint8_t *body, uint8_t *raw, hipStream_t st) {
+  const long n = (long)L.rows * L.units * 9;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_unrepack_q4k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, L,
+                     body, (long)L.units * UB, raw);
+  return hipGetLastError();
 }
 
 hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int mode,
@@ -403,11 +564,12 @@ hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int 
   if (mode == GQ_GEMM_BF16) {
     const dim3 grid((L.rows + BM - 1) / BM, (n + BN - 1) / BN);
     uint16_t *xb = (uint16_t *)workspace;
-    const long total = (long)n * kpad;
-    hipLaunchKernelGGL(k_x_to_bf16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, X, n,
-                       L.k, kpad, xb);
-    hipLaunchKernelGGL(k_gemm_bf16, grid, dim3(512), 0, st, L, (const uint8_t *)w->body,
-                       (const uint16_t *)xb, n, kpad, Y);
+    const int npad = (n + BN - 1) / BN * BN;
+    const long slots = (long)(npad / 16) * (kpad / 32) * 64;
+    hipLaunchKernelGGL(k_x_to_bf16_frag, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st,
+                       X, n, npad, L.k, kpad, xb);
+    hipLaunchKernelGGL(k_gemm_bf16, grid, dim3(512), 0, st, L, (const uint8_t *)w->gemm_raw,
+                       (long)L.units * UB, (const uint16_t *)xb, n, kpad, Y);
   } else {
     int8_t *xq = (int8_t *)workspace;
     float *xs = (float *)((char *)workspace + (((size_t)n * kpad + 255) & ~(size_t)255));

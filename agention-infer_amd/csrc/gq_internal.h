@@ -13,6 +13,7 @@ struct gq_weight {
   uint16_t *d;       // per-unit f16 scales (Q6_K, IQ3_XXS), or nullptr
   size_t ggml_bytes; // size of the tensor in ggml block order
   int device;
+  uint8_t *gemm_raw = nullptr;  // ggml-order copy for the prefill GEMM (made on first use)
 };
 
 namespace gq {
@@ -138,5 +139,6 @@ hipError_t launch_quantize_q8_32(const float *x, long n, uint16_t *scale, int8_t
 hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int mode,
                        void *workspace, size_t ws_bytes, int num_cus, hipStream_t st);
 size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode);
+hipError_t launch_unrepack_q4k(const Layout &L, const uint8_t *body, uint8_t *raw, hipStream_t st);
 
 }  // namespace gq
