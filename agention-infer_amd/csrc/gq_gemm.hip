@@ -146,15 +146,16 @@ __device__ __forceinline__ void store_w_i8(const WRegs &w, int j, uint8_t *dst, 
 // (global_load_lds_dwordx4, no registers):
 //   * waves 4-5 fetch the raw Q4_K units of the block's 160 rows (ggml
 //     order, 144 B per row per 256 k), one unit (4 stages of 64 k) ahead;
-//   * waves 6-7 fetch the X tile (256 tokens x 64 bf16) one stage ahead;
-//   * all four dequantize the next stage's W tile (d*sc*q - dmin*m, bf16).
+//   * all four fetch the X tile (256 tokens x 64 bf16) one stage ahead and
+//     dequantize the next stage's W tile (d*sc*q - dmin*m, bf16).
 // LDS tiles are fragment-major: MFMA operand (ks, t) -- 16 rows or tokens x
 // 32 k -- is 64 lane slots of 16 B (lane l: row / token 16t + l%16, k
 // 32ks + 8(l/16) .. +8), so every operand read is a conflict-free 128-bit
 // load of consecutive slots and every X load writes a whole fragment.
 // Rings (2 slots each): dequantized W, X, raw W units (152 KiB).  One
-// barrier per stage.  A wave's waits count only its own loads, so the two
-// kinds of loads are issued by different waves.
+// barrier per stage.  A wave's waits count only its own loads (in issue
+// order), so the long-lived unit loads are issued after each stage's X
+// loads and only waves 4-5 carry them.
 constexpr int AT = BM / 16, BT = BN / 16;     // 10 row tiles, 16 token tiles
 constexpr int A_FR = 2 * AT, B_FR = 2 * BT;   // fragments per stage
 constexpr int FR16 = 512;                     // bf16 per 1 KiB fragment
@@ -255,8 +256,8 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
   // the unit image [row][144 B]; slots past BM rows land in the pad.
   // (Addresses are recomputed per unit: kept in registers they would
   // compete with the multiply waves' accumulators.)
-  // X: this wave's 16 loads are fragments f = 16(pw-2) + q of the stage:
-  // k-step f/16, token tile f%16 (1 KiB each in the prepass's order).
+  // X: this wave's 8 loads are fragments f = 8pw + q of the stage: k-step
+  // f/16, token tile f%16 (1 KiB each in the prepass's order).
   const int ksteps = kpad / 32;
   const uint16_t *xsrc = Xb + ((long)(n0 / 16) * ksteps * 64 + lane) * 8;
   auto load_w_unit = [&](int u) {  // unit u (clamped) into slot u & 1
@@ -269,11 +270,11 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
             &Wu[u & 1][(12 * (pw & 1) + q) * 1024]);
     }
   };
-  auto load_x = [&](int s) {  // X tile of stage s (clamped) into slot s & 1
+  auto load_x = [&](int s) {  // this wave's 8 X fragments of stage s (clamped) into slot s & 1
     const int sc = min(s, last);
 #pragma unroll 4
-    for (int q = 0; q < 16; q++) {
-      const int f = 16 * (pw & 1) + q, nt = f & 15, ks = f >> 4;
+    for (int q = 0; q < 8; q++) {
+      const int f = 8 * pw + q, nt = f & 15, ks = f >> 4;
       dma16(xsrc + ((long)nt * ksteps + 2 * sc + ks) * 512, &Xs[s & 1][f * FR16]);
     }
   };
@@ -309,8 +310,9 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const uint32_t q = h ? (qw[i] >> 4) & 0x0F0F0F0Fu : qw[i] & 0x0F0F0F0Fu;
-          o[2 * i] = ok ? pack_bf16(ds * ub<0>(q) - mm, ds * ub<1>(q) - mm) : 0u;
-          o[2 * i + 1] = ok ? pack_bf16(ds * ub<2>(q) - mm, ds * ub<3>(q) - mm) : 0u;
+          // one FMA per element (the bf16 rounding that follows dominates)
+          o[2 * i] = ok ? pack_bf16(fmaf(ds, ub<0>(q), -mm), fmaf(ds, ub<1>(q), -mm)) : 0u;
+          o[2 * i + 1] = ok ? pack_bf16(fmaf(ds, ub<2>(q), -mm), fmaf(ds, ub<3>(q), -mm)) : 0u;
         }
         // k 32h + 16qq .. +16 = lane slots 2qq, 2qq+1 of k-step h
         uint16_t *dst = &As[s & 1][((h * AT + (r >> 4)) * 64 + (r & 15) + 32 * qq) * 8];
@@ -324,14 +326,10 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
   // waves can wait for its loads, so it is waited for one stage before its
   // first use and published by that stage's barrier.
   if (!mma) {
-    if (wfetch) {
-      load_w_unit(0);
-      wait_vm<0>();
-      load_w_unit(1);
-    } else {
-      load_x(0);
-      wait_vm<0>();
-    }
+    load_x(0);
+    if (wfetch) load_w_unit(0);
+    wait_vm<0>();
+    if (wfetch) load_w_unit(1);
   }
   __builtin_amdgcn_s_barrier();  // unit 0 and X tile 0 in LDS
   if (!mma) {
@@ -357,18 +355,20 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
             acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[i][jn], 0, 0, 0);
         }
       }
-    } else if (wfetch) {
-      // Unit v is requested at stage 4v - 5, waited for at stage 4v - 2
-      // (the W waves' only outstanding loads) and published by that
-      // stage's barrier; stage 4v, its first, is dequantized at 4v - 1.
-      if ((kt & 3) == 2) wait_vm<0>();
-      dequant(kt + 1);
-      if ((kt & 3) == 3) load_w_unit((kt + 5) >> 2);
-      wait_lgkm0();
     } else {
+      // Every producer wave fetches 8 X fragments of stage kt + 1 and
+      // dequantizes; waves 4-5 also fetch W units.  Unit v is requested at
+      // stage 4v - 5 (after that stage's X loads), waited for at stage
+      // 4v - 2 and published by that stage's barrier; stage 4v, its first,
+      // is dequantized at 4v - 1.
       load_x(kt + 1);
       dequant(kt + 1);
-      wait_vm<0>();
+      if (wfetch && (kt & 3) == 3) {
+        load_w_unit((kt + 5) >> 2);
+        wait_vm<12>();  // X of stage kt + 1 (older than the 12 unit loads)
+      } else {
+        wait_vm<0>();  // X of stage kt + 1 (and, at kt % 4 == 2, unit (kt + 2) / 4)
+      }
       wait_lgkm0();
     }
     __builtin_amdgcn_s_barrier();
