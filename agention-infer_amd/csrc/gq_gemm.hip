@@ -22,6 +22,8 @@
 // Tiling: a block computes BM=160 weight rows x BN=256 tokens.  18944 rows
 // x 512 tokens -> 119 x 2 = 238 blocks: one round on 256 CUs.  K advances
 // 64 elements (one Q4_K group) per stage.
+#include <type_traits>
+
 #include "gq_device.h"
 #include "gq_internal.h"
 #include "../../include/gq.h"
@@ -193,6 +195,36 @@ __device__ __forceinline__ void lds_read2(const uint4 *p0, const uint4 *p1, uint
   b = make_uint4(y[0], y[1], y[2], y[3]);
 }
 
+// Two / four 16-byte LDS reads, one wait.
+__device__ __forceinline__ void lds_read2_a(const uint32_t (&ad)[2], uint4 (&v)[2]) {
+  u32x4_t x0, x1;
+  asm volatile(
+      "ds_read_b128 %0, %2\n\t"
+      "ds_read_b128 %1, %3\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x0), "=&v"(x1)
+      : "v"(ad[0]), "v"(ad[1])
+      : "memory");
+  v[0] = make_uint4(x0[0], x0[1], x0[2], x0[3]);
+  v[1] = make_uint4(x1[0], x1[1], x1[2], x1[3]);
+}
+__device__ __forceinline__ void lds_read4(const uint32_t (&ad)[4], uint4 (&v)[4]) {
+  u32x4_t x0, x1, x2, x3;
+  asm volatile(
+      "ds_read_b128 %0, %4\n\t"
+      "ds_read_b128 %1, %5\n\t"
+      "ds_read_b128 %2, %6\n\t"
+      "ds_read_b128 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3)
+      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3])
+      : "memory");
+  v[0] = make_uint4(x0[0], x0[1], x0[2], x0[3]);
+  v[1] = make_uint4(x1[0], x1[1], x1[2], x1[3]);
+  v[2] = make_uint4(x2[0], x2[1], x2[2], x2[3]);
+  v[3] = make_uint4(x3[0], x3[1], x3[2], x3[3]);
+}
+
 // Six 16-byte LDS reads, one wait.
 __device__ __forceinline__ void lds_read6(const uint32_t (&ad)[6], uint4 (&v)[6]) {
   u32x4_t x0, x1, x2, x3, x4, x5;
@@ -213,6 +245,31 @@ __device__ __forceinline__ void lds_read6(const uint32_t (&ad)[6], uint4 (&v)[6]
   v[3] = make_uint4(x3[0], x3[1], x3[2], x3[3]);
   v[4] = make_uint4(x4[0], x4[1], x4[2], x4[3]);
   v[5] = make_uint4(x5[0], x5[1], x5[2], x5[3]);
+}
+
+// Byte K of w (0..255) as float: one v_cvt_f32_ubyteK.  Written as asm
+// because the compiler otherwise folds a preceding nibble mask into a
+// v_bfe per element.
+template <int K>
+__device__ __forceinline__ float cvt_ubyte(uint32_t w) {
+  float f;
+  if constexpr (K == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(f) : "v"(w));
+  else if constexpr (K == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(f) : "v"(w));
+  else if constexpr (K == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(f) : "v"(w));
+  else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(f) : "v"(w));
+  return f;
+}
+
+// get_scale_min_k4 (src/quant/q4_k.rs:26-35) without branches: both forms,
+// then a select on j < 4.
+__device__ __forceinline__ void scale_min_k4_sel(int j, uint32_t s0, uint32_t s1, uint32_t s2,
+                                                 uint32_t &sc, uint32_t &m) {
+  const uint32_t a = sbyte(s0, s1, s2, j & 7), b = sbyte(s0, s1, s2, j + 4);
+  const uint32_t c = sbyte(s0, s1, s2, (j - 4) & 7);
+  const uint32_t lo_sc = a & 63u, lo_m = b & 63u;
+  const uint32_t hi_sc = (b & 0xFu) | ((c >> 6) << 4), hi_m = (b >> 4) | ((a >> 6) << 4);
+  sc = j < 4 ? lo_sc : hi_sc;
+  m = j < 4 ? lo_m : hi_m;
 }
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -278,47 +335,64 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
       dma16(xsrc + ((long)nt * ksteps + 2 * sc + ks) * 512, &Xs[s & 1][f * FR16]);
     }
   };
-  auto dequant = [&](int s) {  // W tile of stage s into As[s & 1]
+  // Dequantize NR of the stage's 640 tasks (row r, half h, 16-element
+  // quarter qq) -- tasks t0 + 256 * round below 640 -- from raw W unit
+  // s / 4 into As[s & 1].  All LDS reads first (one wait: their latency
+  // under the rest of the block's LDS traffic is long), then the math.
+  auto dequant = [&](int s, int t0, auto nr_tag) {
+    constexpr int NR = decltype(nr_tag)::value;
     const int u = s >> 2, j = s & 3;
     const uint8_t *wu = Wu[u & 1];
-    // Tasks pt, pt + 256, pt + 512 (< 640): row r, half h, 16-element
-    // quarter qq.  All LDS reads first (one wait: latency under the
-    // multiply waves' LDS traffic is long), then the arithmetic.
-    uint32_t ad[6];
-    int tk[3];
+    uint32_t ad[2 * NR];
+    int tk[NR];
 #pragma unroll
-    for (int round = 0; round < 3; round++) {
-      tk[round] = min(pt + 256 * round, 4 * BM - 1);
+    for (int round = 0; round < NR; round++) {
+      tk[round] = min(t0 + 256 * round, 4 * BM - 1);
       const int r = tk[round] >> 2, qq = tk[round] & 1;
       ad[2 * round] = (uint32_t)(uintptr_t)(lds_void_t *)(wu + r * UB);
       ad[2 * round + 1] = (uint32_t)(uintptr_t)(lds_void_t *)(wu + r * UB + 16 + 32 * j + 16 * qq);
     }
-    uint4 v[6];
-    lds_read6(ad, v);
+    uint4 v[2 * NR];
+    if constexpr (NR == 2) {
+      lds_read4(ad, v);
+    } else {
+      lds_read2_a(ad, v);
+    }
 #pragma unroll
-    for (int round = 0; round < 3; round++) {
-      if (round < 2 || pt + 512 < 4 * BM) {
+    for (int round = 0; round < NR; round++) {
+      if (t0 + 256 * round < 4 * BM) {
         const int task = tk[round];
         const int r = task >> 2, h = (task >> 1) & 1, qq = task & 1;
         const uint4 hd = v[2 * round], qs = v[2 * round + 1];
         const bool ok = m0 + r < L.rows;
         uint32_t sc, mn;
-        scale_min_k4(2 * j + h, hd.y, hd.z, hd.w, sc, mn);
-        const float ds = h2f(hd.x) * (float)sc, mm = h2f(hd.x >> 16) * (float)mn;
+        scale_min_k4_sel(2 * j + h, hd.y, hd.z, hd.w, sc, mn);
+        // rows past the matrix: zero scales give zero weights (no branches)
+        const float ds = ok ? h2f(hd.x) * (float)sc : 0.f;
+        const float nm = ok ? -(h2f(hd.x >> 16) * (float)mn) : 0.f;
         const uint32_t qw[4] = {qs.x, qs.y, qs.z, qs.w};
+        const uint32_t sh = 4u * (uint32_t)h;
         uint32_t o[8];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const uint32_t q = h ? (qw[i] >> 4) & 0x0F0F0F0Fu : qw[i] & 0x0F0F0F0Fu;
+          const uint32_t q = (qw[i] >> sh) & 0x0F0F0F0Fu;
           // one FMA per element (the bf16 rounding that follows dominates)
-          o[2 * i] = ok ? pack_bf16(fmaf(ds, ub<0>(q), -mm), fmaf(ds, ub<1>(q), -mm)) : 0u;
-          o[2 * i + 1] = ok ? pack_bf16(fmaf(ds, ub<2>(q), -mm), fmaf(ds, ub<3>(q), -mm)) : 0u;
+          o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(q), nm), fmaf(ds, cvt_ubyte<1>(q), nm));
+          o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(q), nm), fmaf(ds, cvt_ubyte<3>(q), nm));
         }
         // k 32h + 16qq .. +16 = lane slots 2qq, 2qq+1 of k-step h
         uint16_t *dst = &As[s & 1][((h * AT + (r >> 4)) * 64 + (r & 15) + 32 * qq) * 8];
         *(uint4 *)dst = make_uint4(o[0], o[1], o[2], o[3]);
         *(uint4 *)(dst + 128) = make_uint4(o[4], o[5], o[6], o[7]);
       }
+    }
+  };
+  // Multiply waves take tasks 0..255 (one each), producers 256..639.
+  auto dequant_share = [&](int s) {
+    if (mma) {
+      dequant(s, tid, std::integral_constant<int, 1>());
+    } else {
+      dequant(s, 256 + pt, std::integral_constant<int, 2>());
     }
   };
 
@@ -332,10 +406,8 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
     if (wfetch) load_w_unit(1);
   }
   __builtin_amdgcn_s_barrier();  // unit 0 and X tile 0 in LDS
-  if (!mma) {
-    dequant(0);
-    wait_lgkm0();
-  }
+  dequant_share(0);
+  wait_lgkm0();
   __builtin_amdgcn_s_barrier();  // W tile 0 in LDS
 
   for (int kt = 0; kt < stages; kt++) {
@@ -355,6 +427,8 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
             acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[i][jn], 0, 0, 0);
         }
       }
+      dequant_share(kt + 1);  // runs while the MFMAs drain
+      wait_lgkm0();
     } else {
       // Every producer wave fetches 8 X fragments of stage kt + 1 and
       // dequantizes; waves 4-5 also fetch W units.  Unit v is requested at
@@ -362,7 +436,7 @@ __global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw,
       // 4v - 2 and published by that stage's barrier; stage 4v, its first,
       // is dequantized at 4v - 1.
       load_x(kt + 1);
-      dequant(kt + 1);
+      dequant_share(kt + 1);
       if (wfetch && (kt & 3) == 3) {
         load_w_unit((kt + 5) >> 2);
         wait_vm<12>();  // X of stage kt + 1 (older than the 12 unit loads)
