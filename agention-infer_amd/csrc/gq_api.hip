@@ -113,10 +113,22 @@ const char *type_name(int t) {
   }
 }
 
+// LDS a matvec block over w (with pair, over w and a second matrix of its
+// shape) needs.
+size_t matvec_block_lds(const gq_weight *w, bool pair) {
+  gq::MvArgs a{};
+  a.units = w->L.units;
+  a.pair = pair;
+  a.nseg = 1;
+  a.seg[0].rows = std::max(w->L.rows, 1);
+  return gq::matvec_plan(a, g_dev.num_cus);
+}
+
 int check_matvec(const gq_weight *w) {
   if (!w) return fail(GQ_EINVAL, "null weight handle");
-  const int part = (w->L.rt * w->L.units + 63) / 64 * 64;
-  if (gq::matvec_lds_bytes(w->L.dtype, w->L.units, part) > 160 * 1024)
+  if (w->L.rt != std::max(w->L.rows, 1))
+    return fail(GQ_EINVAL, "stacked expert tensors take gq_moe_ffn, not a matvec");
+  if (matvec_block_lds(w, false) > 160 * 1024)
     return fail(GQ_EINVAL, "in_dim %d too large for the LDS-staged matvec", w->L.k);
   return GQ_OK;
 }
@@ -144,7 +156,7 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   w->L.k = in_dim;
   w->L.units = (in_dim + 255) / 256;
   w->L.chunks = gq::unit_chunks(dtype);
-  w->L.rt = gq::choose_rt(dtype, out_dim, w->L.units);
+  w->L.rt = std::max(out_dim, 1);  // one tile: the whole matrix
   // Stacked expert tensors: a tile must not straddle two experts, and only
   // a few experts run per token, so tiles are small (at most three wave
   // iterations: rt * units <= 192) to spread each expert over many waves.
@@ -196,8 +208,9 @@ namespace gq {
 hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, float *const *ys,
                          hipStream_t st, bool pair) {
   const gq_weight *w0 = ws[0];
-  if (pair) {  // {gate, up}: one segment of gate tiles, up as the second matrix
+  if (pair) {  // {gate, up}: gate rows split over the blocks, up streamed alongside
     if (count != 2) return hipErrorInvalidValue;
+    if (w0->L.rows == 0) return hipSuccess;
     MvArgs a{};
     a.in = in;
     a.grid = g_dev.grid;
@@ -206,11 +219,10 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
     a.chunks = w0->L.chunks;
     a.pair = 1;
     a.nseg = 2;
-    a.seg[0] = MvSeg{w0->body, w0->d, ys[0], w0->L.rows, w0->L.rt, 0};
-    a.seg[1] = MvSeg{ws[1]->body, ws[1]->d, nullptr, ws[1]->L.rows, ws[1]->L.rt, 0};
-    a.total_tiles = num_tiles(w0->L);
-    a.part_floats = 2 * ((w0->L.rt * w0->L.units + 63) / 64 * 64);
-    return a.total_tiles ? launch_matvec(a, w0->L.dtype, st) : hipSuccess;
+    a.seg[0] = MvSeg{w0->body, w0->d, ys[0], w0->L.rows, 0, 0};
+    a.seg[1] = MvSeg{ws[1]->body, ws[1]->d, nullptr, ws[1]->L.rows, 0, 0};
+    matvec_plan(a, g_dev.num_cus);
+    return launch_matvec(a, w0->L.dtype, st);
   }
   for (int base = 0; base < count; base += MV_MAX_SEG) {
     MvArgs a{};
@@ -219,19 +231,15 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
     a.k = w0->L.k;
     a.units = w0->L.units;
     a.chunks = w0->L.chunks;
-    int tiles = 0, ns = 0, part = 64;
+    int ns = 0;
     for (int i = base; i < count && i < base + MV_MAX_SEG; i++) {
       const gq_weight *w = ws[i];
       if (w->L.rows == 0) continue;
-      a.seg[ns++] = MvSeg{w->body, w->d, ys[i], w->L.rows, w->L.rt, tiles};
-      tiles += num_tiles(w->L);
-      const int uit = w->L.rt * w->L.units;
-      part = std::max(part, (uit + 63) / 64 * 64);
+      a.seg[ns++] = MvSeg{w->body, w->d, ys[i], w->L.rows, 0, 0};
     }
     if (ns == 0) continue;
     a.nseg = ns;
-    a.total_tiles = tiles;
-    a.part_floats = part;
+    matvec_plan(a, g_dev.num_cus);
     hipError_t e = launch_matvec(a, w0->L.dtype, st);
     if (e != hipSuccess) return e;
   }
@@ -293,7 +301,8 @@ int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down
       down->L.rows != n_experts * h)
     return fail(GQ_EINVAL, "expert shapes disagree: gate %dx%d up %dx%d down %dx%d, experts %d",
                 gate->L.rows, gate->L.k, up->L.rows, up->L.k, down->L.rows, down->L.k, n_experts);
-  if (gate->L.rt != up->L.rt || f % gate->L.rt || h % down->L.rt)
+  if (gate->L.rt != up->L.rt || gate->L.rt > 64 || down->L.rt > 64 || f % gate->L.rt ||
+      h % down->L.rt)
     return fail(GQ_EINVAL, "expert tensors must be uploaded with gq_upload_experts");
   if (!logits_dev || !x_dev || !out_dev) return fail(GQ_EINVAL, "null MoE buffer");
   const int pairs = T * top_k;
@@ -559,9 +568,7 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
         d->wgate[l]->L.dtype != d->wup[l]->L.dtype)
       return fail(GQ_EINVAL, "layer %d: q/k/v and gate/up must share a dtype", l);
     const gq_weight *g = d->wgate[l];
-    if (d->wup[l]->L.rt != g->L.rt ||
-        gq::matvec_lds_bytes(g->L.dtype, g->L.units, 2 * ((g->L.rt * g->L.units + 63) / 64 * 64)) >
-            160 * 1024)
+    if (d->wup[l]->L.rows != g->L.rows || matvec_block_lds(g, true) > 160 * 1024)
       return fail(GQ_EINVAL, "layer %d: ffn_gate/ffn_up layouts do not pair", l);
   }
   if ((rc = check_w(d->lm_head, d->vocab, H, "output", -1))) return rc;

@@ -21,14 +21,23 @@ namespace gq {
 constexpr int MV_MAX_SEG = 4;
 constexpr float LIMB_RANGE = 8323072.0f;  // 127 * 65536: |X| <= this
 
+// One matrix of a matvec launch.  Its rows are split into nblk contiguous
+// ranges of equal size (+-1 row), one per block, blocks blk_begin ..
+// blk_begin + nblk - 1.
 struct MvSeg {
   const uint8_t *body;
   const uint16_t *d;
   float *y;
   int rows;
-  int rt;
-  int tile_begin;  // first global tile (= wave) of this segment
+  int blk_begin;
+  int nblk;
 };
+
+// Threads per matvec block: as many waves as the format's registers allow
+// (bytes in flight set the HBM throughput): 3 per SIMD for Q4_K/Q5_K, 2
+// for the others.
+__host__ __device__ constexpr int mv_threads(int fmt) { return fmt == 12 || fmt == 13 ? 768 : 512; }
+constexpr int MV_BLOCKS_PER_CU = 1;
 
 // Where the matvec input vector comes from.
 enum MvSource {
@@ -52,8 +61,8 @@ struct MvArgs {
   MvIn in;
   const uint32_t *grid;  // IQ3_XXS codebook (device)
   int k, units, chunks;
-  int part_floats;       // LDS floats per wave for per-unit partial sums
-  int total_tiles;
+  int part_floats;       // LDS floats of per-unit partial sums per block
+  int blocks;
   int pair;              // 1: seg[0] = gate, seg[1] = up (same shape); y0 = silu(g) * u
   int nseg;
   MvSeg seg[MV_MAX_SEG];
@@ -79,7 +88,12 @@ struct MoeArgs {
 
 hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st);
 
-size_t matvec_lds_bytes(int dtype, int units, int part_floats);
+// LDS bytes of a matvec block: x limbs, records, codebook and part_total
+// floats of partial sums.
+size_t matvec_lds_bytes(int dtype, int units, int part_total);
+// Split the segments' rows over blocks (about MV_BLOCKS_PER_CU per CU) and
+// size the partial-sum region; returns the LDS bytes a block needs.
+size_t matvec_plan(MvArgs &a, int num_cus);
 hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st);
 
 // Decode step state in device memory (advanced by the argmax kernel).
@@ -121,7 +135,6 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
 const uint32_t *device_grid();
 
 // Rows per tile for a matrix (chosen at upload).
-int choose_rt(int dtype, int rows, int units);
 
 // Re-lay a ggml tensor already on the device into the wave-tiled layout.
 hipError_t launch_repack(const Layout &L, const uint8_t *raw, uint8_t *body, uint16_t *d,

@@ -24,6 +24,8 @@
 //      Q8_0  sum d*q*x               = d*s*sum(q X)
 //  * Per-unit partial sums go to LDS and are reduced per row in a fixed
 //    order (deterministic results).
+#include <algorithm>
+#include <cmath>
 #include <cstdlib>
 
 #include "gq_device.h"
@@ -46,13 +48,13 @@ struct Smem {
   float *red;             // 16 floats of block reduction scratch
 };
 
-__host__ __device__ inline size_t smem_layout(int units, int part_floats, Smem *s, char *base) {
+__host__ __device__ inline size_t smem_layout(int units, int part_total, Smem *s, char *base) {
   size_t o = 0;
   auto take = [&](size_t n) { size_t r = o; o += (n + 15) & ~(size_t)15; return r; };
   const size_t limb = (size_t)units * LIMB_STRIDE;
   const size_t o2 = take(limb), o1 = take(limb), o0 = take(limb);
   const size_t oaux = take((size_t)units * AUX_STRIDE), og = take(1024);
-  const size_t op = take((size_t)4 * part_floats * 4);
+  const size_t op = take((size_t)part_total * 4);
   const size_t ored = take(64);
   if (s) {
     s->red = (float *)(base + ored);
@@ -256,11 +258,16 @@ __device__ __forceinline__ void stage_x(int kpad, int e0, const float (&xv)[16],
       xs += X;
       V[r] = ((uint32_t)X + 0x808080u) ^ 0x808080u;
     }
-    w0[q] = (V[0] & 0xffu) | ((V[1] & 0xffu) << 8) | ((V[2] & 0xffu) << 16) | (V[3] << 24);
-    w1[q] = ((V[0] >> 8) & 0xffu) | (V[1] & 0xff00u) | ((V[2] & 0xff00u) << 8) |
-            ((V[3] >> 8) << 24);
-    w2[q] = ((V[0] >> 16) & 0xffu) | ((V[1] >> 8) & 0xff00u) | (V[2] & 0xff0000u) |
-            ((V[3] >> 16) << 24);
+    // Byte gathers (v_perm_b32: selector byte i picks byte s of {b, a}):
+    // lo = {V0.b0, V1.b0, V0.b1, V1.b1}, hi = {V0.b2, V1.b2, 0, 0} per pair,
+    // then limb byte k of the four values from the two pairs.
+    const uint32_t l01 = __builtin_amdgcn_perm(V[1], V[0], 0x05010400u);
+    const uint32_t l23 = __builtin_amdgcn_perm(V[3], V[2], 0x05010400u);
+    const uint32_t h01 = __builtin_amdgcn_perm(V[1], V[0], 0x0c0c0602u);
+    const uint32_t h23 = __builtin_amdgcn_perm(V[3], V[2], 0x0c0c0602u);
+    w0[q] = __builtin_amdgcn_perm(l23, l01, 0x05040100u);
+    w1[q] = __builtin_amdgcn_perm(l23, l01, 0x07060302u);
+    w2[q] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
   }
   const int lo = (e0 >> 8) * LIMB_STRIDE + (e0 & 255);
   *(uint4 *)(S.l2 + lo) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
@@ -413,73 +420,33 @@ struct XNorm {
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = t;
   }
   __device__ __forceinline__ float scale(const float *red) const {
-    const float t = (red[0] + red[1]) + (red[2] + red[3]);
+    const int nw = blockDim.x >> 6;
+    float t = 0.f;
+    for (int i = 0; i < nw; i++) t += red[i];
     return 1.0f / sqrtf(t / (float)k + eps);
   }
 };
 
-// One wave's work: tile t of a matrix (and with NT = 2 the same tile of a
-// second matrix of the same shape, body2 / d2).
-struct WaveJob {
-  const uint8_t *body;
-  const uint16_t *d;
-  const uint8_t *body2;
-  const uint16_t *d2;
-  float *y;
-  int rows, rt, t;
-  bool valid;
-};
-
-// The body shared by every matvec kernel: stage x (limbs) in LDS, stream
-// the job's tile(s) with two units per lane in flight, reduce rows.  All
-// four waves of the block must share the x source (they share the
-// staging).  The raw loads of the first NP passes of 4096 inputs are
-// issued together, then the first weight unit, which stays in flight
-// while x is converted; later passes follow one by one.  (Issuing more
-// weight units before the staging keeps more registers live through it
-// and costs more in occupancy than it gains.)
-template <int FMT, int NP, int NT, class XS>
-__device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_floats,
-                                            const uint32_t *gsrc, XS &xsrc, char *smem_raw) {
-  Smem S;
-  smem_layout(U, part_floats, &S, smem_raw);
-  constexpr int C = Fmt<FMT>::C;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int t = job.t;
-  const int rows_here = min(job.rt, job.rows - t * job.rt);
-  const int uit = rows_here * U;
-  const int iters = (uit + 63) >> 6;
-  const int nv_last = uit - 64 * (iters - 1);
-  const int total_it = NT * iters;
-  const long tile_base = (long)t * job.rt * U * C * 16;
-  const long dbase = (long)t * job.rt * U;
-  auto unit_ptr = [&](int itg, long &cstride, const uint16_t *&dp) -> const uint8_t * {
-    const bool second = NT == 2 && itg >= iters;
-    const int it = second ? itg - iters : itg;
-    const bool last = it == iters - 1;
-    const int l = last ? min(lane, nv_last - 1) : lane;
-    cstride = last ? 16L * nv_last : 1024L;
-    dp = (second ? job.d2 : job.d) + dbase + 64 * it + l;
-    return (second ? job.body2 : job.body) + tile_base + (long)it * C * 1024 + 16 * l;
-  };
-
-  const int kpad = U * 256;
-  const int passes = (kpad + 4095) >> 12;
-  auto pass_e0 = [&](int p) { return 4096 * p + 16 * tid; };
+// Stage x for a block of NTH threads: the raw loads of the first NP passes
+// of 16 * NTH inputs are issued together, then pre() (which issues the
+// first weight loads, so they are in flight while x is converted), then the
+// conversion; later passes follow one by one.  Ends with a block barrier.
+// (Issuing more weight loads before the staging keeps more registers live
+// through it and costs more in occupancy than it gains.)
+template <int FMT, int NP, int NTH, class XS, class PRE>
+__device__ __forceinline__ void stage_block(XS &xsrc, int kpad, const Smem &S,
+                                            const uint32_t *gsrc, PRE &&pre) {
+  const int tid = threadIdx.x;
+  const int passes = (kpad + 16 * NTH - 1) / (16 * NTH);
+  auto pass_e0 = [&](int p) { return 16 * NTH * p + 16 * tid; };
   typename XS::Raw raw[NP];
 #pragma unroll
   for (int p = 0; p < NP; p++)
     if (p < passes) xsrc.issue(pass_e0(p), raw[p]);
   uint32_t gword = 0;
-  if constexpr (FMT == T_IQ3_XXS) gword = gsrc[tid];
+  if constexpr (FMT == T_IQ3_XXS) gword = gsrc[tid & 255];
   __builtin_amdgcn_sched_barrier(0);
-  Unit<FMT> A, B;
-  {
-    long cs;
-    const uint16_t *dp;
-    const uint8_t *p = unit_ptr(0, cs, dp);
-    load_unit<FMT>(A, p, cs, dp);
-  }
+  pre();
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int p = 0; p < NP; p++) {
@@ -498,86 +465,183 @@ __device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_
     xsrc.make(r1, e0, xv);
     stage_x<FMT == T_Q6_K>(kpad, e0, xv, S);
   }
-  if constexpr (FMT == T_IQ3_XXS) S.grid[tid] = gword;
+  if constexpr (FMT == T_IQ3_XXS)
+    if (tid < 256) S.grid[tid] = gword;
   xsrc.pre_barrier(S.red);
   __syncthreads();
-  const float rscale = xsrc.scale(S.red);
+}
 
-  float *part = S.part + wave * part_floats;
-  auto load_it = [&](Unit<FMT> &dst, int itg) {
-    long cs;
-    const uint16_t *dp;
-    const uint8_t *p = unit_ptr(itg, cs, dp);
-    load_unit<FMT>(dst, p, cs, dp);
+// One wave's work in the MoE kernels: tile t of a stacked expert matrix.
+struct WaveJob {
+  const uint8_t *body;
+  const uint16_t *d;
+  float *y;
+  int rows, rt, t;
+  bool valid;
+};
+
+// The MoE body: a 256-thread block stages x, each wave streams its tile
+// with two units per lane in flight and reduces its rows.
+template <int FMT, class XS>
+__device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_floats,
+                                            const uint32_t *gsrc, XS &xsrc, char *smem_raw) {
+  Smem S;
+  smem_layout(U, 4 * part_floats, &S, smem_raw);
+  constexpr int C = Fmt<FMT>::C;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t = job.t;
+  const int rows_here = min(job.rt, job.rows - t * job.rt);
+  const int uit = rows_here * U;
+  const int iters = (uit + 63) >> 6;
+  const int nv_last = uit - 64 * (iters - 1);
+  const long tile_base = (long)t * job.rt * U * C * 16;
+  const long dbase = (long)t * job.rt * U;
+  auto load_it = [&](Unit<FMT> &dst, int it) {
+    const bool last = it == iters - 1;
+    const int l = last ? min(lane, nv_last - 1) : lane;
+    load_unit<FMT>(dst, job.body + tile_base + (long)it * C * 1024 + 16 * l,
+                   last ? 16L * nv_last : 1024L, job.d + dbase + 64 * it + l);
   };
-  auto consume = [&](const Unit<FMT> &src, int itg) {
-    const bool second = NT == 2 && itg >= iters;
-    const int it = second ? itg - iters : itg;
+  Unit<FMT> A, B;
+  stage_block<FMT, 1, 256>(xsrc, U * 256, S, gsrc, [&] { load_it(A, 0); });
+  const float rscale = xsrc.scale(S.red);
+  float *part = S.part + wave * part_floats;
+  auto consume = [&](const Unit<FMT> &src, int it) {
     const int j = 64 * it + lane;
     const float v = unit_dot<FMT>(src, j % U, S);
-    if (j < uit) part[(second ? 64 * iters : 0) + j] = v;
+    if (j < uit) part[j] = v;
   };
-  // Two units in flight per lane; the wave-uniform conditions keep the
-  // last iterations from loading a unit twice with only two inlined copies
-  // of the unit arithmetic (kernel code size is launch latency: every
-  // launch of a decode step starts with a cold instruction cache).
-  for (int it = 0; it < total_it; it += 2) {
-    const bool hb = it + 1 < total_it;
+  for (int it = 0; it < iters; it += 2) {
+    const bool hb = it + 1 < iters;
     if (hb) load_it(B, it + 1);
     consume(A, it);
-    if (it + 2 < total_it) load_it(A, it + 2);
+    if (it + 2 < iters) load_it(A, it + 2);
     if (hb) consume(B, it + 1);
   }
-  __syncthreads();
-
   // Row sums: 64/RT lanes per row, fixed order.
   const int lpr = 64 / job.rt;
   const int row = lane / lpr, sub = lane % lpr;
-  float v[NT];
-#pragma unroll
-  for (int m = 0; m < NT; m++) {
-    const float *pm = part + m * 64 * iters;
-    float acc = 0.f;
-    if (row < rows_here)
-      for (int c = sub; c < U; c += lpr) acc += pm[row * U + c];
-    for (int off = lpr >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-    v[m] = acc * rscale;
-  }
-  if (job.valid && sub == 0 && row < rows_here) {
-    float out = v[0];
-    if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
-    job.y[t * job.rt + row] = out;
-  }
+  float acc = 0.f;
+  if (row < rows_here)
+    for (int c = sub; c < U; c += lpr) acc += part[row * U + c];
+  for (int off = lpr >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (job.valid && sub == 0 && row < rows_here) job.y[t * job.rt + row] = acc * rscale;
 }
 
-// Plain / multi-segment matvec: one wave per tile over the segments.  With
-// NT = 2 (gate/up pair) there is one segment of tiles and seg[1] supplies
-// the second matrix.
+// Decode matvec over one or more matrices (segments) sharing the input.
+// Weights are one tile per matrix, i.e. the units of the whole matrix in
+// row-major order, 64 per iteration.  Block b of a segment owns rows
+// [r0, r1) = [rows * lb / nblk, rows * (lb + 1) / nblk), i.e. units
+// [r0 * U, r1 * U): the blocks get equal work (+-1 row) and the grid is one
+// block per CU, so every block stages x exactly once and all of them run
+// at the same time.  The block's iterations (first and last ones partial:
+// lanes outside its units load nothing) are dealt round-robin to its
+// waves, each keeping two units per lane in flight; per-unit partial sums
+// go to LDS and are reduced per row in a fixed order.  With NT = 2
+// (gate/up pair) the block streams the same units of seg[1] as well and
+// writes silu(g) * u.
 template <int FMT, bool K4, int SRC, int NP, int NT>
-__global__ __launch_bounds__(256) void k_matvec(MvArgs a) {
+__global__ __launch_bounds__(mv_threads(FMT)) void k_matvec(MvArgs a) {
   extern __shared__ __align__(16) char smem_raw[];
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const bool valid = gw < a.total_tiles;
-  const int gwc = valid ? gw : a.total_tiles - 1;
-  // Segment of this wave (wave-uniform selects over scalar arguments).
+  constexpr int NTH = mv_threads(FMT), NW = NTH / 64;
+  constexpr int C = Fmt<FMT>::C;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
+  const int b = blockIdx.x;
   MvSeg sg = a.seg[0];
   if constexpr (NT == 1) {
 #pragma unroll
     for (int i = 1; i < MV_MAX_SEG; i++)
-      if (i < a.nseg && gwc >= a.seg[i].tile_begin) sg = a.seg[i];
+      if (i < a.nseg && b >= a.seg[i].blk_begin) sg = a.seg[i];
   }
-  const WaveJob job{sg.body, sg.d, a.seg[1].body, a.seg[1].d, sg.y, sg.rows, sg.rt,
-                    gwc - sg.tile_begin, valid};
+  const int U = a.units;
+  const int lb = b - sg.blk_begin;
+  const int r0 = (int)((long)sg.rows * lb / sg.nblk);
+  const int r1 = (int)((long)sg.rows * (lb + 1) / sg.nblk);
+  const int j0 = r0 * U, j1 = r1 * U;
+  const int n_units = sg.rows * U;
+  const int iters = (n_units + 63) >> 6;
+  const int nv_last = n_units - 64 * (iters - 1);
+  const int it0 = j0 >> 6;
+  const int nit = j1 > j0 ? ((j1 + 63) >> 6) - it0 : 0;
+  const int work = NT * nit;
+  Smem S;
+  smem_layout(U, a.part_floats, &S, smem_raw);
+
+  // Work item w: iteration it0 + w % nit of matrix w / nit.
+  auto load_w = [&](Unit<FMT> &dst, int w) {
+    const bool m = NT == 2 && w >= nit;
+    const int it = it0 + (m ? w - nit : w);
+    const int j = 64 * it + lane;
+    const bool last = it == iters - 1;
+    const int l = last ? min(lane, nv_last - 1) : lane;
+    const uint8_t *p = (m ? a.seg[1].body : sg.body) + (long)it * C * 1024 + 16 * l;
+    const uint16_t *dp = (m ? a.seg[1].d : sg.d) + 64L * it + l;
+    if (j >= j0 && j < j1) load_unit<FMT>(dst, p, last ? 16L * nv_last : 1024L, dp);
+  };
+  auto consume = [&](const Unit<FMT> &src, int w) {
+    const int it = it0 + (NT == 2 && w >= nit ? w - nit : w);
+    const int j = 64 * it + lane;
+    const float v = unit_dot<FMT>(src, j % U, S);
+    // (The branch also keeps the scheduler from interleaving two units'
+    // arithmetic, which needs more registers than 2 waves per SIMD have.)
+    if (j >= j0 && j < j1) S.part[64 * w + lane] = v;
+  };
+
+  Unit<FMT> A, B;
+  auto first = [&] {
+    if (wave < work) load_w(A, wave);
+  };
+  float rscale = 1.f;
   if constexpr (SRC == MV_NORM) {
     const float *x = a.in.tok ? a.in.x + (long)(*a.in.tok) * a.k : a.in.x;
-    XNorm<K4> xs{x, a.in.r, a.in.nw, blockIdx.x == 0 ? a.in.xo : nullptr, a.k, a.in.eps};
-    matvec_wave<FMT, NP, NT>(job, a.units, a.part_floats, a.grid, xs, smem_raw);
+    XNorm<K4> xs{x, a.in.r, a.in.nw, b == 0 ? a.in.xo : nullptr, a.k, a.in.eps};
+    stage_block<FMT, NP, NTH>(xs, U * 256, S, a.grid, first);
+    rscale = xs.scale(S.red);
   } else if constexpr (SRC == MV_SWIGLU) {
     XSwiGLU<K4> xs{a.in.xg, a.in.xu, a.k};
-    matvec_wave<FMT, NP, NT>(job, a.units, a.part_floats, a.grid, xs, smem_raw);
+    stage_block<FMT, NP, NTH>(xs, U * 256, S, a.grid, first);
   } else {
     XPlain<K4> xs{a.in.x, a.k};
-    matvec_wave<FMT, NP, NT>(job, a.units, a.part_floats, a.grid, xs, smem_raw);
+    stage_block<FMT, NP, NTH>(xs, U * 256, S, a.grid, first);
+  }
+  // Two units per lane in flight; two inlined copies of the unit arithmetic
+  // (kernel code size is launch latency: every launch of a decode step
+  // starts with a cold instruction cache).
+  for (int w = wave; w < work; w += 2 * NW) {
+    const int wb = w + NW;
+    if (wb < work) load_w(B, wb);
+    consume(A, w);
+    if (w + 2 * NW < work) load_w(A, w + 2 * NW);
+    if (wb < work) consume(B, wb);
+  }
+  __syncthreads();
+
+  // Row sums: G lanes per row (a power of two, at most 8, U and the threads
+  // per row), strided partial sums then a butterfly; a fixed order.  Few
+  // lanes per row: the butterfly steps are dependent LDS round trips.
+  const int rows_b = r1 - r0;
+  int G = 1;
+  while (2 * G <= 8 && 2 * G <= U && 2 * G * rows_b <= NTH) G <<= 1;
+  const int per = NTH / G;
+  const int base = j0 - 64 * it0;
+  for (int rb = 0; rb < rows_b; rb += per) {
+    const int r = rb + tid / G, sub = tid % G;
+    float v[NT];
+#pragma unroll
+    for (int m = 0; m < NT; m++) {
+      const float *pm = S.part + m * 64 * nit + base + r * U;
+      float acc = 0.f;
+      if (r < rows_b)
+        for (int c = sub; c < U; c += G) acc += pm[c];
+      for (int off = G >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+      v[m] = acc * rscale;
+    }
+    if (sub == 0 && r < rows_b) {
+      float out = v[0];
+      if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
+      sg.y[r0 + r] = out;
+    }
   }
 }
 
@@ -597,11 +661,11 @@ __global__ __launch_bounds__(256) void k_moe_gate_up(MoeArgs a) {
   const int gwc = valid ? gw : 2 * tiles - 1;
   const bool is_up = gwc >= tiles;
   const int lt = is_up ? gwc - tiles : gwc;
-  const WaveJob job{is_up ? a.up : a.gate, is_up ? a.up_d : a.gate_d, nullptr, nullptr,
+  const WaveJob job{is_up ? a.up : a.gate, is_up ? a.up_d : a.gate_d,
                     (is_up ? a.tmp_u : a.tmp_g) + (long)p * a.f - (long)e * a.f,
                     a.n_experts * a.f, a.rt_h, e * tiles + lt, valid};
   XPlain<K4> xs{a.x + (long)tok * a.h, a.h};
-  matvec_wave<FMT, 1, 1>(job, a.units_h, a.part_h, a.grid, xs, smem_raw);
+  matvec_wave<FMT>(job, a.units_h, a.part_h, a.grid, xs, smem_raw);
 }
 
 // Stage 2: down_e . (silu(g) * u) for every pair.
@@ -614,10 +678,10 @@ __global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
   const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
   const bool valid = gw < tiles;
   const int gwc = valid ? gw : tiles - 1;
-  const WaveJob job{a.down, a.down_d, nullptr, nullptr, a.tmp_y + (long)p * a.h - (long)e * a.h,
+  const WaveJob job{a.down, a.down_d, a.tmp_y + (long)p * a.h - (long)e * a.h,
                     a.n_experts * a.h, a.rt_f, e * tiles + gwc, valid};
   XSwiGLU<K4> xs{a.tmp_g + (long)p * a.f, a.tmp_u + (long)p * a.f, a.f};
-  matvec_wave<FMT, 1, 1>(job, a.units_f, a.part_f, a.grid, xs, smem_raw);
+  matvec_wave<FMT>(job, a.units_f, a.part_f, a.grid, xs, smem_raw);
 }
 
 // Router: per token, top-k of the logits (ties: lower index) and their
@@ -678,29 +742,41 @@ __global__ void k_moe_combine(const float *tmp_y, const float *w, int T, int top
 }
 
 // ------------------------------------------------------------- launch
-size_t matvec_lds_bytes(int dtype, int units, int part_floats) {
+size_t matvec_lds_bytes(int dtype, int units, int part_total) {
   (void)dtype;
-  return smem_layout(units, part_floats, nullptr, nullptr);
+  return smem_layout(units, part_total, nullptr, nullptr);
 }
 
-// Rows per tile: enough tiles (waves) to fill the GPU, few idle lanes in a
-// tile's last iteration.
-int choose_rt(int dtype, int rows, int units) {
-  (void)dtype;
-  if (const char *e = getenv("GQ_MV_RT")) return atoi(e);
-  int best = 1;
-  double best_score = -1;
-  for (int rt = 1; rt <= 64; rt *= 2) {
-    const long uit = (long)rt * units;
-    if (rt > 1 && uit > 2048) break;  // per-wave partial sums stay <= 8 KiB of LDS
-    const long iters = (uit + 63) / 64;
-    const double lane_eff = (double)uit / (64.0 * iters);
-    const long waves = (rows + rt - 1) / rt;
-    const double fill = waves >= 2048 ? 1.0 : (double)waves / 2048.0;
-    const double score = lane_eff * fill * (iters >= 2 ? 1.0 : 0.97);
-    if (score > best_score + 1e-9) { best_score = score; best = rt; }
+size_t matvec_plan(MvArgs &a, int num_cus) {
+  static const int bpc = [] {
+    const char *e = getenv("GQ_MV_BLOCKS_PER_CU");  // tuning override
+    return e && atoi(e) > 0 ? atoi(e) : MV_BLOCKS_PER_CU;
+  }();
+  const int nt = a.pair ? 2 : 1, nseg = a.pair ? 1 : a.nseg;
+  long total = 0;
+  for (int i = 0; i < nseg; i++) total += a.seg[i].rows;
+  long target = std::max(1, num_cus * bpc);
+  for (;;) {
+    int blk = 0;
+    long max_units = 0;
+    for (int i = 0; i < nseg; i++) {
+      const int rows = a.seg[i].rows;
+      const int nb = (int)std::max(1L, std::min((long)rows, std::lround((double)target * rows / total)));
+      a.seg[i].blk_begin = blk;
+      a.seg[i].nblk = nb;
+      blk += nb;
+      max_units = std::max(max_units, (long)((rows + nb - 1) / nb) * a.units);
+    }
+    // A block's units may start mid-iteration: one more iteration.
+    const int part = (int)(nt * 64 * ((max_units + 63) / 64 + 1));
+    const size_t lds = matvec_lds_bytes(0, a.units, part);
+    if (lds <= 160 * 1024 || target >= total) {
+      a.blocks = blk;
+      a.part_floats = part;
+      return lds;
+    }
+    target *= 2;
   }
-  return best;
 }
 
 template <int FMT, bool K4, int SRC, int NP, int NT>
@@ -709,17 +785,17 @@ static hipError_t launch_t(const MvArgs &a, hipStream_t st) {
   if (lds > 64 * 1024)
     (void)hipFuncSetAttribute((const void *)k_matvec<FMT, K4, SRC, NP, NT>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  const int blocks = (a.total_tiles + 3) / 4;
-  hipLaunchKernelGGL((k_matvec<FMT, K4, SRC, NP, NT>), dim3(blocks), dim3(256), lds, st, a);
+  hipLaunchKernelGGL((k_matvec<FMT, K4, SRC, NP, NT>), dim3(a.blocks), dim3(mv_threads(FMT)), lds, st, a);
   return hipGetLastError();
 }
 
-// Instances: plain x with 1, 4 or 8 staging passes in flight together;
+// Instances: plain x with 1, 4 or (512-thread blocks) 8 staging passes in
+// flight together;
 // the normalised source (k % 4 == 0, one pass in flight) alone or for a
 // gate/up pair; the SwiGLU source with one pass in flight.
 template <int FMT>
 static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
-  const int passes = (a.units + 15) / 16;
+  const int passes = (a.units * 256 + 16 * mv_threads(FMT) - 1) / (16 * mv_threads(FMT));
   const bool k4 = a.k % 4 == 0;
   switch (a.in.src) {
   case MV_NORM:
@@ -732,9 +808,13 @@ static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
     if (a.pair) return hipErrorInvalidValue;
     if (passes == 1)
       return k4 ? launch_t<FMT, true, MV_X, 1, 1>(a, st) : launch_t<FMT, false, MV_X, 1, 1>(a, st);
-    if (passes <= 4)
+    // (Any NP is correct: passes past NP are staged one by one.  768-thread
+    // blocks stage at most 4 passes within the LDS limit.)
+    if (passes <= 4 || mv_threads(FMT) > 512)
       return k4 ? launch_t<FMT, true, MV_X, 4, 1>(a, st) : launch_t<FMT, false, MV_X, 4, 1>(a, st);
-    return k4 ? launch_t<FMT, true, MV_X, 8, 1>(a, st) : launch_t<FMT, false, MV_X, 8, 1>(a, st);
+    if constexpr (mv_threads(FMT) <= 512)
+      return k4 ? launch_t<FMT, true, MV_X, 8, 1>(a, st) : launch_t<FMT, false, MV_X, 8, 1>(a, st);
+    return hipErrorInvalidValue;
   }
 }
 
@@ -745,8 +825,8 @@ hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st) {
   const int pairs = T * a.top_k;
   hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(256), 0, st, a.logits, a.n_experts, a.top_k,
                      a.ids, a.w);
-  const size_t lds1 = matvec_lds_bytes(a.fmt, a.units_h, a.part_h);
-  const size_t lds2 = matvec_lds_bytes(a.fmt, a.units_f, a.part_f);
+  const size_t lds1 = matvec_lds_bytes(a.fmt, a.units_h, 4 * a.part_h);
+  const size_t lds2 = matvec_lds_bytes(a.fmt, a.units_f, 4 * a.part_f);
   const dim3 g1((2 * (a.f / a.rt_h) + 3) / 4, pairs), g2(((a.h / a.rt_f) + 3) / 4, pairs);
 #define GQ_MOE_LAUNCH(F)                                                                     \
   if (a.fmt == F) {                                                                          \
