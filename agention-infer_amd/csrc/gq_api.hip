@@ -553,10 +553,10 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   const int H = d->hidden, hd = d->head_dim, nh = d->n_heads, nkv = d->n_kv_heads;
   if (d->n_layers <= 0 || H <= 0 || H % 4 || (hd != 64 && hd != 128) || nh <= 0 || nkv <= 0 ||
       nh % nkv || nh / nkv > 8 || d->ffn <= 0 || d->vocab <= 0 || d->ctx <= 0 ||
-      d->ctx > 256 * gq::ATT_CHUNK)
+      d->ctx > gq::ATT_MAX_CTX)
     return fail(GQ_EINVAL, "bad model shape (hidden a multiple of 4, head_dim 64 or 128, "
                            "n_heads a multiple of n_kv_heads with at most 8 query heads per KV "
-                           "head, ctx <= %d)", 256 * gq::ATT_CHUNK);
+                           "head, ctx <= %d)", gq::ATT_MAX_CTX);
   for (int l = 0; l < d->n_layers; l++) {
     if ((rc = check_w(d->wq[l], nh * hd, H, "wq", l)) || (rc = check_w(d->wk[l], nkv * hd, H, "wk", l)) ||
         (rc = check_w(d->wv[l], nkv * hd, H, "wv", l)) || (rc = check_w(d->wo[l], H, nh * hd, "wo", l)) ||
@@ -595,9 +595,9 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   const int nb_amax = (d->vocab + gq::ARGMAX_SPAN - 1) / gq::ARGMAX_SPAN;
   const size_t nbuf = 3 * ((size_t)H + 16) + 2 * ((size_t)nh * hd + 16) + 2 * (kvd + 16) +
                       ((size_t)d->ffn + 16) + ((size_t)d->vocab + 16) +
-                      ((size_t)nh * L.att_chunks * (2 + hd) + 16) + (nb_amax + 16);
+                      ((size_t)nh * L.att_chunks * (2 + hd) + 16) + (nb_amax + 16) + (hd / 2 + 16);
   int *ibuf = nullptr;
-  const size_t nibuf = (size_t)nkv + 1 + nb_amax;
+  const size_t nibuf = 1 + (size_t)nb_amax;
   if (!rc) rc = dalloc(m, &buf, nbuf);
   if (!rc) rc = dalloc(m, &ibuf, nibuf);
   if (!rc) rc = dalloc(m, &L.state, 1);
@@ -610,7 +610,8 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   L.k = take(kvd); L.v = take(kvd); L.h = take(d->ffn);
   L.logits = take(d->vocab); L.att_part = take((size_t)nh * L.att_chunks * (2 + hd));
   L.amax_v = take(nb_amax);
-  L.att_count = ibuf; L.amax_count = ibuf + nkv; L.amax_i = ibuf + nkv + 1;
+  L.rope_den = take(hd / 2);
+  L.amax_count = ibuf; L.amax_i = ibuf + 1;
   hipError_t e = hipSuccess;
   for (int l = 0; l < d->n_layers && e == hipSuccess; l++) {
     e = hipMemcpy(norms + (size_t)(2 * l) * H, d->attn_norm[l], H * 4, hipMemcpyHostToDevice);
@@ -622,9 +623,14 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   if (e == hipSuccess)
     e = hipMemcpy(norms + (size_t)2 * d->n_layers * H, d->output_norm, H * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemcpy(embd, d->embd, (size_t)d->vocab * H * 4, hipMemcpyHostToDevice);
+  // RoPE: angle(pos, i) = pos / theta^(2i/hd), the divisor as the CPU path
+  // computes it (cpu_path.rs:99-133).
+  std::vector<float> den(hd / 2);
+  for (int i = 0; i < hd / 2; i++) den[i] = powf(d->theta, 2.0f * (float)i / (float)hd);
   // counters of the last-block merges start (and end every launch) at zero
   if (e == hipSuccess) e = hipMemset(ibuf, 0, nibuf * sizeof(int));
   if (e == hipSuccess) e = hipMemset(buf, 0, nbuf * sizeof(float));
+  if (e == hipSuccess) e = hipMemcpy(L.rope_den, den.data(), den.size() * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) e = hipMemset(L.kcache, 0, (size_t)d->n_layers * d->ctx * kvd * 2);
   if (e == hipSuccess) e = hipMemset(L.vcache, 0, (size_t)d->n_layers * d->ctx * kvd * 2);
   if (e != hipSuccess) { delete m; return fail(GQ_EHIP, "model upload failed: %s", hipGetErrorString(e)); }

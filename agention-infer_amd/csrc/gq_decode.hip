@@ -31,7 +31,9 @@ namespace gq {
 // ----------------------------------------------------------- attention
 // Block (kv head kh, chunk c): positions [c*CH, min((c+1)*CH, n)) for the
 // `group` query heads kh*group .. kh*group+group-1 (GQA: each K/V row is
-// read once for all of them), ATT_WAVES waves of 32 positions each.
+// read once for all of them), ATT_WAVES waves of 16 positions each; short
+// chunks so that the whole GPU shares the work (a 4096-position context is
+// 4 x 65 blocks).
 //   scores  s[g][t] = (q_g . k_t) / sqrt(hd)        (attention_into,
 //   softmax m_g = max s, p = exp(s - m_g), l_g = sum p   cpu_path.rs:141-194)
 //   values  o[g][d] = sum_t p[g][t] v_t[d]
@@ -41,18 +43,19 @@ namespace gq {
 // into f16 hi + lo parts, so each product is exact in fp32 and q is carried
 // to ~22 bits.  The V sum runs on fp32 FMAs, a lane owning HD/64 dims of
 // every row of its wave (no cross-lane reduction), then across waves.
-// The partial (m, l, o) of each (head, chunk) goes to `part`; the last
-// block of a KV head to finish (chunk counter) merges the chunks:
+// The partial (m, l, o) of each (head, chunk) goes to `part`; the next
+// kernel (k_attn_merge) merges the chunks:
 //   att[h] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
+// (A merge by the last block to finish costs every block a device-scope
+// release fence, which writes back its XCD's L2: slower than a launch.)
 // The block holding position pos = n - 1 also rotates the new k, rounds k
 // and v to f16 (KvDtype::F16::pack) and stores them in the cache; it uses
-// the rounded values for position pos itself.
+// the rounded values for position pos itself.  RoPE angles are
+// pos / den[i] with den[i] = theta^(2i/hd) from the host (cpu_path.rs:99-133).
 constexpr int ATT_MAXG = 8;      // query heads per KV head
-constexpr int ATT_MAXCH = 256;   // chunks (ctx <= 256 * ATT_CHUNK)
-constexpr int ATT_WAVES = 8;
+constexpr int ATT_WAVES = 4;
 constexpr int ATT_THREADS = 64 * ATT_WAVES;
-static_assert(ATT_WAVES == ATT_MAXG, "one wave per query head in the softmax");
-static_assert(ATT_CHUNK == 32 * ATT_WAVES, "32 positions per wave");
+static_assert(ATT_CHUNK == 16 * ATT_WAVES, "16 positions per wave");
 
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4a_t __attribute__((ext_vector_type(4)));
@@ -60,42 +63,37 @@ typedef float f32x4a_t __attribute__((ext_vector_type(4)));
 template <int HD>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     const float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc,
-    const DecodeState *st, int group, int kvd, float theta, float *part, int *count, float *att) {
+    const DecodeState *st, int group, int kvd, const float *rope_den, float *part) {
   constexpr int CH = ATT_CHUNK;
   constexpr int NW = ATT_WAVES;
-  constexpr int PW = CH / NW;  // positions per wave
-  constexpr int NT = PW / 16;  // 16-position MFMA tiles per wave
+  constexpr int PW = CH / NW;  // positions per wave: one 16-column MFMA tile
   constexpr int KS = HD / 32;  // MFMA depth steps
   constexpr int DPL = HD / 64; // value dims per lane
   constexpr int HALF = HD / 2;
   __shared__ float sp[ATT_MAXG][CH];
-  __shared__ float ored[NW][ATT_MAXG][HD];  // reused for the merge factors
-  __shared__ float qsh[ATT_MAXG][HD];
+  __shared__ __align__(16) float ored[NW][ATT_MAXG][HD];
+  __shared__ __align__(16) float qsh[ATT_MAXG][HD];
   __shared__ float rs[HALF], rc[HALF];
   __shared__ __align__(16) uint16_t knew[HD];
   __shared__ __align__(16) uint16_t vnew[HD];
   __shared__ float qmax_s[NW];
-  __shared__ int last_s;
-  static_assert(sizeof(ored) >= sizeof(float) * ATT_MAXG * ATT_MAXCH, "merge factors fit");
+  __shared__ float gm_s[ATT_MAXG], gl_s[ATT_MAXG];
 
   const int kh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int pos = st->pos, n = pos + 1, t0 = c * CH;
   if (t0 >= n) return;
-  const int nch = (n + CH - 1) / CH;
   const int nchunk_grid = gridDim.y;
   const int tw = t0 + wave * PW;  // first position of this wave
 
-  // K rows as MFMA B operands (row tw + 16*tt + lane%16, dims
-  // 8*(lane/16) + 32*ks), V dims DPL*lane of the wave's rows; clamped to
-  // n - 1 (unused past n).
-  uint4 kb[NT][KS];
-#pragma unroll
-  for (int tt = 0; tt < NT; tt++) {
-    const int t = min(tw + 16 * tt + (lane & 15), n - 1);
+  // K rows as MFMA B operands (row tw + lane%16, dims 8*(lane/16) + 32*ks),
+  // V dims DPL*lane of the wave's rows; clamped to n - 1 (unused past n).
+  uint4 kb[KS];
+  {
+    const int t = min(tw + (lane & 15), n - 1);
 #pragma unroll
     for (int ks = 0; ks < KS; ks++)
-      kb[tt][ks] = ldw4(kc + (long)t * kvd + (long)kh * HD + 8 * (lane >> 4) + 32 * ks);
+      kb[ks] = ldw4(kc + (long)t * kvd + (long)kh * HD + 8 * (lane >> 4) + 32 * ks);
   }
   uint32_t vr[PW];
 #pragma unroll
@@ -104,11 +102,12 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     vr[j] = DPL == 2 ? ldw1(p) : (uint32_t)ldh(p);
   }
 
-  // RoPE table for pair index i (cpu_path.rs:99-133, NEOX pairs d <-> d + hd/2).
+  // RoPE table for pair index i (NEOX pairs d <-> d + hd/2).
   if (tid < HALF) {
-    const float ang = (float)pos * 1.0f / powf(theta, 2.0f * (float)tid / (float)HD);
-    rs[tid] = sinf(ang);
-    rc[tid] = cosf(ang);
+    float sn, cs;
+    sincosf((float)pos / rope_den[tid], &sn, &cs);
+    rs[tid] = sn;
+    rc[tid] = cs;
   }
   __syncthreads();
   // New K/V row of this KV head: rotate k, round both to f16, store.
@@ -142,7 +141,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
 #pragma unroll
   for (int w = 1; w < NW; w++) qm = fmaxf(qm, qmax_s[w]);
 
-  // A operands: q * 2^e (max in [512, 1024)) as f16 hi + lo.
+  // A operands: q * 2^e (max in [512, 1024)) as f16 hi + lo; lane holds
+  // head lane%16, dims 8*(lane/16) + 32*ks .. +8.
   int ex = 0;
   (void)frexpf(qm, &ex);
   const float qscale = qm > 0.f ? ldexpf(1.0f, 10 - ex) : 1.0f;
@@ -151,9 +151,19 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     const int m = lane & 15;
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
+      float x8[8];
+      if (m < group) {
+        const float4 a = *(const float4 *)&qsh[m][8 * (lane >> 4) + 32 * ks];
+        const float4 b = *(const float4 *)&qsh[m][8 * (lane >> 4) + 32 * ks + 4];
+        x8[0] = a.x; x8[1] = a.y; x8[2] = a.z; x8[3] = a.w;
+        x8[4] = b.x; x8[5] = b.y; x8[6] = b.z; x8[7] = b.w;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) x8[j] = 0.f;
+      }
 #pragma unroll
       for (int j = 0; j < 8; j++) {
-        const float x = m < group ? qsh[m][8 * (lane >> 4) + 32 * ks + j] * qscale : 0.f;
+        const float x = x8[j] * qscale;
         const _Float16 h = (_Float16)x;
         ahi[ks][j] = h;
         alo[ks][j] = (_Float16)(x - (float)h);
@@ -161,55 +171,44 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     }
   }
 
-  // Scores: lane holds S[head 4*(lane/16) + i][position lane%16] per tile.
+  // Scores: lane holds S[head 4*(lane/16) + i][position tw + lane%16].
   {
     const float rsq = sqrtf((float)HD);
     const float inv_scale = 1.0f / qscale;  // a power of two: exact
-    uint4 kn[KS];  // the new row's fragments (read whether used or not)
+    const int tcol = tw + (lane & 15);
+    const bool isnew = tcol == pos;
+    f32x4a_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++) kn[ks] = *(const uint4 *)(knew + 8 * (lane >> 4) + 32 * ks);
+    for (int ks = 0; ks < KS; ks++) {
+      // the new row's fragment (read whether used or not)
+      const uint4 kn = *(const uint4 *)(knew + 8 * (lane >> 4) + 32 * ks);
+      const uint4 raw = make_uint4(isnew ? kn.x : kb[ks].x, isnew ? kn.y : kb[ks].y,
+                                   isnew ? kn.z : kb[ks].z, isnew ? kn.w : kb[ks].w);
+      f16x8_t bk;
+      __builtin_memcpy(&bk, &raw, 16);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, acc, 0, 0, 0);
+    }
 #pragma unroll
-    for (int tt = 0; tt < NT; tt++) {
-      const int tcol = tw + 16 * tt + (lane & 15);
-      const bool isnew = tcol == pos;
-      f32x4a_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KS; ks++) {
-        const uint4 raw = make_uint4(isnew ? kn[ks].x : kb[tt][ks].x, isnew ? kn[ks].y : kb[tt][ks].y,
-                                     isnew ? kn[ks].z : kb[tt][ks].z, isnew ? kn[ks].w : kb[tt][ks].w);
-        f16x8_t bk;
-        __builtin_memcpy(&bk, &raw, 16);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, acc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int g = 4 * (lane >> 4) + i;
-        if (g < group) sp[g][tcol - t0] = tcol < n ? acc[i] * inv_scale / rsq : -INFINITY;
-      }
+    for (int i = 0; i < 4; i++) {
+      const int g = 4 * (lane >> 4) + i;
+      if (g < group) sp[g][tcol - t0] = tcol < n ? acc[i] * inv_scale / rsq : -INFINITY;
     }
   }
   __syncthreads();
 
-  // Softmax statistics: wave g handles head g.
-  float mh = -INFINITY, lh = 0.f;
-  if (wave < group) {
-    float vals[CH / 64];
-#pragma unroll
-    for (int i = 0; i < CH / 64; i++) {
-      vals[i] = sp[wave][lane + 64 * i];
-      mh = fmaxf(mh, vals[i]);
+  // Softmax statistics of the chunk: wave w handles heads w, w + NW, ...;
+  // lane = position.
+  for (int g = wave; g < group; g += NW) {
+    const float val = sp[g][lane];
+    const float mh = wave_max(val);
+    const float p = expf(val - mh);  // exp(-inf) = 0 past n
+    sp[g][lane] = p;
+    const float lh = wave_sum(p);
+    if (lane == 0) {
+      gm_s[g] = mh;
+      gl_s[g] = lh;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) mh = fmaxf(mh, __shfl_xor(mh, off, 64));
-#pragma unroll
-    for (int i = 0; i < CH / 64; i++) {
-      const float p = expf(vals[i] - mh);  // exp(-inf) = 0 past n
-      sp[wave][lane + 64 * i] = p;
-      lh += p;
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) lh += __shfl_xor(lh, off, 64);
   }
   __syncthreads();
 
@@ -258,68 +257,95 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     for (int w = 0; w < NW; w++) s += ored[w][g][d];
     part[((long)(kh * group + g) * nchunk_grid + c) * (2 + HD) + 2 + d] = s;
   }
-  if (lane == 0 && wave < group) {
-    float *pm = part + ((long)(kh * group + wave) * nchunk_grid + c) * (2 + HD);
-    pm[0] = mh;
-    pm[1] = lh;
+  if (tid < group) {
+    float *pm = part + ((long)(kh * group + tid) * nchunk_grid + c) * (2 + HD);
+    pm[0] = gm_s[tid];
+    pm[1] = gl_s[tid];
   }
+}
 
-  // The last block of this KV head merges the chunks.  One thread per
-  // block fences (an agent-scope release writes back this XCD's L2; the
-  // barrier before it orders the whole block's stores), and the last
-  // block's acquire fence invalidates its caches before it reads the other
-  // blocks' partials.
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    const bool last = atomicAdd(count + kh, 1) == nch - 1;
-    if (last) __threadfence();
-    last_s = last;
-  }
-  __syncthreads();
-  if (!last_s) return;
-  float (*fac)[ATT_MAXCH] = (float (*)[ATT_MAXCH])&ored[0][0][0];
-  // fac[g][c] = e^(m_c - M) / L, wave g for head g (0 for c >= nch).
-  if (wave < group) {
-    const float *pm = part + (long)(kh * group + wave) * nchunk_grid * (2 + HD);
-    float m[ATT_MAXCH / 64], l[ATT_MAXCH / 64];
-    float M = -INFINITY;
+// Merge of the chunk partials: block h (query head) of ATT_MQ * HD threads,
+// thread (qq, d) sums dim d over the chunks c = qq, qq + ATT_MQ, ..., then
+// the quarters are added in order:
+//   att[h][d] = sum_c o_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M),
+// M = max_c m_c over the chunks holding positions <= pos.  Every load of
+// the first 16 * ATT_MQ chunks (m, l and o) is issued at the start.
+constexpr int ATT_MQ = 4;
+template <int HD>
+__global__ __launch_bounds__(ATT_MQ * HD) void k_attn_merge(const DecodeState *st, int nchunk_grid,
+                                                             const float *part, float *att) {
+  constexpr int NT = ATT_MQ * HD, NWV = NT / 64, R = 16;
+  __shared__ float fac[ATT_MAX_CTX / ATT_CHUNK];
+  __shared__ float red[NWV];
+  __shared__ float osum[ATT_MQ][HD];
+  const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = (st->pos + ATT_CHUNK) / ATT_CHUNK;
+  const float *ph = part + (long)h * nchunk_grid * (2 + HD);
+  const int qq = tid / HD, d = tid % HD;
+  const float *po = ph + 2 + d;
+  float vals[R];
 #pragma unroll
-    for (int i = 0; i < ATT_MAXCH / 64; i++) {
-      const int cc = lane + 64 * i;
-      m[i] = cc < nch ? pm[(long)cc * (2 + HD)] : -INFINITY;
-      l[i] = cc < nch ? pm[(long)cc * (2 + HD) + 1] : 0.f;
-      M = fmaxf(M, m[i]);
+  for (int j = 0; j < R; j++) {
+    const int c = qq + ATT_MQ * j;
+    vals[j] = c < nch ? po[(long)c * (2 + HD)] : 0.f;
+  }
+  float mv = -INFINITY, lv = 0.f;
+  if (tid < nch) {
+    mv = ph[(long)tid * (2 + HD)];
+    lv = ph[(long)tid * (2 + HD) + 1];
+  }
+  float M = mv;
+  for (int c = tid + NT; c < nch; c += NT) M = fmaxf(M, ph[(long)c * (2 + HD)]);
+  M = wave_max(M);
+  if (lane == 0) red[wave] = M;
+  __syncthreads();
+  M = red[0];
+#pragma unroll
+  for (int w = 1; w < NWV; w++) M = fmaxf(M, red[w]);
+  __syncthreads();
+  float L = 0.f;
+  if (tid < nch) {
+    const float e = expf(mv - M);
+    fac[tid] = e;
+    L = lv * e;
+  }
+  for (int c = tid + NT; c < nch; c += NT) {
+    const float e = expf(ph[(long)c * (2 + HD)] - M);
+    fac[c] = e;
+    L += ph[(long)c * (2 + HD) + 1] * e;
+  }
+  L = wave_sum(L);
+  if (lane == 0) red[wave] = L;
+  __syncthreads();
+  L = red[0];
+#pragma unroll
+  for (int w = 1; w < NWV; w++) L += red[w];
+  float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < R; j++) {
+    const int c = qq + ATT_MQ * j;
+    s4[j & 3] += c < nch ? vals[j] * fac[c] : 0.f;
+  }
+  for (int cb = qq + ATT_MQ * R; cb < nch; cb += ATT_MQ * R) {
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+      const int c = cb + ATT_MQ * j;
+      vals[j] = c < nch ? po[(long)c * (2 + HD)] : 0.f;
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    float L = 0.f;
-#pragma unroll
-    for (int i = 0; i < ATT_MAXCH / 64; i++) {
-      m[i] = lane + 64 * i < nch ? expf(m[i] - M) : 0.f;
-      L += l[i] * m[i];
+    for (int j = 0; j < R; j++) {
+      const int c = cb + ATT_MQ * j;
+      s4[j & 3] += c < nch ? vals[j] * fac[c] : 0.f;
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off, 64);
-    const float inv = 1.0f / L;
-#pragma unroll
-    for (int i = 0; i < ATT_MAXCH / 64; i++) fac[wave][lane + 64 * i] = m[i] * inv;
   }
+  osum[qq][d] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
   __syncthreads();
-  for (int o = tid; o < group * HD; o += ATT_THREADS) {
-    const int g = o / HD, d = o % HD;
-    const float *po = part + (long)(kh * group + g) * nchunk_grid * (2 + HD) + 2 + d;
-    float s4[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int cb = 0; cb < nch; cb += 16) {
-      float vals[16];
+  if (qq == 0) {
+    float o = osum[0][d];
 #pragma unroll
-      for (int j = 0; j < 16; j++) vals[j] = cb + j < nch ? po[(long)(cb + j) * (2 + HD)] : 0.f;
-#pragma unroll
-      for (int j = 0; j < 16; j++) s4[j & 3] += vals[j] * fac[g][cb + j];
-    }
-    att[(long)(kh * group + g) * HD + d] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    for (int i = 1; i < ATT_MQ; i++) o += osum[i][d];
+    att[(long)h * HD + d] = o / L;
   }
-  if (tid == 0) count[kh] = 0;
 }
 
 // -------------------------------------------------------------- argmax
@@ -431,10 +457,16 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     uint16_t *kc = m.kcache + (long)L * m.ctx * kvd, *vc = m.vcache + (long)L * m.ctx * kvd;
     if (hd == 128)
       hipLaunchKernelGGL(k_attn_gqa<128>, dim3(nkv, m.att_chunks), dim3(ATT_THREADS), 0, s, m.q, m.k, m.v,
-                         kc, vc, m.state, group, kvd, m.theta, m.att_part, m.att_count, m.att);
+                         kc, vc, m.state, group, kvd, m.rope_den, m.att_part);
     else
       hipLaunchKernelGGL(k_attn_gqa<64>, dim3(nkv, m.att_chunks), dim3(ATT_THREADS), 0, s, m.q, m.k, m.v,
-                         kc, vc, m.state, group, kvd, m.theta, m.att_part, m.att_count, m.att);
+                         kc, vc, m.state, group, kvd, m.rope_den, m.att_part);
+    if (hd == 128)
+      hipLaunchKernelGGL(k_attn_merge<128>, dim3(m.n_heads), dim3(ATT_MQ * 128), 0, s, m.state, m.att_chunks,
+                         m.att_part, m.att);
+    else
+      hipLaunchKernelGGL(k_attn_merge<64>, dim3(m.n_heads), dim3(ATT_MQ * 64), 0, s, m.state, m.att_chunks,
+                         m.att_part, m.att);
     MvIn ain;
     ain.x = m.att;
     const gq_weight *wo[1] = {m.wo[L]};

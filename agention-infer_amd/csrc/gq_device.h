@@ -101,4 +101,35 @@ __device__ __forceinline__ float dot4u(uint32_t w, float4 x, float acc) {
   return acc;
 }
 
+
+// Wave-wide max / sum of a float, returned to every lane.  DPP steps
+// combine within 16-lane rows (quad swaps, then rotations by 4 and 8), the
+// four row totals are read as scalars; a fixed order, no LDS round trips.
+template <class OP>
+__device__ __forceinline__ float wave_reduce(float x, OP op) {
+  auto dpp = [](float v, int ctrl) -> float {
+    switch (ctrl) {  // the control must be a constant expression
+    case 0: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    case 1: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    case 2: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));
+    default: return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));
+    }
+  };
+  x = op(x, dpp(x, 0));  // quad_perm [1,0,3,2]
+  x = op(x, dpp(x, 1));  // quad_perm [2,3,0,1]
+  x = op(x, dpp(x, 2));  // row_ror 4
+  x = op(x, dpp(x, 3));  // row_ror 8
+  const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return op(op(r0, r1), op(r2, r3));
+}
+__device__ __forceinline__ float wave_max(float x) {
+  return wave_reduce(x, [](float a, float b) { return fmaxf(a, b); });
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  return wave_reduce(x, [](float a, float b) { return a + b; });
+}
+
 }  // namespace gq

@@ -114,16 +114,17 @@ struct DecodeLaunch {
   uint16_t *kcache, *vcache;  // [layer][ctx][kv_dim] f16
   float *xa, *xb;             // residual stream, ping-pong
   float *q, *k, *v, *att, *proj, *h, *logits, *att_part;
+  float *rope_den;            // [head_dim / 2] theta^(2i/head_dim), computed on the host
   float *amax_v;              // per-block argmax partials
   int *amax_i;
-  int *att_count;             // [n_kv_heads] chunk counters (zero between launches)
   int *amax_count;            // argmax block counter (zero between launches)
   DecodeState *state;
   int *tokens;                // [max_tokens] generated tokens
 };
 
 hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s);
-constexpr int ATT_CHUNK = 256;   // positions per attention block
+constexpr int ATT_CHUNK = 64;    // positions per attention block
+constexpr int ATT_MAX_CTX = 65536;
 constexpr int ARGMAX_SPAN = 4096;  // logits per argmax block
 hipError_t launch_set_state(DecodeState *st, int token, int pos, hipStream_t s);
 

@@ -31,7 +31,9 @@ struct Layout {
   int k;       // in_dim
   int units;   // U, units per row
   int chunks;  // C
-  int rt;      // rows per tile (power of two, <= 64)
+  int rt;      // rows per tile: all rows (one tile) for matvec weights; a
+               // power of two <= 64 dividing the rows per expert for stacked
+               // expert tensors
 };
 
 __host__ __device__ constexpr int unit_chunks(int t) {
