@@ -117,6 +117,7 @@ const char *type_name(int t) {
 // shape) needs.
 size_t matvec_block_lds(const gq_weight *w, bool pair) {
   gq::MvArgs a{};
+  a.fmt = w->L.dtype;
   a.units = w->L.units;
   a.pair = pair;
   a.nseg = 1;
@@ -157,14 +158,8 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   w->L.units = (in_dim + 255) / 256;
   w->L.chunks = gq::unit_chunks(dtype);
   w->L.rt = std::max(out_dim, 1);  // one tile: the whole matrix
-  // Stacked expert tensors: a tile must not straddle two experts, and only
-  // a few experts run per token, so tiles are small (at most three wave
-  // iterations: rt * units <= 192) to spread each expert over many waves.
-  if (rows_per_group > 0) {
-    w->L.rt = 1;
-    while (w->L.rt < 64 && 2 * w->L.rt * w->L.units <= 192 && rows_per_group % (2 * w->L.rt) == 0)
-      w->L.rt *= 2;
-  }
+  // Stacked expert tensors: one tile per expert.
+  if (rows_per_group > 0) w->L.rt = rows_per_group;
   w->ggml_bytes = need;
   w->device = g_dev.device;
   const size_t body = (size_t)gq::body_bytes(w->L);
@@ -214,6 +209,7 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
     MvArgs a{};
     a.in = in;
     a.grid = g_dev.grid;
+    a.fmt = w0->L.dtype;
     a.k = w0->L.k;
     a.units = w0->L.units;
     a.chunks = w0->L.chunks;
@@ -228,6 +224,7 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
     MvArgs a{};
     a.in = in;
     a.grid = g_dev.grid;
+    a.fmt = w0->L.dtype;
     a.k = w0->L.k;
     a.units = w0->L.units;
     a.chunks = w0->L.chunks;
@@ -301,12 +298,14 @@ int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down
       down->L.rows != n_experts * h)
     return fail(GQ_EINVAL, "expert shapes disagree: gate %dx%d up %dx%d down %dx%d, experts %d",
                 gate->L.rows, gate->L.k, up->L.rows, up->L.k, down->L.rows, down->L.k, n_experts);
-  if (gate->L.rt != up->L.rt || gate->L.rt > 64 || down->L.rt > 64 || f % gate->L.rt ||
-      h % down->L.rt)
+  if (gate->L.rt != f || up->L.rt != f || down->L.rt != h)
     return fail(GQ_EINVAL, "expert tensors must be uploaded with gq_upload_experts");
   if (!logits_dev || !x_dev || !out_dev) return fail(GQ_EINVAL, "null MoE buffer");
+  if (gq::moe_lds_bytes(gate->L.dtype, h, f, top_k, T, g_dev.num_cus) > 160 * 1024)
+    return fail(GQ_EINVAL, "MoE shape h %d f %d top_k %d too large for the LDS-staged kernels", h, f,
+                top_k);
   const int pairs = T * top_k;
-  const size_t ws = (size_t)pairs * (2 * (size_t)f + (size_t)h) * 4 + (size_t)pairs * 8 + 1024;
+  const size_t ws = (size_t)pairs * (size_t)f * 4 + (size_t)pairs * 8 + 1024;
   char *wsp = nullptr;
   HIP_TRY(hipMallocAsync((void **)&wsp, ws, (hipStream_t)stream));
   gq::MoeArgs a{};
@@ -317,20 +316,15 @@ int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down
   a.f = f;
   a.gate = gate->body; a.up = up->body; a.down = down->body;
   a.gate_d = gate->d; a.up_d = up->d; a.down_d = down->d;
-  a.rt_h = gate->L.rt;
-  a.rt_f = down->L.rt;
   a.units_h = gate->L.units;
   a.units_f = down->L.units;
-  a.part_h = (a.rt_h * a.units_h + 63) / 64 * 64;
-  a.part_f = (a.rt_f * a.units_f + 63) / 64 * 64;
+  a.cus = g_dev.num_cus;
   a.grid = g_dev.grid;
   a.logits = logits_dev;
   a.x = x_dev;
-  a.tmp_g = (float *)wsp;
-  a.tmp_u = a.tmp_g + (size_t)pairs * f;
-  a.tmp_y = a.tmp_u + (size_t)pairs * f;
-  a.ids = ids_dev ? ids_dev : (int *)(a.tmp_y + (size_t)pairs * h);
-  a.w = w_dev ? w_dev : (float *)((int *)(a.tmp_y + (size_t)pairs * h) + pairs);
+  a.hbuf = (float *)wsp;
+  a.ids = ids_dev ? ids_dev : (int *)(a.hbuf + (size_t)pairs * f);
+  a.w = w_dev ? w_dev : (float *)((int *)(a.hbuf + (size_t)pairs * f) + pairs);
   a.out = out_dev;
   hipError_t e = gq::launch_moe(a, T, (hipStream_t)stream);
   (void)hipFreeAsync(wsp, (hipStream_t)stream);

@@ -34,9 +34,11 @@ struct MvSeg {
 };
 
 // Threads per matvec block: as many waves as the format's registers allow
-// (bytes in flight set the HBM throughput): 3 per SIMD for Q4_K/Q5_K, 2
-// for the others.
-__host__ __device__ constexpr int mv_threads(int fmt) { return fmt == 12 || fmt == 13 ? 768 : 512; }
+// (bytes in flight set the HBM throughput): 4 per SIMD for IQ3_XXS, 3 for
+// Q4_K/Q5_K, 2 for the others.
+__host__ __device__ constexpr int mv_threads(int fmt) {
+  return fmt == 18 ? 1024 : fmt == 12 || fmt == 13 ? 768 : 512;
+}
 constexpr int MV_BLOCKS_PER_CU = 1;
 
 // Where the matvec input vector comes from.
@@ -60,7 +62,7 @@ struct MvIn {
 struct MvArgs {
   MvIn in;
   const uint32_t *grid;  // IQ3_XXS codebook (device)
-  int k, units, chunks;
+  int fmt, k, units, chunks;
   int part_floats;       // LDS floats of per-unit partial sums per block
   int blocks;
   int pair;              // 1: seg[0] = gate, seg[1] = up (same shape); y0 = silu(g) * u
@@ -68,24 +70,29 @@ struct MvArgs {
   MvSeg seg[MV_MAX_SEG];
 };
 
-// MoE expert FFN (router, grouped gate/up, down, combine).
+// MoE expert FFN (router; gate/up with the SwiGLU; down with the combine).
 struct MoeArgs {
   int fmt;
   int n_experts, top_k, h, f;       // hidden h, expert intermediate f
-  const uint8_t *gate, *up, *down;  // stacked expert matrices (wave-tiled)
+  const uint8_t *gate, *up, *down;  // stacked expert matrices, one tile per expert
   const uint16_t *gate_d, *up_d, *down_d;
-  int rt_h, rt_f;                   // rows per tile: gate/up (K = h), down (K = f)
-  int units_h, units_f, part_h, part_f;
+  int units_h, units_f;
+  int cus;                          // compute units (grid sizing)
+  int bpp, bpt;                     // blocks per (token, slot) pair / per token
+  int part_h, part_f;               // LDS floats of partial sums per block
   const uint32_t *grid;
   const float *logits;              // [T][n_experts]
   const float *x;                   // [T][h]
   int *ids;                         // [T][top_k]
   float *w;                         // [T][top_k]
-  float *tmp_g, *tmp_u;             // [T*top_k][f]
-  float *tmp_y;                     // [T*top_k][h]
+  float *hbuf;                      // [T*top_k][f] silu(gate . x) * (up . x)
   float *out;                       // [T][h]
 };
 
+constexpr int MOE_ROUTE_MAX = 1024;  // experts routed inside the gate/up kernel
+
+// LDS bytes of the MoE kernels' blocks for this shape (<= 160 KiB to run).
+size_t moe_lds_bytes(int fmt, int h, int f, int top_k, int T, int cus);
 hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st);
 
 // LDS bytes of a matvec block: x limbs, records, codebook and part_total

@@ -43,17 +43,18 @@ constexpr int AUX_STRIDE = 144;   // LDS bytes per unit of the per-16-run record
 struct Smem {
   uint8_t *l2, *l1, *l0;  // limbs, LIMB_STRIDE bytes per 256 elements
   float2 *aux;            // AUX_STRIDE bytes per unit
-  uint32_t *grid;         // IQ3_XXS codebook
+  uint32_t *grid;         // IQ3_XXS: [entry][sign nibble] signed codebook words
   float *part;            // per-wave per-unit partial sums
   float *red;             // 16 floats of block reduction scratch
 };
 
-__host__ __device__ inline size_t smem_layout(int units, int part_total, Smem *s, char *base) {
+__host__ __device__ inline size_t smem_layout(int fmt, int units, int part_total, Smem *s, char *base) {
   size_t o = 0;
   auto take = [&](size_t n) { size_t r = o; o += (n + 15) & ~(size_t)15; return r; };
   const size_t limb = (size_t)units * LIMB_STRIDE;
   const size_t o2 = take(limb), o1 = take(limb), o0 = take(limb);
-  const size_t oaux = take((size_t)units * AUX_STRIDE), og = take(1024);
+  // IQ3_XXS: the codebook with the signs applied, 16 sign nibbles per entry
+  const size_t oaux = take((size_t)units * AUX_STRIDE), og = take(fmt == T_IQ3_XXS ? 4 * 4096 : 0);
   const size_t op = take((size_t)part_total * 4);
   const size_t ored = take(64);
   if (s) {
@@ -216,10 +217,9 @@ __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u
     for (int l = 0; l < 4; l++) {
       const uint32_t sg = ksign7((aux >> (7 * l)) & 127u);
       const uint32_t word = l < 2 ? i0 : i1;
-      const uint32_t g1 = S.grid[(word >> (16 * (l & 1))) & 0xff];
-      const uint32_t g2 = S.grid[(word >> (16 * (l & 1) + 8)) & 0xff];
-      q[2 * l] = neg_bytes(g1, sg & 15u);
-      q[2 * l + 1] = neg_bytes(g2, sg >> 4);
+      const uint32_t e1 = (word >> (16 * (l & 1))) & 0xff, e2 = (word >> (16 * (l & 1) + 8)) & 0xff;
+      q[2 * l] = S.grid[(e1 << 4) | (sg & 15u)];
+      q[2 * l + 1] = S.grid[(e2 << 4) | (sg >> 4)];
     }
     const float s = limbdot<8>(q, S, u * LIMB_STRIDE + 32 * ib);
     const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
@@ -443,8 +443,11 @@ __device__ __forceinline__ void stage_block(XS &xsrc, int kpad, const Smem &S,
 #pragma unroll
   for (int p = 0; p < NP; p++)
     if (p < passes) xsrc.issue(pass_e0(p), raw[p]);
-  uint32_t gword = 0;
-  if constexpr (FMT == T_IQ3_XXS) gword = gsrc[tid & 255];
+  constexpr int GW = FMT == T_IQ3_XXS ? 4096 / NTH : 1;  // signed codebook words per thread
+  uint32_t gword[GW];
+  if constexpr (FMT == T_IQ3_XXS)
+#pragma unroll
+    for (int i = 0; i < GW; i++) gword[i] = gsrc[(tid + NTH * i) >> 4];
   __builtin_amdgcn_sched_barrier(0);
   pre();
   __builtin_amdgcn_sched_barrier(0);
@@ -466,66 +469,109 @@ __device__ __forceinline__ void stage_block(XS &xsrc, int kpad, const Smem &S,
     stage_x<FMT == T_Q6_K>(kpad, e0, xv, S);
   }
   if constexpr (FMT == T_IQ3_XXS)
-    if (tid < 256) S.grid[tid] = gword;
+#pragma unroll
+    for (int i = 0; i < GW; i++) {
+      const int o = tid + NTH * i;
+      S.grid[o] = neg_bytes(gword[i], o & 15);
+    }
   xsrc.pre_barrier(S.red);
   __syncthreads();
 }
 
-// One wave's work in the MoE kernels: tile t of a stacked expert matrix.
-struct WaveJob {
+// A matrix streamed by a block: its body and d arrays (one tile: the units
+// in row-major order) and the first LDS column of the x it meets.
+struct MatRef {
   const uint8_t *body;
   const uint16_t *d;
-  float *y;
-  int rows, rt, t;
-  bool valid;
+  int xcol;
 };
 
-// The MoE body: a 256-thread block stages x, each wave streams its tile
-// with two units per lane in flight and reduces its rows.
-template <int FMT, class XS>
-__device__ __forceinline__ void matvec_wave(const WaveJob &job, int U, int part_floats,
-                                            const uint32_t *gsrc, XS &xsrc, char *smem_raw) {
-  Smem S;
-  smem_layout(U, 4 * part_floats, &S, smem_raw);
-  constexpr int C = Fmt<FMT>::C;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int t = job.t;
-  const int rows_here = min(job.rt, job.rows - t * job.rt);
-  const int uit = rows_here * U;
-  const int iters = (uit + 63) >> 6;
-  const int nv_last = uit - 64 * (iters - 1);
-  const long tile_base = (long)t * job.rt * U * C * 16;
-  const long dbase = (long)t * job.rt * U;
-  auto load_it = [&](Unit<FMT> &dst, int it) {
+// The units [j0, j1) (flat row-major index) of nm matrices of n_units
+// units each, streamed by the NW waves of a block.  Work item w is
+// iteration it0 + w % nit of matrix w / nit (NM: 1, 2 or 0 = any nm); the
+// block's first and last iterations are partial, lanes outside [j0, j1)
+// load nothing.  Items are dealt round-robin to the waves, each keeping
+// two units per lane in flight; per-unit partial sums go to
+// S.part[64 * w + lane].
+template <int FMT, int NW, int NM, class MATF>
+struct BlockStream {
+  MATF mat;
+  int U, j0, j1, iters, nv_last, it0, nit, work, lane, wave;
+  __device__ __forceinline__ BlockStream(MATF m, int U_, int j0_, int j1_, int n_units, int nm,
+                                         int lane_, int wave_)
+      : mat(m), U(U_), j0(j0_), j1(j1_), lane(lane_), wave(wave_) {
+    iters = (n_units + 63) >> 6;
+    nv_last = n_units - 64 * (iters - 1);
+    it0 = j0 >> 6;
+    nit = j1 > j0 ? ((j1 + 63) >> 6) - it0 : 0;
+    work = nm * nit;
+  }
+  __device__ __forceinline__ int mat_of(int w) const {
+    return NM == 1 ? 0 : NM == 2 ? (w >= nit ? 1 : 0) : w / nit;
+  }
+  __device__ __forceinline__ void load(Unit<FMT> &dst, int w) const {
+    const int m = mat_of(w), it = it0 + w - m * nit;
+    const MatRef r = mat(m);
+    const int j = 64 * it + lane;
     const bool last = it == iters - 1;
     const int l = last ? min(lane, nv_last - 1) : lane;
-    load_unit<FMT>(dst, job.body + tile_base + (long)it * C * 1024 + 16 * l,
-                   last ? 16L * nv_last : 1024L, job.d + dbase + 64 * it + l);
-  };
-  Unit<FMT> A, B;
-  stage_block<FMT, 1, 256>(xsrc, U * 256, S, gsrc, [&] { load_it(A, 0); });
-  const float rscale = xsrc.scale(S.red);
-  float *part = S.part + wave * part_floats;
-  auto consume = [&](const Unit<FMT> &src, int it) {
-    const int j = 64 * it + lane;
-    const float v = unit_dot<FMT>(src, j % U, S);
-    if (j < uit) part[j] = v;
-  };
-  for (int it = 0; it < iters; it += 2) {
-    const bool hb = it + 1 < iters;
-    if (hb) load_it(B, it + 1);
-    consume(A, it);
-    if (it + 2 < iters) load_it(A, it + 2);
-    if (hb) consume(B, it + 1);
+    if (j >= j0 && j < j1)
+      load_unit<FMT>(dst, r.body + (long)it * Fmt<FMT>::C * 1024 + 16 * l,
+                     last ? 16L * nv_last : 1024L, r.d + 64L * it + l);
   }
-  // Row sums: 64/RT lanes per row, fixed order.
-  const int lpr = 64 / job.rt;
-  const int row = lane / lpr, sub = lane % lpr;
+  __device__ __forceinline__ void consume(const Unit<FMT> &src, int w, const Smem &S) const {
+    const int m = mat_of(w), it = it0 + w - m * nit;
+    const int j = 64 * it + lane;
+    const float v = unit_dot<FMT>(src, mat(m).xcol + j % U, S);
+    // (The branch also keeps the scheduler from interleaving two units'
+    // arithmetic, which needs more registers than 2 waves per SIMD have.)
+    if (j >= j0 && j < j1) S.part[64 * w + lane] = v;
+  }
+  __device__ __forceinline__ void first(Unit<FMT> &A) const {
+    if (wave < work) load(A, wave);
+  }
+  // Two inlined copies of the unit arithmetic (kernel code size is launch
+  // latency: every launch of a decode step starts with a cold instruction
+  // cache).
+  __device__ __forceinline__ void run(Unit<FMT> &A, Unit<FMT> &B, const Smem &S) const {
+    for (int w = wave; w < work; w += 2 * NW) {
+      const int wb = w + NW;
+      if (wb < work) load(B, wb);
+      consume(A, w, S);
+      if (w + 2 * NW < work) load(A, w + 2 * NW);
+      if (wb < work) consume(B, wb, S);
+    }
+  }
+  // Partial sums of row r (counted from row j0 / U) of matrix m.
+  __device__ __forceinline__ const float *row_part(const Smem &S, int m, int r) const {
+    return S.part + m * 64 * nit + (j0 - 64 * it0) + r * U;
+  }
+};
+
+// Lanes per row of the row sums: a power of two, at most 8, U and the
+// block's threads per row (the butterfly steps are dependent LDS round
+// trips, so few lanes per row).
+__device__ __forceinline__ int row_lanes(int U, int rows, int nth) {
+  int G = 1;
+  while (2 * G <= 8 && 2 * G <= U && 2 * G * rows <= nth) G <<= 1;
+  return G;
+}
+
+// Sum of the U partials at p: lane `sub` of G (G in {1, 2, 4, 8}, groups
+// aligned in the wave) takes c = sub, sub + G, ..., then DPP row shifts by
+// 1, 2, 4 add the group up in its last lane (sub == G - 1, the only lane
+// whose result is defined); a fixed order.
+__device__ __forceinline__ float row_sum(const float *p, int U, int sub, int G, bool valid) {
   float acc = 0.f;
-  if (row < rows_here)
-    for (int c = sub; c < U; c += lpr) acc += part[row * U + c];
-  for (int off = lpr >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-  if (job.valid && sub == 0 && row < rows_here) job.y[t * job.rt + row] = acc * rscale;
+  if (valid)
+    for (int c = sub; c < U; c += G) acc += p[c];
+  if (G >= 2)
+    acc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x111, 0xF, 0xF, true));
+  if (G >= 4)
+    acc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x112, 0xF, 0xF, true));
+  if (G >= 8)
+    acc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x114, 0xF, 0xF, true));
+  return acc;
 }
 
 // Decode matvec over one or more matrices (segments) sharing the input.
@@ -544,7 +590,6 @@ template <int FMT, bool K4, int SRC, int NP, int NT>
 __global__ __launch_bounds__(mv_threads(FMT)) void k_matvec(MvArgs a) {
   extern __shared__ __align__(16) char smem_raw[];
   constexpr int NTH = mv_threads(FMT), NW = NTH / 64;
-  constexpr int C = Fmt<FMT>::C;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
   const int b = blockIdx.x;
@@ -558,40 +603,16 @@ __global__ __launch_bounds__(mv_threads(FMT)) void k_matvec(MvArgs a) {
   const int lb = b - sg.blk_begin;
   const int r0 = (int)((long)sg.rows * lb / sg.nblk);
   const int r1 = (int)((long)sg.rows * (lb + 1) / sg.nblk);
-  const int j0 = r0 * U, j1 = r1 * U;
-  const int n_units = sg.rows * U;
-  const int iters = (n_units + 63) >> 6;
-  const int nv_last = n_units - 64 * (iters - 1);
-  const int it0 = j0 >> 6;
-  const int nit = j1 > j0 ? ((j1 + 63) >> 6) - it0 : 0;
-  const int work = NT * nit;
   Smem S;
-  smem_layout(U, a.part_floats, &S, smem_raw);
-
-  // Work item w: iteration it0 + w % nit of matrix w / nit.
-  auto load_w = [&](Unit<FMT> &dst, int w) {
-    const bool m = NT == 2 && w >= nit;
-    const int it = it0 + (m ? w - nit : w);
-    const int j = 64 * it + lane;
-    const bool last = it == iters - 1;
-    const int l = last ? min(lane, nv_last - 1) : lane;
-    const uint8_t *p = (m ? a.seg[1].body : sg.body) + (long)it * C * 1024 + 16 * l;
-    const uint16_t *dp = (m ? a.seg[1].d : sg.d) + 64L * it + l;
-    if (j >= j0 && j < j1) load_unit<FMT>(dst, p, last ? 16L * nv_last : 1024L, dp);
+  smem_layout(FMT, U, a.part_floats, &S, smem_raw);
+  const MvSeg s1 = a.seg[1];
+  auto mat = [&](int m) {
+    return NT == 2 && m ? MatRef{s1.body, s1.d, 0} : MatRef{sg.body, sg.d, 0};
   };
-  auto consume = [&](const Unit<FMT> &src, int w) {
-    const int it = it0 + (NT == 2 && w >= nit ? w - nit : w);
-    const int j = 64 * it + lane;
-    const float v = unit_dot<FMT>(src, j % U, S);
-    // (The branch also keeps the scheduler from interleaving two units'
-    // arithmetic, which needs more registers than 2 waves per SIMD have.)
-    if (j >= j0 && j < j1) S.part[64 * w + lane] = v;
-  };
-
+  const BlockStream<FMT, NW, NT, decltype(mat)> bs(mat, U, r0 * U, r1 * U, sg.rows * U, NT, lane,
+                                                   wave);
   Unit<FMT> A, B;
-  auto first = [&] {
-    if (wave < work) load_w(A, wave);
-  };
+  auto first = [&] { bs.first(A); };
   float rscale = 1.f;
   if constexpr (SRC == MV_NORM) {
     const float *x = a.in.tok ? a.in.x + (long)(*a.in.tok) * a.k : a.in.x;
@@ -605,39 +626,17 @@ __global__ __launch_bounds__(mv_threads(FMT)) void k_matvec(MvArgs a) {
     XPlain<K4> xs{a.in.x, a.k};
     stage_block<FMT, NP, NTH>(xs, U * 256, S, a.grid, first);
   }
-  // Two units per lane in flight; two inlined copies of the unit arithmetic
-  // (kernel code size is launch latency: every launch of a decode step
-  // starts with a cold instruction cache).
-  for (int w = wave; w < work; w += 2 * NW) {
-    const int wb = w + NW;
-    if (wb < work) load_w(B, wb);
-    consume(A, w);
-    if (w + 2 * NW < work) load_w(A, w + 2 * NW);
-    if (wb < work) consume(B, wb);
-  }
+  bs.run(A, B, S);
   __syncthreads();
 
-  // Row sums: G lanes per row (a power of two, at most 8, U and the threads
-  // per row), strided partial sums then a butterfly; a fixed order.  Few
-  // lanes per row: the butterfly steps are dependent LDS round trips.
   const int rows_b = r1 - r0;
-  int G = 1;
-  while (2 * G <= 8 && 2 * G <= U && 2 * G * rows_b <= NTH) G <<= 1;
-  const int per = NTH / G;
-  const int base = j0 - 64 * it0;
+  const int G = row_lanes(U, rows_b, NTH), per = NTH / G;
   for (int rb = 0; rb < rows_b; rb += per) {
     const int r = rb + tid / G, sub = tid % G;
     float v[NT];
 #pragma unroll
-    for (int m = 0; m < NT; m++) {
-      const float *pm = S.part + m * 64 * nit + base + r * U;
-      float acc = 0.f;
-      if (r < rows_b)
-        for (int c = sub; c < U; c += G) acc += pm[c];
-      for (int off = G >> 1; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
-      v[m] = acc * rscale;
-    }
-    if (sub == 0 && r < rows_b) {
+    for (int m = 0; m < NT; m++) v[m] = row_sum(bs.row_part(S, m, r), U, sub, G, r < rows_b) * rscale;
+    if (sub == G - 1 && r < rows_b) {
       float out = v[0];
       if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
       sg.y[r0 + r] = out;
@@ -647,41 +646,171 @@ __global__ __launch_bounds__(mv_threads(FMT)) void k_matvec(MvArgs a) {
 
 // ------------------------------------------------------------------- MoE
 // Pair p = (token p / top_k, slot p % top_k) routed to expert ids[p].
-// Stage 1: gate_e . x_t and up_e . x_t for every pair (blockIdx.y = p,
-// waves over the 2 * F / rt tiles of the two expert matrices).
-template <int FMT, bool K4>
-__global__ __launch_bounds__(256) void k_moe_gate_up(MoeArgs a) {
+// Expert tensors are one tile per expert (rows_per_expert rows, units in
+// row-major order), so expert e's matrix starts at tile e.
+// Stage 1: h_p = silu(gate_e . x_t) * (up_e . x_t) (the SwiGLU of
+// ffn_gate_up, src/model/llama/cpu_path.rs:225-227): the blocks are split
+// evenly over the pairs (bpp per pair), block lb of pair p owns rows
+// [f * lb / bpp, f * (lb + 1) / bpp) of both matrices of its expert.
+// With ROUTE (n_experts <= MOE_ROUTE_MAX) the block also routes: it ranks
+// the token's logits (ties: lower index, like k_moe_route) to find its
+// slot's expert, and block 0 of the pair stores ids[p] and the softmax
+// weight w[p] for stage 2.
+template <int FMT, bool K4, bool ROUTE>
+__global__ __launch_bounds__(mv_threads(FMT)) void k_moe_gate_up(MoeArgs a) {
   extern __shared__ __align__(16) char smem_raw[];
-  const int p = blockIdx.y;
-  const int e = a.ids[p];
+  constexpr int NTH = mv_threads(FMT), NW = NTH / 64, C = Fmt<FMT>::C;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.x, p = b / a.bpp, lb = b - p * a.bpp;
   const int tok = p / a.top_k;
-  const int tiles = a.f / a.rt_h;  // tiles per expert matrix
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const bool valid = gw < 2 * tiles;
-  const int gwc = valid ? gw : 2 * tiles - 1;
-  const bool is_up = gwc >= tiles;
-  const int lt = is_up ? gwc - tiles : gwc;
-  const WaveJob job{is_up ? a.up : a.gate, is_up ? a.up_d : a.gate_d,
-                    (is_up ? a.tmp_u : a.tmp_g) + (long)p * a.f - (long)e * a.f,
-                    a.n_experts * a.f, a.rt_h, e * tiles + lt, valid};
+  const int U = a.units_h, f = a.f;
+  const int r0 = (int)((long)f * lb / a.bpp), r1 = (int)((long)f * (lb + 1) / a.bpp);
+  Smem S;
+  smem_layout(FMT, U, a.part_h, &S, smem_raw);
+  int e = 0;  // the pair's expert (set before the first weight load)
+  auto mat = [&](int m) {
+    const long tb = (long)e * f * U;  // first unit of expert e
+    return m ? MatRef{a.up + tb * C * 16, a.up_d + tb, 0} : MatRef{a.gate + tb * C * 16, a.gate_d + tb, 0};
+  };
+  const BlockStream<FMT, NW, 2, decltype(mat)> bs(mat, U, r0 * U, r1 * U, f * U, 2, lane, wave);
+  Unit<FMT> A, B;
   XPlain<K4> xs{a.x + (long)tok * a.h, a.h};
-  matvec_wave<FMT>(job, a.units_h, a.part_h, a.grid, xs, smem_raw);
+  // Routing runs while the x loads are in flight.
+  auto route = [&] {
+    if constexpr (ROUTE) {
+      __shared__ __align__(16) float lv[MOE_ROUTE_MAX];
+      __shared__ int prank[4][MOE_ROUTE_MAX / 4];
+      __shared__ float rmax[NW], rsum[NW];
+      __shared__ int eid_s;
+      const int E = a.n_experts, slot = p - tok * a.top_k;
+      const float *lg = a.logits + (long)tok * E;
+      // Logits padded with -inf to a multiple of 16 (-inf past E beats
+      // nothing and, at a higher index, ties with nothing).
+      const int E16 = (E + 15) & ~15;
+      if (tid == 0) eid_s = 0;  // (NaN logits can leave a rank unused)
+      float mx = -INFINITY;
+      for (int i = tid; i < E16; i += NTH) {
+        lv[i] = i < E ? lg[i] : -INFINITY;
+        mx = fmaxf(mx, lv[i]);
+      }
+      __syncthreads();
+      // rank(i) = #{o : l_o > l_i or (l_o == l_i and o < i)}; with 4 * E16
+      // threads or more, thread (q, i) counts over the quarter q of o.
+      const bool split = 4 * E16 <= NTH;
+      const int nq = split ? 4 : 1, span = E16 / nq;
+      for (int t = tid; t < nq * E16; t += NTH) {
+        const int i = t % E16, q = t / E16;
+        const float me = lv[i];
+        int rank = 0;
+#pragma unroll 4
+        for (int o = q * span; o < (q + 1) * span; o += 4) {
+          const float4 ov = *(const float4 *)&lv[o];
+          rank += (ov.x > me) || (ov.x == me && o < i);
+          rank += (ov.y > me) || (ov.y == me && o + 1 < i);
+          rank += (ov.z > me) || (ov.z == me && o + 2 < i);
+          rank += (ov.w > me) || (ov.w == me && o + 3 < i);
+        }
+        if (split) prank[q][i] = rank;
+        else if (i < E && rank == slot) eid_s = i;
+      }
+      if (split) {
+        __syncthreads();
+        if (tid < E && prank[0][tid] + prank[1][tid] + prank[2][tid] + prank[3][tid] == slot)
+          eid_s = tid;
+      }
+      if (lb == 0) {  // softmax over all experts (k_moe_route)
+        mx = wave_max(mx);
+        if (lane == 0) rmax[wave] = mx;
+        __syncthreads();
+        mx = rmax[0];
+        for (int w = 1; w < NW; w++) mx = fmaxf(mx, rmax[w]);
+        float sum = 0.f;
+        for (int i = tid; i < E; i += NTH) sum += expf(lv[i] - mx);
+        sum = wave_sum(sum);
+        if (lane == 0) rsum[wave] = sum;
+      }
+      __syncthreads();
+      e = eid_s;
+      if (lb == 0 && tid == 0) {
+        float sum = 0.f;
+        for (int w = 0; w < NW; w++) sum += rsum[w];
+        a.ids[p] = e;
+        a.w[p] = expf(lv[e] - mx) / sum;
+      }
+    } else {
+      e = a.ids[p];
+    }
+  };
+  stage_block<FMT, 1, NTH>(xs, U * 256, S, a.grid, [&] {
+    route();
+    bs.first(A);
+  });
+  bs.run(A, B, S);
+  __syncthreads();
+  const int rows_b = r1 - r0;
+  const int G = row_lanes(U, rows_b, NTH), per = NTH / G;
+  for (int rb = 0; rb < rows_b; rb += per) {
+    const int r = rb + tid / G, sub = tid % G;
+    const float g = row_sum(bs.row_part(S, 0, r), U, sub, G, r < rows_b);
+    const float u = row_sum(bs.row_part(S, 1, r), U, sub, G, r < rows_b);
+    if (sub == G - 1 && r < rows_b) a.hbuf[(long)p * f + r0 + r] = g / (1.0f + expf(-g)) * u;
+  }
 }
 
-// Stage 2: down_e . (silu(g) * u) for every pair.
+// The top_k inputs h_(t, s) of a token, one after another, each padded to
+// whole units: element e is element e % (U_f * 256) of slot e / (U_f * 256).
+template <bool K4>
+struct XSlots {
+  const float *h;  // [pairs][f]
+  int f, span, top_k, p0;
+  struct Raw { float v[16]; };
+  __device__ __forceinline__ void issue(int e0, Raw &r) const {
+    const int s = min(e0 / span, top_k - 1), i0 = e0 - s * span;
+    load_x16<K4>(h + (long)(p0 + s) * f, f, i0 < span ? i0 : span, r.v);
+  }
+  __device__ __forceinline__ void make(const Raw &r, int, float (&xv)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) xv[i] = r.v[i];
+  }
+  __device__ __forceinline__ void pre_barrier(float *) const {}
+  __device__ __forceinline__ float scale(const float *) const { return 1.f; }
+};
+
+// Stage 2 with the weighted combine (moe_ffn): out[t] = sum_s w[t][s] *
+// (down_(e_s) . h_(t, s)), slots in order.  Block lb of token t (bpt per
+// token) owns rows [h * lb / bpt, h * (lb + 1) / bpt) and streams those
+// rows of all top_k routed experts against the token's staged inputs.
 template <int FMT, bool K4>
-__global__ __launch_bounds__(256) void k_moe_down(MoeArgs a) {
+__global__ __launch_bounds__(mv_threads(FMT)) void k_moe_down(MoeArgs a) {
   extern __shared__ __align__(16) char smem_raw[];
-  const int p = blockIdx.y;
-  const int e = a.ids[p];
-  const int tiles = a.h / a.rt_f;
-  const int gw = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const bool valid = gw < tiles;
-  const int gwc = valid ? gw : tiles - 1;
-  const WaveJob job{a.down, a.down_d, a.tmp_y + (long)p * a.h - (long)e * a.h,
-                    a.n_experts * a.h, a.rt_f, e * tiles + gwc, valid};
-  XSwiGLU<K4> xs{a.tmp_g + (long)p * a.f, a.tmp_u + (long)p * a.f, a.f};
-  matvec_wave<FMT>(job, a.units_f, a.part_f, a.grid, xs, smem_raw);
+  constexpr int NTH = mv_threads(FMT), NW = NTH / 64, C = Fmt<FMT>::C;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = blockIdx.x, t = b / a.bpt, lb = b - t * a.bpt;
+  const int U = a.units_f, h = a.h, K = a.top_k, p0 = t * K;
+  const int r0 = (int)((long)h * lb / a.bpt), r1 = (int)((long)h * (lb + 1) / a.bpt);
+  Smem S;
+  smem_layout(FMT, K * U, a.part_f, &S, smem_raw);
+  auto mat = [&](int m) {
+    const long tb = (long)a.ids[p0 + m] * h * U;
+    return MatRef{a.down + tb * C * 16, a.down_d + tb, m * U};
+  };
+  const BlockStream<FMT, NW, 0, decltype(mat)> bs(mat, U, r0 * U, r1 * U, h * U, K, lane, wave);
+  Unit<FMT> A, B;
+  XSlots<K4> xs{a.hbuf, a.f, U * 256, K, p0};
+  stage_block<FMT, 4, NTH>(xs, K * U * 256, S, a.grid, [&] { bs.first(A); });
+  bs.run(A, B, S);
+  __syncthreads();
+  const int rows_b = r1 - r0;
+  const int G = row_lanes(U, rows_b, NTH), per = NTH / G;
+  for (int rb = 0; rb < rows_b; rb += per) {
+    const int r = rb + tid / G, sub = tid % G;
+    float out = 0.f;
+    for (int m = 0; m < K; m++)
+      out += a.w[p0 + m] * row_sum(bs.row_part(S, m, r), U, sub, G, r < rows_b);
+    if (sub == G - 1 && r < rows_b) a.out[(long)t * h + r0 + r] = out;
+  }
 }
 
 // Router: per token, top-k of the logits (ties: lower index) and their
@@ -730,21 +859,9 @@ __global__ __launch_bounds__(256) void k_moe_route(const float *logits, int n_ex
   }
 }
 
-// out[t][i] = sum_s w[t][s] * y[t*k+s][i], slots in order.
-__global__ void k_moe_combine(const float *tmp_y, const float *w, int T, int top_k, int h,
-                              float *out) {
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long)T * h) return;
-  const int t = (int)(i / h), c = (int)(i % h);
-  float acc = 0.f;
-  for (int s = 0; s < top_k; s++) acc += w[t * top_k + s] * tmp_y[((long)t * top_k + s) * h + c];
-  out[i] = acc;
-}
-
 // ------------------------------------------------------------- launch
 size_t matvec_lds_bytes(int dtype, int units, int part_total) {
-  (void)dtype;
-  return smem_layout(units, part_total, nullptr, nullptr);
+  return smem_layout(dtype, units, part_total, nullptr, nullptr);
 }
 
 size_t matvec_plan(MvArgs &a, int num_cus) {
@@ -769,7 +886,7 @@ size_t matvec_plan(MvArgs &a, int num_cus) {
     }
     // A block's units may start mid-iteration: one more iteration.
     const int part = (int)(nt * 64 * ((max_units + 63) / 64 + 1));
-    const size_t lds = matvec_lds_bytes(0, a.units, part);
+    const size_t lds = matvec_lds_bytes(a.fmt, a.units, part);
     if (lds <= 160 * 1024 || target >= total) {
       a.blocks = blk;
       a.part_floats = part;
@@ -818,36 +935,89 @@ static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
   }
 }
 
-hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st) {
-  if (a.fmt != T_IQ3_XXS && a.fmt != T_Q4_K && a.fmt != T_Q6_K && a.fmt != T_Q8_0 &&
-      a.fmt != T_Q5_K)
-    return hipErrorInvalidValue;
+// Blocks per pair (gate/up) and per token (down): about one block per CU
+// in all, more while a block's partial sums would not fit in LDS.
+static size_t moe_plan(MoeArgs &a, int T, int cus) {
   const int pairs = T * a.top_k;
-  hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(256), 0, st, a.logits, a.n_experts, a.top_k,
-                     a.ids, a.w);
-  const size_t lds1 = matvec_lds_bytes(a.fmt, a.units_h, 4 * a.part_h);
-  const size_t lds2 = matvec_lds_bytes(a.fmt, a.units_f, 4 * a.part_f);
-  const dim3 g1((2 * (a.f / a.rt_h) + 3) / 4, pairs), g2(((a.h / a.rt_f) + 3) / 4, pairs);
-#define GQ_MOE_LAUNCH(F)                                                                     \
-  if (a.fmt == F) {                                                                          \
-    if (a.h % 4 == 0)                                                                        \
-      hipLaunchKernelGGL((k_moe_gate_up<F, true>), g1, dim3(256), lds1, st, a);              \
-    else                                                                                     \
-      hipLaunchKernelGGL((k_moe_gate_up<F, false>), g1, dim3(256), lds1, st, a);             \
-    if (a.f % 4 == 0)                                                                        \
-      hipLaunchKernelGGL((k_moe_down<F, true>), g2, dim3(256), lds2, st, a);                 \
-    else                                                                                     \
-      hipLaunchKernelGGL((k_moe_down<F, false>), g2, dim3(256), lds2, st, a);                \
+  a.bpp = std::max(1, std::min(a.f, cus / pairs));
+  a.bpt = std::max(1, std::min(a.h, cus / T));
+  size_t l1, l2;
+  for (;;) {
+    const long u1 = (long)((a.f + a.bpp - 1) / a.bpp) * a.units_h;
+    a.part_h = (int)(2 * 64 * ((u1 + 63) / 64 + 1));
+    l1 = matvec_lds_bytes(a.fmt, a.units_h, a.part_h) + MOE_ROUTE_MAX * 8 + 256;  // + routing
+    if (l1 <= 160 * 1024 || a.bpp >= a.f) break;
+    a.bpp = std::min(a.f, 2 * a.bpp);
   }
-  GQ_MOE_LAUNCH(T_IQ3_XXS)
-  GQ_MOE_LAUNCH(T_Q4_K)
-  GQ_MOE_LAUNCH(T_Q5_K)
-  GQ_MOE_LAUNCH(T_Q6_K)
-  GQ_MOE_LAUNCH(T_Q8_0)
-#undef GQ_MOE_LAUNCH
-  const long tot = (long)T * a.h;
-  hipLaunchKernelGGL(k_moe_combine, dim3((unsigned)((tot + 255) / 256)), dim3(256), 0, st,
-                     a.tmp_y, a.w, T, a.top_k, a.h, a.out);
+  for (;;) {
+    const long u2 = (long)((a.h + a.bpt - 1) / a.bpt) * a.units_f;
+    a.part_f = (int)(a.top_k * 64 * ((u2 + 63) / 64 + 1));
+    l2 = matvec_lds_bytes(a.fmt, a.top_k * a.units_f, a.part_f);
+    if (l2 <= 160 * 1024 || a.bpt >= a.h) break;
+    a.bpt = std::min(a.h, 2 * a.bpt);
+  }
+  return std::max(l1, l2);
+}
+
+size_t moe_lds_bytes(int fmt, int h, int f, int top_k, int T, int cus) {
+  MoeArgs a{};
+  a.fmt = fmt;
+  a.h = h;
+  a.f = f;
+  a.top_k = top_k;
+  a.units_h = (h + 255) / 256;
+  a.units_f = (f + 255) / 256;
+  return moe_plan(a, T, cus);
+}
+
+template <int F, bool R>
+static void moe_launch_f(const MoeArgs &a, int T, size_t lds1, size_t lds2, hipStream_t st) {
+  const dim3 g1(T * a.top_k * a.bpp), g2(T * a.bpt), nt(mv_threads(F));
+  auto big = [](const void *fn, size_t lds) {
+    if (lds > 64 * 1024)
+      (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  };
+  if (a.h % 4 == 0) {
+    big((const void *)k_moe_gate_up<F, true, R>, lds1);
+    hipLaunchKernelGGL((k_moe_gate_up<F, true, R>), g1, nt, lds1, st, a);
+  } else {
+    big((const void *)k_moe_gate_up<F, false, R>, lds1);
+    hipLaunchKernelGGL((k_moe_gate_up<F, false, R>), g1, nt, lds1, st, a);
+  }
+  if (a.f % 4 == 0) {
+    big((const void *)k_moe_down<F, true>, lds2);
+    hipLaunchKernelGGL((k_moe_down<F, true>), g2, nt, lds2, st, a);
+  } else {
+    big((const void *)k_moe_down<F, false>, lds2);
+    hipLaunchKernelGGL((k_moe_down<F, false>), g2, nt, lds2, st, a);
+  }
+}
+
+hipError_t launch_moe(const MoeArgs &args, int T, hipStream_t st) {
+  MoeArgs a = args;
+  if (moe_plan(a, T, a.cus) > 160 * 1024) return hipErrorInvalidValue;
+  const size_t lds1 = matvec_lds_bytes(a.fmt, a.units_h, a.part_h);  // dynamic part
+  const size_t lds2 = matvec_lds_bytes(a.fmt, a.top_k * a.units_f, a.part_f);
+  // Few experts: the gate/up blocks route (one launch less); many: the
+  // router kernel first.
+  const bool fused = a.n_experts <= MOE_ROUTE_MAX;
+  if (!fused)
+    hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(256), 0, st, a.logits, a.n_experts, a.top_k,
+                       a.ids, a.w);
+#define GQ_MOE_F(F)                                                                     \
+  case F:                                                                               \
+    if (fused) moe_launch_f<F, true>(a, T, lds1, lds2, st);                             \
+    else moe_launch_f<F, false>(a, T, lds1, lds2, st);                                  \
+    break;
+  switch (a.fmt) {
+    GQ_MOE_F(T_IQ3_XXS)
+    GQ_MOE_F(T_Q4_K)
+    GQ_MOE_F(T_Q5_K)
+    GQ_MOE_F(T_Q6_K)
+    GQ_MOE_F(T_Q8_0)
+  default: return hipErrorInvalidValue;
+  }
+#undef GQ_MOE_F
   return hipGetLastError();
 }
 
