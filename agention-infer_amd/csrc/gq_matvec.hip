@@ -7,10 +7,13 @@
 // the reference GPU kernels (src/ops/kernels_wgpu.rs:1067-1706).
 //
 // Design (HBM-bound; every weight byte is read exactly once):
-//  * Weights sit in the wave-tiled layout (gq_layout.h): one lane owns one
-//    256-element unit, and a wave-wide 128-bit load reads 1 KiB of
-//    contiguous HBM with a nontemporal hint.  Each lane keeps its next unit
-//    in flight while it computes the current one.
+//  * Weights sit in the wave-tiled layout (gq_layout.h), one tile per
+//    matrix (per expert for stacked experts): one lane owns one 256-element
+//    unit, and a wave-wide 128-bit load reads 1 KiB of contiguous HBM with
+//    a nontemporal hint.  Each lane keeps its next unit in flight while it
+//    computes the current one.
+//  * One block per CU: block b owns an equal range of rows (+-1), stages x
+//    once and streams the range's units with all its waves.
 //  * x is staged per block in LDS as fixed-point int8 "limbs": for each run
 //    of 32 elements, s = max|x| / (127 * 2^16), X = rint(x / s) (|X| <=
 //    127 * 2^16) and X = x2 * 2^16 + x1 * 2^8 + x0 with signed bytes.

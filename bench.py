@@ -218,7 +218,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the 7B decode leg")
-    ap.add_argument("--only", choices=["decode", "gemm", "moe"],
+    ap.add_argument("--only", choices=["matvec", "decode", "gemm", "moe"],
                     help="run only this leg and print its figures (for profiling)")
     ap.add_argument("--cpu-decode-steps", type=int, default=3)
     ap.add_argument("--calib-copy", action="store_true",
@@ -367,6 +367,9 @@ def main():
     if not args.no_cpu:
         nthreads = min(len(os.sched_getaffinity(0)), 16)
         out["cpu_baseline"] = cpu_baseline(mats, host, xs, nthreads, args.cpu_seconds)
+    if args.only == "matvec":
+        print(json.dumps(out), flush=True)
+        return
     out["gemm"] = gemm_leg(be, gq, syn, torch, not args.no_cpu)
     out["moe"] = moe_leg(be, gq, syn, torch, not args.no_cpu)
     if not args.no_decode:
