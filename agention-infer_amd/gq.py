@@ -63,6 +63,36 @@ SIGNATURES = {
 }
 
 
+# Every entry point of include/gq_host.h (libgq_host.so: GGUF files, uploads).
+_U32, _U64, _I64 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int64
+_PP = ctypes.POINTER(_P)
+HOST_SIGNATURES = {
+    "gqh_last_error": (ctypes.c_char_p, []),
+    "gqh_gguf_open": (_I, [ctypes.c_char_p, _PP]),
+    "gqh_gguf_parse": (_I, [_P, _SZ, _PP]),
+    "gqh_gguf_close": (_I, [_P]),
+    "gqh_gguf_header": (_I, [_P, ctypes.POINTER(_U32), ctypes.POINTER(_U64), ctypes.POINTER(_U64),
+                             ctypes.POINTER(_U64)]),
+    "gqh_gguf_tensor": (_I, [_P, _U64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U32),
+                             ctypes.POINTER(_U64), ctypes.POINTER(_U32), ctypes.POINTER(_U64),
+                             ctypes.POINTER(_U64)]),
+    "gqh_gguf_find_tensor": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_U64)]),
+    "gqh_gguf_tensor_data": (_I, [_P, _U64, _PP, ctypes.POINTER(_SZ)]),
+    "gqh_gguf_meta_type": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_U32)]),
+    "gqh_gguf_meta_u64": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_U64)]),
+    "gqh_gguf_meta_i64": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_I64)]),
+    "gqh_gguf_meta_f32": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_float)]),
+    "gqh_gguf_meta_bool": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_I)]),
+    "gqh_gguf_meta_str": (_I, [_P, ctypes.c_char_p, _PP, ctypes.POINTER(_SZ)]),
+    "gqh_gguf_meta_array": (_I, [_P, ctypes.c_char_p, ctypes.POINTER(_U32), ctypes.POINTER(_U64)]),
+    "gqh_gguf_meta_array_i64": (_I, [_P, ctypes.c_char_p, _U64, ctypes.POINTER(_I64)]),
+    "gqh_gguf_meta_array_str": (_I, [_P, ctypes.c_char_p, _U64, _PP, ctypes.POINTER(_SZ)]),
+    "gqh_parse_split_index": (_I, [ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
+    "gqh_gguf_upload": (_I, [_P, ctypes.c_char_p, _PP]),
+}
+HOST_LIB_PATH = os.environ.get("GQ_HOST_LIBRARY") or os.path.join(_HERE, "libgq_host.so")
+
+
 class GqError(RuntimeError):
     def __init__(self, code, msg):
         super().__init__(f"gq error {code}: {msg}")
@@ -89,6 +119,34 @@ def lib():
             f.argtypes = args
         _lib = L
     return _lib
+
+
+_host = None
+
+
+def host_lib():
+    """Load libgq_host.so (the C++ host library: GGUF files, uploads)."""
+    global _host
+    if _host is None:
+        lib()  # libgq.so (and torch's HIP runtime) first
+        if not os.path.exists(HOST_LIB_PATH):
+            raise GqError(-6, f"{HOST_LIB_PATH} not built; run __graft_entry__.build()")
+        L = ctypes.CDLL(HOST_LIB_PATH)
+        for name, (res, args) in HOST_SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _host = L
+    return _host
+
+
+class GgufError(GqError):
+    """A GGUF parse / load failure; .code is the GQH_E* kind (gq_host.h)."""
+
+
+def _hcheck(rc):
+    if rc != 0:
+        raise GgufError(rc, host_lib().gqh_last_error().decode())
 
 
 def _check(rc):
@@ -337,6 +395,177 @@ class DecodeModel:
         out = np.zeros(n_steps, np.int32)
         _check(lib().gq_model_generate(self._h, token, pos, n_steps, _ptr(out), _stream(stream)))
         return out
+
+
+class TensorInfo:
+    """TensorInfo (src/types.rs): name, dims (dims[0] fastest), GGML type id,
+    byte offset from the data section, byte size."""
+
+    def __init__(self, name, dims, ggml_type, byte_offset, nbytes):
+        self.name, self.dims, self.ggml_type = name, dims, ggml_type
+        self.byte_offset, self.nbytes = byte_offset, nbytes
+
+    def n_elements(self):
+        n = 1
+        for d in self.dims:
+            n *= d
+        return n
+
+    def __repr__(self):
+        return f"TensorInfo({self.name!r}, {self.dims}, type {self.ggml_type})"
+
+
+class GgufFile:
+    """A GGUF file parsed and mapped once by libgq_host (loader::load; a
+    "-00001-of-0000N.gguf" name opens all N parts), or parsed from bytes
+    (parser::parse).  Metadata via .get(key) / get_u64 / get_f32 /
+    get_string / get_bool / get_i64_array / get_str_array; tensor bytes are
+    read from the mapping; .upload(name) puts a weight on the GPU once."""
+
+    def __init__(self, path=None, data=None):
+        h = ctypes.c_void_p()
+        if path is not None:
+            _hcheck(host_lib().gqh_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        else:
+            buf = bytes(data)
+            _hcheck(host_lib().gqh_gguf_parse(buf, len(buf), ctypes.byref(h)))
+        self._h = h
+        v, tc, mc, do = _U32(), _U64(), _U64(), _U64()
+        _hcheck(host_lib().gqh_gguf_header(h, ctypes.byref(v), ctypes.byref(tc), ctypes.byref(mc),
+                                           ctypes.byref(do)))
+        self.version, self.tensor_count = v.value, tc.value
+        self.metadata_count, self.data_offset = mc.value, do.value
+        self.tensors = [self._tensor(i) for i in range(self.tensor_count)]
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and _host is not None:
+            _host.gqh_gguf_close(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def _tensor(self, i):
+        name, nd, ty = ctypes.c_char_p(), _U32(), _U32()
+        dims, off, nb = (_U64 * 8)(), _U64(), _U64()
+        _hcheck(host_lib().gqh_gguf_tensor(self._h, i, ctypes.byref(name), ctypes.byref(nd), dims,
+                                           ctypes.byref(ty), ctypes.byref(off), ctypes.byref(nb)))
+        return TensorInfo(name.value.decode(), [dims[k] for k in range(min(nd.value, 8))],
+                          ty.value, off.value, nb.value)
+
+    def find(self, name):
+        for t in self.tensors:
+            if t.name == name:
+                return t
+        return None
+
+    def tensor_bytes(self, name):
+        """The tensor's bytes (a numpy uint8 copy out of the mapping)."""
+        idx = _U64()
+        _hcheck(host_lib().gqh_gguf_find_tensor(self._h, name.encode(), ctypes.byref(idx)))
+        p, n = ctypes.c_void_p(), _SZ()
+        _hcheck(host_lib().gqh_gguf_tensor_data(self._h, idx.value, ctypes.byref(p), ctypes.byref(n)))
+        return np.ctypeslib.as_array((ctypes.c_uint8 * n.value).from_address(p.value)).copy()
+
+    # metadata (GgufFile::get_* in src/types.rs); None when absent
+    def _meta(self, fn, key, out):
+        rc = fn(self._h, key.encode(), ctypes.byref(out))
+        if rc == -107:  # GQH_EMISSING
+            return None
+        _hcheck(rc)
+        return out.value
+
+    def get_u64(self, key):
+        return self._meta(host_lib().gqh_gguf_meta_u64, key, _U64())
+
+    def get_i64(self, key):
+        return self._meta(host_lib().gqh_gguf_meta_i64, key, _I64())
+
+    def get_f32(self, key):
+        return self._meta(host_lib().gqh_gguf_meta_f32, key, ctypes.c_float())
+
+    def get_bool(self, key):
+        v = self._meta(host_lib().gqh_gguf_meta_bool, key, _I())
+        return None if v is None else bool(v)
+
+    def get_string(self, key):
+        p, n = ctypes.c_void_p(), _SZ()
+        rc = host_lib().gqh_gguf_meta_str(self._h, key.encode(), ctypes.byref(p), ctypes.byref(n))
+        if rc == -107:
+            return None
+        _hcheck(rc)
+        return ctypes.string_at(p.value, n.value).decode()
+
+    def _array(self, key):
+        et, cnt = _U32(), _U64()
+        rc = host_lib().gqh_gguf_meta_array(self._h, key.encode(), ctypes.byref(et), ctypes.byref(cnt))
+        if rc == -107:
+            return None, 0
+        _hcheck(rc)
+        return et.value, cnt.value
+
+    def get_i64_array(self, key):
+        et, cnt = self._array(key)
+        if et is None:
+            return None
+        out, v = [], _I64()
+        for k in range(cnt):
+            _hcheck(host_lib().gqh_gguf_meta_array_i64(self._h, key.encode(), k, ctypes.byref(v)))
+            out.append(v.value)
+        return out
+
+    def get_str_array(self, key):
+        et, cnt = self._array(key)
+        if et is None:
+            return None
+        out, p, n = [], ctypes.c_void_p(), _SZ()
+        for k in range(cnt):
+            _hcheck(host_lib().gqh_gguf_meta_array_str(self._h, key.encode(), k, ctypes.byref(p),
+                                                       ctypes.byref(n)))
+            out.append(ctypes.string_at(p.value, n.value).decode())
+        return out
+
+    def meta_type(self, key):
+        t = _U32()
+        rc = host_lib().gqh_gguf_meta_type(self._h, key.encode(), ctypes.byref(t))
+        if rc == -107:
+            return None
+        _hcheck(rc)
+        return t.value
+
+    def get(self, key):
+        """The value of any kind (arrays as lists), or None."""
+        t = self.meta_type(key)
+        if t is None:
+            return None
+        if t in (0, 2, 4, 10):
+            return self.get_u64(key)
+        if t in (1, 3, 5, 11):
+            return self.get_i64(key)
+        if t in (6, 12):
+            return self.get_f32(key)
+        if t == 7:
+            return self.get_bool(key)
+        if t == 8:
+            return self.get_string(key)
+        et, _ = self._array(key)
+        return self.get_str_array(key) if et == 8 else self.get_i64_array(key)
+
+    def architecture(self):
+        return self.get_string("general.architecture")
+
+    def upload(self, name):
+        """HipBackend::upload_tensor: a 2-D weight tensor, resident once."""
+        t = self.find(name)
+        h = ctypes.c_void_p()
+        _hcheck(host_lib().gqh_gguf_upload(self._h, name.encode(), ctypes.byref(h)))
+        return GpuWeightHandle(h.value, t.ggml_type, t.dims[0], t.dims[1])
+
+
+def parse_split_index(file_name):
+    """loader::parse_split_index: "x-00002-of-00005.gguf" -> (2, 5), else None."""
+    i, t = _U64(), _U64()
+    rc = host_lib().gqh_parse_split_index(file_name.encode(), ctypes.byref(i), ctypes.byref(t))
+    return None if rc != 0 else (i.value, t.value)
 
 
 def create_backend(preference="hip", device=0):

@@ -61,3 +61,33 @@ def test_no_device_fails_loudly():
         gq.create_backend("hip")
     with pytest.raises(gq.GqError):
         gq.create_backend("cpu")  # no CPU arm inside libgq: never a silent fallback
+
+
+HOST_HEADER = os.path.join(ROOT, "include", "gq_host.h")
+HOST_LIB = os.path.join(ROOT, "agention-infer_amd", "libgq_host.so")
+
+
+def declared_host():
+    text = open(HOST_HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    return sorted(set(re.findall(r"\b(gqh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_host_library_exports_every_declared_symbol():
+    assert os.path.exists(HOST_LIB), "run __graft_entry__.build() first"
+    out = subprocess.run(["nm", "-D", "--defined-only", HOST_LIB], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    names = declared_host()
+    assert "gqh_gguf_open" in names and "gqh_gguf_upload" in names
+    missing = [n for n in names if n not in exported]
+    assert not missing, missing
+
+
+def test_host_ctypes_signatures_cover_header():
+    import gq
+    assert sorted(gq.HOST_SIGNATURES) == declared_host()
+    L = gq.host_lib()
+    for n in declared_host():
+        assert hasattr(L, n)
