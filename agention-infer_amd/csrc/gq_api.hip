@@ -426,6 +426,32 @@ int gq_dequant_rows(const gq_weight *w, int row0, int nrows, float *out_dev, voi
   return GQ_OK;
 }
 
+int gq_dequant_rows_host(const gq_weight *w, int row0, int nrows, float *out_host) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (!w) return fail(GQ_EINVAL, "null weight handle");
+  if (row0 < 0 || nrows < 0 || row0 + nrows > w->L.rows)
+    return fail(GQ_EINVAL, "row index %d out of range (tensor has %d rows)", row0 + nrows - 1,
+                w->L.rows);
+  if (nrows == 0) return GQ_OK;
+  if (!out_host) return fail(GQ_EINVAL, "null out");
+  // Rows in batches of at most 64 MiB of f32 through one device buffer.
+  const int per = std::max(1, (int)std::min<long>(nrows, (64l << 20) / (4l * w->L.k)));
+  float *buf = nullptr;
+  HIP_TRY(hipMalloc(&buf, (size_t)per * w->L.k * 4));
+  hipError_t e = hipSuccess;
+  for (int r = 0; r < nrows && e == hipSuccess; r += per) {
+    const int n = std::min(per, nrows - r);
+    e = gq::launch_dequant(w, g_dev.grid, row0 + r, n, buf, nullptr);
+    if (e == hipSuccess)
+      e = hipMemcpy(out_host + (size_t)r * w->L.k, buf, (size_t)n * w->L.k * 4,
+                    hipMemcpyDeviceToHost);
+  }
+  (void)hipFree(buf);
+  if (e != hipSuccess) return fail(GQ_EHIP, "dequant failed: %s", hipGetErrorString(e));
+  return GQ_OK;
+}
+
 int gq_quantize_q8_32(const float *x_dev, int n, uint16_t *scale_dev, int8_t *q_dev,
                       void *stream) {
   int rc = ensure_init();
@@ -558,9 +584,8 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
         (rc = check_w(d->wup[l], d->ffn, H, "ffn_up", l)) ||
         (rc = check_w(d->wdown[l], H, d->ffn, "ffn_down", l)))
       return rc;
-    if (d->wq[l]->L.dtype != d->wk[l]->L.dtype || d->wq[l]->L.dtype != d->wv[l]->L.dtype ||
-        d->wgate[l]->L.dtype != d->wup[l]->L.dtype)
-      return fail(GQ_EINVAL, "layer %d: q/k/v and gate/up must share a dtype", l);
+    if (d->wgate[l]->L.dtype != d->wup[l]->L.dtype)
+      return fail(GQ_EINVAL, "layer %d: ffn_gate and ffn_up must share a dtype", l);
     const gq_weight *g = d->wgate[l];
     if (d->wup[l]->L.rows != g->L.rows || matvec_block_lds(g, true) > 160 * 1024)
       return fail(GQ_EINVAL, "layer %d: ffn_gate/ffn_up layouts do not pair", l);

@@ -451,9 +451,25 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     in.nw = m.attn_norm[L];
     in.xo = m.xb;
     in.eps = m.eps;
+    // One launch per distinct dtype among q/k/v (GGUF Q4_K_M files carry
+    // attn_v in Q6_K on some layers); each launch recomputes the norm and
+    // stores the same x_b.
     const gq_weight *qkv[3] = {m.wq[L], m.wk[L], m.wv[L]};
     float *qkv_out[3] = {m.q, m.k, m.v};
-    if ((e = matvec_launch(qkv, 3, in, qkv_out, s)) != hipSuccess) return e;
+    bool done[3] = {false, false, false};
+    for (int i = 0; i < 3; i++) {
+      if (done[i]) continue;
+      const gq_weight *grp[3];
+      float *gout[3];
+      int n = 0;
+      for (int j = i; j < 3; j++)
+        if (!done[j] && qkv[j]->L.dtype == qkv[i]->L.dtype) {
+          grp[n] = qkv[j];
+          gout[n++] = qkv_out[j];
+          done[j] = true;
+        }
+      if ((e = matvec_launch(grp, n, in, gout, s)) != hipSuccess) return e;
+    }
     uint16_t *kc = m.kcache + (long)L * m.ctx * kvd, *vc = m.vcache + (long)L * m.ctx * kvd;
     if (hd == 128)
       hipLaunchKernelGGL(k_attn_gqa<128>, dim3(nkv, m.att_chunks), dim3(ATT_THREADS), 0, s, m.q, m.k, m.v,

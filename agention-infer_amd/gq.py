@@ -47,6 +47,7 @@ SIGNATURES = {
     "gq_matmul_dequant_preloaded": (_I, [_P, _P, _P]),
     "gq_matmul_dequant_host": (_I, [_I, _P, _SZ, _P, _SZ, _P, _SZ]),
     "gq_dequant_rows": (_I, [_P, _I, _I, _P, _P]),
+    "gq_dequant_rows_host": (_I, [_P, _I, _I, _P]),
     "gq_gemm": (_I, [_P, _P, _I, _P, _I, _P]),
     "gq_quantize_q8_32": (_I, [_P, _I, _P, _P, _P]),
     "gq_set_iq3xxs_grid": (_I, [_P]),
@@ -89,7 +90,19 @@ HOST_SIGNATURES = {
     "gqh_gguf_meta_array_str": (_I, [_P, ctypes.c_char_p, _U64, _PP, ctypes.POINTER(_SZ)]),
     "gqh_parse_split_index": (_I, [ctypes.c_char_p, ctypes.POINTER(_U64), ctypes.POINTER(_U64)]),
     "gqh_gguf_upload": (_I, [_P, ctypes.c_char_p, _PP]),
+    "gqh_model_load": (_I, [_P, _I, _I, _PP]),
+    "gqh_model_free": (_I, [_P]),
+    "gqh_model_config_get": (_I, [_P, _P]),
+    "gqh_model_handle": (_I, [_P, _PP]),
 }
+
+
+class _HostModelConfig(ctypes.Structure):
+    _fields_ = [(n, _U64) for n in ("context_length", "embedding_length", "block_count",
+                                     "head_count", "head_count_kv", "head_dim",
+                                     "feed_forward_length", "vocab_size")] + \
+        [("rope_freq_base", ctypes.c_float), ("layer_norm_rms_epsilon", ctypes.c_float),
+         ("ctx", ctypes.c_int), ("architecture", ctypes.c_char * 64)]
 HOST_LIB_PATH = os.environ.get("GQ_HOST_LIBRARY") or os.path.join(_HERE, "libgq_host.so")
 
 
@@ -559,6 +572,37 @@ class GgufFile:
         h = ctypes.c_void_p()
         _hcheck(host_lib().gqh_gguf_upload(self._h, name.encode(), ctypes.byref(h)))
         return GpuWeightHandle(h.value, t.ggml_type, t.dims[0], t.dims[1])
+
+
+    def load_model(self, ctx=0, max_tokens=4096):
+        """LlamaModel::new + pre_upload_gpu: the whole decoder on the GPU."""
+        return GgufModel(self, ctx, max_tokens)
+
+
+class GgufModel(DecodeModel):
+    """A dense decoder loaded from a GGUF file by libgq_host (gqh_model_load);
+    decode / generate / kv_upload / kv_download as DecodeModel.  .config is
+    ModelConfig::from_gguf (architecture, embedding_length, ...)."""
+
+    def __init__(self, gguf, ctx=0, max_tokens=4096):
+        h = ctypes.c_void_p()
+        _hcheck(host_lib().gqh_model_load(gguf._h, int(ctx), int(max_tokens), ctypes.byref(h)))
+        self._owner = h
+        c = _HostModelConfig()
+        _hcheck(host_lib().gqh_model_config_get(h, ctypes.byref(c)))
+        self.config = {k: getattr(c, k) for k, _ in _HostModelConfig._fields_}
+        self.config["architecture"] = c.architecture.decode()
+        self.cfg = dict(n_layers=c.block_count, hidden=c.embedding_length, n_heads=c.head_count,
+                        n_kv_heads=c.head_count_kv, head_dim=c.head_dim, vocab=c.vocab_size,
+                        ctx=c.ctx, eps=c.layer_norm_rms_epsilon, theta=c.rope_freq_base)
+        m = ctypes.c_void_p()
+        _hcheck(host_lib().gqh_model_handle(h, ctypes.byref(m)))
+        self._h = m
+
+    def __del__(self):
+        if getattr(self, "_owner", None) is not None and _host is not None:
+            _host.gqh_model_free(self._owner)
+            self._owner = self._h = None
 
 
 def parse_split_index(file_name):

@@ -7,6 +7,14 @@
 #include "../../include/gq_host.h"
 #include "gguf.h"
 #include "hip_backend.h"
+#include "model.h"
+
+#include <sys/mman.h>
+#include <unistd.h>
+
+struct gqh_model {
+  std::unique_ptr<gqh::ResidentModel> m;
+};
 
 struct gqh_gguf {
   gqh::GgufFile file;
@@ -270,6 +278,59 @@ int gqh_gguf_upload(const gqh_gguf *f, const char *name, gq_weight **out) {
     *out = be.upload_weight(t->ggml_type, p, t->byte_size(), (size_t)t->dims[0]).release();
     return GQH_OK;
   });
+}
+
+int gqh_model_load(const gqh_gguf *f, int ctx, int max_tokens, gqh_model **out) {
+  if (!f || !out) return fail(GQH_EINVAL, "null argument");
+  *out = nullptr;
+  if (ctx < 0 || max_tokens <= 0) return fail(GQH_EINVAL, "ctx must be >= 0 and max_tokens > 0");
+  return guard([&]() -> int {
+    auto bytes = [f](const gqh::TensorInfo &t) { return tensor_bytes(f, t); };
+    // Pages of a file mapping that the upload has consumed go back to the
+    // page cache's control (a private read-only mapping re-reads on access).
+    gqh::ReleaseBytes release;
+    if (!f->single) {
+      release = [](const uint8_t *p, size_t n) {
+        const uintptr_t pg = (uintptr_t)sysconf(_SC_PAGESIZE);
+        const uintptr_t a = ((uintptr_t)p + pg - 1) & ~(pg - 1), b = ((uintptr_t)p + n) & ~(pg - 1);
+        if (b > a) (void)madvise((void *)a, b - a, MADV_DONTNEED);
+      };
+    }
+    auto h = std::make_unique<gqh_model>();
+    h->m = gqh::ResidentModel::load(f->file, bytes, ctx, max_tokens, release);
+    *out = h.release();
+    return GQH_OK;
+  });
+}
+
+int gqh_model_free(gqh_model *m) {
+  delete m;
+  return GQH_OK;
+}
+
+int gqh_model_config_get(const gqh_model *m, gqh_model_config *cfg) {
+  if (!m || !cfg) return fail(GQH_EINVAL, "null argument");
+  const gqh::ModelConfig &c = m->m->config();
+  std::memset(cfg, 0, sizeof(*cfg));
+  cfg->context_length = c.context_length;
+  cfg->embedding_length = c.embedding_length;
+  cfg->block_count = c.block_count;
+  cfg->head_count = c.head_count;
+  cfg->head_count_kv = c.head_count_kv;
+  cfg->head_dim = c.head_dim;
+  cfg->feed_forward_length = c.feed_forward_length;
+  cfg->vocab_size = c.vocab_size;
+  cfg->rope_freq_base = c.rope_freq_base;
+  cfg->layer_norm_rms_epsilon = c.layer_norm_rms_epsilon;
+  cfg->ctx = m->m->ctx();
+  std::strncpy(cfg->architecture, c.architecture.c_str(), sizeof(cfg->architecture) - 1);
+  return GQH_OK;
+}
+
+int gqh_model_handle(const gqh_model *m, gq_model **out) {
+  if (!m || !out) return fail(GQH_EINVAL, "null argument");
+  *out = m->m->handle();
+  return GQH_OK;
 }
 
 }  // extern "C"

@@ -98,6 +98,9 @@ int gq_matmul_dequant_host(int dtype, const void *w_host, size_t nbytes, const f
 /* quant::dequant_row (src/quant/mod.rs:25-45) for rows [row0, row0+nrows):
  * out_dev[nrows][in_dim] f32, bit-identical to the CPU dequant. */
 int gq_dequant_rows(const gq_weight *w, int row0, int nrows, float *out_dev, void *stream);
+/* The same into host memory, synchronous (WeightMap::dequant_tensor /
+ * dequant_row, src/model/mod.rs:307-349): out_host[nrows][in_dim]. */
+int gq_dequant_rows_host(const gq_weight *w, int row0, int nrows, float *out_host);
 
 /* launch_only_batch (src/ops/wgpu_backend/resident.rs:76-104) and the
  * prefill path of WeightMap::matmul_batch_into (src/model/mod.rs:414-464):

@@ -83,6 +83,30 @@ int gqh_parse_split_index(const char *file_name, uint64_t *index, uint64_t *tota
  * out_dim], type Q8_0/Q4_K/Q5_K/Q6_K/IQ3_XXS.  Free with gq_weight_free. */
 int gqh_gguf_upload(const gqh_gguf *f, const char *name, gq_weight **out);
 
+/* ---- A dense decoder from a GGUF file, resident on the GPU ------------
+ * LlamaModel::new (src/model/llama/mod.rs:130-300) with ModelConfig::
+ * from_gguf (src/model/mod.rs:212-272) and pre_upload_gpu (src/model/llama/
+ * gpu_resident.rs:69-229): every matmul weight uploaded once in file order,
+ * norms and the embedding table dequantized, then gq_model_create.  ctx = 0
+ * takes the file's context_length (at most 65536).  Files whose layers use
+ * another mixer, QK-norm or RoPE scaling fail with GQH_EBACKEND naming what
+ * the GPU-resident decode does not cover. The file may be closed after. */
+typedef struct gqh_model gqh_model;
+typedef struct {
+  uint64_t context_length, embedding_length, block_count, head_count, head_count_kv, head_dim,
+      feed_forward_length, vocab_size;
+  float rope_freq_base, layer_norm_rms_epsilon;
+  int ctx;                /* KV cache positions allocated */
+  char architecture[64];  /* NUL-terminated, truncated */
+} gqh_model_config;
+
+int gqh_model_load(const gqh_gguf *f, int ctx, int max_tokens, gqh_model **out);
+int gqh_model_free(gqh_model *m);
+int gqh_model_config_get(const gqh_model *m, gqh_model_config *cfg);
+/* The gq_model (include/gq.h) for gq_model_decode / _generate / _kv_*;
+ * owned by m. */
+int gqh_model_handle(const gqh_model *m, gq_model **out);
+
 #ifdef __cplusplus
 }
 #endif

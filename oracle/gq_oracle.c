@@ -813,13 +813,16 @@ int gqo_decode_step(const gqo_model *m, int token, int pos, float *logits, int n
     float *vall = (float *)malloc(sizeof(float) * (size_t)n * kvd);
     int rc = 0;
     memcpy(x, m->embd + (size_t)token * H, sizeof(float) * H);
-    const size_t rb_a = gqo_type_size(m->attn_type, H), rb_g = gqo_type_size(m->gate_up_type, H);
-    const size_t rb_d = gqo_type_size(m->down_type, F);
     for (int L = 0; L < m->n_layers && !rc; L++) {
+        const int *lt = m->layer_types ? m->layer_types + 7 * L : NULL;
+        const int tq = lt ? lt[0] : m->attn_type, tk = lt ? lt[1] : m->attn_type;
+        const int tv = lt ? lt[2] : m->attn_type, to = lt ? lt[3] : m->attn_type;
+        const int tg = lt ? lt[4] : m->gate_up_type, tu = lt ? lt[5] : m->gate_up_type;
+        const int td = lt ? lt[6] : m->down_type;
         rms_norm(x, m->attn_norm[L], H, m->eps, xn);
-        rc |= gqo_matmul_into(m->attn_type, m->wq[L], rb_a * nh * hd, xn, H, q, nh * hd, nthreads);
-        rc |= gqo_matmul_into(m->attn_type, m->wk[L], rb_a * kvd, xn, H, k, kvd, nthreads);
-        rc |= gqo_matmul_into(m->attn_type, m->wv[L], rb_a * kvd, xn, H, v, kvd, nthreads);
+        rc |= gqo_matmul_into(tq, m->wq[L], gqo_type_size(tq, H) * nh * hd, xn, H, q, nh * hd, nthreads);
+        rc |= gqo_matmul_into(tk, m->wk[L], gqo_type_size(tk, H) * kvd, xn, H, k, kvd, nthreads);
+        rc |= gqo_matmul_into(tv, m->wv[L], gqo_type_size(tv, H) * kvd, xn, H, v, kvd, nthreads);
         rope(q, k, nh, nkv, hd, m->theta, pos);
         uint16_t *kc = m->kcache[L], *vc = m->vcache[L];
         for (int i = 0; i < kvd; i++) {
@@ -847,13 +850,13 @@ int gqo_decode_step(const gqo_model *m, int token, int pos, float *logits, int n
             pthread_create(&th[t], NULL, attn_worker, &jobs[t]);
         }
         for (int t = 0; t < nt; t++) pthread_join(th[t], NULL);
-        rc |= gqo_matmul_into(m->attn_type, m->wo[L], rb_a * H, att, nh * hd, proj, H, nthreads);
+        rc |= gqo_matmul_into(to, m->wo[L], gqo_type_size(to, nh * hd) * H, att, nh * hd, proj, H, nthreads);
         for (int i = 0; i < H; i++) x[i] += proj[i];
         rms_norm(x, m->ffn_norm[L], H, m->eps, xn);
-        rc |= gqo_matmul_into(m->gate_up_type, m->wgate[L], rb_g * F, xn, H, g, F, nthreads);
-        rc |= gqo_matmul_into(m->gate_up_type, m->wup[L], rb_g * F, xn, H, u, F, nthreads);
+        rc |= gqo_matmul_into(tg, m->wgate[L], gqo_type_size(tg, H) * F, xn, H, g, F, nthreads);
+        rc |= gqo_matmul_into(tu, m->wup[L], gqo_type_size(tu, H) * F, xn, H, u, F, nthreads);
         for (int i = 0; i < F; i++) act[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
-        rc |= gqo_matmul_into(m->down_type, m->wdown[L], rb_d * H, act, F, proj, H, nthreads);
+        rc |= gqo_matmul_into(td, m->wdown[L], gqo_type_size(td, F) * H, act, F, proj, H, nthreads);
         for (int i = 0; i < H; i++) x[i] += proj[i];
     }
     if (!rc) {

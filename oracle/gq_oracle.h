@@ -119,6 +119,11 @@ typedef struct {
     const uint8_t *const *wq, *const *wk, *const *wv, *const *wo;
     const uint8_t *const *wgate, *const *wup, *const *wdown;
     uint16_t *const *kcache, *const *vcache;
+    /* Optional per-tensor types [n_layers][7] in the order wq, wk, wv, wo,
+     * wgate, wup, wdown (a GGUF file types each tensor on its own, as
+     * matmul_into dispatches per tensor, model/mod.rs:358-380); NULL: the
+     * uniform attn/gate_up/down types above. */
+    const int *layer_types;
 } gqo_model;
 
 /* LlamaModel::run (model/llama/cpu_path.rs:695-818) for the Attention

@@ -206,7 +206,7 @@ class _Model(ctypes.Structure):
         [(n, ctypes.c_int) for n in ("attn_type", "gate_up_type", "down_type", "head_type")] + \
         [(n, ctypes.c_void_p) for n in ("embd", "output_norm", "lm_head", "attn_norm",
                                          "ffn_norm", "wq", "wk", "wv", "wo", "wgate", "wup",
-                                         "wdown", "kcache", "vcache")]
+                                         "wdown", "kcache", "vcache", "layer_types")]
 
 
 class DecoderModel:
@@ -244,6 +244,10 @@ class DecoderModel:
             kk, vv = kv_init
             self.kc[:, :kk.shape[1]] = kk
             self.vc[:, :vv.shape[1]] = vv
+        if "layer_types" in w:  # [n_layers][7] per-tensor types (wq .. wdown)
+            lt = np.ascontiguousarray(w["layer_types"], np.int32).reshape(L, 7)
+            self.keep.append(lt)
+            m.layer_types = lt.ctypes.data
         m.kcache = ptr_array([self.kc[l] for l in range(L)])
         m.vcache = ptr_array([self.vc[l] for l in range(L)])
         self.m = m

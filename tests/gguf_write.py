@@ -55,3 +55,56 @@ def build_file(metadata=(), tensors=(), version=3, align=32):
     for (_, _, _, data), o in zip(tensors, offsets):
         body[o:o + len(data)] = bytes(data)
     return bytes(meta) + bytes(body), offsets
+
+
+GGML_F32, GGML_F16 = 0, 1
+_NAMES = dict(wq="attn_q", wk="attn_k", wv="attn_v", wo="attn_output", wgate="ffn_gate",
+              wup="ffn_up", wdown="ffn_down")
+ORDER = ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown")
+
+
+def decoder_tensors(cfg, w, layer_types, embd=None, head_type=None, norm_f16=False):
+    """The tensors of a dense decoder in GGUF naming (blk.N.attn_q.weight ...,
+    dims [in_dim, out_dim]).  w as gq_synth.make_decoder; layer_types
+    [n_layers][7] per-tensor types in ORDER; embd = (ggml_type, bytes) of
+    token_embd.weight ((GGML_F32, f32 table) if None); head_type None ties
+    lm_head to token_embd (no output.weight)."""
+    import numpy as np
+    H, F, V = cfg["hidden"], cfg["ffn"], cfg["vocab"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    dims = dict(wq=[H, qd], wk=[H, kvd], wv=[H, kvd], wo=[qd, H], wgate=[H, F], wup=[H, F],
+                wdown=[F, H])
+
+    def norm(a):
+        a = np.asarray(a, np.float32)
+        return (GGML_F16, a.astype(np.float16).tobytes()) if norm_f16 else (GGML_F32, a.tobytes())
+
+    et, eb = embd if embd is not None else (GGML_F32, np.asarray(w["embd"], np.float32).tobytes())
+    out = [("token_embd.weight", [H, V], et, eb)]
+    for l in range(cfg["n_layers"]):
+        b = f"blk.{l}."
+        nt, nb = norm(w["attn_norm"][l])
+        out.append((b + "attn_norm.weight", [H], nt, nb))
+        for k, t in zip(ORDER, layer_types[l]):
+            out.append((b + _NAMES[k] + ".weight", dims[k], t, bytes(w[k][l])))
+        nt, nb = norm(w["ffn_norm"][l])
+        out.append((b + "ffn_norm.weight", [H], nt, nb))
+    nt, nb = norm(w["output_norm"])
+    out.append(("output_norm.weight", [H], nt, nb))
+    if head_type is not None:
+        out.append(("output.weight", [H, V], head_type, bytes(w["lm_head"])))
+    return out
+
+
+def decoder_metadata(cfg, arch="qwen2", context_length=None, extra=()):
+    md = [("general.architecture", STRING, arch), ("general.name", STRING, "synthetic"),
+          (f"{arch}.block_count", U32, cfg["n_layers"]),
+          (f"{arch}.embedding_length", U32, cfg["hidden"]),
+          (f"{arch}.feed_forward_length", U32, cfg["ffn"]),
+          (f"{arch}.attention.head_count", U32, cfg["n_heads"]),
+          (f"{arch}.attention.head_count_kv", U32, cfg["n_kv_heads"]),
+          (f"{arch}.rope.freq_base", F32, cfg["theta"]),
+          (f"{arch}.attention.layer_norm_rms_epsilon", F32, cfg["eps"])]
+    if context_length is not None:
+        md.append((f"{arch}.context_length", U32, context_length))
+    return md + list(extra)

@@ -192,3 +192,67 @@ def test_split_files(tmp_path):
     with pytest.raises(gq.GgufError) as e:
         gq.GgufFile(path=str(tmp_path / "m-00001-of-00002.gguf"))
     assert _code(e) == -111
+
+
+# ---- gqh_model_load: what is refused before any device work -------------
+
+def _decoder_file(tmp_path, extra_meta=(), extra_tensors=(), drop=()):
+    H, V = 64, 10
+    md = gw.decoder_metadata(dict(n_layers=1, hidden=H, ffn=128, n_heads=2, n_kv_heads=1,
+                                  theta=1e6, eps=1e-6), extra=extra_meta)
+    z32 = np.zeros(H, np.float32).tobytes()
+    q4 = lambda rows, cols: bytes(rows * (cols // 256 + (cols % 256 > 0)) * 144)
+    ts = [("token_embd.weight", [H, V], 0, np.zeros((V, H), np.float32).tobytes()),
+          ("blk.0.attn_norm.weight", [H], 0, z32), ("blk.0.ffn_norm.weight", [H], 0, z32),
+          ("blk.0.attn_q.weight", [H, H], 12, b""), ("output_norm.weight", [H], 0, z32)]
+    ts = [t for t in ts if t[0] not in drop] + list(extra_tensors)
+    path = str(tmp_path / "m.gguf")
+    gw.write(path, md, ts)
+    return gq.GgufFile(path)
+
+
+@pytest.mark.parametrize("extra,what", [
+    ([("blk.0.shortconv.conv.weight", [3, 64], 0, bytes(768))], "ShortConv"),
+    ([("blk.0.ssm_alpha.weight", [64, 2], 0, bytes(512))], "GatedDeltaNet"),
+    ([("blk.0.attn_q_norm.weight", [32], 0, bytes(128))], "QK-norm"),
+])
+def test_model_load_refuses_uncovered_mixers(tmp_path, extra, what):
+    f = _decoder_file(tmp_path, extra_tensors=extra)
+    with pytest.raises(gq.GgufError) as e:
+        f.load_model()
+    assert _code(e) == -112 and what in str(e.value)
+
+
+def test_model_load_refuses_gated_attention(tmp_path):
+    f = _decoder_file(tmp_path, drop=("blk.0.attn_q.weight",),
+                      extra_tensors=[("blk.0.attn_q.weight", [64, 128], 12, b"")])
+    with pytest.raises(gq.GgufError) as e:
+        f.load_model()
+    assert _code(e) == -112 and "GatedAttention" in str(e.value)
+
+
+def test_model_load_refuses_rope_scaling(tmp_path):
+    f = _decoder_file(tmp_path, extra_meta=[("qwen2.rope.scaling.type", gw.STRING, "yarn")])
+    with pytest.raises(gq.GgufError) as e:
+        f.load_model()
+    assert _code(e) == -112 and "yarn" in str(e.value)
+
+
+@pytest.mark.parametrize("drop,what", [("token_embd.weight", "token_embd.weight"),
+                                       ("blk.0.attn_q.weight", "blk.0.attn_q.weight")])
+def test_model_load_missing_tensors(tmp_path, drop, what):
+    f = _decoder_file(tmp_path, drop=(drop,))
+    with pytest.raises(gq.GgufError) as e:
+        f.load_model()
+    assert _code(e) == -107 and what in str(e.value)
+
+
+def test_model_load_missing_head_count(tmp_path):
+    f = _decoder_file(tmp_path)
+    data = open(f"{tmp_path}/m.gguf", "rb").read()
+    f.close()
+    g = gq.GgufFile(data=data.replace(b"qwen2.attention.head_count\x04",
+                                      b"qwen2.attention.head_xxxxx\x04"))
+    with pytest.raises(gq.GgufError) as e:
+        g.load_model()
+    assert _code(e) == -107 and "attention.head_count" in str(e.value)
