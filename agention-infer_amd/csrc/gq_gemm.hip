@@ -19,9 +19,11 @@
 //                dot); its result is scaled by (d*sc)*xs and the min term
 //                dmin*m*xs*sum(q) is subtracted in fp32.
 //
-// Tiling: a block computes BM=160 weight rows x BN=256 tokens.  18944 rows
-// x 512 tokens -> 119 x 2 = 238 blocks: one round on 256 CUs.  K advances
-// 64 elements (one Q4_K group) per stage.
+// Tiling (bf16): a block computes 80 weight rows x 512 tokens when the
+// batch is longer than 256 tokens (18944 rows x 512 tokens -> 237 blocks:
+// one round on 256 CUs, every weight element dequantized once), else 160
+// rows x 256 tokens.  K advances 64 elements (one Q4_K group) per stage.
+// int8: 160 rows x 128 tokens.
 #include <type_traits>
 
 #include "gq_device.h"
@@ -60,12 +62,24 @@ __global__ void k_x_to_bf16_frag(const float *X, int n, int npad, int k, int kpa
   const int nt = (int)(f / ksteps), ks = (int)(f % ksteps);
   const int t = 16 * nt + (l & 15), c0 = 32 * ks + 8 * (l >> 4);
   uint32_t o[4];
+  if ((k & 7) == 0) {  // the 8 values are one aligned 32-byte run (or all padding)
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (t < n && c0 < k) {
+      a = *(const float4 *)(X + (long)t * k + c0);
+      b = *(const float4 *)(X + (long)t * k + c0 + 4);
+    }
+    o[0] = f2bf(a.x) | (f2bf(a.y) << 16);
+    o[1] = f2bf(a.z) | (f2bf(a.w) << 16);
+    o[2] = f2bf(b.x) | (f2bf(b.y) << 16);
+    o[3] = f2bf(b.z) | (f2bf(b.w) << 16);
+  } else {
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
-    const int c = c0 + 2 * e;
-    const float a = t < n && c < k ? X[(long)t * k + c] : 0.f;
-    const float b = t < n && c + 1 < k ? X[(long)t * k + c + 1] : 0.f;
-    o[e] = f2bf(a) | (f2bf(b) << 16);
+    for (int e = 0; e < 4; e++) {
+      const int c = c0 + 2 * e;
+      const float a = t < n && c < k ? X[(long)t * k + c] : 0.f;
+      const float b = t < n && c + 1 < k ? X[(long)t * k + c + 1] : 0.f;
+      o[e] = f2bf(a) | (f2bf(b) << 16);
+    }
   }
   *(uint4 *)(out + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
 }
@@ -286,187 +300,230 @@ constexpr int UB = 144;                        // bytes per Q4_K unit
 constexpr int WU_SLOT = 24 * 1024;             // one unit of BM rows (23040 B) + pad
 constexpr int W_INSTR = WU_SLOT / 1024;        // 24 loads of 64 x 16 B per unit
 
-__global__ __launch_bounds__(512) void k_gemm_bf16(Layout L, const uint8_t *raw, long row_bytes,
-                                                   const uint16_t *Xb, int n, int kpad,
-                                                   float *Y) {
-  __shared__ __align__(16) uint16_t As[2][A_FR * FR16];
-  __shared__ __align__(16) uint16_t Xs[2][B_FR * FR16];
-  __shared__ __align__(16) uint8_t Wu[2][WU_SLOT];
+// ----------------------------------------------------------- bf16 kernel, ring pipeline
+// Block tile TBM rows x TBN tokens, 4 multiply waves of 80 x 128 (as in
+// k_gemm_bf16: fragment-major LDS operands) and 4 producer waves, with a
+// deeper pipeline than k_gemm_bf16:
+//   * W is fetched per stage, only the bytes the stage needs (the unit's
+//     16-byte header and the group's 32 quant bytes per row), two stages
+//     ahead, into a ring private to each producer wave: producer wave p
+//     fetches and dequantizes rows TBM/4 * p .. + TBM/4 itself, so it waits
+//     only for its own loads and no W bytes cross waves;
+//   * X fragments go through an NXR-slot ring, fetched NXR - 1 stages ahead;
+//   * the multiply waves only multiply.
+// With TBN = 512 (80 x 512 tiles) a block covers all tokens of a 512-token
+// batch, so every weight element is dequantized once per call.
+// Iteration kt: multiply waves run stage kt; producer waves issue the loads
+// of stage kt + NXR - 1 (X) and kt + 2 (W), wait for W of stage kt + 1,
+// dequantize it, and (NXR = 2) wait for X of stage kt + 1.  One barrier per
+// iteration.  Blocks are numbered so that the token tiles of a row tile are
+// 8 apart, i.e. on the same XCD (consecutive blocks go to consecutive
+// XCDs): the row tile's W bytes are fetched into one L2.
+constexpr int WR = 3;  // W ring slots
+
+template <int TBM, int TBN, int NXR>
+struct Ring {
+  static constexpr int AT_ = TBM / 16, BT_ = TBN / 16;
+  static constexpr int A_FR_ = 2 * AT_, B_FR_ = 2 * BT_;
+  static constexpr int PROWS = TBM / 4;        // rows per producer wave
+  static constexpr int WSLOTS = 3 * PROWS;     // 16-byte W chunks per producer wave per stage
+  static constexpr int WINS = (WSLOTS + 63) / 64;
+  static constexpr int XPW = B_FR_ / 4;        // X fragment loads per producer wave per stage
+  static constexpr int WGM = TBM / WM;         // multiply waves along the rows
+  static_assert(WGM * (TBN / WN) == 4, "4 multiply waves");
+  static constexpr int TASKS = 4 * PROWS;      // 16-element dequant tasks per producer wave
+  static constexpr int ROUNDS = (TASKS + 63) / 64;
+};
+
+template <int TBM, int TBN, int NXR>
+__global__ __launch_bounds__(512) void k_gemm_bf16_ring(Layout L, const uint8_t *raw,
+                                                        long row_bytes, const uint16_t *Xb, int n,
+                                                        int kpad, int mtiles, int ntiles,
+                                                        float *Y) {
+  using R = Ring<TBM, TBN, NXR>;
+  constexpr int AT_ = R::AT_, BT_ = R::BT_, PROWS = R::PROWS, WSLOTS = R::WSLOTS;
+  constexpr int WINS = R::WINS, XPW = R::XPW;
+  __shared__ __align__(16) uint16_t As[2][R::A_FR_ * FR16];
+  __shared__ __align__(16) uint16_t Xs[NXR][R::B_FR_ * FR16];
+  __shared__ __align__(16) uint8_t Wg[4][WR][WSLOTS * 16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
-  const int stages = kpad / BK, last = stages - 1, lastu = L.units - 1;
+  // block -> (row tile, token tile): blocks b, b + 8, b + 16, ... of a group
+  // of 8 * ntiles share the row tile
+  const int b = blockIdx.x, grp = b / (8 * ntiles), rem = b % (8 * ntiles);
+  const int mt = 8 * grp + (rem & 7), ntile = rem >> 3;
+  if (mt >= mtiles) return;
+  const int m0 = mt * TBM, n0 = ntile * TBN;
+  const int stages = kpad / BK, last = stages - 1;
   const bool mma = wave < 4;
 
-  // ---- consumer state
-  const int wm = wave & 1, wn = (wave >> 1) & 1;
+  if (!mma) {
+    const int pw = wave - 4;
+    const int ksteps = kpad / 32;
+    const uint16_t *xsrc = Xb + ((long)(n0 / 16) * ksteps * 64 + lane) * 8;
+    // W chunk slots of this wave: q = 64 i + lane (q < WSLOTS): row
+    // PROWS * pw + q / 3, chunk q % 3 (header, quant bytes 0-15, 16-31 of
+    // the group).
+    const uint8_t *wrow[WINS];
+    int wc[WINS];
+#pragma unroll
+    for (int i = 0; i < WINS; i++) {
+      const int q = min(64 * i + lane, WSLOTS - 1);
+      const int row = min(m0 + PROWS * pw + q / 3, L.rows - 1);
+      wrow[i] = raw + (long)row * row_bytes;
+      wc[i] = q % 3;
+    }
+    auto issue_x = [&](int s) {  // X fragments of stage s (clamped) into slot s % NXR
+      const int sc = min(s, last);
+#pragma unroll
+      for (int qd = 0; qd < XPW; qd++) {
+        const int f = XPW * pw + qd, nt = f % BT_, ks = f / BT_;
+        dma16(xsrc + ((long)nt * ksteps + 2 * sc + ks) * 512, &Xs[s % NXR][f * FR16]);
+      }
+    };
+    auto issue_w = [&](int s) {  // this wave's W rows of stage s (clamped) into slot s % WR
+      const int sc = min(s, last);
+      const int u = sc >> 2, j = sc & 3;
+#pragma unroll
+      for (int i = 0; i < WINS; i++) {
+        const int off = wc[i] == 0 ? 0 : 16 + 32 * j + 16 * (wc[i] - 1);
+        if (64 * i + lane < WSLOTS) dma16(wrow[i] + (long)u * UB + off, &Wg[pw][s % WR][1024 * i]);
+      }
+    };
+    // Dequantize stage s of this wave's rows: task t = 4 rr + 2 h + qq (row
+    // rr, nibble half h, 16-element quarter qq), t = lane + 64 round.
+    auto dequant = [&](int s) {
+      const int j = s & 3;
+      const uint8_t *wg = Wg[pw][s % WR];
+      // (asm reads: a plain LDS read would make the compiler wait for every
+      // outstanding load straight to LDS, the ones just issued included)
+      uint4 hd[3], qs[3];
+      uint32_t ad[6];
+#pragma unroll
+      for (int round = 0; round < 3; round++) {
+        const int t = min(lane + 64 * round, R::TASKS - 1);
+        const int rr = t >> 2, qq = t & 1;
+        ad[2 * round] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 48 * rr);
+        ad[2 * round + 1] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 48 * rr + 16 + 16 * qq);
+      }
+      if constexpr (R::ROUNDS == 3) {
+        uint4 v6[6];
+        lds_read6(ad, v6);
+        hd[0] = v6[0]; qs[0] = v6[1]; hd[1] = v6[2]; qs[1] = v6[3]; hd[2] = v6[4]; qs[2] = v6[5];
+      } else {
+        static_assert(R::ROUNDS == 2, "2 or 3 dequant rounds");
+        const uint32_t ad4[4] = {ad[0], ad[1], ad[2], ad[3]};
+        uint4 v4[4];
+        lds_read4(ad4, v4);
+        hd[0] = v4[0]; qs[0] = v4[1]; hd[1] = v4[2]; qs[1] = v4[3];
+      }
+#pragma unroll
+      for (int round = 0; round < R::ROUNDS; round++) {
+        const int t = lane + 64 * round;
+        if (round < R::ROUNDS - 1 || t < R::TASKS) {
+          const int rr = t >> 2, h = (t >> 1) & 1, qq = t & 1;
+          const int r = PROWS * pw + rr;
+          const bool ok = m0 + r < L.rows;
+          uint32_t sc, mn;
+          scale_min_k4_sel(2 * j + h, hd[round].y, hd[round].z, hd[round].w, sc, mn);
+          const float ds = ok ? h2f(hd[round].x) * (float)sc : 0.f;
+          const float nm = ok ? -(h2f(hd[round].x >> 16) * (float)mn) : 0.f;
+          const uint32_t qw[4] = {qs[round].x, qs[round].y, qs[round].z, qs[round].w};
+          const uint32_t sh = 4u * (uint32_t)h;
+          uint32_t o[8];
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const uint32_t qv = (qw[i] >> sh) & 0x0F0F0F0Fu;
+            o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(qv), nm), fmaf(ds, cvt_ubyte<1>(qv), nm));
+            o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(qv), nm), fmaf(ds, cvt_ubyte<3>(qv), nm));
+          }
+          uint16_t *dst = &As[s & 1][((h * AT_ + (r >> 4)) * 64 + (r & 15) + 32 * qq) * 8];
+          *(uint4 *)dst = make_uint4(o[0], o[1], o[2], o[3]);
+          *(uint4 *)(dst + 128) = make_uint4(o[4], o[5], o[6], o[7]);
+        }
+      }
+    };
+    if constexpr (NXR == 3) {
+      // prologue: stages 0 and 1 in flight, stage 0 dequantized
+      issue_x(0);
+      issue_w(0);
+      issue_x(1);
+      issue_w(1);
+      wait_vm<XPW + WINS>();
+      dequant(0);
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+      for (int kt = 0; kt < stages; kt++) {
+        issue_x(kt + 2);
+        issue_w(kt + 2);
+        wait_vm<XPW + WINS>();  // stage kt + 1 (X and this wave's W rows) in LDS
+        if (kt + 1 < stages) dequant(kt + 1);
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();
+      }
+    } else {
+      static_assert(NXR == 2, "2 or 3 X slots");
+      issue_x(0);
+      issue_w(0);
+      issue_w(1);
+      wait_vm<WINS>();  // X and W of stage 0
+      dequant(0);
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+      for (int kt = 0; kt < stages; kt++) {
+        issue_x(kt + 1);
+        issue_w(kt + 2);
+        wait_vm<XPW + WINS>();  // W of stage kt + 1
+        if (kt + 1 < stages) dequant(kt + 1);
+        wait_vm<WINS>();  // X of stage kt + 1
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();
+      }
+    }
+    wait_vm<0>();  // drain the clamped loads before the block ends
+    return;
+  }
+
+  // ---- multiply waves
+  const int wm = wave % R::WGM, wn = wave / R::WGM;
   f32x4_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; i++)
 #pragma unroll
-    for (int j = 0; j < TN; j++) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  // ---- producers: waves 4-5 fetch raw W units, waves 6-7 fetch X tiles;
-  // all four dequantize (640 tasks of 16 elements per stage).
-  const int pw = (wave - 4) & 3, pt = tid & 255;
-  const bool wfetch = pw < 2;
-  // raw W: this wave's 12 loads cover 16-byte slots (12pw + q)*64 + lane of
-  // the unit image [row][144 B]; slots past BM rows land in the pad.
-  // (Addresses are recomputed per unit: kept in registers they would
-  // compete with the multiply waves' accumulators.)
-  // X: this wave's 8 loads are fragments f = 8pw + q of the stage: k-step
-  // f/16, token tile f%16 (1 KiB each in the prepass's order).
-  const int ksteps = kpad / 32;
-  const uint16_t *xsrc = Xb + ((long)(n0 / 16) * ksteps * 64 + lane) * 8;
-  auto load_w_unit = [&](int u) {  // unit u (clamped) into slot u & 1
-    const int uc = min(u, lastu);
-#pragma unroll 4
-    for (int q = 0; q < 12; q++) {
-      const int sl = min((12 * (pw & 1) + q) * 64 + lane, BM * 9 - 1);
-      const int row = min(m0 + sl / 9, L.rows - 1);
-      dma16(raw + (long)row * row_bytes + (long)uc * UB + 16 * (sl % 9),
-            &Wu[u & 1][(12 * (pw & 1) + q) * 1024]);
-    }
-  };
-  auto load_x = [&](int s) {  // this wave's 8 X fragments of stage s (clamped) into slot s & 1
-    const int sc = min(s, last);
-#pragma unroll 4
-    for (int q = 0; q < 8; q++) {
-      const int f = 8 * pw + q, nt = f & 15, ks = f >> 4;
-      dma16(xsrc + ((long)nt * ksteps + 2 * sc + ks) * 512, &Xs[s & 1][f * FR16]);
-    }
-  };
-  // Dequantize NR of the stage's 640 tasks (row r, half h, 16-element
-  // quarter qq) -- tasks t0 + 256 * round below 640 -- from raw W unit
-  // s / 4 into As[s & 1].  All LDS reads first (one wait: their latency
-  // under the rest of the block's LDS traffic is long), then the math.
-  auto dequant = [&](int s, int t0, auto nr_tag) {
-    constexpr int NR = decltype(nr_tag)::value;
-    const int u = s >> 2, j = s & 3;
-    const uint8_t *wu = Wu[u & 1];
-    uint32_t ad[2 * NR];
-    int tk[NR];
-#pragma unroll
-    for (int round = 0; round < NR; round++) {
-      tk[round] = min(t0 + 256 * round, 4 * BM - 1);
-      const int r = tk[round] >> 2, qq = tk[round] & 1;
-      ad[2 * round] = (uint32_t)(uintptr_t)(lds_void_t *)(wu + r * UB);
-      ad[2 * round + 1] = (uint32_t)(uintptr_t)(lds_void_t *)(wu + r * UB + 16 + 32 * j + 16 * qq);
-    }
-    uint4 v[2 * NR];
-    if constexpr (NR == 2) {
-      lds_read4(ad, v);
-    } else {
-      lds_read2_a(ad, v);
-    }
-#pragma unroll
-    for (int round = 0; round < NR; round++) {
-      if (t0 + 256 * round < 4 * BM) {
-        const int task = tk[round];
-        const int r = task >> 2, h = (task >> 1) & 1, qq = task & 1;
-        const uint4 hd = v[2 * round], qs = v[2 * round + 1];
-        const bool ok = m0 + r < L.rows;
-        uint32_t sc, mn;
-        scale_min_k4_sel(2 * j + h, hd.y, hd.z, hd.w, sc, mn);
-        // rows past the matrix: zero scales give zero weights (no branches)
-        const float ds = ok ? h2f(hd.x) * (float)sc : 0.f;
-        const float nm = ok ? -(h2f(hd.x >> 16) * (float)mn) : 0.f;
-        const uint32_t qw[4] = {qs.x, qs.y, qs.z, qs.w};
-        const uint32_t sh = 4u * (uint32_t)h;
-        uint32_t o[8];
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const uint32_t q = (qw[i] >> sh) & 0x0F0F0F0Fu;
-          // one FMA per element (the bf16 rounding that follows dominates)
-          o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(q), nm), fmaf(ds, cvt_ubyte<1>(q), nm));
-          o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(q), nm), fmaf(ds, cvt_ubyte<3>(q), nm));
-        }
-        // k 32h + 16qq .. +16 = lane slots 2qq, 2qq+1 of k-step h
-        uint16_t *dst = &As[s & 1][((h * AT + (r >> 4)) * 64 + (r & 15) + 32 * qq) * 8];
-        *(uint4 *)dst = make_uint4(o[0], o[1], o[2], o[3]);
-        *(uint4 *)(dst + 128) = make_uint4(o[4], o[5], o[6], o[7]);
-      }
-    }
-  };
-  // Multiply waves take tasks 0..255 (one each), producers 256..639.
-  auto dequant_share = [&](int s) {
-    if (mma) {
-      dequant(s, tid, std::integral_constant<int, 1>());
-    } else {
-      dequant(s, 256 + pt, std::integral_constant<int, 2>());
-    }
-  };
-
-  // ---- prologue.  A W unit is read by all producer waves but only the W
-  // waves can wait for its loads, so it is waited for one stage before its
-  // first use and published by that stage's barrier.
-  if (!mma) {
-    load_x(0);
-    if (wfetch) load_w_unit(0);
-    wait_vm<0>();
-    if (wfetch) load_w_unit(1);
-  }
-  __builtin_amdgcn_s_barrier();  // unit 0 and X tile 0 in LDS
-  dequant_share(0);
-  wait_lgkm0();
-  __builtin_amdgcn_s_barrier();  // W tile 0 in LDS
-
+    for (int jj = 0; jj < TN; jj++) acc[i][jj] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  __builtin_amdgcn_s_barrier();  // stage 0 in LDS
   for (int kt = 0; kt < stages; kt++) {
-    if (mma) {
-      const uint16_t *A = As[kt & 1], *B = Xs[kt & 1];
+    const uint16_t *A = As[kt & 1], *B = Xs[kt % NXR];
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        bf16x8_t a[TM];
+    for (int ks = 0; ks < 2; ks++) {
+      bf16x8_t a[TM];
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+        a[i] = *(const bf16x8_t *)(A + ((ks * AT_ + TM * wm + i) * 64 + lane) * 8);
+#pragma unroll
+      for (int jn = 0; jn < TN; jn++) {
+        const bf16x8_t bb = *(const bf16x8_t *)(B + ((ks * BT_ + TN * wn + jn) * 64 + lane) * 8);
 #pragma unroll
         for (int i = 0; i < TM; i++)
-          a[i] = *(const bf16x8_t *)(A + ((ks * AT + TM * wm + i) * 64 + lane) * 8);
-#pragma unroll
-        for (int jn = 0; jn < TN; jn++) {
-          const bf16x8_t b = *(const bf16x8_t *)(B + ((ks * BT + TN * wn + jn) * 64 + lane) * 8);
-#pragma unroll
-          for (int i = 0; i < TM; i++)
-            acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b, acc[i][jn], 0, 0, 0);
-        }
+          acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bb, acc[i][jn], 0, 0, 0);
       }
-      dequant_share(kt + 1);  // runs while the MFMAs drain
-      wait_lgkm0();
-    } else {
-      // Every producer wave fetches 8 X fragments of stage kt + 1 and
-      // dequantizes; waves 4-5 also fetch W units.  Unit v is requested at
-      // stage 4v - 5 (after that stage's X loads), waited for at stage
-      // 4v - 2 and published by that stage's barrier; stage 4v, its first,
-      // is dequantized at 4v - 1.
-      load_x(kt + 1);
-      dequant_share(kt + 1);
-      if (wfetch && (kt & 3) == 3) {
-        load_w_unit((kt + 5) >> 2);
-        wait_vm<12>();  // X of stage kt + 1 (older than the 12 unit loads)
-      } else {
-        wait_vm<0>();  // X of stage kt + 1 (and, at kt % 4 == 2, unit (kt + 2) / 4)
-      }
-      wait_lgkm0();
     }
+    wait_lgkm0();
     __builtin_amdgcn_s_barrier();
   }
-  if (!mma) {
-    wait_vm<0>();  // drain the clamped reloads before the block ends
-    return;
-  }
-
-  // D layout: lane holds rows 4*(lane/16)+r (weight rows) of column lane%16 (token).
 #pragma unroll
   for (int i = 0; i < TM; i++) {
     const int m = m0 + WM * wm + 16 * i + 4 * (lane >> 4);
 #pragma unroll
-    for (int j = 0; j < TN; j++) {
-      const int t = n0 + WN * wn + 16 * j + (lane & 15);
+    for (int jj = 0; jj < TN; jj++) {
+      const int t = n0 + WN * wn + 16 * jj + (lane & 15);
       if (t >= n) continue;
       float *yp = Y + (long)t * L.rows + m;
       if (m + 3 < L.rows && (L.rows & 3) == 0) {
-        *(float4 *)yp = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+        *(float4 *)yp = make_float4(acc[i][jj][0], acc[i][jj][1], acc[i][jj][2], acc[i][jj][3]);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; r++)
-          if (m + r < L.rows) yp[r] = acc[i][j][r];
+          if (m + r < L.rows) yp[r] = acc[i][jj][r];
       }
     }
   }
@@ -603,7 +660,7 @@ __global__ __launch_bounds__(256) void k_gemm_i8(Layout L, const uint8_t *body, 
 size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode) {
   if (w->L.dtype != T_Q4_K) return (size_t)-1;
   const size_t kpad = (size_t)w->L.units * 256;
-  if (mode == GQ_GEMM_BF16) return (size_t)((n + BN - 1) / BN * BN) * kpad * 2 + 256;
+  if (mode == GQ_GEMM_BF16) return (size_t)((n + 511) / 512 * 512) * kpad * 2 + 256;
   // int8: q [n][kpad] + scale f32 [n][kpad/32] + qsum int [n][kpad/32]
   return (size_t)n * kpad + (size_t)n * (kpad / 32) * 8 + 512;
 }
@@ -638,12 +695,21 @@ hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int 
   if (mode == GQ_GEMM_BF16) {
     const dim3 grid((L.rows + BM - 1) / BM, (n + BN - 1) / BN);
     uint16_t *xb = (uint16_t *)workspace;
-    const int npad = (n + BN - 1) / BN * BN;
+    const int npad = (n + 511) / 512 * 512;  // a multiple of every token tile
     const long slots = (long)(npad / 16) * (kpad / 32) * 64;
     hipLaunchKernelGGL(k_x_to_bf16_frag, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st,
                        X, n, npad, L.k, kpad, xb);
-    hipLaunchKernelGGL(k_gemm_bf16, grid, dim3(512), 0, st, L, (const uint8_t *)w->gemm_raw,
-                       (long)L.units * UB, (const uint16_t *)xb, n, kpad, Y);
+    // 80 x 512 tiles when the batch is longer than one 256-token tile (each
+    // weight element dequantized once per 512 tokens), else 160 x 256
+    const bool wide = n > BN;
+    const int tbm = wide ? 80 : BM, tbn = wide ? 512 : BN;
+    const int mtiles = (L.rows + tbm - 1) / tbm, ntiles = (n + tbn - 1) / tbn;
+    // 8 * ntiles consecutive blocks hold 8 row tiles x all token tiles
+    const long nb = (long)((mtiles + 7) / 8) * 8 * ntiles;
+    if (nb > 0x7fffffffL) return hipErrorInvalidValue;
+    auto kern = wide ? k_gemm_bf16_ring<80, 512, 2> : k_gemm_bf16_ring<160, 256, 3>;
+    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(512), 0, st, L, (const uint8_t *)w->gemm_raw,
+                       (long)L.units * UB, (const uint16_t *)xb, n, kpad, mtiles, ntiles, Y);
   } else {
     int8_t *xq = (int8_t *)workspace;
     float *xs = (float *)((char *)workspace + (((size_t)n * kpad + 255) & ~(size_t)255));
