@@ -490,6 +490,26 @@ int gq_get_iq3xxs_grid(uint32_t *grid_host) {
   return GQ_OK;
 }
 
+// The bf16 GEMM streams per-stage records of a weight (made once, on first
+// use, from the tiled body).
+static int gq_ensure_gemm_records(const gq_weight *w, hipStream_t stream) {
+  if (w->gemm_raw) return GQ_OK;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (w->gemm_raw) return GQ_OK;
+  uint8_t *rec = nullptr;
+  const size_t bytes = gq::gemm_records_bytes(w->L);
+  if (hipMalloc(&rec, bytes) != hipSuccess)
+    return fail(GQ_ENOMEM, "hipMalloc of %zu bytes (GEMM weight records) failed", bytes);
+  hipError_t e = gq::launch_gemm_records(w, rec, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) {
+    (void)hipFree(rec);
+    return fail(GQ_EHIP, "GEMM weight records failed: %s", hipGetErrorString(e));
+  }
+  const_cast<gq_weight *>(w)->gemm_raw = rec;
+  return GQ_OK;
+}
+
 int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mode,
             void *stream) {
   int rc = ensure_init();
@@ -498,25 +518,13 @@ int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mod
   if (n < 0) return fail(GQ_EINVAL, "negative batch");
   if (n == 0 || w->L.rows == 0) return GQ_OK;
   if (mode != GQ_GEMM_BF16 && mode != GQ_GEMM_INT8) return fail(GQ_EINVAL, "bad gemm mode %d", mode);
-  const size_t ws = gq::gemm_workspace_bytes(w, n, mode);
+  const size_t ws = gq::gemm_workspace_bytes(w, n, mode, g_dev.num_cus);
   if (ws == (size_t)-1)
-    return fail(GQ_EDTYPE, "gq_gemm: %s weights with in_dim %d not supported in this mode",
-                type_name(w->L.dtype), w->L.k);
-  if (mode == GQ_GEMM_BF16 && !w->gemm_raw) {
-    // The bf16 GEMM streams whole 144-byte units of each row, which the
-    // tiled matvec layout scatters; keep a ggml-order copy (made once).
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (!w->gemm_raw) {
-      uint8_t *raw = nullptr;
-      if (hipMalloc(&raw, w->ggml_bytes) != hipSuccess)
-        return fail(GQ_ENOMEM, "hipMalloc of %zu bytes (GEMM weight copy) failed", w->ggml_bytes);
-      hipError_t e = gq::launch_unrepack_q4k(w->L, w->body, raw, (hipStream_t)stream);
-      if (e != hipSuccess) {
-        (void)hipFree(raw);
-        return fail(GQ_EHIP, "GEMM weight copy failed: %s", hipGetErrorString(e));
-      }
-      const_cast<gq_weight *>(w)->gemm_raw = raw;
-    }
+    return fail(GQ_EDTYPE, "gq_gemm: %s weights not supported in %s mode", type_name(w->L.dtype),
+                mode == GQ_GEMM_BF16 ? "bf16" : "int8");
+  if (mode == GQ_GEMM_BF16) {
+    int rc2 = gq_ensure_gemm_records(w, (hipStream_t)stream);
+    if (rc2) return rc2;
   }
   void *wsp = nullptr;
   if (ws) HIP_TRY(hipMallocAsync(&wsp, ws, (hipStream_t)stream));

@@ -293,128 +293,229 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-// Raw (ggml-order) Q4_K bytes for the GEMM: a row's 144-byte units are
-// contiguous, so a producer fetches whole units (2.25 cache lines) instead
-// of the scattered 16-byte chunks of the tiled matvec layout.
-constexpr int UB = 144;                        // bytes per Q4_K unit
-constexpr int WU_SLOT = 24 * 1024;             // one unit of BM rows (23040 B) + pad
-constexpr int W_INSTR = WU_SLOT / 1024;        // 24 loads of 64 x 16 B per unit
+// ----------------------------------------------------------- bf16 GEMM weights
+// The bf16 GEMM streams its own copy of a weight, made once: per row, one
+// record per 64-element stage (K-step), holding exactly the bytes the
+// stage's dequant needs, so that a producer fetches each stage's rows as
+// whole 16-byte chunks:
+//   Q4_K: the ggml block order itself (144-byte units); a stage reads the
+//                unit's 16-byte header (d, dmin, 12 scale bytes; the same
+//                bytes for the unit's 4 stages, so 3 of 4 reads hit L2) and
+//                the group's 32 quant bytes (byte i holds element i in its
+//                low and element 32 + i in its high nibble);
+//   Q6_K (64 B): chunk 0 = the 4 int8 scales of the stage's 16-element
+//                groups, then d (f16); chunks 1-2 = the low 4 bits of the
+//                6-bit codes in the same nibble order as Q4_K; chunk 3 = the
+//                high 2 bits, dword g (16-element group g) holding element
+//                16 g + i at bits 2i, 2i + 1.
+template <int FMT> struct GemmFmt;
+template <> struct GemmFmt<T_Q4_K> { static constexpr int C = 3; };
+template <> struct GemmFmt<T_Q6_K> { static constexpr int C = 4; };
+// Bytes of the copy per unit (4 stages) of a row.
+__host__ __device__ constexpr int gemm_unit_bytes(int fmt) { return fmt == T_Q6_K ? 256 : 144; }
+// Offset of chunk c of stage s within a row of the copy.
+template <int FMT>
+__device__ __forceinline__ long gemm_chunk_off(int s, int c) {
+  if constexpr (FMT == T_Q6_K) return (long)s * 64 + 16 * c;
+  else return (long)(s >> 2) * 144 + (c == 0 ? 0 : 16 + 32 * (s & 3) + 16 * (c - 1));
+}
+
+// Record of stage j (0..3) of one unit from the unit's ggml bytes u[] (Q6_K:
+// ql 0..127, qh 128..191, scales 192..207, d at 208).
+__device__ void q6k_stage_record(const uint8_t *u, int j, uint8_t *rec) {
+  for (int i = 0; i < 64; i++) rec[i] = 0;
+  for (int g = 0; g < 4; g++) {
+    for (int i = 0; i < 16; i++) {
+      const int x = 16 * g + i, e = 64 * j + x;  // element of the unit (dequant_q6_k order)
+      const int nh = e >> 7, r = e & 127, p = r >> 5, l = r & 31;
+      const uint8_t qlb = u[64 * nh + l + 32 * (p & 1)];
+      const int lo = (p >> 1) ? qlb >> 4 : qlb & 15;
+      const int hi = (u[128 + 32 * nh + l] >> (2 * p)) & 3;
+      // low nibble: byte 16 (g & 1) + i of chunks 1-2, nibble g >> 1
+      rec[16 + 16 * (g & 1) + i] |= (uint8_t)(lo << (4 * (g >> 1)));
+      rec[48 + 4 * g + (i >> 2)] |= (uint8_t)(hi << (2 * (i & 3)));
+      if (i == 0) rec[g] = u[192 + 8 * nh + (l >> 4) + 2 * p];
+    }
+  }
+  rec[4] = u[208];
+  rec[5] = u[209];
+}
+
+// One thread per (row, unit): the unit's part of the GEMM copy, from the
+// tiled body.
+__global__ void k_gemm_records(Layout L, const uint8_t *body, const uint16_t *dd, uint8_t *out) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (long)L.rows * L.units) return;
+  const int r = (int)(i / L.units), u = (int)(i % L.units);
+  const int t = r / L.rt, j = (r % L.rt) * L.units + u;
+  uint8_t *dst = out + ((long)r * L.units + u) * gemm_unit_bytes(L.dtype);
+  if (L.dtype == T_Q4_K) {
+    for (int c = 0; c < 9; c++)
+      *(uint4 *)(dst + 16 * c) = *(const uint4 *)(body + chunk_offset(L, t, j, c));
+  } else {
+    uint8_t ub[210];
+    for (int c = 0; c < 13; c++) {
+      const uint4 v = *(const uint4 *)(body + chunk_offset(L, t, j, c));
+      __builtin_memcpy(ub + 16 * c, &v, 16);
+    }
+    const uint16_t dv = dd[unit_index(L, t, j)];
+    ub[208] = (uint8_t)dv;
+    ub[209] = (uint8_t)(dv >> 8);
+    for (int s = 0; s < 4; s++) {
+      uint8_t rb[64];
+      q6k_stage_record(ub, s, rb);
+      for (int q = 0; q < 4; q++) {
+        uint4 v;
+        __builtin_memcpy(&v, rb + 16 * q, 16);
+        *(uint4 *)(dst + 64 * s + 16 * q) = v;
+      }
+    }
+  }
+}
 
 // ----------------------------------------------------------- bf16 kernel, ring pipeline
-// Block tile TBM rows x TBN tokens, 4 multiply waves of 80 x 128 (as in
-// k_gemm_bf16: fragment-major LDS operands) and 4 producer waves, with a
-// deeper pipeline than k_gemm_bf16:
-//   * W is fetched per stage, only the bytes the stage needs (the unit's
-//     16-byte header and the group's 32 quant bytes per row), two stages
-//     ahead, into a ring private to each producer wave: producer wave p
-//     fetches and dequantizes rows TBM/4 * p .. + TBM/4 itself, so it waits
-//     only for its own loads and no W bytes cross waves;
-//   * X fragments go through an NXR-slot ring, fetched NXR - 1 stages ahead;
-//   * the multiply waves only multiply.
-// With TBN = 512 (80 x 512 tiles) a block covers all tokens of a 512-token
-// batch, so every weight element is dequantized once per call.
-// Iteration kt: multiply waves run stage kt; producer waves issue the loads
-// of stage kt + NXR - 1 (X) and kt + 2 (W), wait for W of stage kt + 1,
-// dequantize it, and (NXR = 2) wait for X of stage kt + 1.  One barrier per
-// iteration.  Blocks are numbered so that the token tiles of a row tile are
-// 8 apart, i.e. on the same XCD (consecutive blocks go to consecutive
-// XCDs): the row tile's W bytes are fetched into one L2.
-constexpr int WR = 3;  // W ring slots
+// Block tile TBM rows x TBN tokens, 512 threads.  Waves 0-3 multiply: each
+// owns an 80 x 128 tile (5 x 8 MFMA tiles) and reads fragment-major LDS
+// operands (MFMA operand (ks, t), 16 rows or tokens x 32 k, is 64 lane slots
+// of 16 B: conflict-free 128-bit reads).  Waves 4-7 produce:
+//   * each fetches, two stages ahead, the stage records of its own TBM / 4
+//     rows into a ring private to the wave and dequantizes them (Q4_K:
+//     d*sc*q - dmin*m; Q6_K: d*sc*(q - 32); both rounded to bf16, RNE) into
+//     the next A tile, so it waits only for its own loads;
+//   * together they fetch the X fragments (bf16, written by a pre-pass in
+//     fragment order) into an NXR-slot ring, NXR - 1 stages ahead.
+// Loads go straight to LDS (global_load_lds_dwordx4); a producer's LDS
+// reads are inline asm with their own waits (a plain LDS read would make
+// the compiler first drain every outstanding load to LDS, the ones just
+// issued included).  One barrier per stage.
+// Blocks: (row tile, token tile, K split).  A launch covers up to
+// GEMM_MAX_SEG matrices sharing the input (row tiles numbered across them);
+// with ksplit > 1 a block covers stages [S*s/ksplit, S*(s+1)/ksplit) and
+// writes a partial product, which gemm_reduce sums in a fixed order.
 
-template <int TBM, int TBN, int NXR>
+template <int TBM, int TBN, int NXR, int FMT>
 struct Ring {
   static constexpr int AT_ = TBM / 16, BT_ = TBN / 16;
   static constexpr int A_FR_ = 2 * AT_, B_FR_ = 2 * BT_;
+  static constexpr int C = GemmFmt<FMT>::C;    // 16-byte chunks per stage record
   static constexpr int PROWS = TBM / 4;        // rows per producer wave
-  static constexpr int WSLOTS = 3 * PROWS;     // 16-byte W chunks per producer wave per stage
+  static constexpr int WSLOTS = C * PROWS;     // W chunks per producer wave per stage
   static constexpr int WINS = (WSLOTS + 63) / 64;
   static constexpr int XPW = B_FR_ / 4;        // X fragment loads per producer wave per stage
   static constexpr int WGM = TBM / WM;         // multiply waves along the rows
   static_assert(WGM * (TBN / WN) == 4, "4 multiply waves");
   static constexpr int TASKS = 4 * PROWS;      // 16-element dequant tasks per producer wave
   static constexpr int ROUNDS = (TASKS + 63) / 64;
+  static_assert(ROUNDS == 2 || ROUNDS == 3, "2 or 3 dequant rounds");
+  // W ring slots: 2 suffice (stage kt + 2 is fetched into the slot stage kt
+  // was dequantized from, one iteration earlier); a third where LDS allows
+  // keeps a fetch off the slot read in the iteration just before.
+  static constexpr size_t LDS2 = (size_t)2 * A_FR_ * FR16 * 2 + (size_t)NXR * B_FR_ * FR16 * 2 +
+                                 (size_t)4 * 2 * WSLOTS * 16;
+  static constexpr int WR = LDS2 + (size_t)4 * WSLOTS * 16 <= 163840 ? 3 : 2;
 };
 
-template <int TBM, int TBN, int NXR>
-__global__ __launch_bounds__(512) void k_gemm_bf16_ring(Layout L, const uint8_t *raw,
-                                                        long row_bytes, const uint16_t *Xb, int n,
-                                                        int kpad, int mtiles, int ntiles,
-                                                        float *Y) {
-  using R = Ring<TBM, TBN, NXR>;
-  constexpr int AT_ = R::AT_, BT_ = R::BT_, PROWS = R::PROWS, WSLOTS = R::WSLOTS;
-  constexpr int WINS = R::WINS, XPW = R::XPW;
+template <int TBM, int TBN, int NXR, int FMT>
+__global__ __launch_bounds__(512) void k_gemm_bf16_ring(GemmArgs a) {
+  using R = Ring<TBM, TBN, NXR, FMT>;
+  constexpr int AT_ = R::AT_, BT_ = R::BT_, PROWS = R::PROWS, WSLOTS = R::WSLOTS, C = R::C;
+  constexpr int WINS = R::WINS, XPW = R::XPW, WR = R::WR;
   __shared__ __align__(16) uint16_t As[2][R::A_FR_ * FR16];
   __shared__ __align__(16) uint16_t Xs[NXR][R::B_FR_ * FR16];
   __shared__ __align__(16) uint8_t Wg[4][WR][WSLOTS * 16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // block -> (row tile, token tile): blocks b, b + 8, b + 16, ... of a group
-  // of 8 * ntiles share the row tile
-  const int b = blockIdx.x, grp = b / (8 * ntiles), rem = b % (8 * ntiles);
-  const int mt = 8 * grp + (rem & 7), ntile = rem >> 3;
-  if (mt >= mtiles) return;
-  const int m0 = mt * TBM, n0 = ntile * TBN;
-  const int stages = kpad / BK, last = stages - 1;
+  const int b = blockIdx.x, split = b % a.ksplit, rest = b / a.ksplit;
+  const int ntile = rest % a.ntiles, tile = rest / a.ntiles;
+  GemmSeg sg = a.seg[0];
+#pragma unroll
+  for (int i = 1; i < GEMM_MAX_SEG; i++)
+    if (i < a.nseg && tile >= a.seg[i].tile_begin) sg = a.seg[i];
+  const int m0 = (tile - sg.tile_begin) * TBM, n0 = ntile * TBN, rows = sg.rows;
+  const int stages_all = a.kpad / BK;
+  const int s0 = (int)((long)stages_all * split / a.ksplit);
+  const int stages = (int)((long)stages_all * (split + 1) / a.ksplit) - s0, last = stages - 1;
+  const long row_stride = (long)(stages_all / 4) * gemm_unit_bytes(FMT);
   const bool mma = wave < 4;
 
   if (!mma) {
     const int pw = wave - 4;
-    const int ksteps = kpad / 32;
-    const uint16_t *xsrc = Xb + ((long)(n0 / 16) * ksteps * 64 + lane) * 8;
+    const int ksteps = a.kpad / 32;
+    const uint16_t *xsrc = a.xb + ((long)(n0 / 16) * ksteps * 64 + lane) * 8;
     // W chunk slots of this wave: q = 64 i + lane (q < WSLOTS): row
-    // PROWS * pw + q / 3, chunk q % 3 (header, quant bytes 0-15, 16-31 of
-    // the group).
-    const uint8_t *wrow[WINS];
+    // PROWS * pw + q / C, chunk q % C of the stage record.
+    const uint8_t *wsrc[WINS];
     int wc[WINS];
 #pragma unroll
     for (int i = 0; i < WINS; i++) {
       const int q = min(64 * i + lane, WSLOTS - 1);
-      const int row = min(m0 + PROWS * pw + q / 3, L.rows - 1);
-      wrow[i] = raw + (long)row * row_bytes;
-      wc[i] = q % 3;
+      const int row = min(m0 + PROWS * pw + q / C, rows - 1);
+      wsrc[i] = sg.rec + (long)row * row_stride;
+      wc[i] = q % C;
     }
-    auto issue_x = [&](int s) {  // X fragments of stage s (clamped) into slot s % NXR
-      const int sc = min(s, last);
+    auto issue_x = [&](int s) {  // X fragments of local stage s (clamped) into slot s % NXR
+      const int sc = s0 + min(s, last);
 #pragma unroll
       for (int qd = 0; qd < XPW; qd++) {
         const int f = XPW * pw + qd, nt = f % BT_, ks = f / BT_;
         dma16(xsrc + ((long)nt * ksteps + 2 * sc + ks) * 512, &Xs[s % NXR][f * FR16]);
       }
     };
-    auto issue_w = [&](int s) {  // this wave's W rows of stage s (clamped) into slot s % WR
-      const int sc = min(s, last);
-      const int u = sc >> 2, j = sc & 3;
+    auto issue_w = [&](int s) {  // this wave's rows of local stage s (clamped) into slot s % WR
+      const int sg_ = s0 + min(s, last);
 #pragma unroll
-      for (int i = 0; i < WINS; i++) {
-        const int off = wc[i] == 0 ? 0 : 16 + 32 * j + 16 * (wc[i] - 1);
-        if (64 * i + lane < WSLOTS) dma16(wrow[i] + (long)u * UB + off, &Wg[pw][s % WR][1024 * i]);
-      }
+      for (int i = 0; i < WINS; i++)
+        if (64 * i + lane < WSLOTS)
+          dma16(wsrc[i] + gemm_chunk_off<FMT>(sg_, wc[i]), &Wg[pw][s % WR][1024 * i]);
     };
-    // Dequantize stage s of this wave's rows: task t = 4 rr + 2 h + qq (row
-    // rr, nibble half h, 16-element quarter qq), t = lane + 64 round.
+    // Dequantize local stage s of this wave's rows: task t = 4 rr + 2 h + qq
+    // (row rr, half h of the 64 elements, 16-element quarter qq of the half),
+    // t = lane + 64 round.
     auto dequant = [&](int s) {
-      const int j = s & 3;
+      const int j = (s0 + s) & 3;  // group of the unit (Q4_K scale pick)
       const uint8_t *wg = Wg[pw][s % WR];
-      // (asm reads: a plain LDS read would make the compiler wait for every
-      // outstanding load straight to LDS, the ones just issued included)
-      uint4 hd[3], qs[3];
-      uint32_t ad[6];
+      uint4 hd[3], qs[3], qh[3];
+      {
+        uint32_t ad[3 * 3];
 #pragma unroll
-      for (int round = 0; round < 3; round++) {
-        const int t = min(lane + 64 * round, R::TASKS - 1);
-        const int rr = t >> 2, qq = t & 1;
-        ad[2 * round] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 48 * rr);
-        ad[2 * round + 1] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 48 * rr + 16 + 16 * qq);
-      }
-      if constexpr (R::ROUNDS == 3) {
-        uint4 v6[6];
-        lds_read6(ad, v6);
-        hd[0] = v6[0]; qs[0] = v6[1]; hd[1] = v6[2]; qs[1] = v6[3]; hd[2] = v6[4]; qs[2] = v6[5];
-      } else {
-        static_assert(R::ROUNDS == 2, "2 or 3 dequant rounds");
-        const uint32_t ad4[4] = {ad[0], ad[1], ad[2], ad[3]};
-        uint4 v4[4];
-        lds_read4(ad4, v4);
-        hd[0] = v4[0]; qs[0] = v4[1]; hd[1] = v4[2]; qs[1] = v4[3];
+        for (int round = 0; round < 3; round++) {
+          const int t = min(lane + 64 * round, R::TASKS - 1);
+          const int rr = t >> 2, qq = t & 1;
+          ad[3 * round] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr);
+          ad[3 * round + 1] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr + 16 + 16 * qq);
+          ad[3 * round + 2] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr + 48);
+        }
+        if constexpr (FMT == T_Q4_K) {
+          if constexpr (R::ROUNDS == 3) {
+            const uint32_t a6[6] = {ad[0], ad[1], ad[3], ad[4], ad[6], ad[7]};
+            uint4 v[6];
+            lds_read6(a6, v);
+            hd[0] = v[0]; qs[0] = v[1]; hd[1] = v[2]; qs[1] = v[3]; hd[2] = v[4]; qs[2] = v[5];
+          } else {
+            const uint32_t a4[4] = {ad[0], ad[1], ad[3], ad[4]};
+            uint4 v[4];
+            lds_read4(a4, v);
+            hd[0] = v[0]; qs[0] = v[1]; hd[1] = v[2]; qs[1] = v[3];
+          }
+        } else {
+          if constexpr (R::ROUNDS == 3) {
+            const uint32_t a6[6] = {ad[0], ad[1], ad[2], ad[3], ad[4], ad[5]};
+            uint4 v[6];
+            lds_read6(a6, v);
+            hd[0] = v[0]; qs[0] = v[1]; qh[0] = v[2]; hd[1] = v[3]; qs[1] = v[4]; qh[1] = v[5];
+            const uint32_t a2[2] = {ad[6], ad[7]};
+            uint4 w[2];
+            lds_read2_a(a2, w);
+            hd[2] = w[0]; qs[2] = w[1];
+            const uint32_t a1[2] = {ad[8], ad[8]};
+            lds_read2_a(a1, w);
+            qh[2] = w[0];
+          } else {
+            const uint32_t a6[6] = {ad[0], ad[1], ad[2], ad[3], ad[4], ad[5]};
+            uint4 v[6];
+            lds_read6(a6, v);
+            hd[0] = v[0]; qs[0] = v[1]; qh[0] = v[2]; hd[1] = v[3]; qs[1] = v[4]; qh[1] = v[5];
+          }
+        }
       }
 #pragma unroll
       for (int round = 0; round < R::ROUNDS; round++) {
@@ -422,19 +523,36 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_ring(Layout L, const uint8_t 
         if (round < R::ROUNDS - 1 || t < R::TASKS) {
           const int rr = t >> 2, h = (t >> 1) & 1, qq = t & 1;
           const int r = PROWS * pw + rr;
-          const bool ok = m0 + r < L.rows;
-          uint32_t sc, mn;
-          scale_min_k4_sel(2 * j + h, hd[round].y, hd[round].z, hd[round].w, sc, mn);
-          const float ds = ok ? h2f(hd[round].x) * (float)sc : 0.f;
-          const float nm = ok ? -(h2f(hd[round].x >> 16) * (float)mn) : 0.f;
+          const bool ok = m0 + r < rows;
           const uint32_t qw[4] = {qs[round].x, qs[round].y, qs[round].z, qs[round].w};
           const uint32_t sh = 4u * (uint32_t)h;
           uint32_t o[8];
+          if constexpr (FMT == T_Q4_K) {
+            uint32_t sc, mn;
+            scale_min_k4_sel(2 * j + h, hd[round].y, hd[round].z, hd[round].w, sc, mn);
+            const float ds = ok ? h2f(hd[round].x) * (float)sc : 0.f;
+            const float nm = ok ? -(h2f(hd[round].x >> 16) * (float)mn) : 0.f;
 #pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const uint32_t qv = (qw[i] >> sh) & 0x0F0F0F0Fu;
-            o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(qv), nm), fmaf(ds, cvt_ubyte<1>(qv), nm));
-            o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(qv), nm), fmaf(ds, cvt_ubyte<3>(qv), nm));
+            for (int i = 0; i < 4; i++) {
+              const uint32_t qv = (qw[i] >> sh) & 0x0F0F0F0Fu;
+              o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(qv), nm), fmaf(ds, cvt_ubyte<1>(qv), nm));
+              o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(qv), nm), fmaf(ds, cvt_ubyte<3>(qv), nm));
+            }
+          } else {
+            // dequant_q6_k: (d * sc) * (q - 32), one rounding: fma(ds, q, -32 ds)
+            const int g = 2 * h + qq;
+            const int sc8 = (int)(int8_t)(hd[round].x >> (8 * g));
+            const float ds = ok ? h2f(hd[round].y) * (float)sc8 : 0.f;
+            const float nm = -32.0f * ds;
+            const uint32_t hw = g == 0 ? qh[round].x : g == 1 ? qh[round].y : g == 2 ? qh[round].z : qh[round].w;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const uint32_t b2 = (hw >> (8 * i)) & 0xFFu;
+              const uint32_t hi = (b2 | (b2 << 6) | (b2 << 12) | (b2 << 18)) & 0x03030303u;
+              const uint32_t qv = ((qw[i] >> sh) & 0x0F0F0F0Fu) | (hi << 4);
+              o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(qv), nm), fmaf(ds, cvt_ubyte<1>(qv), nm));
+              o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(qv), nm), fmaf(ds, cvt_ubyte<3>(qv), nm));
+            }
           }
           uint16_t *dst = &As[s & 1][((h * AT_ + (r >> 4)) * 64 + (r & 15) + 32 * qq) * 8];
           *(uint4 *)dst = make_uint4(o[0], o[1], o[2], o[3]);
@@ -495,36 +613,58 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_ring(Layout L, const uint8_t 
     const uint16_t *A = As[kt & 1], *B = Xs[kt % NXR];
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      bf16x8_t a[TM];
+      bf16x8_t av[TM];
 #pragma unroll
       for (int i = 0; i < TM; i++)
-        a[i] = *(const bf16x8_t *)(A + ((ks * AT_ + TM * wm + i) * 64 + lane) * 8);
+        av[i] = *(const bf16x8_t *)(A + ((ks * AT_ + TM * wm + i) * 64 + lane) * 8);
 #pragma unroll
       for (int jn = 0; jn < TN; jn++) {
         const bf16x8_t bb = *(const bf16x8_t *)(B + ((ks * BT_ + TN * wn + jn) * 64 + lane) * 8);
 #pragma unroll
         for (int i = 0; i < TM; i++)
-          acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bb, acc[i][jn], 0, 0, 0);
+          acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i], bb, acc[i][jn], 0, 0, 0);
       }
     }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
   }
+  // D layout: lane holds rows 4*(lane/16)+r (weight rows) of column lane%16 (token).
+  float *Y = a.ksplit > 1 ? sg.part + (long)split * a.n * rows : sg.y;
 #pragma unroll
   for (int i = 0; i < TM; i++) {
     const int m = m0 + WM * wm + 16 * i + 4 * (lane >> 4);
 #pragma unroll
     for (int jj = 0; jj < TN; jj++) {
       const int t = n0 + WN * wn + 16 * jj + (lane & 15);
-      if (t >= n) continue;
-      float *yp = Y + (long)t * L.rows + m;
-      if (m + 3 < L.rows && (L.rows & 3) == 0) {
+      if (t >= a.n) continue;
+      float *yp = Y + (long)t * rows + m;
+      if (m + 3 < rows && (rows & 3) == 0) {
         *(float4 *)yp = make_float4(acc[i][jj][0], acc[i][jj][1], acc[i][jj][2], acc[i][jj][3]);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; r++)
-          if (m + r < L.rows) yp[r] = acc[i][jj][r];
+          if (m + r < rows) yp[r] = acc[i][jj][r];
       }
+    }
+  }
+}
+
+// y[t][r] = (add ? y[t][r] : 0) + sum_s part[s][t][r], s in order.
+__global__ void k_gemm_reduce(const float *part, int ksplit, long count, float *y, int add) {
+  const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i >= count) return;
+  if (i + 3 < count) {
+    float4 s = add ? *(const float4 *)(y + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < ksplit; k++) {
+      const float4 p = *(const float4 *)(part + (long)k * count + i);
+      s.x += p.x; s.y += p.y; s.z += p.z; s.w += p.w;
+    }
+    *(float4 *)(y + i) = s;
+  } else {
+    for (long e = i; e < count; e++) {
+      float s = add ? y[e] : 0.f;
+      for (int k = 0; k < ksplit; k++) s += part[(long)k * count + e];
+      y[e] = s;
     }
   }
 }
@@ -657,59 +797,132 @@ __global__ __launch_bounds__(256) void k_gemm_i8(Layout L, const uint8_t *body, 
 }
 
 // ----------------------------------------------------------- host side
-size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode) {
-  if (w->L.dtype != T_Q4_K) return (size_t)-1;
+size_t gemm_records_bytes(const Layout &L) {
+  return (size_t)L.rows * L.units * gemm_unit_bytes(L.dtype);
+}
+
+hipError_t launch_gemm_records(const gq_weight *w, uint8_t *out, hipStream_t st) {
+  const Layout &L = w->L;
+  const long n = (long)L.rows * L.units;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_gemm_records, dim3((unsigned)((n + 127) / 128)), dim3(128), 0, st, L,
+                     w->body, w->d, out);
+  return hipGetLastError();
+}
+
+int gemm_ksplit(int tiles, int stages, int num_cus) {
+  // enough blocks for about one per CU, at least 4 stages per split
+  int ks = tiles >= num_cus ? 1 : (num_cus + tiles / 2) / tiles;
+  ks = std::min(ks, std::max(1, stages / 4));
+  return std::max(ks, 1);
+}
+
+namespace {
+struct GemmPlan {
+  bool wide;
+  int tbm, tbn, ntiles, tiles, ksplit;
+};
+GemmPlan gemm_plan(const gq_weight *const *ws, int count, int n, int num_cus, bool add) {
+  GemmPlan p;
+  p.wide = n > BN;
+  p.tbm = p.wide ? 80 : BM;
+  p.tbn = p.wide ? 512 : BN;
+  p.ntiles = (n + p.tbn - 1) / p.tbn;
+  int mt = 0;
+  for (int i = 0; i < count; i++) mt += (ws[i]->L.rows + p.tbm - 1) / p.tbm;
+  p.tiles = mt * p.ntiles;
+  p.ksplit = gemm_ksplit(p.tiles, ws[0]->L.units * 4, num_cus);
+  // an accumulating launch adds its product in gemm_reduce
+  if (add && p.ksplit == 1) p.ksplit = ws[0]->L.units * 4 >= 2 ? 2 : 1;
+  return p;
+}
+}  // namespace
+
+size_t gemm_part_floats(const gq_weight *const *ws, int count, int n, int num_cus, bool add) {
+  const GemmPlan p = gemm_plan(ws, count, n, num_cus, add);
+  if (p.ksplit == 1) return 0;
+  size_t rows = 0;
+  for (int i = 0; i < count; i++) rows += (size_t)ws[i]->L.rows;
+  return (size_t)p.ksplit * n * rows;
+}
+
+size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode, int num_cus) {
   const size_t kpad = (size_t)w->L.units * 256;
-  if (mode == GQ_GEMM_BF16) return (size_t)((n + 511) / 512 * 512) * kpad * 2 + 256;
+  if (mode == GQ_GEMM_BF16) {
+    if (w->L.dtype != T_Q4_K && w->L.dtype != T_Q6_K) return (size_t)-1;
+    const size_t xb = (size_t)((n + GEMM_NPAD - 1) / GEMM_NPAD * GEMM_NPAD) * kpad * 2;
+    return ((xb + 255) & ~(size_t)255) + gemm_part_floats(&w, 1, n, num_cus, false) * 4 + 256;
+  }
+  if (w->L.dtype != T_Q4_K) return (size_t)-1;
   // int8: q [n][kpad] + scale f32 [n][kpad/32] + qsum int [n][kpad/32]
   return (size_t)n * kpad + (size_t)n * (kpad / 32) * 8 + 512;
 }
 
-// ggml-order copy of a Q4_K tiled body: chunk c of unit u of a row holds
-// the unit's bytes 16c .. 16c+15.
-__global__ void k_unrepack_q4k(Layout L, const uint8_t *body, long row_bytes, uint8_t *raw) {
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (long)L.rows * L.units * 9) return;
-  const int c = (int)(i % 9);
-  const long ru = i / 9;
-  const int r = (int)(ru / L.units), u = (int)(ru % L.units);
-  const int t = r / L.rt, j = (r % L.rt) * L.units + u;
-  *(uint4 *)(raw + (long)r * row_bytes + (long)u * UB + 16 * c) =
-      *(const uint4 *)(body + chunk_offset(L, t, j, c));
+hipError_t launch_x_to_frag(const float *X, int n, int k, uint16_t *xb, hipStream_t st) {
+  const int kpad = (k + 255) / 256 * 256;
+  const int npad = (n + GEMM_NPAD - 1) / GEMM_NPAD * GEMM_NPAD;
+  const long slots = (long)(npad / 16) * (kpad / 32) * 64;
+  hipLaunchKernelGGL(k_x_to_bf16_frag, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st, X,
+                     n, npad, k, kpad, xb);
+  return hipGetLastError();
 }
 
-hipError_t launch_unrepack_q4k(const Layout &L, const uint8_t *body, uint8_t *raw, hipStream_t st) {
-  const long n = (long)L.rows * L.units * 9;
-  if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(k_unrepack_q4k, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, L,
-                     body, (long)L.units * UB, raw);
+hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int count,
+                            const uint16_t *xb, int n, float *part, bool add, int num_cus,
+                            hipStream_t st) {
+  if (count < 1 || count > GEMM_MAX_SEG || n <= 0) return hipErrorInvalidValue;
+  const int fmt = ws[0]->L.dtype;
+  const GemmPlan p = gemm_plan(ws, count, n, num_cus, add);
+  GemmArgs a{};
+  a.nseg = count;
+  a.ntiles = p.ntiles;
+  a.ksplit = p.ksplit;
+  a.n = n;
+  a.kpad = ws[0]->L.units * 256;
+  a.xb = xb;
+  int tb = 0;
+  size_t po = 0;
+  for (int i = 0; i < count; i++) {
+    if (ws[i]->L.dtype != fmt || ws[i]->L.units != ws[0]->L.units || !ws[i]->gemm_raw)
+      return hipErrorInvalidValue;
+    a.seg[i].rec = ws[i]->gemm_raw;
+    a.seg[i].y = ys[i];
+    a.seg[i].rows = ws[i]->L.rows;
+    a.seg[i].tile_begin = tb;
+    a.seg[i].part = p.ksplit > 1 ? part + po : nullptr;
+    tb += (ws[i]->L.rows + p.tbm - 1) / p.tbm;
+    po += (size_t)p.ksplit * n * ws[i]->L.rows;
+  }
+  if (p.ksplit > 1 && !part) return hipErrorInvalidValue;
+  const long nb = (long)tb * p.ntiles * p.ksplit;
+  if (nb > 0x7fffffffL) return hipErrorInvalidValue;
+  void (*kern)(GemmArgs);
+  if (fmt == T_Q4_K) kern = p.wide ? k_gemm_bf16_ring<80, 512, 2, T_Q4_K> : k_gemm_bf16_ring<160, 256, 3, T_Q4_K>;
+  else if (fmt == T_Q6_K) kern = p.wide ? k_gemm_bf16_ring<80, 512, 2, T_Q6_K> : k_gemm_bf16_ring<160, 256, 3, T_Q6_K>;
+  else return hipErrorInvalidValue;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(512), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || p.ksplit == 1) return e;
+  for (int i = 0; i < count; i++) {
+    const long cnt = (long)n * a.seg[i].rows;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((cnt / 4 + 255) / 256 + 1)), dim3(256), 0, st,
+                       a.seg[i].part, p.ksplit, cnt, a.seg[i].y, add ? 1 : 0);
+  }
   return hipGetLastError();
 }
 
 hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int mode,
                        void *workspace, size_t ws_bytes, int num_cus, hipStream_t st) {
   (void)ws_bytes;
-  (void)num_cus;
   const Layout &L = w->L;
   const int kpad = L.units * 256;
   if (mode == GQ_GEMM_BF16) {
-    const dim3 grid((L.rows + BM - 1) / BM, (n + BN - 1) / BN);
     uint16_t *xb = (uint16_t *)workspace;
-    const int npad = (n + 511) / 512 * 512;  // a multiple of every token tile
-    const long slots = (long)(npad / 16) * (kpad / 32) * 64;
-    hipLaunchKernelGGL(k_x_to_bf16_frag, dim3((unsigned)((slots + 255) / 256)), dim3(256), 0, st,
-                       X, n, npad, L.k, kpad, xb);
-    // 80 x 512 tiles when the batch is longer than one 256-token tile (each
-    // weight element dequantized once per 512 tokens), else 160 x 256
-    const bool wide = n > BN;
-    const int tbm = wide ? 80 : BM, tbn = wide ? 512 : BN;
-    const int mtiles = (L.rows + tbm - 1) / tbm, ntiles = (n + tbn - 1) / tbn;
-    // 8 * ntiles consecutive blocks hold 8 row tiles x all token tiles
-    const long nb = (long)((mtiles + 7) / 8) * 8 * ntiles;
-    if (nb > 0x7fffffffL) return hipErrorInvalidValue;
-    auto kern = wide ? k_gemm_bf16_ring<80, 512, 2> : k_gemm_bf16_ring<160, 256, 3>;
-    hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(512), 0, st, L, (const uint8_t *)w->gemm_raw,
-                       (long)L.units * UB, (const uint16_t *)xb, n, kpad, mtiles, ntiles, Y);
+    const size_t xbb = (size_t)((n + GEMM_NPAD - 1) / GEMM_NPAD * GEMM_NPAD) * kpad * 2;
+    float *part = (float *)((char *)workspace + ((xbb + 255) & ~(size_t)255));
+    hipError_t e = launch_x_to_frag(X, n, L.k, xb, st);
+    if (e != hipSuccess) return e;
+    return launch_gemm_bf16(&w, &Y, 1, xb, n, part, false, num_cus, st);
   } else {
     int8_t *xq = (int8_t *)workspace;
     float *xs = (float *)((char *)workspace + (((size_t)n * kpad + 255) & ~(size_t)255));

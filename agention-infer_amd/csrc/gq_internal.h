@@ -13,7 +13,7 @@ struct gq_weight {
   uint16_t *d;       // per-unit f16 scales (Q6_K, IQ3_XXS), or nullptr
   size_t ggml_bytes; // size of the tensor in ggml block order
   int device;
-  uint8_t *gemm_raw = nullptr;  // ggml-order copy for the prefill GEMM (made on first use)
+  uint8_t *gemm_raw = nullptr;  // per-stage records for the bf16 GEMM (made on first use)
 };
 
 namespace gq {
@@ -159,7 +159,42 @@ hipError_t launch_quantize_q8_32(const float *x, long n, uint16_t *scale, int8_t
 // Prefill GEMM.
 hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int mode,
                        void *workspace, size_t ws_bytes, int num_cus, hipStream_t st);
-size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode);
-hipError_t launch_unrepack_q4k(const Layout &L, const uint8_t *body, uint8_t *raw, hipStream_t st);
+size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode, int num_cus);
+// The bf16 GEMM's per-stage weight records (Q4_K, Q6_K): their size, and
+// their construction from the device's tiled body.
+size_t gemm_records_bytes(const Layout &L);
+hipError_t launch_gemm_records(const gq_weight *w, uint8_t *out, hipStream_t st);
+
+// One matrix of a bf16 GEMM launch: Y [n][rows] (token-major), or with a K
+// split the partial products part [ksplit][n][rows].
+constexpr int GEMM_MAX_SEG = 3;
+struct GemmSeg {
+  const uint8_t *rec;  // stage records
+  float *y;
+  float *part;
+  int rows;
+  int tile_begin;      // first row tile of this matrix in the launch
+};
+struct GemmArgs {
+  GemmSeg seg[GEMM_MAX_SEG];
+  int nseg, ntiles, ksplit, n, kpad;
+  const uint16_t *xb;  // X as bf16 MFMA fragments [npad/16][kpad/32][64 lanes][8]
+};
+// Token tiles are 512 wide when n > 256 (else 256): X fragments must cover
+// n rounded up to GEMM_NPAD.
+constexpr int GEMM_NPAD = 512;
+// K split of a launch with this many row x token tiles and stages.
+int gemm_ksplit(int tiles, int stages, int num_cus);
+// Y_i (+)= W_i . X for count <= GEMM_MAX_SEG weights of one dtype (Q4_K or
+// Q6_K) and in_dim, on X already in fragment form (xb, n tokens).  add: Y_i
+// += (else =; an accumulating launch always splits K and adds in the
+// reduction).  part: gemm_part_floats floats.
+hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int count,
+                            const uint16_t *xb, int n, float *part, bool add, int num_cus,
+                            hipStream_t st);
+size_t gemm_part_floats(const gq_weight *const *ws, int count, int n, int num_cus, bool add);
+// X fp32 [n][k] -> bf16 fragments (kpad = k rounded up to 256, npad = n
+// rounded up to GEMM_NPAD, zero padding).
+hipError_t launch_x_to_frag(const float *X, int n, int k, uint16_t *xb, hipStream_t st);
 
 }  // namespace gq

@@ -105,7 +105,9 @@ int gq_dequant_rows_host(const gq_weight *w, int row0, int nrows, float *out_hos
 /* launch_only_batch (src/ops/wgpu_backend/resident.rs:76-104) and the
  * prefill path of WeightMap::matmul_batch_into (src/model/mod.rs:414-464):
  * X_dev [n][in_dim] fp32 token-major -> Y_dev [n][out_dim] fp32.
- * mode GQ_GEMM_BF16 or GQ_GEMM_INT8 (Q4_K weights). */
+ * mode GQ_GEMM_BF16 (Q4_K or Q6_K weights) or GQ_GEMM_INT8 (Q4_K weights).
+ * The first bf16 call on a weight builds its GEMM copy (per-stage records)
+ * and synchronizes the stream once. */
 int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mode, void *stream);
 
 /* Per-32 Q8 activation pack used by GQ_GEMM_INT8, identical to

@@ -35,16 +35,16 @@ def bf16_round(a):
     return r.astype(np.uint32).view(np.float32)
 
 
-def run(backend, orc, rows, k, n, mode, seed):
+def run(backend, orc, rows, k, n, mode, seed, dtype=Q4_K):
     import torch
     import gq
-    w = syn.make_blocks(Q4_K, rows, k, seed=seed)
+    w = syn.make_blocks(dtype, rows, k, seed=seed)
     X = syn.make_x(k, seed=seed + 1, batch=n)
-    h = backend.upload_weight(Q4_K, w, k, rows)
+    h = backend.upload_weight(dtype, w, k, rows)
     Y = h.launch_only_batch(torch.from_numpy(X).cuda(), mode=mode)
     torch.cuda.synchronize()
-    Wf = orc.dequant(Q4_K, w.reshape(-1), rows * k).reshape(rows, k) if k % 256 == 0 else \
-        orc.dequant_rows(Q4_K, w, k)
+    Wf = orc.dequant(dtype, w.reshape(-1), rows * k).reshape(rows, k) if k % 256 == 0 else \
+        orc.dequant_rows(dtype, w, k)
     return w, X, Wf, Y.cpu().numpy()
 
 
@@ -56,6 +56,19 @@ def check(y, ref, what, tol=TOL):
 
 
 SHAPES = [(331, 512, 37), (1024, 3584, 64), (160, 256, 256), (7, 300, 5), (2000, 1024, 300)]
+Q6_K = 14
+# Q6_K (the ffn_down / attn_v type of Q4_K_M files): narrow and wide token
+# tiles, K splits (few row tiles), a partial last unit.
+Q6_SHAPES = [(331, 512, 37), (512, 2048, 300), (100, 768, 20), (3584, 2048, 512), (40, 300, 3)]
+
+
+@pytest.mark.parametrize("rows,k,n", Q6_SHAPES)
+def test_gemm_bf16_q6k(backend, orc, rows, k, n):
+    import gq
+    say(f"gemm bf16 Q6_K rows={rows} k={k} n={n}")
+    w, X, Wf, Y = run(backend, orc, rows, k, n, gq.GQ_GEMM_BF16, seed=rows + 7 * k, dtype=Q6_K)
+    ref = bf16_round(X).astype(np.float64) @ bf16_round(Wf).astype(np.float64).T
+    check(Y, ref, "bf16 Q6_K vs same-operand fp64")
 
 
 @pytest.mark.parametrize("rows,k,n", SHAPES)
@@ -112,10 +125,14 @@ def test_gemm_full_config(backend, orc):
 def test_gemm_errors_and_edges(backend):
     import gq
     import torch
-    w = syn.make_blocks(6 + 8, 4, 256, seed=1)  # Q6_K: no GEMM mode
+    w = syn.make_blocks(6 + 8, 4, 256, seed=1)  # Q6_K: bf16 only
     h = backend.upload_weight(14, w, 256, 4)
     with pytest.raises(gq.GqError, match="not supported"):
-        h.launch_only_batch(torch.zeros((2, 256), device="cuda"))
+        h.launch_only_batch(torch.zeros((2, 256), device="cuda"), mode=gq.GQ_GEMM_INT8)
+    w8 = syn.make_blocks(8, 4, 256, seed=1)  # Q8_0: no GEMM mode
+    h8 = backend.upload_weight(8, w8, 256, 4)
+    with pytest.raises(gq.GqError, match="not supported"):
+        h8.launch_only_batch(torch.zeros((2, 256), device="cuda"))
     w4 = syn.make_blocks(Q4_K, 4, 256, seed=1)
     h4 = backend.upload_weight(Q4_K, w4, 256, 4)
     with pytest.raises(gq.GqError, match="mode"):
