@@ -545,6 +545,7 @@ struct gq_model {
   std::vector<void *> owned;  // device allocations
   hipGraphExec_t graph = nullptr;
   hipStream_t graph_stream = nullptr;
+  gq::PrefillBufs pf{};  // allocated by the first prefill
   ~gq_model() {
     if (graph) (void)hipGraphExecDestroy(graph);
     for (void *p : owned) (void)hipFree(p);
@@ -747,6 +748,69 @@ int gq_model_generate(gq_model *m, int token, int pos, int n_steps, int *tokens_
   if (tokens_host && n_steps > 0) {
     HIP_TRY(hipMemcpyAsync(tokens_host, m->L.tokens, (size_t)n_steps * 4, hipMemcpyDeviceToHost, s));
     HIP_TRY(hipStreamSynchronize(s));
+  }
+  return GQ_OK;
+}
+
+// LlamaModel::run_batch (src/model/llama/cpu_path.rs:834-991): tokens at
+// positions pos .. pos + n - 1 through every layer in passes of up to
+// PREFILL_MAX tokens, K/V of every position written to the cache, logits of
+// the last position.
+int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float *logits_host,
+                     int *next_token, void *stream) {
+  if (!m) return fail(GQ_EINVAL, "null model");
+  if (!tokens_host || n < 1) return fail(GQ_EINVAL, "prefill needs at least one token");
+  if (pos < 0 || (long)pos + n > m->L.ctx)
+    return fail(GQ_EINVAL, "%d tokens from position %d exceed the context (%d)", n, pos, m->L.ctx);
+  for (int i = 0; i < n; i++)
+    if (tokens_host[i] < 0 || tokens_host[i] >= m->L.vocab)
+      return fail(GQ_EINVAL, "token %d out of range", tokens_host[i]);
+  hipStream_t s = (hipStream_t)stream;
+  auto &L = m->L;
+  for (int l = 0; l < L.n_layers; l++) {
+    const gq_weight *ws[7] = {L.wq[l], L.wk[l], L.wv[l], L.wo[l], L.wgate[l], L.wup[l], L.wdown[l]};
+    for (const gq_weight *w : ws) {
+      if (w->L.dtype != gq::T_Q4_K && w->L.dtype != gq::T_Q6_K)
+        return fail(GQ_EDTYPE, "layer %d: prefill needs Q4_K or Q6_K projection weights, not %s", l,
+                    type_name(w->L.dtype));
+      int rc = gq_ensure_gemm_records(w, s);
+      if (rc) return rc;
+    }
+  }
+  if (!m->pf.x) {
+    const int H = L.hidden, qd = L.n_heads * L.head_dim, kvd = L.n_kv_heads * L.head_dim;
+    const size_t np = gq::PREFILL_MAX;
+    const size_t kmax = (size_t)((std::max(std::max(H, L.ffn), qd) + 255) / 256 * 256);
+    int rc = dalloc(m, &m->pf.x, np * H);
+    if (!rc) rc = dalloc(m, &m->pf.q, np * qd);
+    if (!rc) rc = dalloc(m, &m->pf.k, np * kvd);
+    if (!rc) rc = dalloc(m, &m->pf.v, np * kvd);
+    if (!rc) rc = dalloc(m, &m->pf.att, np * qd);
+    if (!rc) rc = dalloc(m, &m->pf.g, np * L.ffn);
+    if (!rc) rc = dalloc(m, &m->pf.u, np * L.ffn);
+    if (!rc) rc = dalloc(m, &m->pf.part, std::max<size_t>(1, gq::prefill_part_floats(L, gq::PREFILL_MAX, g_dev.num_cus)));
+    if (!rc) rc = dalloc(m, &m->pf.xb, (size_t)gq::GEMM_NPAD * kmax);
+    if (!rc) rc = dalloc(m, &m->pf.tokens, np);
+    if (rc) { m->pf.x = nullptr; return rc; }
+  }
+  for (int off = 0; off < n; off += gq::PREFILL_MAX) {
+    const int c = std::min(n - off, gq::PREFILL_MAX);
+    HIP_TRY(hipMemcpyAsync(m->pf.tokens, tokens_host + off, (size_t)c * 4, hipMemcpyHostToDevice, s));
+    hipError_t e = gq::launch_prefill(L, m->pf, m->pf.tokens, c, pos + off, g_dev.num_cus, s);
+    if (e != hipSuccess) return fail(GQ_EHIP, "prefill launch failed: %s", hipGetErrorString(e));
+    // the token upload of the next pass reuses the buffer
+    HIP_TRY(hipStreamSynchronize(s));
+  }
+  if (logits_host || next_token) {
+    std::vector<float> lg((size_t)L.vocab);
+    HIP_TRY(hipMemcpy(lg.data(), L.logits, lg.size() * 4, hipMemcpyDeviceToHost));
+    if (logits_host) memcpy(logits_host, lg.data(), lg.size() * 4);
+    if (next_token) {  // first maximum (sampler.rs:120-131)
+      int best = 0;
+      for (int i = 1; i < L.vocab; i++)
+        if (lg[i] > lg[best]) best = i;
+      *next_token = best;
+    }
   }
   return GQ_OK;
 }

@@ -130,6 +130,20 @@ struct DecodeLaunch {
 };
 
 hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s);
+
+// Batched prefill (gq_prefill.hip): buffers for passes of up to
+// PREFILL_MAX tokens.
+constexpr int PREFILL_MAX = 512;
+struct PrefillBufs {
+  float *x;        // [n][hidden] residual stream
+  float *q, *k, *v, *att, *g, *u;
+  float *part;     // GEMM K-split partials (prefill_part_floats)
+  uint16_t *xb;    // GEMM X fragments [512][max(hidden, ffn, q_dim) rounded to 256] bf16
+  int *tokens;     // [PREFILL_MAX]
+};
+size_t prefill_part_floats(const DecodeLaunch &m, int nmax, int num_cus);
+hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int *tokens_dev, int n,
+                          int pos0, int num_cus, hipStream_t s);
 constexpr int ATT_CHUNK = 64;    // positions per attention block
 constexpr int ATT_MAX_CTX = 65536;
 constexpr int ARGMAX_SPAN = 4096;  // logits per argmax block

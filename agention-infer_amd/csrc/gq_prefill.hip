@@ -1,0 +1,408 @@
+// gq_prefill.hip -- batched prefill of a dense Llama/Qwen2-style decoder:
+// n prompt tokens at positions pos0 .. pos0 + n - 1 through every layer in
+// one pass, K/V written to the cache for every position, logits of the last
+// position (LlamaModel::run_batch, src/model/llama/cpu_path.rs:834-991).
+//
+// Per layer (as run_batch, with the projections on the bf16 GEMM):
+//   xn = RMSNorm(x) * attn_norm      -> bf16 MFMA fragments (k_norm_to_frag)
+//   q, k, v = xn . Wq/Wk/Wv          (one GEMM launch, K split)
+//   RoPE of q and k, f16 K/V rows into the cache (k_rope_kv)
+//   att = causal attention of every query over the cache (k_attn_prefill)
+//   x += att . Wo                    (GEMM, K split, accumulating reduction)
+//   xn = RMSNorm(x) * ffn_norm; g, u = xn . Wgate/Wup
+//   x += (silu(g) * u) . Wdown       (k_swiglu_to_frag, GEMM)
+// then the output head on RMSNorm(x[n - 1]) (the decode matvec).
+// The GEMM operands are bf16 (weights: bf16 of the exact dequant;
+// activations: bf16 of the fp32 values), accumulation fp32; everything
+// else is fp32 as on the CPU path.
+#include <algorithm>
+
+#include "gq_device.h"
+#include "gq_internal.h"
+
+namespace gq {
+
+typedef _Float16 pf16x8_t __attribute__((ext_vector_type(8)));
+typedef float pf32x4_t __attribute__((ext_vector_type(4)));
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint32_t bf16_bits(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
+  return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Position of elements (t, c .. c + 7) (c % 8 == 0) in the GEMM's X
+// fragments: fragment (t / 16, c / 32) of 64 lanes x 8 bf16, lane
+// t % 16 + 16 * ((c % 32) / 8).
+__device__ __forceinline__ long frag_slot(int t, int c, int ksteps) {
+  return (((long)(t >> 4) * ksteps + (c >> 5)) * 64 + (t & 15) + 16 * ((c & 31) >> 3)) * 8;
+}
+
+__device__ __forceinline__ void put_frag8(uint16_t *xb, long slot, const float (&v)[8]) {
+  const uint4 o = make_uint4(bf16_bits(v[0]) | (bf16_bits(v[1]) << 16),
+                             bf16_bits(v[2]) | (bf16_bits(v[3]) << 16),
+                             bf16_bits(v[4]) | (bf16_bits(v[5]) << 16),
+                             bf16_bits(v[6]) | (bf16_bits(v[7]) << 16));
+  *(uint4 *)(xb + slot) = o;
+}
+
+__device__ __forceinline__ float block_sum256(float v, float *red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  const float s = (red[0] + red[1]) + (red[2] + red[3]);
+  __syncthreads();
+  return s;
+}
+
+// x[t] = embd[tokens[t]] (the embedding rows, fp32 on the device).
+__global__ void k_embed_rows(const float *embd, const int *tokens, int H, float *x) {
+  const int t = blockIdx.x;
+  const float *src = embd + (long)tokens[t] * H;
+  for (int i = threadIdx.x; i < H; i += blockDim.x) x[(long)t * H + i] = src[i];
+}
+
+// Fragments of RMSNorm(x[t]) * w (rms_norm_into, cpu_path.rs:67-74:
+// w * x / sqrt(sum(x^2) / H + eps)) for tokens t < n, zeros for n <= t <
+// npad and for columns past H.  One block (256 threads) per token.
+__global__ __launch_bounds__(256) void k_norm_to_frag(const float *x, const float *w, int n, int H,
+                                                      int kpad, float eps, uint16_t *xb) {
+  __shared__ float red[4];
+  const int t = blockIdx.x, ksteps = kpad / 32;
+  const float *xt = x + (long)t * H;
+  float ss = 0.f;
+  if (t < n)
+    for (int i = threadIdx.x; i < H; i += 256) ss += xt[i] * xt[i];
+  ss = block_sum256(ss, red);
+  const float rms = sqrtf(ss / (float)H + eps);
+  for (int c = 8 * threadIdx.x; c < kpad; c += 8 * 256) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = t < n && c + e < H ? w[c + e] * xt[c + e] / rms : 0.f;
+    put_frag8(xb, frag_slot(t, c, ksteps), v);
+  }
+}
+
+// Fragments of silu(g) * u (ffn_gate_up, cpu_path.rs:225-227), g and u
+// [n][F]; zeros past n and F.
+__global__ __launch_bounds__(256) void k_swiglu_to_frag(const float *g, const float *u, int n, int F,
+                                                        int kpad, uint16_t *xb) {
+  const int t = blockIdx.x, ksteps = kpad / 32;
+  for (int c = 8 * threadIdx.x; c < kpad; c += 8 * 256) {
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      if (t < n && c + e < F) {
+        const float gv = g[(long)t * F + c + e];
+        v[e] = gv / (1.0f + expf(-gv)) * u[(long)t * F + c + e];
+      } else {
+        v[e] = 0.f;
+      }
+    }
+    put_frag8(xb, frag_slot(t, c, ksteps), v);
+  }
+}
+
+// NEOX RoPE (cpu_path.rs:99-133, angle pos / theta^(2i/hd)) of q [n][nh*hd]
+// and k [n][nkv*hd] in place for positions pos0 + t, and the f16 K/V rows
+// (KvDtype::F16::pack, round to nearest even) into the cache.  One block
+// per token.
+__global__ __launch_bounds__(256) void k_rope_kv(float *q, float *k, const float *v, uint16_t *kc,
+                                                 uint16_t *vc, int pos0, int nh, int nkv, int hd,
+                                                 const float *rope_den) {
+  __shared__ float sn[64], cs[64];
+  const int t = blockIdx.x, pos = pos0 + t, half = hd / 2, kvd = nkv * hd;
+  for (int i = threadIdx.x; i < half; i += 256) {
+    float s, c;
+    sincosf((float)pos / rope_den[i], &s, &c);
+    sn[i] = s;
+    cs[i] = c;
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < (nh + nkv) * half; o += 256) {
+    const int hh = o / half, i = o % half;
+    float *p = hh < nh ? q + (long)t * nh * hd + (long)hh * hd : k + (long)t * kvd + (long)(hh - nh) * hd;
+    const float x0 = p[i], x1 = p[i + half];
+    p[i] = x0 * cs[i] - x1 * sn[i];
+    p[i + half] = x0 * sn[i] + x1 * cs[i];
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < kvd; o += 256) {
+    kc[(long)pos * kvd + o] = __half_as_ushort(__float2half_rn(k[(long)t * kvd + o]));
+    vc[(long)pos * kvd + o] = __half_as_ushort(__float2half_rn(v[(long)t * kvd + o]));
+  }
+}
+
+// Causal attention of queries t = 0 .. n-1 (position pos0 + t, head h)
+// over cache rows 0 .. pos0 + t (attention_into, cpu_path.rs:141-194:
+// scores q.k / sqrt(hd), softmax, weighted sum of V), flash-style: block
+// (64-query tile, head h), 4 waves of 16 queries; 64-key chunks of K and
+// V^T staged in LDS (the next chunk's rows prefetched into registers).
+// Scores and the V sum run on v_mfma_f32_16x16x32_f16: K and V are f16
+// already; q (scaled by a power of two) and the probabilities are split
+// into f16 hi + lo parts, so the products are exact in fp32.  Softmax is
+// online (running max m, running sum l; O rescaled when m grows).
+constexpr int PF_Q = 64;  // queries per block
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint16_t *kc,
+                                                      const uint16_t *vc, int pos0, int n, int nh,
+                                                      int group, float *att) {
+  constexpr int KS = HD / 32, DT = HD / 16;
+  constexpr int KP = HD + 8;   // K row stride (halves): rows 16 B apart in bank order
+  constexpr int VP = 64 + 8;   // V^T and P row stride (halves)
+  constexpr int LD = HD / 8;   // 16-byte loads per key row
+  constexpr int NLD = 64 * LD / 256;  // per thread per chunk (K and V each)
+  __shared__ __align__(16) uint16_t Ks[64 * KP];
+  __shared__ __align__(16) uint16_t Vt[HD * VP];
+  __shared__ __align__(16) uint16_t Ph[4][16 * VP];
+  __shared__ __align__(16) uint16_t Pl[4][16 * VP];
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.y, qt0 = blockIdx.x * PF_Q;
+  const int kvd = nh / group * HD, kh = h / group;
+  const uint16_t *kbase = kc + (long)kh * HD, *vbase = vc + (long)kh * HD;
+
+  // q A-fragments: lane row = query qt0 + 16 wave + lane % 16, dims
+  // 8 (lane / 16) + 32 ks .. + 8.
+  const int tq = qt0 + 16 * wave + (lane & 15);
+  float qv[KS][8];
+  float qm = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < KS; ks++) {
+    const float *src = q + (long)tq * nh * HD + (long)h * HD + 8 * (lane >> 4) + 32 * ks;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      qv[ks][e] = tq < n ? src[e] : 0.f;
+      qm = fmaxf(qm, fabsf(qv[ks][e]));
+    }
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) qm = fmaxf(qm, __shfl_xor(qm, off, 64));
+  if (lane == 0) red[wave] = qm;
+  __syncthreads();
+  qm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int ex = 0;
+  (void)frexpf(qm, &ex);
+  const float qscale = qm > 0.f ? ldexpf(1.0f, 10 - ex) : 1.0f;
+  const float inv_scale = 1.0f / qscale;  // a power of two: exact
+  const float rsq = sqrtf((float)HD);
+  pf16x8_t qhi[KS], qlo[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ks++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float x = qv[ks][e] * qscale;
+      const _Float16 hi = (_Float16)x;
+      qhi[ks][e] = hi;
+      qlo[ks][e] = (_Float16)(x - (float)hi);
+    }
+
+  const int tlast = min(qt0 + PF_Q, n) - 1;
+  const int kend = pos0 + tlast + 1;  // keys [0, kend)
+  const int nch = (kend + 63) / 64;
+  // rows of the D layout: query qt0 + 16 wave + 4 (lane / 16) + i
+  int qrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) qrow[i] = qt0 + 16 * wave + 4 * (lane >> 4) + i;
+  float mrow[4], lrow[4];
+  pf32x4_t O[DT];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    mrow[i] = -INFINITY;
+    lrow[i] = 0.f;
+  }
+#pragma unroll
+  for (int d = 0; d < DT; d++) O[d] = pf32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  uint4 kr[NLD], vr[NLD];
+  auto fetch = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      const int idx = tid + 256 * j, key = idx / LD, col = idx % LD;
+      const long p = min(64 * c + key, kend - 1);
+      kr[j] = *(const uint4 *)(kbase + p * kvd + 8 * col);
+      vr[j] = *(const uint4 *)(vbase + p * kvd + 8 * col);
+    }
+  };
+  fetch(0);
+  for (int c = 0; c < nch; c++) {
+    __syncthreads();  // the previous chunk's readers are done
+#pragma unroll
+    for (int j = 0; j < NLD; j++) {
+      const int idx = tid + 256 * j, key = idx / LD, col = idx % LD;
+      *(uint4 *)&Ks[key * KP + 8 * col] = kr[j];
+      const uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        Vt[(8 * col + e) * VP + key] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
+    }
+    __syncthreads();
+    if (c + 1 < nch) fetch(c + 1);
+
+    // scores of this wave's 16 queries x 64 keys (4 column tiles)
+    pf32x4_t s[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++) {
+      pf32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) {
+        const uint4 raw = *(const uint4 *)&Ks[(16 * ct + (lane & 15)) * KP + 8 * (lane >> 4) + 32 * ks];
+        pf16x8_t b;
+        __builtin_memcpy(&b, &raw, 16);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi[ks], b, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo[ks], b, acc, 0, 0, 0);
+      }
+      const int key = 64 * c + 16 * ct + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float sc = acc[i] * inv_scale / rsq;
+        // rows past n stay finite (discarded); past the causal limit: -inf
+        s[ct][i] = qrow[i] >= n ? 0.f : key > pos0 + qrow[i] ? -INFINITY : sc;
+      }
+    }
+    // online softmax per row (a row's 64 values: 4 tiles x 16 lanes)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float mx = fmaxf(fmaxf(s[0][i], s[1][i]), fmaxf(s[2][i], s[3][i]));
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+      const float mnew = fmaxf(mrow[i], mx);
+      const float alpha = expf(mrow[i] - mnew);  // row 0 holds key 0: mnew is finite
+      float ps = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < 4; ct++) {
+        const float p = expf(s[ct][i] - mnew);
+        s[ct][i] = p;
+        ps += p;
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off, 64);
+      lrow[i] = lrow[i] * alpha + ps;
+      mrow[i] = mnew;
+#pragma unroll
+      for (int d = 0; d < DT; d++) O[d][i] *= alpha;
+    }
+    // P (hi + lo f16) to LDS in [query][key] order for the A operands
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int r = 4 * (lane >> 4) + i, kk = 16 * ct + (lane & 15);
+        const _Float16 hi = (_Float16)s[ct][i];
+        const _Float16 lo = (_Float16)(s[ct][i] - (float)hi);
+        Ph[wave][r * VP + kk] = __builtin_bit_cast(uint16_t, hi);
+        Pl[wave][r * VP + kk] = __builtin_bit_cast(uint16_t, lo);
+      }
+    __syncthreads();
+    // O += P . V over the chunk's 64 keys (2 depth steps)
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      const uint4 rh = *(const uint4 *)&Ph[wave][(lane & 15) * VP + 8 * (lane >> 4) + 32 * ks];
+      const uint4 rl = *(const uint4 *)&Pl[wave][(lane & 15) * VP + 8 * (lane >> 4) + 32 * ks];
+      pf16x8_t ah, al;
+      __builtin_memcpy(&ah, &rh, 16);
+      __builtin_memcpy(&al, &rl, 16);
+#pragma unroll
+      for (int d = 0; d < DT; d++) {
+        const uint4 raw = *(const uint4 *)&Vt[(16 * d + (lane & 15)) * VP + 8 * (lane >> 4) + 32 * ks];
+        pf16x8_t b;
+        __builtin_memcpy(&b, &raw, 16);
+        O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, O[d], 0, 0, 0);
+        O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, O[d], 0, 0, 0);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if (qrow[i] >= n) continue;
+    float *dst = att + (long)qrow[i] * nh * HD + (long)h * HD + (lane & 15);
+#pragma unroll
+    for (int d = 0; d < DT; d++) dst[16 * d] = O[d][i] / lrow[i];
+  }
+}
+
+// ------------------------------------------------------------------ host
+static int round_up(int v, int m) { return (v + m - 1) / m * m; }
+
+// The largest K-split partial buffer of any launch of a pass of up to nmax
+// tokens.  Passes of up to 256 tokens use taller row tiles (fewer tiles, a
+// larger split), so both tile regimes are sized at their largest batch.
+size_t prefill_part_floats(const DecodeLaunch &m, int nmax, int num_cus) {
+  size_t best = 0;
+  for (int nn : {std::min(nmax, 256), nmax})
+  for (int L = 0; L < m.n_layers; L++) {
+    const int nmax = nn;
+    const gq_weight *qkv[3] = {m.wq[L], m.wk[L], m.wv[L]};
+    for (int i = 0; i < 3; i++) best = std::max(best, gemm_part_floats(&qkv[i], 1, nmax, num_cus, false));
+    if (qkv[0]->L.dtype == qkv[1]->L.dtype && qkv[1]->L.dtype == qkv[2]->L.dtype)
+      best = std::max(best, gemm_part_floats(qkv, 3, nmax, num_cus, false));
+    best = std::max(best, gemm_part_floats(&m.wo[L], 1, nmax, num_cus, true));
+    const gq_weight *gu[2] = {m.wgate[L], m.wup[L]};
+    best = std::max(best, gemm_part_floats(gu, 2, nmax, num_cus, false));
+    best = std::max(best, gemm_part_floats(&m.wdown[L], 1, nmax, num_cus, true));
+  }
+  return best;
+}
+
+// One pass of n <= PREFILL_MAX tokens (tokens_dev) at positions pos0 ..
+// pos0 + n - 1; logits of the last position into m.logits.
+hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int *tokens_dev, int n,
+                          int pos0, int num_cus, hipStream_t s) {
+  if (n < 1 || n > PREFILL_MAX) return hipErrorInvalidValue;
+  const int H = m.hidden, hd = m.head_dim, nh = m.n_heads, nkv = m.n_kv_heads;
+  const int kvd = nkv * hd, qd = nh * hd, F = m.ffn, group = nh / nkv;
+  const int npad = round_up(n, GEMM_NPAD);
+  hipError_t e;
+  hipLaunchKernelGGL(k_embed_rows, dim3(n), dim3(256), 0, s, m.embd, tokens_dev, H, b.x);
+  for (int L = 0; L < m.n_layers; L++) {
+    hipLaunchKernelGGL(k_norm_to_frag, dim3(npad), dim3(256), 0, s, b.x, m.attn_norm[L], n, H,
+                       round_up(H, 256), m.eps, b.xb);
+    // q, k, v: one launch per distinct dtype (attn_v is Q6_K in some files)
+    const gq_weight *qkv[3] = {m.wq[L], m.wk[L], m.wv[L]};
+    float *outs[3] = {b.q, b.k, b.v};
+    bool done[3] = {false, false, false};
+    for (int i = 0; i < 3; i++) {
+      if (done[i]) continue;
+      const gq_weight *grp[3];
+      float *gout[3];
+      int c = 0;
+      for (int j = i; j < 3; j++)
+        if (!done[j] && qkv[j]->L.dtype == qkv[i]->L.dtype) {
+          grp[c] = qkv[j];
+          gout[c++] = outs[j];
+          done[j] = true;
+        }
+      if ((e = launch_gemm_bf16(grp, gout, c, b.xb, n, b.part, false, num_cus, s)) != hipSuccess) return e;
+    }
+    uint16_t *kc = m.kcache + (long)L * m.ctx * kvd, *vc = m.vcache + (long)L * m.ctx * kvd;
+    hipLaunchKernelGGL(k_rope_kv, dim3(n), dim3(256), 0, s, b.q, b.k, b.v, kc, vc, pos0, nh, nkv, hd,
+                       m.rope_den);
+    const dim3 ag((n + PF_Q - 1) / PF_Q, nh);
+    if (hd == 128)
+      hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
+    else
+      hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(256), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
+    if ((e = launch_x_to_frag(b.att, n, qd, b.xb, s)) != hipSuccess) return e;
+    float *xo[1] = {b.x};
+    if ((e = launch_gemm_bf16(&m.wo[L], xo, 1, b.xb, n, b.part, true, num_cus, s)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_norm_to_frag, dim3(npad), dim3(256), 0, s, b.x, m.ffn_norm[L], n, H,
+                       round_up(H, 256), m.eps, b.xb);
+    const gq_weight *gu[2] = {m.wgate[L], m.wup[L]};
+    float *guo[2] = {b.g, b.u};
+    if ((e = launch_gemm_bf16(gu, guo, 2, b.xb, n, b.part, false, num_cus, s)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_swiglu_to_frag, dim3(npad), dim3(256), 0, s, b.g, b.u, n, F, round_up(F, 256), b.xb);
+    if ((e = launch_gemm_bf16(&m.wdown[L], xo, 1, b.xb, n, b.part, true, num_cus, s)) != hipSuccess) return e;
+  }
+  // logits of RMSNorm(x[n - 1]) (the decode head matvec)
+  MvIn hin;
+  hin.src = MV_NORM;
+  hin.x = b.x + (long)(n - 1) * H;
+  hin.nw = m.output_norm;
+  hin.eps = m.eps;
+  float *lo[1] = {m.logits};
+  return matvec_launch(&m.lm_head, 1, hin, lo, s);
+}
+
+}  // namespace gq

@@ -60,6 +60,7 @@ SIGNATURES = {
     "gq_model_kv_download": (_I, [_P, _I, _P, _P, _I]),
     "gq_model_decode": (_I, [_P, _I, _I, _P, ctypes.POINTER(_I)]),
     "gq_model_generate": (_I, [_P, _I, _I, _I, _P, _P]),
+    "gq_model_prefill": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(_I), _P]),
     "gq_moe_ffn": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _P]),
 }
 
@@ -401,6 +402,17 @@ class DecodeModel:
         logits = np.zeros(self.cfg["vocab"], np.float32) if want_logits else None
         nxt = ctypes.c_int()
         _check(lib().gq_model_decode(self._h, token, pos, _ptr(logits), ctypes.byref(nxt)))
+        return nxt.value, logits
+
+    def prefill(self, tokens, pos, want_logits=True, stream=None):
+        """LlamaModel::run_batch: the prompt tokens at positions pos .. through
+        every layer at once; returns (greedy next token, last-position logits
+        or None)."""
+        toks = np.ascontiguousarray(tokens, np.int32)
+        logits = np.zeros(self.cfg["vocab"], np.float32) if want_logits else None
+        nxt = ctypes.c_int()
+        _check(lib().gq_model_prefill(self._h, _ptr(toks), toks.size, pos, _ptr(logits),
+                                      ctypes.byref(nxt), _stream(stream)))
         return nxt.value, logits
 
     def generate(self, token, pos, n_steps, stream=None):

@@ -20,6 +20,8 @@ import os
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "agention-infer_amd"))
 
@@ -160,6 +162,41 @@ def moe_leg(be, gq, syn, torch, cpu):
     return out
 
 
+PREFILL_TOKENS = 512
+
+
+def prefill_flops(cfg, n, pos0):
+    """GEMM flops of one prefill pass plus the attention's (QK and PV)."""
+    H, F, L = cfg["hidden"], cfg["ffn"], cfg["n_layers"]
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    gemm = 2.0 * n * L * (H * (qd + 2 * kvd) + qd * H + 3 * H * F)
+    keys = n * pos0 + n * (n + 1) / 2  # causal (query, key) pairs
+    att = 4.0 * L * cfg["n_heads"] * cfg["head_dim"] * keys
+    return gemm, att
+
+
+def prefill_leg(m, cfg, torch):
+    """Batched prefill (run_batch) of PREFILL_TOKENS synthetic tokens through
+    the 7B-shaped model: from position 0, and after 3584 cached positions.
+    The first call builds the GEMM weight copies; 3 timed calls each."""
+    toks = np.random.default_rng(99).integers(0, cfg["vocab"], PREFILL_TOKENS).astype(np.int32)
+    m.prefill(toks, 0, want_logits=False)  # GEMM copies + warm
+    out = {"tokens": PREFILL_TOKENS}
+    for pos0 in (0, 3584):
+        ts = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            m.prefill(toks, pos0, want_logits=False)
+            ts.append(time.perf_counter() - t0)
+        ms = 1e3 * sorted(ts)[1]
+        gemm, att = prefill_flops(cfg, PREFILL_TOKENS, pos0)
+        out[f"pos{pos0}"] = {"ms": round(ms, 2), "tok_s": round(PREFILL_TOKENS / (ms * 1e-3), 1),
+                             "gemm_tflop": round(gemm / 1e12, 3), "attn_tflop": round(att / 1e12, 3),
+                             "TFLOP/s": round((gemm + att) / (ms * 1e-3) / 1e12, 1)}
+    return out
+
+
 def decode_leg(be, gq, syn, torch, cpu_steps):
     """GPU-resident 7B-shape Q4_K_M decode (28 layers,
     f16 KV prefilled to 4096 positions, 128 greedy steps, one HIP graph
@@ -194,6 +231,7 @@ def decode_leg(be, gq, syn, torch, cpu_steps):
            "first_tokens": [int(t) for t in tokens[:4]],
            "model": "Qwen2.5-7B-shaped Q4_K_M (random init), 28 layers, hidden 3584, "
                     "28/4 heads, ffn 18944, vocab 152064"}
+    out["prefill"] = prefill_leg(m, cfg, torch)
     if cpu_steps > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle

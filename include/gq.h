@@ -175,6 +175,17 @@ int gq_model_kv_download(gq_model *m, int layer, uint16_t *k_host, uint16_t *v_h
  * position pos; logits_host[vocab] (may be NULL) and the greedy next token. */
 int gq_model_decode(gq_model *m, int token, int pos, float *logits_host, int *next_token);
 
+/* Batched prefill (LlamaModel::run_batch, src/model/llama/cpu_path.rs:834-991):
+ * tokens_host[n] at positions pos .. pos + n - 1 through every layer, in
+ * passes of up to 512 tokens; K/V of every position into the cache;
+ * logits_host[vocab] (may be NULL) and the greedy next token (may be NULL)
+ * of the last position.  Projection GEMMs run in bf16 (weights: bf16 of the
+ * exact dequant; activations: bf16), everything else in fp32.  Needs Q4_K or
+ * Q6_K projection weights; the first call builds their GEMM copies.
+ * Synchronous on `stream`. */
+int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float *logits_host,
+                     int *next_token, void *stream);
+
 /* n_steps greedy steps from (token, pos) (runner::greedy_run decode loop,
  * src/runner.rs:67-135): each step is one replay of a captured HIP graph;
  * the argmax feeds the next step on the device.  tokens_host[n_steps]

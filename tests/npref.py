@@ -207,3 +207,71 @@ def decode_step(cfg, w, kc, vc, token, pos):
         x = x + mat(cfg["down_type"], w["wdown"][L], H, F) @ act
     xn = norm(x, w["output_norm"].astype(np.float64))
     return mat(cfg["head_type"], w["lm_head"], cfg["vocab"], H) @ xn
+
+
+def bf16(a):
+    """Round float32 values to bfloat16 (nearest even), returned as float64."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+def prefill_bf16(cfg, w, kc, vc, tokens, pos0):
+    """Batched prefill (run_batch: every layer over all prompt tokens at
+    once) in float64 with the GPU prefill's operand rounding at each
+    projection: weights rounded to bf16 from their fp32 dequant, the
+    activations entering a projection (normed x, attention output,
+    silu(g) * u) rounded to fp32 and then to bf16.  RoPE, the f16 K/V cache,
+    the causal softmax and the residual adds stay float64; the output head
+    is unrounded (the GPU runs it on the matvec).  kc / vc are updated.
+    Returns the logits of the last token."""
+    H, hd = cfg["hidden"], cfg["head_dim"]
+    nh, nkv, F = cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"]
+    half, group = hd // 2, nh // nkv
+    n = len(tokens)
+
+    def matb(dtype, blob, rows, cols):
+        return bf16(np.stack([dequant(dtype, blob[r], cols) for r in range(rows)]))
+
+    def mat(dtype, blob, rows, cols):
+        return np.stack([dequant(dtype, blob[r], cols) for r in range(rows)]).astype(np.float64)
+
+    def norm(x, g):  # rows of x
+        return g * x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + cfg["eps"])
+
+    pos = pos0 + np.arange(n)
+    i = np.arange(half)
+    ang = pos[:, None] / np.power(float(cfg["theta"]), 2.0 * i / hd)[None, :]
+    cs, sn = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+
+    def rope(v):  # v [n, heads, hd]
+        a, b = v[..., :half].copy(), v[..., half:].copy()
+        return np.concatenate([a * cs - b * sn, a * sn + b * cs], axis=2)
+
+    x = w["embd"][np.asarray(tokens)].astype(np.float64)
+    for L in range(cfg["n_layers"]):
+        xn = bf16(norm(x, w["attn_norm"][L].astype(np.float64)))
+        q = xn @ matb(cfg["attn_type"], w["wq"][L], nh * hd, H).T
+        k = xn @ matb(cfg["attn_type"], w["wk"][L], nkv * hd, H).T
+        v = xn @ matb(cfg["attn_type"], w["wv"][L], nkv * hd, H).T
+        q = rope(q.reshape(n, nh, hd))
+        k = rope(k.reshape(n, nkv, hd)).reshape(n, -1)
+        kc[L, pos0:pos0 + n] = k.astype(np.float16).view(np.uint16)
+        vc[L, pos0:pos0 + n] = v.astype(np.float16).view(np.uint16)
+        K = kc[L, :pos0 + n].view(np.float16).astype(np.float64).reshape(pos0 + n, nkv, hd)
+        V = vc[L, :pos0 + n].view(np.float16).astype(np.float64).reshape(pos0 + n, nkv, hd)
+        att = np.empty((n, nh, hd))
+        for h in range(nh):
+            s = q[:, h, :] @ K[:, h // group, :].T / np.sqrt(hd)  # [n, pos0 + n]
+            s[np.arange(pos0 + n)[None, :] > pos[:, None]] = -np.inf
+            p = np.exp(s - s.max(axis=1, keepdims=True))
+            att[:, h, :] = (p / p.sum(axis=1, keepdims=True)) @ V[:, h // group, :]
+        x = x + bf16(att.reshape(n, -1)) @ matb(cfg["attn_type"], w["wo"][L], H, nh * hd).T
+        xn = bf16(norm(x, w["ffn_norm"][L].astype(np.float64)))
+        g = xn @ matb(cfg["gate_up_type"], w["wgate"][L], F, H).T
+        u = xn @ matb(cfg["gate_up_type"], w["wup"][L], F, H).T
+        with np.errstate(over="ignore"):
+            act = g / (1.0 + np.exp(-g)) * u
+        x = x + bf16(act) @ matb(cfg["down_type"], w["wdown"][L], H, F).T
+    xn = norm(x[-1:], w["output_norm"].astype(np.float64))[0]
+    return mat(cfg["head_type"], w["lm_head"], cfg["vocab"], H) @ xn

@@ -1,0 +1,152 @@
+"""GPU batched prefill (gq_model_prefill) against two CPU references.
+
+1. npref.prefill_bf16: run_batch (src/model/llama/cpu_path.rs:834-991)
+   restated in float64 with the GPU prefill's operand rounding at each
+   projection (weights: bf16 of the exact fp32 dequant; activations: fp32
+   then bf16).  Same operands up to rounding ties: an activation whose fp32
+   value lies within an fp32 ulp of a bf16 (or f16 K/V) rounding tie may
+   round the other way (a 2^-9 step in one GEMM input).  The K/V rows of
+   the first layer agree to a few f16 ulps; later layers inherit the ties'
+   steps, so the median row agrees to <= 1e-4 of max|value| (observed 0)
+   and the worst row to 1e-2 (observed <= 6e-3 at 600 tokens); the logits
+   to <= 2e-3 * max|ref| (observed 2e-7 .. 8e-4).
+2. The oracle's sequential fp32 path (LlamaModel::run, cpu_path.rs:695-818;
+   prefilling a prompt is, token by token, the same arithmetic).  The bf16
+   operands (2^-9 relative each) set the distance: logits <= 2e-2 * max|ref|,
+   and the greedy token is compared where the top-2 margin exceeds the error.
+The synthetic decoders' activations are large (attention scores ~ 1e4, a
+near-argmax softmax): keys within an fp32 rounding of a tie swap between
+any two summation orders, and after the first layer a few tokens' K/V rows
+move by percents.  The same-rounding checks therefore scale the attention
+norm weights down (scores ~ 10); the fp32-path check uses the model as is.
+"""
+import numpy as np
+import pytest
+
+import gq_synth as syn
+import npref
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+             ctx=1400, eps=1e-6, theta=1e6, attn_type=syn.Q4_K, gate_up_type=syn.Q4_K,
+             down_type=syn.Q6_K, head_type=syn.Q6_K)
+HD128 = dict(SMALL, hidden=512, n_heads=4, n_kv_heads=1, head_dim=128, ffn=768)
+
+TOL_SAME = 2e-3   # vs the same-rounding reference (logits)
+KV_SAME = 1e-2    # K/V rows vs the same-rounding reference (worst row), of max|value|
+KV_MEDIAN = 1e-4  # ... and the median row (rounding ties are rare: observed 0)
+TOL_FP32 = 2e-2   # vs the fp32 CPU path (bf16 operands)
+ATTN_SCALE = 0.05  # attention-norm scale of the same-rounding models
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+def _build(backend, cfg, seed, n_ctx, embd_scale=1.0, attn_scale=1.0):
+    import gq
+    w = syn.make_decoder(cfg, seed, embd_scale=embd_scale)
+    if attn_scale != 1.0:  # smaller q, k, v: a well-conditioned softmax
+        w["attn_norm"] = [np.float32(attn_scale) * a for a in w["attn_norm"]]
+    kv = syn.make_kv(cfg, n_ctx, seed + 1) if n_ctx else None
+    hw = syn.upload_decoder(backend, cfg, w)
+    gm = gq.DecodeModel(dict(cfg, max_tokens=1024), hw)
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    kc = np.zeros((cfg["n_layers"], cfg["ctx"], kvd), np.uint16)
+    vc = kc.copy()
+    if kv is not None:
+        for l in range(cfg["n_layers"]):
+            gm.kv_upload(l, kv[0][l], kv[1][l])
+            kc[l, :n_ctx], vc[l, :n_ctx] = kv[0][l], kv[1][l]
+    return gm, w, kv, kc, vc
+
+
+def _f16(a):
+    return a.view(np.float16).astype(np.float32)
+
+
+CASES = [("SMALL", 0, 37), ("SMALL", 100, 64), ("HD128", 70, 130), ("SMALL", 5, 600),
+         ("HD128", 0, 300)]
+
+
+@pytest.mark.parametrize("cfg_name,n_ctx,n", CASES)
+def test_prefill_same_rounding(backend, cfg_name, n_ctx, n):
+    """Logits and every K/V row written against npref.prefill_bf16; the
+    rows before the prompt are untouched.  n = 600 takes two passes."""
+    cfg = {"SMALL": SMALL, "HD128": HD128}[cfg_name]
+    say(f"prefill {cfg_name} n_ctx={n_ctx} n={n}")
+    gm, w, kv, kc, vc = _build(backend, cfg, seed=11 + n, n_ctx=n_ctx, attn_scale=ATTN_SCALE)
+    toks = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
+    nxt, got = gm.prefill(toks, n_ctx)
+    ref = npref.prefill_bf16(cfg, w, kc, vc, toks, n_ctx)
+    err = float(np.abs(got - ref).max())
+    say(f"  logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
+    assert err <= TOL_SAME * float(np.abs(ref).max())
+    assert nxt == int(np.argmax(got))
+    for l in range(cfg["n_layers"]):
+        k, v = gm.kv_download(l, n_ctx + n)
+        if n_ctx:
+            np.testing.assert_array_equal(k[:n_ctx], kv[0][l])
+            np.testing.assert_array_equal(v[:n_ctx], kv[1][l])
+        for nm, got_rows, ref_rows in (("K", k, kc[l]), ("V", v, vc[l])):
+            g, r = _f16(got_rows[n_ctx:]), _f16(ref_rows[n_ctx:n_ctx + n])
+            rows = np.abs(g - r).max(axis=1)
+            top = float(np.abs(r).max())
+            say(f"  layer {l} {nm} max|err| {rows.max():.3g} median {np.median(rows):.3g} of {top:.3g}")
+            assert rows.max() <= KV_SAME * top
+            assert np.median(rows) <= KV_MEDIAN * top
+
+
+@pytest.mark.parametrize("cfg_name,n_ctx,n", [("SMALL", 100, 64), ("HD128", 70, 130)])
+def test_prefill_vs_fp32_oracle(backend, cfg_name, n_ctx, n):
+    cfg = {"SMALL": SMALL, "HD128": HD128}[cfg_name]
+    gm, w, kv, _, _ = _build(backend, cfg, seed=11 + n, n_ctx=n_ctx)
+    om = oracle.DecoderModel(cfg, w, kv)
+    toks = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
+    nxt, got = gm.prefill(toks, n_ctx)
+    for i, t in enumerate(toks):
+        ref = om.step(int(t), n_ctx + i)
+    err = float(np.abs(got - ref).max())
+    say(f"fp32 path: logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
+    assert err <= TOL_FP32 * float(np.abs(ref).max())
+    top = np.sort(ref)[-2:]
+    if top[1] - top[0] > 2 * err:
+        assert nxt == oracle.argmax(ref)
+
+
+def test_prefill_then_generate(backend):
+    """A token-driven model (large embedding): the prompt through prefill,
+    then greedy decode on the GPU, against the oracle stepping the prompt
+    and decoding."""
+    cfg = SMALL
+    gm, w, kv, _, _ = _build(backend, cfg, seed=21, n_ctx=40, embd_scale=1e5)
+    om = oracle.DecoderModel(cfg, w, kv)
+    toks = np.random.default_rng(7).integers(0, cfg["vocab"], 50).astype(np.int32)
+    nxt, _ = gm.prefill(toks, 40, want_logits=False)
+    for i, t in enumerate(toks):
+        ref = om.step(int(t), 40 + i)
+    assert nxt == oracle.argmax(ref)
+    got = gm.generate(nxt, 90, 16)
+    exp = []
+    tok = nxt
+    for i in range(16):
+        tok = oracle.argmax(om.step(tok, 90 + i))
+        exp.append(tok)
+    np.testing.assert_array_equal(got, np.array(exp, np.int32))
+
+
+def test_prefill_errors(backend):
+    import gq
+    gm = _build(backend, SMALL, seed=3, n_ctx=0)[0]
+    with pytest.raises(gq.GqError, match="out of range"):
+        gm.prefill(np.array([1, SMALL["vocab"]], np.int32), 0)
+    with pytest.raises(gq.GqError, match="exceed the context"):
+        gm.prefill(np.zeros(10, np.int32), SMALL["ctx"] - 5)
+    with pytest.raises(gq.GqError, match="at least one token"):
+        gm.prefill(np.zeros(0, np.int32), 0)
+    q8 = dict(SMALL, attn_type=syn.Q8_0)
+    gq8 = _build(backend, q8, seed=4, n_ctx=0)[0]
+    with pytest.raises(gq.GqError, match="Q4_K or Q6_K"):
+        gq8.prefill(np.zeros(4, np.int32), 0)
