@@ -767,6 +767,8 @@ int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float 
       return fail(GQ_EINVAL, "token %d out of range", tokens_host[i]);
   hipStream_t s = (hipStream_t)stream;
   auto &L = m->L;
+  if (L.hidden % 8 || L.hidden > 8 * 256 * 4 || L.ffn % 8 || (L.n_heads * L.head_dim) % 8)
+    return fail(GQ_EINVAL, "prefill needs hidden <= 8192 and hidden, ffn multiples of 8");
   for (int l = 0; l < L.n_layers; l++) {
     const gq_weight *ws[7] = {L.wq[l], L.wk[l], L.wv[l], L.wo[l], L.wgate[l], L.wup[l], L.wdown[l]};
     for (const gq_weight *w : ws) {

@@ -66,43 +66,72 @@ __global__ void k_embed_rows(const float *embd, const int *tokens, int H, float 
 
 // Fragments of RMSNorm(x[t]) * w (rms_norm_into, cpu_path.rs:67-74:
 // w * x / sqrt(sum(x^2) / H + eps)) for tokens t < n, zeros for n <= t <
-// npad and for columns past H.  One block (256 threads) per token.
+// npad and for columns past H.  One block (256 threads) per token; a
+// thread keeps its groups of 8 values in registers across the reduction
+// (H <= NORM_GROUPS * 8 * 256, H % 8 == 0 for the vector loads).
+constexpr int NORM_GROUPS = 4;
 __global__ __launch_bounds__(256) void k_norm_to_frag(const float *x, const float *w, int n, int H,
                                                       int kpad, float eps, uint16_t *xb) {
   __shared__ float red[4];
   const int t = blockIdx.x, ksteps = kpad / 32;
   const float *xt = x + (long)t * H;
+  float v[NORM_GROUPS][8];
   float ss = 0.f;
-  if (t < n)
-    for (int i = threadIdx.x; i < H; i += 256) ss += xt[i] * xt[i];
+#pragma unroll
+  for (int j = 0; j < NORM_GROUPS; j++) {
+    const int c = 8 * (threadIdx.x + 256 * j);
+    if (t < n && c < H) {
+      const float4 a = *(const float4 *)(xt + c), b = *(const float4 *)(xt + c + 4);
+      v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
+      v[j][4] = b.x; v[j][5] = b.y; v[j][6] = b.z; v[j][7] = b.w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[j][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss += v[j][e] * v[j][e];
+  }
   ss = block_sum256(ss, red);
   const float rms = sqrtf(ss / (float)H + eps);
-  for (int c = 8 * threadIdx.x; c < kpad; c += 8 * 256) {
-    float v[8];
 #pragma unroll
-    for (int e = 0; e < 8; e++) v[e] = t < n && c + e < H ? w[c + e] * xt[c + e] / rms : 0.f;
-    put_frag8(xb, frag_slot(t, c, ksteps), v);
+  for (int j = 0; j < NORM_GROUPS; j++) {
+    const int c = 8 * (threadIdx.x + 256 * j);
+    if (c >= kpad) continue;
+    float o[8];
+    if (t < n && c < H) {
+      const float4 a = *(const float4 *)(w + c), b = *(const float4 *)(w + c + 4);
+      const float wv[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[e] = wv[e] * v[j][e] / rms;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) o[e] = 0.f;
+    }
+    put_frag8(xb, frag_slot(t, c, ksteps), o);
   }
 }
 
 // Fragments of silu(g) * u (ffn_gate_up, cpu_path.rs:225-227), g and u
-// [n][F]; zeros past n and F.
+// [n][F] (F % 8 == 0); zeros past n and F.  Block (token t, 2048 columns).
 __global__ __launch_bounds__(256) void k_swiglu_to_frag(const float *g, const float *u, int n, int F,
                                                         int kpad, uint16_t *xb) {
-  const int t = blockIdx.x, ksteps = kpad / 32;
-  for (int c = 8 * threadIdx.x; c < kpad; c += 8 * 256) {
-    float v[8];
+  const int t = blockIdx.y, ksteps = kpad / 32;
+  const int c = 8 * (blockIdx.x * 256 + threadIdx.x);
+  if (c >= kpad) return;
+  float v[8];
+  if (t < n && c < F) {
+    const float *gp = g + (long)t * F + c, *up = u + (long)t * F + c;
+    const float4 g0 = *(const float4 *)gp, g1 = *(const float4 *)(gp + 4);
+    const float4 u0 = *(const float4 *)up, u1 = *(const float4 *)(up + 4);
+    const float gv[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+    const float uv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      if (t < n && c + e < F) {
-        const float gv = g[(long)t * F + c + e];
-        v[e] = gv / (1.0f + expf(-gv)) * u[(long)t * F + c + e];
-      } else {
-        v[e] = 0.f;
-      }
-    }
-    put_frag8(xb, frag_slot(t, c, ksteps), v);
+    for (int e = 0; e < 8; e++) v[e] = gv[e] / (1.0f + expf(-gv[e])) * uv[e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; e++) v[e] = 0.f;
   }
+  put_frag8(xb, frag_slot(t, c, ksteps), v);
 }
 
 // NEOX RoPE (cpu_path.rs:99-133, angle pos / theta^(2i/hd)) of q [n][nh*hd]
@@ -392,7 +421,9 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
     const gq_weight *gu[2] = {m.wgate[L], m.wup[L]};
     float *guo[2] = {b.g, b.u};
     if ((e = launch_gemm_bf16(gu, guo, 2, b.xb, n, b.part, false, num_cus, s)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_swiglu_to_frag, dim3(npad), dim3(256), 0, s, b.g, b.u, n, F, round_up(F, 256), b.xb);
+    const int kpf = round_up(F, 256);
+    hipLaunchKernelGGL(k_swiglu_to_frag, dim3((kpf / 8 + 255) / 256, npad), dim3(256), 0, s, b.g, b.u, n, F,
+                       kpf, b.xb);
     if ((e = launch_gemm_bf16(&m.wdown[L], xo, 1, b.xb, n, b.part, true, num_cus, s)) != hipSuccess) return e;
   }
   // logits of RMSNorm(x[n - 1]) (the decode head matvec)
