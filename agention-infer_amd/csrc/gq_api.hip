@@ -582,10 +582,12 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   const int H = d->hidden, hd = d->head_dim, nh = d->n_heads, nkv = d->n_kv_heads;
   if (d->n_layers <= 0 || H <= 0 || H % 4 || (hd != 64 && hd != 128) || nh <= 0 || nkv <= 0 ||
       nh % nkv || nh / nkv > 8 || d->ffn <= 0 || d->vocab <= 0 || d->ctx <= 0 ||
-      d->ctx > gq::ATT_MAX_CTX)
+      d->ctx > gq::ATT_MAX_CTX ||
+      (d->kv_dtype != 0 && d->kv_dtype != GQ_TYPE_F16 && d->kv_dtype != GQ_TYPE_Q8_0) ||
+      (d->kv_dtype == GQ_TYPE_Q8_0 && (nkv * hd) % 32))
     return fail(GQ_EINVAL, "bad model shape (hidden a multiple of 4, head_dim 64 or 128, "
                            "n_heads a multiple of n_kv_heads with at most 8 query heads per KV "
-                           "head, ctx <= %d)", gq::ATT_MAX_CTX);
+                           "head, ctx <= %d, KV type F16 or Q8_0)", gq::ATT_MAX_CTX);
   for (int l = 0; l < d->n_layers; l++) {
     if ((rc = check_w(d->wq[l], nh * hd, H, "wq", l)) || (rc = check_w(d->wk[l], nkv * hd, H, "wk", l)) ||
         (rc = check_w(d->wv[l], nkv * hd, H, "wv", l)) || (rc = check_w(d->wo[l], H, nh * hd, "wo", l)) ||
@@ -617,8 +619,12 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   float *norms = nullptr, *embd = nullptr;
   rc = dalloc(m, &norms, (size_t)(2 * d->n_layers + 1) * H);
   if (!rc) rc = dalloc(m, &embd, (size_t)d->vocab * H);
-  if (!rc) rc = dalloc(m, &L.kcache, (size_t)d->n_layers * d->ctx * kvd);
-  if (!rc) rc = dalloc(m, &L.vcache, (size_t)d->n_layers * d->ctx * kvd);
+  L.kv_q8 = d->kv_dtype == GQ_TYPE_Q8_0;
+  // Q8_0: int8 codes in the first half of the f16-sized allocation
+  if (!rc) rc = dalloc(m, &L.kcache, (size_t)d->n_layers * d->ctx * kvd / (L.kv_q8 ? 2 : 1) + 1);
+  if (!rc) rc = dalloc(m, &L.vcache, (size_t)d->n_layers * d->ctx * kvd / (L.kv_q8 ? 2 : 1) + 1);
+  if (!rc && L.kv_q8) rc = dalloc(m, &L.kscale, (size_t)d->n_layers * d->ctx * (kvd / 32));
+  if (!rc && L.kv_q8) rc = dalloc(m, &L.vscale, (size_t)d->n_layers * d->ctx * (kvd / 32));
   float *buf = nullptr;
   const int nb_amax = (d->vocab + gq::ARGMAX_SPAN - 1) / gq::ARGMAX_SPAN;
   const size_t nbuf = 3 * ((size_t)H + 16) + 2 * ((size_t)nh * hd + 16) + 2 * (kvd + 16) +
@@ -659,8 +665,11 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   if (e == hipSuccess) e = hipMemset(ibuf, 0, nibuf * sizeof(int));
   if (e == hipSuccess) e = hipMemset(buf, 0, nbuf * sizeof(float));
   if (e == hipSuccess) e = hipMemcpy(L.rope_den, den.data(), den.size() * 4, hipMemcpyHostToDevice);
-  if (e == hipSuccess) e = hipMemset(L.kcache, 0, (size_t)d->n_layers * d->ctx * kvd * 2);
-  if (e == hipSuccess) e = hipMemset(L.vcache, 0, (size_t)d->n_layers * d->ctx * kvd * 2);
+  const size_t kv_bytes = (size_t)d->n_layers * d->ctx * kvd * (L.kv_q8 ? 1 : 2);
+  if (e == hipSuccess) e = hipMemset(L.kcache, 0, kv_bytes);
+  if (e == hipSuccess) e = hipMemset(L.vcache, 0, kv_bytes);
+  if (e == hipSuccess && L.kv_q8) e = hipMemset(L.kscale, 0, (size_t)d->n_layers * d->ctx * (kvd / 32) * 2);
+  if (e == hipSuccess && L.kv_q8) e = hipMemset(L.vscale, 0, (size_t)d->n_layers * d->ctx * (kvd / 32) * 2);
   if (e != hipSuccess) { delete m; return fail(GQ_EHIP, "model upload failed: %s", hipGetErrorString(e)); }
   L.attn_norm = m->an.data(); L.ffn_norm = m->fn.data();
   L.output_norm = norms + (size_t)2 * d->n_layers * H;
@@ -674,25 +683,64 @@ int gq_model_free(gq_model *m) {
   return GQ_OK;
 }
 
-static int kv_copy(gq_model *m, int layer, uint16_t *k, uint16_t *v, int n_pos, bool up) {
+// KV rows in the cache's KvDtype byte format on the host; the device keeps
+// Q8_0 as codes [ctx][kvd] and f16 scales [ctx][kvd / 32].
+static int kv_copy(gq_model *m, int layer, void *k, void *v, int n_pos, bool up) {
   if (!m || layer < 0 || layer >= m->L.n_layers || n_pos < 0 || n_pos > m->L.ctx)
     return fail(GQ_EINVAL, "bad KV range (layer %d, %d positions)", layer, n_pos);
+  if (n_pos > 0 && (!k || !v)) return fail(GQ_EINVAL, "null KV buffer");
   const size_t kvd = (size_t)m->L.n_kv_heads * m->L.head_dim;
-  const size_t off = (size_t)layer * m->L.ctx * kvd, bytes = (size_t)n_pos * kvd * 2;
-  hipError_t e = up ? hipMemcpy(m->L.kcache + off, k, bytes, hipMemcpyHostToDevice)
-                    : hipMemcpy(k, m->L.kcache + off, bytes, hipMemcpyDeviceToHost);
-  if (e == hipSuccess)
-    e = up ? hipMemcpy(m->L.vcache + off, v, bytes, hipMemcpyHostToDevice)
-           : hipMemcpy(v, m->L.vcache + off, bytes, hipMemcpyDeviceToHost);
-  if (e != hipSuccess) return fail(GQ_EHIP, "KV copy failed: %s", hipGetErrorString(e));
+  if (!m->L.kv_q8) {
+    const size_t off = (size_t)layer * m->L.ctx * kvd, bytes = (size_t)n_pos * kvd * 2;
+    hipError_t e = up ? hipMemcpy(m->L.kcache + off, k, bytes, hipMemcpyHostToDevice)
+                      : hipMemcpy(k, m->L.kcache + off, bytes, hipMemcpyDeviceToHost);
+    if (e == hipSuccess)
+      e = up ? hipMemcpy(m->L.vcache + off, v, bytes, hipMemcpyHostToDevice)
+             : hipMemcpy(v, m->L.vcache + off, bytes, hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return fail(GQ_EHIP, "KV copy failed: %s", hipGetErrorString(e));
+    return GQ_OK;
+  }
+  const size_t nb = kvd / 32, rows = (size_t)n_pos;
+  std::vector<int8_t> codes(rows * kvd);
+  std::vector<uint16_t> scales(rows * nb);
+  void *host[2] = {k, v};
+  int8_t *dq[2] = {(int8_t *)m->L.kcache + (size_t)layer * m->L.ctx * kvd,
+                   (int8_t *)m->L.vcache + (size_t)layer * m->L.ctx * kvd};
+  uint16_t *ds[2] = {m->L.kscale + (size_t)layer * m->L.ctx * nb,
+                     m->L.vscale + (size_t)layer * m->L.ctx * nb};
+  for (int i = 0; i < 2; i++) {
+    uint8_t *hb = (uint8_t *)host[i];
+    hipError_t e = hipSuccess;
+    if (up) {
+      for (size_t r = 0; r < rows; r++)
+        for (size_t b = 0; b < nb; b++) {
+          const uint8_t *blk = hb + (r * nb + b) * 34;
+          scales[r * nb + b] = (uint16_t)(blk[0] | (blk[1] << 8));
+          memcpy(&codes[r * kvd + 32 * b], blk + 2, 32);
+        }
+      e = hipMemcpy(dq[i], codes.data(), codes.size(), hipMemcpyHostToDevice);
+      if (e == hipSuccess) e = hipMemcpy(ds[i], scales.data(), scales.size() * 2, hipMemcpyHostToDevice);
+    } else {
+      e = hipMemcpy(codes.data(), dq[i], codes.size(), hipMemcpyDeviceToHost);
+      if (e == hipSuccess) e = hipMemcpy(scales.data(), ds[i], scales.size() * 2, hipMemcpyDeviceToHost);
+      for (size_t r = 0; r < rows && e == hipSuccess; r++)
+        for (size_t b = 0; b < nb; b++) {
+          uint8_t *blk = hb + (r * nb + b) * 34;
+          blk[0] = (uint8_t)scales[r * nb + b];
+          blk[1] = (uint8_t)(scales[r * nb + b] >> 8);
+          memcpy(blk + 2, &codes[r * kvd + 32 * b], 32);
+        }
+    }
+    if (e != hipSuccess) return fail(GQ_EHIP, "KV copy failed: %s", hipGetErrorString(e));
+  }
   return GQ_OK;
 }
 
-int gq_model_kv_upload(gq_model *m, int layer, const uint16_t *k, const uint16_t *v, int n_pos) {
-  return kv_copy(m, layer, (uint16_t *)k, (uint16_t *)v, n_pos, true);
+int gq_model_kv_upload(gq_model *m, int layer, const void *k, const void *v, int n_pos) {
+  return kv_copy(m, layer, (void *)k, (void *)v, n_pos, true);
 }
 
-int gq_model_kv_download(gq_model *m, int layer, uint16_t *k, uint16_t *v, int n_pos) {
+int gq_model_kv_download(gq_model *m, int layer, void *k, void *v, int n_pos) {
   return kv_copy(m, layer, k, v, n_pos, false);
 }
 
@@ -767,6 +815,7 @@ int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float 
       return fail(GQ_EINVAL, "token %d out of range", tokens_host[i]);
   hipStream_t s = (hipStream_t)stream;
   auto &L = m->L;
+  if (L.kv_q8) return fail(GQ_EINVAL, "prefill supports the F16 KV cache only");
   if (L.hidden % 8 || L.hidden > 8 * 256 * 4 || L.ffn % 8 || (L.n_heads * L.head_dim) % 8)
     return fail(GQ_EINVAL, "prefill needs hidden <= 8192 and hidden, ffn multiples of 8");
   for (int l = 0; l < L.n_layers; l++) {

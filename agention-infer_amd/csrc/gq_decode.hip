@@ -60,10 +60,17 @@ static_assert(ATT_CHUNK == 16 * ATT_WAVES, "16 positions per wave");
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4a_t __attribute__((ext_vector_type(4)));
 
-template <int HD>
+// Q8 (the Q8_0 KV cache, KvDtype::Q8_0, src/model/mod.rs:540-603): kc / vc
+// hold int8 codes [ctx][kvd] and ksc / vsc the f16 scales of each 32-value
+// block [ctx][kvd / 32].  A 32-deep MFMA step is exactly one block: it runs
+// on the codes (int8 -> f16 is exact) and its result is scaled by the key's
+// block scale; V values are code * scale.  The new row is packed like
+// KvDtype::Q8_0::pack (scale = max|x| / 127 stored as f16, codes =
+// round(x / scale) in [-127, 127]) and used as stored for its position.
+template <int HD, bool Q8>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
-    const float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc,
-    const DecodeState *st, int group, int kvd, const float *rope_den, float *part) {
+    const float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc, uint16_t *ksc,
+    uint16_t *vsc, const DecodeState *st, int group, int kvd, const float *rope_den, float *part) {
   constexpr int CH = ATT_CHUNK;
   constexpr int NW = ATT_WAVES;
   constexpr int PW = CH / NW;  // positions per wave: one 16-column MFMA tile
@@ -74,8 +81,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   __shared__ __align__(16) float ored[NW][ATT_MAXG][HD];
   __shared__ __align__(16) float qsh[ATT_MAXG][HD];
   __shared__ float rs[HALF], rc[HALF];
-  __shared__ __align__(16) uint16_t knew[HD];
+  __shared__ __align__(16) uint16_t knew[HD];  // f16 bits (Q8: the code as f16)
   __shared__ __align__(16) uint16_t vnew[HD];
+  __shared__ float knew_sc[HD / 32], vnew_sc[HD / 32];  // Q8: the new row's scales
   __shared__ float qmax_s[NW];
   __shared__ float gm_s[ATT_MAXG], gl_s[ATT_MAXG];
 
@@ -88,18 +96,37 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
 
   // K rows as MFMA B operands (row tw + lane%16, dims 8*(lane/16) + 32*ks),
   // V dims DPL*lane of the wave's rows; clamped to n - 1 (unused past n).
+  const int8_t *kq8 = (const int8_t *)kc, *vq8 = (const int8_t *)vc;
+  const int nbr = kvd / 32;  // Q8 blocks per row
   uint4 kb[KS];
+  float kscl[KS];
   {
     const int t = min(tw + (lane & 15), n - 1);
 #pragma unroll
-    for (int ks = 0; ks < KS; ks++)
-      kb[ks] = ldw4(kc + (long)t * kvd + (long)kh * HD + 8 * (lane >> 4) + 32 * ks);
+    for (int ks = 0; ks < KS; ks++) {
+      if constexpr (Q8) {
+        const uint2 w = ldw2(kq8 + (long)t * kvd + (long)kh * HD + 8 * (lane >> 4) + 32 * ks);
+        kb[ks] = make_uint4(w.x, w.y, 0u, 0u);
+        kscl[ks] = h2f(ldh(ksc + (long)t * nbr + (kh * HD) / 32 + ks));
+      } else {
+        kb[ks] = ldw4(kc + (long)t * kvd + (long)kh * HD + 8 * (lane >> 4) + 32 * ks);
+      }
+    }
   }
   uint32_t vr[PW];
+  float vscl[PW];
 #pragma unroll
   for (int j = 0; j < PW; j++) {
-    const uint16_t *p = vc + (long)min(tw + j, n - 1) * kvd + (long)kh * HD + DPL * lane;
-    vr[j] = DPL == 2 ? ldw1(p) : (uint32_t)ldh(p);
+    const long row = min(tw + j, n - 1);
+    if constexpr (Q8) {
+      const int8_t *p = vq8 + row * kvd + (long)kh * HD + DPL * lane;
+      vr[j] = DPL == 2 ? (uint32_t)ldh((const uint16_t *)p) : (uint32_t)(uint8_t)*p;
+      vscl[j] = h2f(ldh(vsc + row * nbr + (kh * HD + DPL * lane) / 32));
+    } else {
+      const uint16_t *p = vc + row * kvd + (long)kh * HD + DPL * lane;
+      vr[j] = DPL == 2 ? ldw1(p) : (uint32_t)ldh(p);
+      vscl[j] = 1.f;
+    }
   }
 
   // RoPE table for pair index i (NEOX pairs d <-> d + hd/2).
@@ -116,12 +143,38 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     const float *pk = k + (long)kh * HD;
     const float own = pk[d], par = pk[(d + HALF) % HD];
     const float rot = d < HALF ? own * rc[i] - par * rs[i] : par * rs[i] + own * rc[i];
-    const uint16_t kbits = __half_as_ushort(__float2half_rn(rot));
-    const uint16_t vbits = __half_as_ushort(__float2half_rn(v[(long)kh * HD + d]));
-    knew[d] = kbits;
-    vnew[d] = vbits;
-    kc[(long)pos * kvd + (long)kh * HD + d] = kbits;
-    vc[(long)pos * kvd + (long)kh * HD + d] = vbits;
+    const float vv = v[(long)kh * HD + d];
+    if constexpr (Q8) {
+      // 32-lane groups are the 32-value blocks (HD is a multiple of 64)
+      float km = fabsf(rot), vm = fabsf(vv);
+#pragma unroll
+      for (int off = 16; off > 0; off >>= 1) {
+        km = fmaxf(km, __shfl_xor(km, off, 32));
+        vm = fmaxf(vm, __shfl_xor(vm, off, 32));
+      }
+      const float kscale = km > 0.f ? km / 127.0f : 1.0f, vscale = vm > 0.f ? vm / 127.0f : 1.0f;
+      const float kcode = fminf(fmaxf(roundf(rot / kscale), -127.f), 127.f);
+      const float vcode = fminf(fmaxf(roundf(vv / vscale), -127.f), 127.f);
+      const uint16_t ks16 = __half_as_ushort(__float2half_rn(kscale));
+      const uint16_t vs16 = __half_as_ushort(__float2half_rn(vscale));
+      knew[d] = __half_as_ushort(__float2half_rn(kcode));
+      vnew[d] = __half_as_ushort(__float2half_rn(vcode));
+      ((int8_t *)kc)[(long)pos * kvd + (long)kh * HD + d] = (int8_t)kcode;
+      ((int8_t *)vc)[(long)pos * kvd + (long)kh * HD + d] = (int8_t)vcode;
+      if ((d & 31) == 0) {
+        knew_sc[d / 32] = h2f(ks16);
+        vnew_sc[d / 32] = h2f(vs16);
+        ksc[(long)pos * nbr + (kh * HD + d) / 32] = ks16;
+        vsc[(long)pos * nbr + (kh * HD + d) / 32] = vs16;
+      }
+    } else {
+      const uint16_t kbits = __half_as_ushort(__float2half_rn(rot));
+      const uint16_t vbits = __half_as_ushort(__float2half_rn(vv));
+      knew[d] = kbits;
+      vnew[d] = vbits;
+      kc[(long)pos * kvd + (long)kh * HD + d] = kbits;
+      vc[(long)pos * kvd + (long)kh * HD + d] = vbits;
+    }
   }
   // Rotated q of the group's heads, and its max |q|.
   float qm = 0.f;
@@ -182,12 +235,30 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     for (int ks = 0; ks < KS; ks++) {
       // the new row's fragment (read whether used or not)
       const uint4 kn = *(const uint4 *)(knew + 8 * (lane >> 4) + 32 * ks);
-      const uint4 raw = make_uint4(isnew ? kn.x : kb[ks].x, isnew ? kn.y : kb[ks].y,
-                                   isnew ? kn.z : kb[ks].z, isnew ? kn.w : kb[ks].w);
       f16x8_t bk;
-      __builtin_memcpy(&bk, &raw, 16);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, acc, 0, 0, 0);
+      if constexpr (Q8) {
+        _Float16 h8[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+          h8[e] = (_Float16)(float)(int8_t)(((e < 4 ? kb[ks].x : kb[ks].y) >> (8 * (e & 3))) & 0xffu);
+        uint4 raw;
+        __builtin_memcpy(&raw, h8, 16);
+        raw = make_uint4(isnew ? kn.x : raw.x, isnew ? kn.y : raw.y, isnew ? kn.z : raw.z,
+                         isnew ? kn.w : raw.w);
+        __builtin_memcpy(&bk, &raw, 16);
+        f32x4a_t part_acc = {0.f, 0.f, 0.f, 0.f};
+        part_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, part_acc, 0, 0, 0);
+        part_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, part_acc, 0, 0, 0);
+        const float sc = isnew ? knew_sc[ks] : kscl[ks];
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(sc, part_acc[i], acc[i]);
+      } else {
+        const uint4 raw = make_uint4(isnew ? kn.x : kb[ks].x, isnew ? kn.y : kb[ks].y,
+                                     isnew ? kn.z : kb[ks].z, isnew ? kn.w : kb[ks].w);
+        __builtin_memcpy(&bk, &raw, 16);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, acc, 0, 0, 0);
+      }
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -221,9 +292,20 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
       // Rows past pos were clamped to row pos, which this launch is still
       // writing: their p is 0, but 0 * (stale NaN/inf) is not, so they
       // read as 0; row pos itself is the freshly rounded one.
-      const uint32_t raw = tw + j == pos ? vn : (tw + j > pos ? 0u : vr[j]);
+      if constexpr (Q8) {
+        // the new row's values were stored as the f16 of its codes
 #pragma unroll
-      for (int e = 0; e < DPL; e++) vf[j][e] = h2f(raw >> (16 * e));
+        for (int e = 0; e < DPL; e++) {
+          const float code = tw + j == pos ? h2f(vn >> (16 * e))
+                                           : (float)(int8_t)((vr[j] >> (8 * e)) & 0xffu);
+          const float sc = tw + j == pos ? vnew_sc[(DPL * lane) / 32] : vscl[j];
+          vf[j][e] = tw + j > pos ? 0.f : code * sc;
+        }
+      } else {
+        const uint32_t raw = tw + j == pos ? vn : (tw + j > pos ? 0u : vr[j]);
+#pragma unroll
+        for (int e = 0; e < DPL; e++) vf[j][e] = h2f(raw >> (16 * e));
+      }
     }
 #pragma unroll
     for (int g = 0; g < ATT_MAXG; g++) {
@@ -470,13 +552,26 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
         }
       if ((e = matvec_launch(grp, n, in, gout, s)) != hipSuccess) return e;
     }
-    uint16_t *kc = m.kcache + (long)L * m.ctx * kvd, *vc = m.vcache + (long)L * m.ctx * kvd;
-    if (hd == 128)
-      hipLaunchKernelGGL(k_attn_gqa<128>, dim3(nkv, m.att_chunks), dim3(ATT_THREADS), 0, s, m.q, m.k, m.v,
-                         kc, vc, m.state, group, kvd, m.rope_den, m.att_part);
+    // F16: [layer][ctx][kvd] f16; Q8: [layer][ctx][kvd] int8 codes (in the
+    // same allocation) and [layer][ctx][kvd / 32] f16 scales
+    const long lo = (long)L * m.ctx * kvd;
+    uint16_t *kc = m.kv_q8 ? (uint16_t *)((int8_t *)m.kcache + lo) : m.kcache + lo;
+    uint16_t *vc = m.kv_q8 ? (uint16_t *)((int8_t *)m.vcache + lo) : m.vcache + lo;
+    uint16_t *ksc = m.kv_q8 ? m.kscale + (long)L * m.ctx * (kvd / 32) : nullptr;
+    uint16_t *vsc = m.kv_q8 ? m.vscale + (long)L * m.ctx * (kvd / 32) : nullptr;
+    const dim3 ag(nkv, m.att_chunks), at(ATT_THREADS);
+    if (hd == 128 && m.kv_q8)
+      hipLaunchKernelGGL((k_attn_gqa<128, true>), ag, at, 0, s, m.q, m.k, m.v, kc, vc, ksc, vsc, m.state,
+                         group, kvd, m.rope_den, m.att_part);
+    else if (hd == 128)
+      hipLaunchKernelGGL((k_attn_gqa<128, false>), ag, at, 0, s, m.q, m.k, m.v, kc, vc, ksc, vsc, m.state,
+                         group, kvd, m.rope_den, m.att_part);
+    else if (m.kv_q8)
+      hipLaunchKernelGGL((k_attn_gqa<64, true>), ag, at, 0, s, m.q, m.k, m.v, kc, vc, ksc, vsc, m.state,
+                         group, kvd, m.rope_den, m.att_part);
     else
-      hipLaunchKernelGGL(k_attn_gqa<64>, dim3(nkv, m.att_chunks), dim3(ATT_THREADS), 0, s, m.q, m.k, m.v,
-                         kc, vc, m.state, group, kvd, m.rope_den, m.att_part);
+      hipLaunchKernelGGL((k_attn_gqa<64, false>), ag, at, 0, s, m.q, m.k, m.v, kc, vc, ksc, vsc, m.state,
+                         group, kvd, m.rope_den, m.att_part);
     if (hd == 128)
       hipLaunchKernelGGL(k_attn_merge<128>, dim3(m.n_heads), dim3(ATT_MQ * 128), 0, s, m.state, m.att_chunks,
                          m.att_part, m.att);

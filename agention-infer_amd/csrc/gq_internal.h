@@ -118,7 +118,9 @@ struct DecodeLaunch {
   const gq_weight *lm_head;
   const float *const *attn_norm, *const *ffn_norm;  // host arrays of device pointers
   const float *output_norm, *embd;
-  uint16_t *kcache, *vcache;  // [layer][ctx][kv_dim] f16
+  uint16_t *kcache, *vcache;  // [layer][ctx][kv_dim] f16 (kv_q8: int8 codes)
+  int kv_q8;                  // KvDtype::Q8_0 cache
+  uint16_t *kscale, *vscale;  // kv_q8: [layer][ctx][kv_dim / 32] f16 block scales
   float *xa, *xb;             // residual stream, ping-pong
   float *q, *k, *v, *att, *proj, *h, *logits, *att_part;
   float *rope_den;            // [head_dim / 2] theta^(2i/head_dim), computed on the host

@@ -338,7 +338,8 @@ class _ModelDesc(ctypes.Structure):
         [("eps", ctypes.c_float), ("theta", ctypes.c_float)] + \
         [(n, ctypes.c_void_p) for n in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown",
                                          "lm_head", "attn_norm", "ffn_norm", "output_norm",
-                                         "embd")]
+                                         "embd")] + \
+        [("kv_dtype", ctypes.c_int)]
 
 
 class DecodeModel:
@@ -356,6 +357,9 @@ class DecodeModel:
                   "ctx"):
             setattr(d, k, int(cfg[k]))
         d.max_tokens = int(cfg.get("max_tokens", 4096))
+        # KvDtype::parse (model/mod.rs:540-547): "f16" (default) or "q8_0"
+        self.kv_q8 = str(cfg.get("kv_dtype", "f16")).lower() in ("q8_0", "q8")
+        d.kv_dtype = Q8_0 if self.kv_q8 else 0
         d.eps, d.theta = float(cfg["eps"]), float(cfg["theta"])
         L = cfg["n_layers"]
         for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown"):
@@ -385,15 +389,24 @@ class DecodeModel:
             _lib.gq_model_free(self._h)
             self._h = None
 
-    def kv_upload(self, layer, k_f16, v_f16):
-        k = np.ascontiguousarray(k_f16, np.uint16)
-        v = np.ascontiguousarray(v_f16, np.uint16)
+    def _kv_row(self):
+        kvd = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
+        return (kvd // 32 * 34, np.uint8) if self.kv_q8 else (kvd, np.uint16)
+
+    def kv_upload(self, layer, k_rows, v_rows):
+        """Rows [n_pos][...] in the cache's KvDtype format: f16 bits
+        (uint16) or Q8_0 blocks (uint8, kv_dim/32 * 34 bytes per row)."""
+        width, dt = self._kv_row()
+        k = np.ascontiguousarray(k_rows, dt)
+        v = np.ascontiguousarray(v_rows, dt)
+        if k.shape != v.shape or k.ndim != 2 or k.shape[1] != width:
+            raise ValueError(f"KV rows must be [n_pos][{width}] {np.dtype(dt).name}")
         _check(lib().gq_model_kv_upload(self._h, layer, _ptr(k), _ptr(v), k.shape[0]))
 
     def kv_download(self, layer, n_pos):
-        kvd = self.cfg["n_kv_heads"] * self.cfg["head_dim"]
-        k = np.zeros((n_pos, kvd), np.uint16)
-        v = np.zeros((n_pos, kvd), np.uint16)
+        width, dt = self._kv_row()
+        k = np.zeros((n_pos, width), dt)
+        v = np.zeros((n_pos, width), dt)
         _check(lib().gq_model_kv_download(self._h, layer, _ptr(k), _ptr(v), n_pos))
         return k, v
 

@@ -197,6 +197,36 @@ def prefill_leg(m, cfg, torch):
     return out
 
 
+def q8_kv_leg(gq, cfg, hw, torch, stream):
+    """The same decode with a Q8_0 KV cache (KvDtype::Q8_0): the context as
+    synthetic Q8_0 rows (int8 codes ~ U[-127, 127], f16 scales ~ |N(0,1)|/127)
+    prefilled to DECODE_PREFILL positions; DECODE_STEPS greedy steps."""
+    m = gq.DecodeModel(dict(cfg, max_tokens=DECODE_STEPS, kv_dtype="q8_0"), hw)
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    nb = kvd // 32
+    rng = np.random.default_rng(13)
+    for layer in range(cfg["n_layers"]):
+        rows = []
+        for _ in range(2):
+            blk = np.empty((DECODE_PREFILL, nb, 34), np.uint8)
+            sc = (np.abs(rng.standard_normal((DECODE_PREFILL, nb))) / 127.0).astype(np.float16)
+            blk[:, :, :2] = sc.view(np.uint8).reshape(DECODE_PREFILL, nb, 2)
+            blk[:, :, 2:] = rng.integers(-127, 128, (DECODE_PREFILL, nb, 32)).astype(np.int8).view(np.uint8)
+            rows.append(blk.reshape(DECODE_PREFILL, nb * 34))
+        m.kv_upload(layer, rows[0], rows[1])
+    m.generate(1234, DECODE_PREFILL, 8, stream=stream.cuda_stream)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    m.generate(1234, DECODE_PREFILL, DECODE_STEPS, stream=stream.cuda_stream)
+    e1.record()
+    torch.cuda.synchronize()
+    ms_tok = e0.elapsed_time(e1) / DECODE_STEPS
+    kv_bytes = 2 * cfg["n_layers"] * (DECODE_PREFILL + DECODE_STEPS // 2) * kvd * 34 // 32
+    return {"tok_s": round(1e3 / ms_tok, 1), "ms_per_token": round(ms_tok, 4),
+            "kv_bytes_per_step": kv_bytes}
+
+
 def decode_leg(be, gq, syn, torch, cpu_steps):
     """GPU-resident 7B-shape Q4_K_M decode (28 layers,
     f16 KV prefilled to 4096 positions, 128 greedy steps, one HIP graph
@@ -232,6 +262,8 @@ def decode_leg(be, gq, syn, torch, cpu_steps):
            "model": "Qwen2.5-7B-shaped Q4_K_M (random init), 28 layers, hidden 3584, "
                     "28/4 heads, ffn 18944, vocab 152064"}
     out["prefill"] = prefill_leg(m, cfg, torch)
+    del m
+    out["q8_0_kv"] = q8_kv_leg(gq, cfg, hw, torch, stream)
     if cpu_steps > 0:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle
@@ -244,7 +276,6 @@ def decode_leg(be, gq, syn, torch, cpu_steps):
         el = time.perf_counter() - t0
         out["cpu_tok_s"] = round(cpu_steps / el, 3)
         out["cpu_sample"] = f"{cpu_steps} oracle decode steps (gqo_decode_step, all host threads)"
-    del m
     return out
 
 

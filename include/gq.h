@@ -28,6 +28,7 @@ extern "C" {
 #define GQ_ENODEV (-6)   /* no gfx950 device / not initialised */
 
 /* GgmlType ids, the on-disk tensor type ids (src/types.rs:9-46). */
+#define GQ_TYPE_F16 1
 #define GQ_TYPE_Q8_0 8
 #define GQ_TYPE_Q4_K 12
 #define GQ_TYPE_Q5_K 13
@@ -159,17 +160,20 @@ typedef struct {
   const float *const *attn_norm, *const *ffn_norm;  /* host [n_layers][hidden] */
   const float *output_norm;                         /* host [hidden] */
   const float *embd;                                /* host [vocab][hidden] */
+  /* KV cache type (KvDtype, src/model/mod.rs:530-603): 0 (or GQ_TYPE_F16)
+   * f16 rows, GQ_TYPE_Q8_0 Q8_0 blocks (kv_dim a multiple of 32). */
+  int kv_dtype;
 } gq_model_desc;
 
 int gq_model_create(const gq_model_desc *desc, gq_model **out);
 int gq_model_free(gq_model *m);
 
-/* Fill / read back KV cache rows [0, n_pos) of a layer (f16 bits,
- * [n_pos][n_kv_heads * head_dim]), e.g. a prefilled context
- * (KvCache::write_range, src/model/mod.rs:671-680). */
-int gq_model_kv_upload(gq_model *m, int layer, const uint16_t *k_host, const uint16_t *v_host,
-                       int n_pos);
-int gq_model_kv_download(gq_model *m, int layer, uint16_t *k_host, uint16_t *v_host, int n_pos);
+/* Fill / read back KV cache rows [0, n_pos) of a layer, e.g. a prefilled
+ * context (KvCache::write_range, src/model/mod.rs:671-680), in the cache's
+ * KvDtype byte format: F16 rows of kv_dim f16 (uint16), Q8_0 rows of
+ * kv_dim / 32 blocks of 34 bytes (f16 scale, 32 int8). */
+int gq_model_kv_upload(gq_model *m, int layer, const void *k_host, const void *v_host, int n_pos);
+int gq_model_kv_download(gq_model *m, int layer, void *k_host, void *v_host, int n_pos);
 
 /* One decode step (Model::forward, src/model/llama/mod.rs:336-363): token at
  * position pos; logits_host[vocab] (may be NULL) and the greedy next token. */

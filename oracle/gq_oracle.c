@@ -812,6 +812,7 @@ int gqo_decode_step(const gqo_model *m, int token, int pos, float *logits, int n
     float *kall = (float *)malloc(sizeof(float) * (size_t)n * kvd);
     float *vall = (float *)malloc(sizeof(float) * (size_t)n * kvd);
     int rc = 0;
+    if (m->kv_q8 && (kvd % 32 || kvd > 32768)) rc = -1;
     memcpy(x, m->embd + (size_t)token * H, sizeof(float) * H);
     for (int L = 0; L < m->n_layers && !rc; L++) {
         const int *lt = m->layer_types ? m->layer_types + 7 * L : NULL;
@@ -824,15 +825,43 @@ int gqo_decode_step(const gqo_model *m, int token, int pos, float *logits, int n
         rc |= gqo_matmul_into(tk, m->wk[L], gqo_type_size(tk, H) * kvd, xn, H, k, kvd, nthreads);
         rc |= gqo_matmul_into(tv, m->wv[L], gqo_type_size(tv, H) * kvd, xn, H, v, kvd, nthreads);
         rope(q, k, nh, nkv, hd, m->theta, pos);
-        uint16_t *kc = m->kcache[L], *vc = m->vcache[L];
-        for (int i = 0; i < kvd; i++) {
-            kc[(size_t)pos * kvd + i] = gqo_f32_to_f16(k[i]);
-            vc[(size_t)pos * kvd + i] = gqo_f32_to_f16(v[i]);
-        }
         const float *tab = f16_table();
-        for (size_t i = 0; i < (size_t)n * kvd; i++) {
-            kall[i] = tab[kc[i]];
-            vall[i] = tab[vc[i]];
+        if (m->kv_q8) {
+            /* KvDtype::Q8_0: pack (model/mod.rs:574-583) the new row, unpack
+             * (:595-602) every row up to pos. */
+            const int nb = kvd / 32;
+            const size_t rowb = (size_t)nb * 34;
+            uint8_t *kc = (uint8_t *)m->kcache[L], *vc = (uint8_t *)m->vcache[L];
+            uint16_t sc[2][1024];
+            int8_t qq[2][32768];
+            gqo_quantize_q8_32(k, (size_t)kvd, sc[0], qq[0]);
+            gqo_quantize_q8_32(v, (size_t)kvd, sc[1], qq[1]);
+            for (int b = 0; b < nb; b++) {
+                uint8_t *kb = kc + (size_t)pos * rowb + 34 * b, *vb = vc + (size_t)pos * rowb + 34 * b;
+                kb[0] = (uint8_t)sc[0][b]; kb[1] = (uint8_t)(sc[0][b] >> 8);
+                vb[0] = (uint8_t)sc[1][b]; vb[1] = (uint8_t)(sc[1][b] >> 8);
+                memcpy(kb + 2, qq[0] + 32 * b, 32);
+                memcpy(vb + 2, qq[1] + 32 * b, 32);
+            }
+            for (size_t t = 0; t < (size_t)n; t++)
+                for (int b = 0; b < nb; b++) {
+                    const uint8_t *kb = kc + t * rowb + 34 * b, *vb = vc + t * rowb + 34 * b;
+                    const float ks = tab[kb[0] | (kb[1] << 8)], vs = tab[vb[0] | (vb[1] << 8)];
+                    for (int e = 0; e < 32; e++) {
+                        kall[t * kvd + 32 * b + e] = (float)(int8_t)kb[2 + e] * ks;
+                        vall[t * kvd + 32 * b + e] = (float)(int8_t)vb[2 + e] * vs;
+                    }
+                }
+        } else {
+            uint16_t *kc = m->kcache[L], *vc = m->vcache[L];
+            for (int i = 0; i < kvd; i++) {
+                kc[(size_t)pos * kvd + i] = gqo_f32_to_f16(k[i]);
+                vc[(size_t)pos * kvd + i] = gqo_f32_to_f16(v[i]);
+            }
+            for (size_t i = 0; i < (size_t)n * kvd; i++) {
+                kall[i] = tab[kc[i]];
+                vall[i] = tab[vc[i]];
+            }
         }
         /* attention_into (cpu_path.rs:141-194); heads are independent and
          * are computed on separate threads (same arithmetic per head). */

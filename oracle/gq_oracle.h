@@ -124,6 +124,10 @@ typedef struct {
      * matmul_into dispatches per tensor, model/mod.rs:358-380); NULL: the
      * uniform attn/gate_up/down types above. */
     const int *layer_types;
+    /* KvDtype (model/mod.rs:540-603): 0 = F16 (kcache/vcache rows of kv_dim
+     * f16), 1 = Q8_0 (rows of kv_dim/32 blocks of 34 bytes: f16 scale, 32
+     * int8; kcache/vcache point to those bytes). */
+    int kv_q8;
 } gqo_model;
 
 /* LlamaModel::run (model/llama/cpu_path.rs:695-818) for the Attention

@@ -206,14 +206,16 @@ class _Model(ctypes.Structure):
         [(n, ctypes.c_int) for n in ("attn_type", "gate_up_type", "down_type", "head_type")] + \
         [(n, ctypes.c_void_p) for n in ("embd", "output_norm", "lm_head", "attn_norm",
                                          "ffn_norm", "wq", "wk", "wv", "wo", "wgate", "wup",
-                                         "wdown", "kcache", "vcache", "layer_types")]
+                                         "wdown", "kcache", "vcache", "layer_types")] + \
+        [("kv_q8", ctypes.c_int)]
 
 
 class DecoderModel:
-    """LlamaModel::run restated on the CPU (gqo_decode_step) with its own f16
-    KV cache [layer][ctx][kv_dim]."""
+    """LlamaModel::run restated on the CPU (gqo_decode_step) with its own KV
+    cache: f16 [layer][ctx][kv_dim] (kv_dtype "f16"), or the reference's
+    Q8_0 blocks [layer][ctx][kv_dim/32 * 34] bytes (kv_dtype "q8_0")."""
 
-    def __init__(self, cfg, w, kv_init=None):
+    def __init__(self, cfg, w, kv_init=None, kv_dtype="f16"):
         self.cfg = cfg
         self.keep = []
         m = _Model()
@@ -238,8 +240,12 @@ class DecoderModel:
             setattr(m, k, ptr_array(w[k]))
         L, ctx = cfg["n_layers"], cfg["ctx"]
         kvd = cfg["n_kv_heads"] * cfg["head_dim"]
-        self.kc = np.zeros((L, ctx, kvd), np.uint16)
-        self.vc = np.zeros((L, ctx, kvd), np.uint16)
+        if kv_dtype == "q8_0":
+            m.kv_q8 = 1
+            self.kc = np.zeros((L, ctx, kvd // 32 * 34), np.uint8)
+        else:
+            self.kc = np.zeros((L, ctx, kvd), np.uint16)
+        self.vc = np.zeros_like(self.kc)
         if kv_init is not None:
             kk, vv = kv_init
             self.kc[:, :kk.shape[1]] = kk

@@ -134,6 +134,29 @@ def quantize_q8_32(x):
     return scale.astype(np.float16).view(np.uint16), q.reshape(-1)
 
 
+def pack_q8_0_rows(x):
+    """One KV row as KvDtype::Q8_0 bytes (model/mod.rs:574-583): per 32
+    values an f16 scale (little endian) then 32 int8."""
+    sc, q = quantize_q8_32(np.asarray(x, np.float32))
+    nb = sc.size
+    out = np.empty((nb, 34), np.uint8)
+    out[:, 0] = sc & 0xFF
+    out[:, 1] = sc >> 8
+    out[:, 2:] = q.view(np.uint8).reshape(nb, 32)
+    return out.reshape(-1)
+
+
+def unpack_q8_0_rows(rows):
+    """KvDtype::Q8_0::unpack (model/mod.rs:595-602): rows [n][nb*34] ->
+    float64 [n][nb*32]."""
+    r = np.asarray(rows, np.uint8)
+    n = r.shape[0]
+    b = r.reshape(n, -1, 34)
+    sc = f16((b[:, :, 0].astype(np.uint16) | (b[:, :, 1].astype(np.uint16) << 8))).astype(np.float64)
+    q = b[:, :, 2:].view(np.int8).astype(np.float64)
+    return (q * sc[:, :, None]).reshape(n, -1)
+
+
 def quantize_row_q8_k(x):
     """quantize_row_q8_k (src/quant/q8_k.rs:49-91)."""
     x = np.asarray(x, np.float32)
@@ -162,7 +185,10 @@ def decode_step(cfg, w, kc, vc, token, pos):
     causal softmax attention with grouped KV heads, SwiGLU FFN, residual
     adds), with the weights dequantized by the numpy block decoders above.
     kc / vc: float16 bit arrays [n_layers][ctx][kv_dim], updated at pos
-    with k / v rounded to f16.  Returns the logits (float64)."""
+    with k / v rounded to f16; or (uint8) KvDtype::Q8_0 rows
+    [n_layers][ctx][kv_dim/32 * 34], packed with quantize_q8_32 from the
+    fp32 values and read back as q * f16(scale).  Returns the logits
+    (float64)."""
     H, hd = cfg["hidden"], cfg["head_dim"]
     nh, nkv, F = cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"]
     half, group = hd // 2, nh // nkv
@@ -189,10 +215,16 @@ def decode_step(cfg, w, kc, vc, token, pos):
         v = mat(cfg["attn_type"], w["wv"][L], nkv * hd, H) @ xn
         q = rope(q.reshape(nh, hd))
         k = rope(k.reshape(nkv, hd)).reshape(-1)
-        kc[L, pos] = k.astype(np.float16).view(np.uint16)
-        vc[L, pos] = v.astype(np.float16).view(np.uint16)
-        K = kc[L, :pos + 1].view(np.float16).astype(np.float64).reshape(pos + 1, nkv, hd)
-        V = vc[L, :pos + 1].view(np.float16).astype(np.float64).reshape(pos + 1, nkv, hd)
+        if kc.dtype == np.uint8:
+            kc[L, pos] = pack_q8_0_rows(k)
+            vc[L, pos] = pack_q8_0_rows(v)
+            K = unpack_q8_0_rows(kc[L, :pos + 1]).reshape(pos + 1, nkv, hd)
+            V = unpack_q8_0_rows(vc[L, :pos + 1]).reshape(pos + 1, nkv, hd)
+        else:
+            kc[L, pos] = k.astype(np.float16).view(np.uint16)
+            vc[L, pos] = v.astype(np.float16).view(np.uint16)
+            K = kc[L, :pos + 1].view(np.float16).astype(np.float64).reshape(pos + 1, nkv, hd)
+            V = vc[L, :pos + 1].view(np.float16).astype(np.float64).reshape(pos + 1, nkv, hd)
         att = np.empty((nh, hd))
         for h in range(nh):
             s = K[:, h // group, :] @ q[h] / np.sqrt(hd)

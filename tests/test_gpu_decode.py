@@ -133,3 +133,61 @@ def test_generate_qwen25_7b_shape(backend):
         if scale != 1.0:
             assert len(set(ref)) > 1, "token stream should vary"
         del gm, om
+
+
+def _q8_kv(cfg, n_ctx, seed):
+    """A prefilled context as KvDtype::Q8_0 rows: random values packed with
+    the reference's pack (npref.pack_q8_0_rows)."""
+    import npref
+    L, kvd = cfg["n_layers"], cfg["n_kv_heads"] * cfg["head_dim"]
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(2):
+        rows = np.stack([np.stack([npref.pack_q8_0_rows(rng.standard_normal(kvd).astype(np.float32))
+                                   for _ in range(n_ctx)]) for _ in range(L)])
+        out.append(rows)
+    return out
+
+
+@pytest.mark.parametrize("cfg_name,n_ctx", [("SMALL", 300), ("HD128", 130)])
+def test_decode_q8_0_kv(backend, cfg_name, n_ctx):
+    """The Q8_0 KV cache (KvDtype::Q8_0): teacher-forced steps over a
+    prefilled Q8_0 context against the oracle's decode step with the same
+    cache type; the new rows' codes within one step of the oracle's (the
+    packed k / v differ in their last fp32 bits), the prefilled rows
+    untouched; greedy tokens identical."""
+    import gq
+    import npref
+    cfg = dict(SMALL if cfg_name == "SMALL" else
+               dict(SMALL, hidden=512, n_heads=4, n_kv_heads=1, head_dim=128, ffn=768), kv_dtype="q8_0")
+    w = syn.make_decoder(cfg, 31, embd_scale=1e4)
+    kv = _q8_kv(cfg, n_ctx, 32)
+    hw = syn.upload_decoder(backend, cfg, w)
+    gm = gq.DecodeModel(dict(cfg, max_tokens=256), hw)
+    for l in range(cfg["n_layers"]):
+        gm.kv_upload(l, kv[0][l], kv[1][l])
+    om = oracle.DecoderModel(cfg, w, kv, kv_dtype="q8_0")
+    toks = np.random.default_rng(n_ctx).integers(0, cfg["vocab"], 3)
+    for pos, token in zip(range(n_ctx, n_ctx + 3), toks):
+        ref = om.step(int(token), pos)
+        nxt, got = gm.decode(int(token), pos)
+        err = np.abs(got - ref).max()
+        assert err <= 1e-3 * np.abs(ref).max(), (pos, err)
+        assert nxt == oracle.argmax(ref)
+    for l in range(cfg["n_layers"]):
+        k, v = gm.kv_download(l, n_ctx + 3)
+        np.testing.assert_array_equal(k[:n_ctx], kv[0][l])
+        np.testing.assert_array_equal(v[:n_ctx], kv[1][l])
+        for got_rows, ref_rows in ((k, om.kc[l]), (v, om.vc[l])):
+            a = npref.unpack_q8_0_rows(got_rows[n_ctx:n_ctx + 3])
+            b = npref.unpack_q8_0_rows(ref_rows[n_ctx:n_ctx + 3])
+            step = np.repeat(np.abs(b).reshape(3, -1, 32).max(axis=2) / 127.0, 32, axis=1)
+            assert np.all(np.abs(a - b) <= 1.01 * step + 1e-30)
+    got = gm.generate(int(toks[-1]), n_ctx + 3, 12)
+    exp, tok = [], int(toks[-1])
+    for i in range(12):
+        tok = oracle.argmax(om.step(tok, n_ctx + 3 + i))
+        exp.append(tok)
+    np.testing.assert_array_equal(got, np.array(exp, np.int32))
+    with pytest.raises(gq.GqError, match="F16 KV cache"):
+        gm.prefill(np.zeros(4, np.int32), 0)

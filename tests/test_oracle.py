@@ -376,6 +376,30 @@ def test_decode_step_vs_numpy(orc):
         assert np.allclose(a, b, rtol=2e-3, atol=1e-3)
 
 
+def test_decode_step_q8_0_kv_vs_numpy(orc):
+    """The Q8_0 KV cache (KvDtype::Q8_0, model/mod.rs:540-603) in the
+    oracle's decode step against the float64 restatement packing with
+    npref.quantize_q8_32: same logits to fp32 error, and every stored value
+    within one quantization step (inputs that differ in the last fp32 bits
+    may round to neighbouring int8 codes)."""
+    cfg = TINY_MODEL
+    w = syn.make_decoder(cfg, 25, embd_scale=1e4)
+    om = orc.DecoderModel(cfg, w, kv_dtype="q8_0")
+    kc = np.zeros_like(om.kc)
+    vc = np.zeros_like(om.vc)
+    assert kc.dtype == np.uint8 and kc.shape[2] == cfg["n_kv_heads"] * cfg["head_dim"] // 32 * 34
+    for pos, tok in enumerate((7, 250, 0, 33)):
+        got = om.step(tok, pos)
+        ref = npref.decode_step(cfg, w, kc, vc, tok, pos)
+        assert np.abs(got - ref).max() <= 1e-4 * np.abs(ref).max(), pos
+    for arr_o, arr_r in ((om.kc, kc), (om.vc, vc)):
+        for l in range(cfg["n_layers"]):
+            a = npref.unpack_q8_0_rows(arr_o[l, :4])
+            b = npref.unpack_q8_0_rows(arr_r[l, :4])
+            step = np.repeat(np.abs(b).reshape(4, -1, 32).max(axis=2) / 127.0, 32, axis=1)
+            assert np.all(np.abs(a - b) <= 1.01 * step + 1e-30)
+
+
 def test_decode_step_first_position(orc):
     """At position 0 RoPE is the identity and attention over one position
     returns v itself: the oracle's step equals the numpy step there too."""
