@@ -167,7 +167,8 @@ __global__ __launch_bounds__(256) void k_rope_kv(float *q, float *k, const float
 // Causal attention of queries t = 0 .. n-1 (position pos0 + t, head h)
 // over cache rows 0 .. pos0 + t (attention_into, cpu_path.rs:141-194:
 // scores q.k / sqrt(hd), softmax, weighted sum of V), flash-style: block
-// (64-query tile, head h), 4 waves of 16 queries; 64-key chunks of K and
+// (64-query tile, head h), 4 waves of 16 queries; the softmax runs in base
+// 2 (scores scaled by log2 e, exp2); 64-key chunks of K and
 // V^T staged in LDS (the next chunk's rows prefetched into registers).
 // Scores and the V sum run on v_mfma_f32_16x16x32_f16: K and V are f16
 // already; q (scaled by a power of two) and the probabilities are split
@@ -189,8 +190,15 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
   __shared__ __align__(16) uint16_t Pl[4][16 * VP];
   __shared__ float red[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = blockIdx.y, qt0 = blockIdx.x * PF_Q;
-  const int kvd = nh / group * HD, kh = h / group;
+  // Block b -> (query tile, query head): the group's heads of one (tile,
+  // KV head) item G sit 8 blocks apart, i.e. on one XCD (consecutive blocks
+  // go to consecutive XCDs), so they share the K/V chunks in one L2.
+  const int nkv = nh / group, nqt = (n + PF_Q - 1) / PF_Q;
+  const int bx = blockIdx.x % 8, bk = blockIdx.x / 8;
+  const int G = 8 * (bk / group) + bx, gi = bk % group;
+  if (G >= nqt * nkv) return;
+  const int kh = G % nkv, qt0 = (G / nkv) * PF_Q, h = kh * group + gi;
+  const int kvd = nkv * HD;
   const uint16_t *kbase = kc + (long)kh * HD, *vbase = vc + (long)kh * HD;
 
   // q A-fragments: lane row = query qt0 + 16 wave + lane % 16, dims
@@ -215,8 +223,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
   int ex = 0;
   (void)frexpf(qm, &ex);
   const float qscale = qm > 0.f ? ldexpf(1.0f, 10 - ex) : 1.0f;
-  const float inv_scale = 1.0f / qscale;  // a power of two: exact
-  const float rsq = sqrtf((float)HD);
+  // scores in base-2 units: s2 = (q.k / sqrt(hd)) * log2(e), so that
+  // exp(s - m) = exp2(s2 - m2)
+  const float s2scale = (1.0f / qscale) / sqrtf((float)HD) * 1.4426950408889634f;
   pf16x8_t qhi[KS], qlo[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ks++)
@@ -286,7 +295,7 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
       const int key = 64 * c + 16 * ct + (lane & 15);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float sc = acc[i] * inv_scale / rsq;
+        const float sc = acc[i] * s2scale;
         // rows past n stay finite (discarded); past the causal limit: -inf
         s[ct][i] = qrow[i] >= n ? 0.f : key > pos0 + qrow[i] ? -INFINITY : sc;
       }
@@ -298,11 +307,11 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
 #pragma unroll
       for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
       const float mnew = fmaxf(mrow[i], mx);
-      const float alpha = expf(mrow[i] - mnew);  // row 0 holds key 0: mnew is finite
+      const float alpha = exp2f(mrow[i] - mnew);  // row 0 holds key 0: mnew is finite
       float ps = 0.f;
 #pragma unroll
       for (int ct = 0; ct < 4; ct++) {
-        const float p = expf(s[ct][i] - mnew);
+        const float p = exp2f(s[ct][i] - mnew);
         s[ct][i] = p;
         ps += p;
       }
@@ -408,7 +417,8 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
     uint16_t *kc = m.kcache + (long)L * m.ctx * kvd, *vc = m.vcache + (long)L * m.ctx * kvd;
     hipLaunchKernelGGL(k_rope_kv, dim3(n), dim3(256), 0, s, b.q, b.k, b.v, kc, vc, pos0, nh, nkv, hd,
                        m.rope_den);
-    const dim3 ag((n + PF_Q - 1) / PF_Q, nh);
+    const int items = (n + PF_Q - 1) / PF_Q * nkv;  // (query tile, KV head)
+    const dim3 ag(8 * group * ((items + 7) / 8));
     if (hd == 128)
       hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
     else
