@@ -4,13 +4,13 @@
 // restating the arithmetic of LlamaModel::run, src/model/llama/
 // cpu_path.rs:695-818).
 //
-// One step is 5 launches per layer plus 2:
+// One step is 6 launches per layer plus 2:
 //   qkv matvec   input RMSNorm(x + proj) (residual add fused; block 0 stores
 //                the new residual stream; layer 0 reads the embedding row)
 //   attention    RoPE of q and of the new k, f16 KV row store, scores,
 //                softmax and the weighted V sum for all query heads of one
-//                KV head over a chunk of positions; the last chunk block of
-//                a KV head combines the chunks
+//                KV head over a chunk of positions
+//   merge        the chunk partials of each query head combined
 //   o matvec
 //   gate/up      one matvec over both matrices with input RMSNorm(x + o)
 //                and output silu(gate) * up
@@ -19,9 +19,9 @@
 //
 // Step state (token, position, step counter) lives in device memory so that
 // a captured HIP graph of one step can be replayed for every greedy step:
-// the argmax writes the next token and advances the position.  The chunk
-// counters used by the last-block merges return to zero at the end of
-// every launch, so a replay starts from the same state.
+// the argmax writes the next token and advances the position.  The argmax
+// block counter returns to zero at the end of every launch, so a replay
+// starts from the same state.
 #include "gq_device.h"
 #include "gq_internal.h"
 
@@ -31,9 +31,8 @@ namespace gq {
 // ----------------------------------------------------------- attention
 // Block (kv head kh, chunk c): positions [c*CH, min((c+1)*CH, n)) for the
 // `group` query heads kh*group .. kh*group+group-1 (GQA: each K/V row is
-// read once for all of them), ATT_WAVES waves of 16 positions each; short
-// chunks so that the whole GPU shares the work (a 4096-position context is
-// 4 x 65 blocks).
+// read once for all of them), ATT_WAVES waves; short chunks so that the
+// whole GPU shares the work (a 4096-position context is 4 x 65 blocks).
 //   scores  s[g][t] = (q_g . k_t) / sqrt(hd)        (attention_into,
 //   softmax m_g = max s, p = exp(s - m_g), l_g = sum p   cpu_path.rs:141-194)
 //   values  o[g][d] = sum_t p[g][t] v_t[d]
@@ -41,8 +40,12 @@ namespace gq {
 // positions, depth = head dims): K rows are f16 already and go straight
 // from HBM into the B operands; q is scaled by a power of two and split
 // into f16 hi + lo parts, so each product is exact in fp32 and q is carried
-// to ~22 bits.  The V sum runs on fp32 FMAs, a lane owning HD/64 dims of
-// every row of its wave (no cross-lane reduction), then across waves.
+// to ~22 bits.  The V sum runs on fp32 FMAs: wave w owns a quarter of the
+// dims, a lane 2 dims of a group of consecutive positions, and the groups'
+// sums are added in order across lanes.  Everything that does not depend on
+// the position (q, the new k and v, the RoPE denominators) is loaded before
+// the position is read, and each thread computes the one RoPE angle it
+// needs, so the block has three barriers.
 // The partial (m, l, o) of each (head, chunk) goes to `part`; the next
 // kernel (k_attn_merge) merges the chunks:
 //   att[h] = sum_c o_c e^(m_c - M) / sum_c l_c e^(m_c - M).
@@ -73,14 +76,18 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     uint16_t *vsc, const DecodeState *st, int group, int kvd, const float *rope_den, float *part) {
   constexpr int CH = ATT_CHUNK;
   constexpr int NW = ATT_WAVES;
-  constexpr int PW = CH / NW;  // positions per wave: one 16-column MFMA tile
+  constexpr int PW = CH / NW;  // positions per wave in the scores: one 16-column MFMA tile
   constexpr int KS = HD / 32;  // MFMA depth steps
-  constexpr int DPL = HD / 64; // value dims per lane
   constexpr int HALF = HD / 2;
+  // V sum: wave w owns dims [w*HD/NW, (w+1)*HD/NW), 2 per lane; the lanes
+  // of a wave form RG row groups of RPG consecutive positions each.
+  constexpr int LPR = HD / (2 * NW);  // lanes per row group
+  constexpr int RG = 64 / LPR;
+  constexpr int RPG = CH / RG;
+  constexpr int QIT = ATT_MAXG * HD / ATT_THREADS;  // q values per thread
+  static_assert(ATT_THREADS % HD == 0 && RPG % 4 == 0, "attention layout");
   __shared__ float sp[ATT_MAXG][CH];
-  __shared__ __align__(16) float ored[NW][ATT_MAXG][HD];
   __shared__ __align__(16) float qsh[ATT_MAXG][HD];
-  __shared__ float rs[HALF], rc[HALF];
   __shared__ __align__(16) uint16_t knew[HD];  // f16 bits (Q8: the code as f16)
   __shared__ __align__(16) uint16_t vnew[HD];
   __shared__ float knew_sc[HD / 32], vnew_sc[HD / 32];  // Q8: the new row's scales
@@ -89,13 +96,30 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
 
   const int kh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
+  // The loads that do not depend on the position go out first: this
+  // thread's q values (dim d of heads g = (tid + it*ATT_THREADS) / HD, and
+  // the NEOX partner dim), the new k / v values and the RoPE denominator.
+  const int d = tid % HD, ir = d % HALF, dp = (d + HALF) % HD;
+  const float den = rope_den[ir];
+  float qown[QIT], qpar[QIT];
+#pragma unroll
+  for (int it = 0; it < QIT; it++) {
+    const int g = (tid + it * ATT_THREADS) / HD;
+    const float *qh = q + (long)(kh * group + min(g, group - 1)) * HD;
+    qown[it] = qh[d];
+    qpar[it] = qh[dp];
+  }
+  const float kown = k[(long)kh * HD + d], kpar = k[(long)kh * HD + dp];
+  const float vv = v[(long)kh * HD + d];
+
   const int pos = st->pos, n = pos + 1, t0 = c * CH;
   if (t0 >= n) return;
   const int nchunk_grid = gridDim.y;
-  const int tw = t0 + wave * PW;  // first position of this wave
+  const int tw = t0 + wave * PW;  // first scores position of this wave
 
-  // K rows as MFMA B operands (row tw + lane%16, dims 8*(lane/16) + 32*ks),
-  // V dims DPL*lane of the wave's rows; clamped to n - 1 (unused past n).
+  // K rows as MFMA B operands (row tw + lane%16, dims 8*(lane/16) + 32*ks);
+  // V: dims 2*(lane%LPR) of the wave's dim slice, rows RPG*(lane/LPR) + j.
+  // Rows are clamped to n - 1 (unused past n).
   const int8_t *kq8 = (const int8_t *)kc, *vq8 = (const int8_t *)vc;
   const int nbr = kvd / 32;  // Q8 blocks per row
   uint4 kb[KS];
@@ -113,37 +137,28 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
       }
     }
   }
-  uint32_t vr[PW];
-  float vscl[PW];
+  const int vdim = wave * (HD / NW) + 2 * (lane % LPR);  // first of this lane's 2 dims
+  const int vrow = t0 + RPG * (lane / LPR);              // first of its RPG rows
+  uint32_t vr[RPG];
+  float vscl[RPG];
 #pragma unroll
-  for (int j = 0; j < PW; j++) {
-    const long row = min(tw + j, n - 1);
+  for (int j = 0; j < RPG; j++) {
+    const long row = min(vrow + j, n - 1);
     if constexpr (Q8) {
-      const int8_t *p = vq8 + row * kvd + (long)kh * HD + DPL * lane;
-      vr[j] = DPL == 2 ? (uint32_t)ldh((const uint16_t *)p) : (uint32_t)(uint8_t)*p;
-      vscl[j] = h2f(ldh(vsc + row * nbr + (kh * HD + DPL * lane) / 32));
+      vr[j] = ldh((const uint16_t *)(vq8 + row * kvd + (long)kh * HD + vdim));
+      vscl[j] = h2f(ldh(vsc + row * nbr + (kh * HD + vdim) / 32));
     } else {
-      const uint16_t *p = vc + row * kvd + (long)kh * HD + DPL * lane;
-      vr[j] = DPL == 2 ? ldw1(p) : (uint32_t)ldh(p);
+      vr[j] = ldw1(vc + row * kvd + (long)kh * HD + vdim);
       vscl[j] = 1.f;
     }
   }
 
-  // RoPE table for pair index i (NEOX pairs d <-> d + hd/2).
-  if (tid < HALF) {
-    float sn, cs;
-    sincosf((float)pos / rope_den[tid], &sn, &cs);
-    rs[tid] = sn;
-    rc[tid] = cs;
-  }
-  __syncthreads();
+  // RoPE angle of pair index ir (NEOX pairs d <-> d + hd/2): pos / den.
+  float sn, cs;
+  sincosf((float)pos / den, &sn, &cs);
   // New K/V row of this KV head: rotate k, round both to f16, store.
   if (pos < t0 + CH && tid < HD) {
-    const int d = tid, i = d % HALF;
-    const float *pk = k + (long)kh * HD;
-    const float own = pk[d], par = pk[(d + HALF) % HD];
-    const float rot = d < HALF ? own * rc[i] - par * rs[i] : par * rs[i] + own * rc[i];
-    const float vv = v[(long)kh * HD + d];
+    const float rot = d < HALF ? kown * cs - kpar * sn : kpar * sn + kown * cs;
     if constexpr (Q8) {
       // 32-lane groups are the 32-value blocks (HD is a multiple of 64)
       float km = fabsf(rot), vm = fabsf(vv);
@@ -178,13 +193,14 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   }
   // Rotated q of the group's heads, and its max |q|.
   float qm = 0.f;
-  for (int o = tid; o < group * HD; o += ATT_THREADS) {
-    const int g = o / HD, d = o % HD, i = d % HALF;
-    const float *qh = q + (long)(kh * group + g) * HD;
-    const float own = qh[d], par = qh[(d + HALF) % HD];
-    const float rot = d < HALF ? own * rc[i] - par * rs[i] : par * rs[i] + own * rc[i];
-    qsh[g][d] = rot;
-    qm = fmaxf(qm, fabsf(rot));
+#pragma unroll
+  for (int it = 0; it < QIT; it++) {
+    const int g = (tid + it * ATT_THREADS) / HD;
+    if (g < group) {
+      const float rot = d < HALF ? qown[it] * cs - qpar[it] * sn : qpar[it] * sn + qown[it] * cs;
+      qsh[g][d] = rot;
+      qm = fmaxf(qm, fabsf(rot));
+    }
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) qm = fmaxf(qm, __shfl_xor(qm, off, 64));
@@ -268,76 +284,83 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   }
   __syncthreads();
 
-  // Softmax statistics of the chunk: wave w handles heads w, w + NW, ...;
+  // Softmax statistics of the chunk: wave w handles heads w and w + NW;
   // lane = position.
-  for (int g = wave; g < group; g += NW) {
-    const float val = sp[g][lane];
-    const float mh = wave_max(val);
-    const float p = expf(val - mh);  // exp(-inf) = 0 past n
-    sp[g][lane] = p;
-    const float lh = wave_sum(p);
-    if (lane == 0) {
-      gm_s[g] = mh;
-      gl_s[g] = lh;
+  {
+    constexpr int GPW = ATT_MAXG / NW;
+    float val[GPW], mh[GPW], p[GPW], lh[GPW];
+#pragma unroll
+    for (int i = 0; i < GPW; i++) val[i] = wave + NW * i < group ? sp[wave + NW * i][lane] : 0.f;
+#pragma unroll
+    for (int i = 0; i < GPW; i++) mh[i] = wave_max(val[i]);
+#pragma unroll
+    for (int i = 0; i < GPW; i++) p[i] = expf(val[i] - mh[i]);  // exp(-inf) = 0 past n
+#pragma unroll
+    for (int i = 0; i < GPW; i++) lh[i] = wave_sum(p[i]);
+#pragma unroll
+    for (int i = 0; i < GPW; i++) {
+      const int g = wave + NW * i;
+      if (g < group) {
+        sp[g][lane] = p[i];
+        if (lane == 0) {
+          gm_s[g] = mh[i];
+          gl_s[g] = lh[i];
+        }
+      }
     }
   }
   __syncthreads();
 
-  // Values: lane owns dims DPL*lane .. +DPL of the wave's PW rows.
+  // Values: o[g][d] = sum over the row groups (in order) of the sums over
+  // their rows (in order) of p * v, for this lane's 2 dims.
   {
-    const uint32_t vn = DPL == 2 ? *(const uint32_t *)(vnew + DPL * lane) : (uint32_t)vnew[lane];
-    float vf[PW][DPL];
+    const uint32_t vn = *(const uint32_t *)(vnew + vdim);
+    float vf[RPG][2];
 #pragma unroll
-    for (int j = 0; j < PW; j++) {
+    for (int j = 0; j < RPG; j++) {
       // Rows past pos were clamped to row pos, which this launch is still
       // writing: their p is 0, but 0 * (stale NaN/inf) is not, so they
       // read as 0; row pos itself is the freshly rounded one.
+      const int t = vrow + j;
       if constexpr (Q8) {
         // the new row's values were stored as the f16 of its codes
 #pragma unroll
-        for (int e = 0; e < DPL; e++) {
-          const float code = tw + j == pos ? h2f(vn >> (16 * e))
-                                           : (float)(int8_t)((vr[j] >> (8 * e)) & 0xffu);
-          const float sc = tw + j == pos ? vnew_sc[(DPL * lane) / 32] : vscl[j];
-          vf[j][e] = tw + j > pos ? 0.f : code * sc;
+        for (int e = 0; e < 2; e++) {
+          const float code = t == pos ? h2f(vn >> (16 * e))
+                                      : (float)(int8_t)((vr[j] >> (8 * e)) & 0xffu);
+          const float sc = t == pos ? vnew_sc[vdim / 32] : vscl[j];
+          vf[j][e] = t > pos ? 0.f : code * sc;
         }
       } else {
-        const uint32_t raw = tw + j == pos ? vn : (tw + j > pos ? 0u : vr[j]);
+        const uint32_t raw = t == pos ? vn : (t > pos ? 0u : vr[j]);
 #pragma unroll
-        for (int e = 0; e < DPL; e++) vf[j][e] = h2f(raw >> (16 * e));
+        for (int e = 0; e < 2; e++) vf[j][e] = h2f(raw >> (16 * e));
       }
     }
+    const int rbase = vrow - t0, rlane = lane % LPR;
+    float *pout = part + ((long)(kh * group) * nchunk_grid + c) * (2 + HD) + 2 + vdim;
 #pragma unroll
     for (int g = 0; g < ATT_MAXG; g++) {
       if (g < group) {
-        float pr[PW];
+        float acc[2] = {0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < PW; j += 4) {
-          const float4 p4 = *(const float4 *)&sp[g][wave * PW + j];
-          pr[j] = p4.x;
-          pr[j + 1] = p4.y;
-          pr[j + 2] = p4.z;
-          pr[j + 3] = p4.w;
+        for (int j = 0; j < RPG; j += 4) {
+          const float4 p4 = *(const float4 *)&sp[g][rbase + j];
+          const float pr[4] = {p4.x, p4.y, p4.z, p4.w};
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++)
+#pragma unroll
+            for (int e = 0; e < 2; e++) acc[e] += pr[jj] * vf[j + jj][e];
         }
-        float acc[DPL];
+        float o[2] = {acc[0], acc[1]};
 #pragma unroll
-        for (int e = 0; e < DPL; e++) acc[e] = 0.f;
+        for (int r = 1; r < RG; r++)
 #pragma unroll
-        for (int j = 0; j < PW; j++)
-#pragma unroll
-          for (int e = 0; e < DPL; e++) acc[e] += pr[j] * vf[j][e];
-#pragma unroll
-        for (int e = 0; e < DPL; e++) ored[wave][g][DPL * lane + e] = acc[e];
+          for (int e = 0; e < 2; e++) o[e] += __shfl(acc[e], rlane + r * LPR, 64);
+        if (lane < LPR)
+          *(float2 *)(pout + (long)g * nchunk_grid * (2 + HD)) = make_float2(o[0], o[1]);
       }
     }
-  }
-  __syncthreads();
-  for (int o = tid; o < group * HD; o += ATT_THREADS) {
-    const int g = o / HD, d = o % HD;
-    float s = 0.f;
-#pragma unroll
-    for (int w = 0; w < NW; w++) s += ored[w][g][d];
-    part[((long)(kh * group + g) * nchunk_grid + c) * (2 + HD) + 2 + d] = s;
   }
   if (tid < group) {
     float *pm = part + ((long)(kh * group + tid) * nchunk_grid + c) * (2 + HD);
@@ -361,7 +384,8 @@ __global__ __launch_bounds__(ATT_MQ * HD) void k_attn_merge(const DecodeState *s
   __shared__ float red[NWV];
   __shared__ float osum[ATT_MQ][HD];
   const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nch = (st->pos + ATT_CHUNK) / ATT_CHUNK;
+  // The first loads go out before the position is known: chunks of the
+  // grid past the last one in use are read and then ignored.
   const float *ph = part + (long)h * nchunk_grid * (2 + HD);
   const int qq = tid / HD, d = tid % HD;
   const float *po = ph + 2 + d;
@@ -369,13 +393,15 @@ __global__ __launch_bounds__(ATT_MQ * HD) void k_attn_merge(const DecodeState *s
 #pragma unroll
   for (int j = 0; j < R; j++) {
     const int c = qq + ATT_MQ * j;
-    vals[j] = c < nch ? po[(long)c * (2 + HD)] : 0.f;
+    vals[j] = c < nchunk_grid ? po[(long)c * (2 + HD)] : 0.f;
   }
-  float mv = -INFINITY, lv = 0.f;
-  if (tid < nch) {
-    mv = ph[(long)tid * (2 + HD)];
-    lv = ph[(long)tid * (2 + HD) + 1];
+  float mraw = -INFINITY, lraw = 0.f;
+  if (tid < nchunk_grid) {
+    mraw = ph[(long)tid * (2 + HD)];
+    lraw = ph[(long)tid * (2 + HD) + 1];
   }
+  const int nch = (st->pos + ATT_CHUNK) / ATT_CHUNK;
+  const float mv = tid < nch ? mraw : -INFINITY, lv = tid < nch ? lraw : 0.f;
   float M = mv;
   for (int c = tid + NT; c < nch; c += NT) M = fmaxf(M, ph[(long)c * (2 + HD)]);
   M = wave_max(M);
