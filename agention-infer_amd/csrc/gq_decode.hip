@@ -42,7 +42,7 @@ namespace gq {
 // into f16 hi + lo parts, so each product is exact in fp32 and q is carried
 // to ~22 bits.  The V sum runs on fp32 FMAs: wave w owns a quarter of the
 // dims, a lane 2 dims of a group of consecutive positions, and the groups'
-// sums are added in order across lanes.  Everything that does not depend on
+// sums are added across lanes with lane swaps.  Everything that does not depend on
 // the position (q, the new k and v, the RoPE denominators) is loaded before
 // the position is read, and each thread computes the one RoPE angle it
 // needs, so the block has three barriers.
@@ -70,6 +70,21 @@ typedef float f32x4a_t __attribute__((ext_vector_type(4)));
 // block scale; V values are code * scale.  The new row is packed like
 // KvDtype::Q8_0::pack (scale = max|x| / 127 stored as f16, codes =
 // round(x / scale) in [-127, 127]) and used as stored for its position.
+// Sum of x over the row groups of LPR lanes (LPR = 8 or 16) of a wave, in
+// every lane: pairs of 8-lane halves by a row rotation, then 16-lane rows
+// and 32-lane halves by the gfx950 lane swaps (each sum is the same in
+// both lanes of a pair, so every lane gets the identical total).
+template <int LPR>
+__device__ __forceinline__ float row_groups_sum(float x) {
+  static_assert(LPR == 8 || LPR == 16, "row groups of 8 or 16 lanes");
+  if constexpr (LPR == 8)
+    x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+}
+
 template <int HD, bool Q8>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     const float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc, uint16_t *ksc,
@@ -311,8 +326,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   }
   __syncthreads();
 
-  // Values: o[g][d] = sum over the row groups (in order) of the sums over
-  // their rows (in order) of p * v, for this lane's 2 dims.
+  // Values: o[g][d] = sum over the row groups of the sums over their rows
+  // (in order) of p * v, for this lane's 2 dims.
   {
     const uint32_t vn = *(const uint32_t *)(vnew + vdim);
     float vf[RPG][2];
@@ -337,7 +352,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
         for (int e = 0; e < 2; e++) vf[j][e] = h2f(raw >> (16 * e));
       }
     }
-    const int rbase = vrow - t0, rlane = lane % LPR;
+    const int rbase = vrow - t0;
     float *pout = part + ((long)(kh * group) * nchunk_grid + c) * (2 + HD) + 2 + vdim;
 #pragma unroll
     for (int g = 0; g < ATT_MAXG; g++) {
@@ -350,13 +365,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
 #pragma unroll
           for (int jj = 0; jj < 4; jj++)
 #pragma unroll
-            for (int e = 0; e < 2; e++) acc[e] += pr[jj] * vf[j + jj][e];
+            for (int e = 0; e < 2; e++) acc[e] = fmaf(pr[jj], vf[j + jj][e], acc[e]);
         }
-        float o[2] = {acc[0], acc[1]};
+        float o[2];
 #pragma unroll
-        for (int r = 1; r < RG; r++)
-#pragma unroll
-          for (int e = 0; e < 2; e++) o[e] += __shfl(acc[e], rlane + r * LPR, 64);
+        for (int e = 0; e < 2; e++) o[e] = row_groups_sum<LPR>(acc[e]);
         if (lane < LPR)
           *(float2 *)(pout + (long)g * nchunk_grid * (2 + HD)) = make_float2(o[0], o[1]);
       }
