@@ -38,9 +38,9 @@ namespace gq {
 //   values  o[g][d] = sum_t p[g][t] v_t[d]
 // Scores run on v_mfma_f32_16x16x32_f16 (rows = query heads, columns =
 // positions, depth = head dims): K rows are f16 already and go straight
-// from HBM into the B operands; q is scaled by a power of two and split
-// into f16 hi + lo parts, so each product is exact in fp32 and q is carried
-// to ~22 bits.  The V sum runs on fp32 FMAs: wave w owns a quarter of the
+// from HBM into the B operands; each 32-dim chunk of q is scaled by a power
+// of two and split into f16 hi + lo parts, so each product is exact in fp32
+// and q is carried to ~22 bits.  The V sum runs on fp32 FMAs: wave w owns a quarter of the
 // dims, a lane 2 dims of a group of consecutive positions, and the groups'
 // sums are added across lanes with lane swaps.  Everything that does not depend on
 // the position (q, the new k and v, the RoPE denominators) is loaded before
@@ -85,6 +85,18 @@ __device__ __forceinline__ float row_groups_sum(float x) {
   return __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
 }
 
+// Max of x over each 32-lane half of a wave, in every lane: row rotations
+// by 8, 4, 2, 1 within the 16-lane rows, then the rows of a pair by the
+// gfx950 lane swap.
+__device__ __forceinline__ float max32(float x) {
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xF, 0xF, false)));
+  x = fmaxf(x, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xF, 0xF, false)));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <int HD, bool Q8>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
     const float *q, const float *k, const float *v, uint16_t *kc, uint16_t *vc, uint16_t *ksc,
@@ -102,11 +114,11 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   constexpr int QIT = ATT_MAXG * HD / ATT_THREADS;  // q values per thread
   static_assert(ATT_THREADS % HD == 0 && RPG % 4 == 0, "attention layout");
   __shared__ float sp[ATT_MAXG][CH];
-  __shared__ __align__(16) float qsh[ATT_MAXG][HD];
+  __shared__ __align__(16) _Float16 qhi[ATT_MAXG][HD], qlo[ATT_MAXG][HD];
+  __shared__ __align__(16) float qinv[KS][16];  // 2^-e of each (32-dim chunk, head); 16 MFMA rows
   __shared__ __align__(16) uint16_t knew[HD];  // f16 bits (Q8: the code as f16)
   __shared__ __align__(16) uint16_t vnew[HD];
   __shared__ float knew_sc[HD / 32], vnew_sc[HD / 32];  // Q8: the new row's scales
-  __shared__ float qmax_s[NW];
   __shared__ float gm_s[ATT_MAXG], gl_s[ATT_MAXG];
 
   const int kh = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
@@ -206,59 +218,48 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
       vc[(long)pos * kvd + (long)kh * HD + d] = vbits;
     }
   }
-  // Rotated q of the group's heads, and its max |q|.
-  float qm = 0.f;
+  // Rotated q of the group's heads as MFMA A operands: each 32-dim chunk
+  // of a head is scaled by 2^e (its max |q| in [512, 1024); the chunk is 32
+  // consecutive lanes) and split into f16 hi + lo, so q is carried to ~22
+  // bits and each product with an f16 key is exact in fp32.
 #pragma unroll
   for (int it = 0; it < QIT; it++) {
-    const int g = (tid + it * ATT_THREADS) / HD;
+    const int g = (tid + it * ATT_THREADS) / HD;  // uniform per wave
     if (g < group) {
       const float rot = d < HALF ? qown[it] * cs - qpar[it] * sn : qpar[it] * sn + qown[it] * cs;
-      qsh[g][d] = rot;
-      qm = fmaxf(qm, fabsf(rot));
+      const float m32 = max32(fabsf(rot));
+      int ex = 0;
+      (void)frexpf(m32, &ex);
+      const float qscale = m32 > 0.f ? ldexpf(1.0f, 10 - ex) : 1.0f;
+      const float x = rot * qscale;  // exact (a power of two)
+      const _Float16 h = (_Float16)x;
+      qhi[g][d] = h;
+      qlo[g][d] = (_Float16)(x - (float)h);
+      if ((d & 31) == 0) qinv[d / 32][g] = 1.0f / qscale;  // exact
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) qm = fmaxf(qm, __shfl_xor(qm, off, 64));
-  if (lane == 0) qmax_s[wave] = qm;
   __syncthreads();
-  qm = qmax_s[0];
-#pragma unroll
-  for (int w = 1; w < NW; w++) qm = fmaxf(qm, qmax_s[w]);
 
-  // A operands: q * 2^e (max in [512, 1024)) as f16 hi + lo; lane holds
-  // head lane%16, dims 8*(lane/16) + 32*ks .. +8.
-  int ex = 0;
-  (void)frexpf(qm, &ex);
-  const float qscale = qm > 0.f ? ldexpf(1.0f, 10 - ex) : 1.0f;
+  // A operands: lane holds head lane%16, dims 8*(lane/16) + 32*ks .. +8.
   f16x8_t ahi[KS], alo[KS];
   {
     const int m = lane & 15;
 #pragma unroll
     for (int ks = 0; ks < KS; ks++) {
-      float x8[8];
       if (m < group) {
-        const float4 a = *(const float4 *)&qsh[m][8 * (lane >> 4) + 32 * ks];
-        const float4 b = *(const float4 *)&qsh[m][8 * (lane >> 4) + 32 * ks + 4];
-        x8[0] = a.x; x8[1] = a.y; x8[2] = a.z; x8[3] = a.w;
-        x8[4] = b.x; x8[5] = b.y; x8[6] = b.z; x8[7] = b.w;
+        ahi[ks] = *(const f16x8_t *)&qhi[m][8 * (lane >> 4) + 32 * ks];
+        alo[ks] = *(const f16x8_t *)&qlo[m][8 * (lane >> 4) + 32 * ks];
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; j++) x8[j] = 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; j++) {
-        const float x = x8[j] * qscale;
-        const _Float16 h = (_Float16)x;
-        ahi[ks][j] = h;
-        alo[ks][j] = (_Float16)(x - (float)h);
+        for (int j = 0; j < 8; j++) ahi[ks][j] = alo[ks][j] = (_Float16)0.f;
       }
     }
   }
 
-  // Scores: lane holds S[head 4*(lane/16) + i][position tw + lane%16].
+  // Scores: lane holds S[head 4*(lane/16) + i][position tw + lane%16]; each
+  // chunk's product is rescaled by its heads' 2^-e (exactly).
   {
     const float rsq = sqrtf((float)HD);
-    const float inv_scale = 1.0f / qscale;  // a power of two: exact
     const int tcol = tw + (lane & 15);
     const bool isnew = tcol == pos;
     f32x4a_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -277,24 +278,31 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
         raw = make_uint4(isnew ? kn.x : raw.x, isnew ? kn.y : raw.y, isnew ? kn.z : raw.z,
                          isnew ? kn.w : raw.w);
         __builtin_memcpy(&bk, &raw, 16);
+        const float sc = isnew ? knew_sc[ks] : kscl[ks];
         f32x4a_t part_acc = {0.f, 0.f, 0.f, 0.f};
         part_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, part_acc, 0, 0, 0);
         part_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, part_acc, 0, 0, 0);
-        const float sc = isnew ? knew_sc[ks] : kscl[ks];
+        const float4 iv = *(const float4 *)&qinv[ks][4 * (lane >> 4)];
+        const float ivs[4] = {iv.x, iv.y, iv.z, iv.w};
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[i] = fmaf(sc, part_acc[i], acc[i]);
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(sc * ivs[i], part_acc[i], acc[i]);
       } else {
         const uint4 raw = make_uint4(isnew ? kn.x : kb[ks].x, isnew ? kn.y : kb[ks].y,
                                      isnew ? kn.z : kb[ks].z, isnew ? kn.w : kb[ks].w);
         __builtin_memcpy(&bk, &raw, 16);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, acc, 0, 0, 0);
+        f32x4a_t part_acc = {0.f, 0.f, 0.f, 0.f};
+        part_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ahi[ks], bk, part_acc, 0, 0, 0);
+        part_acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(alo[ks], bk, part_acc, 0, 0, 0);
+        const float4 iv = *(const float4 *)&qinv[ks][4 * (lane >> 4)];
+        const float ivs[4] = {iv.x, iv.y, iv.z, iv.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = fmaf(ivs[i], part_acc[i], acc[i]);
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int g = 4 * (lane >> 4) + i;
-      if (g < group) sp[g][tcol - t0] = tcol < n ? acc[i] * inv_scale / rsq : -INFINITY;
+      if (g < group) sp[g][tcol - t0] = tcol < n ? acc[i] / rsq : -INFINITY;
     }
   }
   __syncthreads();
@@ -382,20 +390,21 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   }
 }
 
-// Merge of the chunk partials: block h (query head) of ATT_MQ * HD threads,
-// thread (qq, d) sums dim d over the chunks c = qq, qq + ATT_MQ, ..., then
-// the quarters are added in order:
+// Merge of the chunk partials: block h (query head) of 1024 threads, thread
+// (qq, d) (qq < MQ = 1024 / HD) sums dim d over the chunks c = qq, qq + MQ,
+// ..., then the MQ partial sums are added in order:
 //   att[h][d] = sum_c o_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M),
 // M = max_c m_c over the chunks holding positions <= pos.  Every load of
-// the first 16 * ATT_MQ chunks (m, l and o) is issued at the start.
-constexpr int ATT_MQ = 4;
+// the first 16 * MQ chunks (m, l and o: 8192 positions) is issued at the
+// start.
+constexpr int ATT_MERGE_THREADS = 1024;
 template <int HD>
-__global__ __launch_bounds__(ATT_MQ * HD) void k_attn_merge(const DecodeState *st, int nchunk_grid,
+__global__ __launch_bounds__(ATT_MERGE_THREADS) void k_attn_merge(const DecodeState *st, int nchunk_grid,
                                                              const float *part, float *att) {
-  constexpr int NT = ATT_MQ * HD, NWV = NT / 64, R = 16;
+  constexpr int NT = ATT_MERGE_THREADS, MQ = NT / HD, NWV = NT / 64, R = 16;
   __shared__ float fac[ATT_MAX_CTX / ATT_CHUNK];
   __shared__ float red[NWV];
-  __shared__ float osum[ATT_MQ][HD];
+  __shared__ float osum[MQ][HD];
   const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // The first loads go out before the position is known: chunks of the
   // grid past the last one in use are read and then ignored.
@@ -405,7 +414,7 @@ __global__ __launch_bounds__(ATT_MQ * HD) void k_attn_merge(const DecodeState *s
   float vals[R];
 #pragma unroll
   for (int j = 0; j < R; j++) {
-    const int c = qq + ATT_MQ * j;
+    const int c = qq + MQ * j;
     vals[j] = c < nchunk_grid ? po[(long)c * (2 + HD)] : 0.f;
   }
   float mraw = -INFINITY, lraw = 0.f;
@@ -444,18 +453,18 @@ __global__ __launch_bounds__(ATT_MQ * HD) void k_attn_merge(const DecodeState *s
   float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int j = 0; j < R; j++) {
-    const int c = qq + ATT_MQ * j;
+    const int c = qq + MQ * j;
     s4[j & 3] += c < nch ? vals[j] * fac[c] : 0.f;
   }
-  for (int cb = qq + ATT_MQ * R; cb < nch; cb += ATT_MQ * R) {
+  for (int cb = qq + MQ * R; cb < nch; cb += MQ * R) {
 #pragma unroll
     for (int j = 0; j < R; j++) {
-      const int c = cb + ATT_MQ * j;
+      const int c = cb + MQ * j;
       vals[j] = c < nch ? po[(long)c * (2 + HD)] : 0.f;
     }
 #pragma unroll
     for (int j = 0; j < R; j++) {
-      const int c = cb + ATT_MQ * j;
+      const int c = cb + MQ * j;
       s4[j & 3] += c < nch ? vals[j] * fac[c] : 0.f;
     }
   }
@@ -464,7 +473,7 @@ __global__ __launch_bounds__(ATT_MQ * HD) void k_attn_merge(const DecodeState *s
   if (qq == 0) {
     float o = osum[0][d];
 #pragma unroll
-    for (int i = 1; i < ATT_MQ; i++) o += osum[i][d];
+    for (int i = 1; i < MQ; i++) o += osum[i][d];
     att[(long)h * HD + d] = o / L;
   }
 }
@@ -612,10 +621,10 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
       hipLaunchKernelGGL((k_attn_gqa<64, false>), ag, at, 0, s, m.q, m.k, m.v, kc, vc, ksc, vsc, m.state,
                          group, kvd, m.rope_den, m.att_part);
     if (hd == 128)
-      hipLaunchKernelGGL(k_attn_merge<128>, dim3(m.n_heads), dim3(ATT_MQ * 128), 0, s, m.state, m.att_chunks,
+      hipLaunchKernelGGL(k_attn_merge<128>, dim3(m.n_heads), dim3(ATT_MERGE_THREADS), 0, s, m.state, m.att_chunks,
                          m.att_part, m.att);
     else
-      hipLaunchKernelGGL(k_attn_merge<64>, dim3(m.n_heads), dim3(ATT_MQ * 64), 0, s, m.state, m.att_chunks,
+      hipLaunchKernelGGL(k_attn_merge<64>, dim3(m.n_heads), dim3(ATT_MERGE_THREADS), 0, s, m.state, m.att_chunks,
                          m.att_part, m.att);
     MvIn ain;
     ain.x = m.att;
