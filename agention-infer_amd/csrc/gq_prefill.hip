@@ -164,32 +164,108 @@ __global__ __launch_bounds__(256) void k_rope_kv(float *q, float *k, const float
   }
 }
 
+// Max / sum of x over the 4 lane groups (lanes 16 apart) of a wave, the
+// same value in every lane (gfx950 lane swaps; each combination is
+// symmetric, so every lane computes the identical bits).
+__device__ __forceinline__ float lane_groups_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float lane_groups_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+constexpr int PF_Q = 64;  // queries per block
+typedef short pf16x4s_t __attribute__((ext_vector_type(4)));
+typedef short pf16x8s_t __attribute__((ext_vector_type(8)));
+typedef uint32_t pu32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t pu32x2_t __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void pf_lds_t;
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return (uint32_t)(uintptr_t)(const pf_lds_t *)p;
+}
+// LDS reads as asm: K/V arrive by direct-to-LDS loads, and the compiler
+// would drain all of those (vmcnt(0)) before any LDS read it emits itself.
+// The results are not ready until lds_wait(), which takes them as in/out
+// operands so that nothing uses them earlier.
+__device__ __forceinline__ pu32x4_t lds_b128(uint32_t a) {
+  pu32x4_t v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+// ds_read_b64_tr_b16: within each 16 lanes, the 4 halves lane r reads are
+// elements 4r .. 4r+3 of a 64-element list; lane r receives elements r,
+// r+16, r+32, r+48 of it.  With lane r pointing at row k0 + r/4, columns
+// d0 + 4 (r % 4) of a row-major tile, lane r gets column d0 + r of rows
+// k0 .. k0+3.
+__device__ __forceinline__ pu32x2_t lds_tr16(uint32_t a) {
+  pu32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(v) : "v"(a) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(pu32x4_t (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; i++) asm volatile("" : "+v"(v[i]));
+}
+template <int N>
+__device__ __forceinline__ void lds_wait(pu32x2_t (&v)[N]) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < N; i++) asm volatile("" : "+v"(v[i]));
+}
+__device__ __forceinline__ void vm_wait_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// K / V tile of 64 keys in LDS: row-major, HD/8 blocks of 16 B per row,
+// block b of row r stored at block b ^ (r % (HD/8)) (the reads of a
+// fragment then spread over the banks).
+template <int HD>
+__device__ __forceinline__ uint32_t kv_slot(int row, int blk) {
+  constexpr int NB = HD / 8;
+  return (uint32_t)(row * NB + (blk ^ (row & (NB - 1)))) * 16u;
+}
+
 // Causal attention of queries t = 0 .. n-1 (position pos0 + t, head h)
 // over cache rows 0 .. pos0 + t (attention_into, cpu_path.rs:141-194:
 // scores q.k / sqrt(hd), softmax, weighted sum of V), flash-style: block
-// (64-query tile, head h), 4 waves of 16 queries; the softmax runs in base
-// 2 (scores scaled by log2 e, exp2); 64-key chunks of K and
-// V^T staged in LDS (the next chunk's rows prefetched into registers).
-// Scores and the V sum run on v_mfma_f32_16x16x32_f16: K and V are f16
-// already; q (scaled by a power of two) and the probabilities are split
-// into f16 hi + lo parts, so the products are exact in fp32.  Softmax is
-// online (running max m, running sum l; O rescaled when m grows).
-constexpr int PF_Q = 64;  // queries per block
+// (64-query tile, head h), 4 waves of 16 queries.  64-key chunks of K and
+// V go straight from memory to LDS (global_load_lds_dwordx4, no registers;
+// two buffers, the next chunk loading while this one is used), one
+// barrier per chunk.
+// Both products run transposed on v_mfma_f32_16x16x32_f16 so that no
+// operand needs a shuffle or an LDS round trip:
+//   S^T = K . q^T   A = K rows from LDS, B = q (registers): a lane holds 4
+//                   keys (4 (lane/16) + i of each 16-key tile) of query
+//                   lane % 16, so the online softmax of its query is its
+//                   own 16 values plus two lane swaps across the groups;
+//   O^T = V^T . P^T B = the lane's own probabilities (the depth runs over
+//                   the keys in the order the S^T layout holds them: slot
+//                   8 g + j is key 16 t0 + 4 g + j, j < 4, and 16 t1 + 4 g +
+//                   j - 4 otherwise), A = V^T in that key order, read from
+//                   the row-major V by the gfx950 transpose load
+//                   ds_read_b64_tr_b16.
+// O^T puts one query per lane too, so the rescale by exp2(m_old - m_new)
+// is per lane.  K and V are f16 already; q (scaled by a power of two) and
+// the probabilities are split into f16 hi + lo parts, so the products are
+// exact in fp32.  The softmax runs in base 2 (scores scaled by log2 e).
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint16_t *kc,
                                                       const uint16_t *vc, int pos0, int n, int nh,
                                                       int group, float *att) {
   constexpr int KS = HD / 32, DT = HD / 16;
-  constexpr int KP = HD + 8;   // K row stride (halves): rows 16 B apart in bank order
-  constexpr int VP = 64 + 8;   // V^T and P row stride (halves)
-  constexpr int LD = HD / 8;   // 16-byte loads per key row
-  constexpr int NLD = 64 * LD / 256;  // per thread per chunk (K and V each)
-  __shared__ __align__(16) uint16_t Ks[64 * KP];
-  __shared__ __align__(16) uint16_t Vt[HD * VP];
-  __shared__ __align__(16) uint16_t Ph[4][16 * VP];
-  __shared__ __align__(16) uint16_t Pl[4][16 * VP];
+  constexpr int NB = HD / 8;                 // 16-byte blocks per K/V row
+  constexpr int TILE = 64 * HD * 2;          // bytes of one K or V tile
+  constexpr int NDMA = 64 * NB / 256;        // 16-byte loads per thread per tile
+  __shared__ __align__(16) uint8_t kvs[2][2][TILE];  // [buffer][K, V]
   __shared__ float red[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g4 = 4 * (lane >> 4);
   // Block b -> (query tile, query head): the group's heads of one (tile,
   // KV head) item G sit 8 blocks apart, i.e. on one XCD (consecutive blocks
   // go to consecutive XCDs), so they share the K/V chunks in one L2.
@@ -201,8 +277,27 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
   const int kvd = nkv * HD;
   const uint16_t *kbase = kc + (long)kh * HD, *vbase = vc + (long)kh * HD;
 
-  // q A-fragments: lane row = query qt0 + 16 wave + lane % 16, dims
-  // 8 (lane / 16) + 32 ks .. + 8.
+  const int tlast = min(qt0 + PF_Q, n) - 1;
+  const int kend = pos0 + tlast + 1;  // keys [0, kend)
+  const int nch = (kend + 63) / 64;
+  // Chunk c's rows into buffer c & 1: load j of wave w fills the 64 slots
+  // s = 64 (NDMA w + j) + lane, slot s = row s / NB, stored block s % NB
+  // (global block (s % NB) ^ (row % NB)); rows past kend - 1 repeat it.
+  auto dma = [&](int c) {
+    uint8_t *kt = kvs[c & 1][0], *vt = kvs[c & 1][1];
+#pragma unroll
+    for (int j = 0; j < NDMA; j++) {
+      const int sb = 64 * (NDMA * wave + j), sl = sb + lane;
+      const int row = sl / NB, blk = (sl % NB) ^ (row & (NB - 1));
+      const long r = min(64 * c + row, kend - 1);
+      __builtin_amdgcn_global_load_lds(kbase + r * kvd + 8 * blk, (pf_lds_t *)(kt + 16 * sb), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(vbase + r * kvd + 8 * blk, (pf_lds_t *)(vt + 16 * sb), 16, 0, 0);
+    }
+  };
+  dma(0);
+
+  // q fragments (the B operand of S^T): lane column = query qt0 + 16 wave
+  // + lane % 16, dims 8 (lane / 16) + 32 ks .. + 8.
   const int tq = qt0 + 16 * wave + (lane & 15);
   float qv[KS][8];
   float qm = 0.f;
@@ -237,127 +332,103 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
       qlo[ks][e] = (_Float16)(x - (float)hi);
     }
 
-  const int tlast = min(qt0 + PF_Q, n) - 1;
-  const int kend = pos0 + tlast + 1;  // keys [0, kend)
-  const int nch = (kend + 63) / 64;
-  // rows of the D layout: query qt0 + 16 wave + 4 (lane / 16) + i
-  int qrow[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) qrow[i] = qt0 + 16 * wave + 4 * (lane >> 4) + i;
-  float mrow[4], lrow[4];
-  pf32x4_t O[DT];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    mrow[i] = -INFINITY;
-    lrow[i] = 0.f;
-  }
+  float mrow = -INFINITY, lrow = 0.f;  // of query tq
+  pf32x4_t O[DT];                      // O^T: dims 16 d + 4 (lane / 16) + i of query tq
 #pragma unroll
   for (int d = 0; d < DT; d++) O[d] = pf32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  uint4 kr[NLD], vr[NLD];
-  auto fetch = [&](int c) {
-#pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      const int idx = tid + 256 * j, key = idx / LD, col = idx % LD;
-      const long p = min(64 * c + key, kend - 1);
-      kr[j] = *(const uint4 *)(kbase + p * kvd + 8 * col);
-      vr[j] = *(const uint4 *)(vbase + p * kvd + 8 * col);
-    }
-  };
-  fetch(0);
   for (int c = 0; c < nch; c++) {
-    __syncthreads();  // the previous chunk's readers are done
-#pragma unroll
-    for (int j = 0; j < NLD; j++) {
-      const int idx = tid + 256 * j, key = idx / LD, col = idx % LD;
-      *(uint4 *)&Ks[key * KP + 8 * col] = kr[j];
-      const uint32_t w4[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
-#pragma unroll
-      for (int e = 0; e < 8; e++)
-        Vt[(8 * col + e) * VP + key] = (uint16_t)(w4[e >> 1] >> (16 * (e & 1)));
-    }
-    __syncthreads();
-    if (c + 1 < nch) fetch(c + 1);
+    const uint32_t kt = lds_addr(kvs[c & 1][0]), vt = lds_addr(kvs[c & 1][1]);
+    vm_wait_all();     // this wave's loads of chunk c
+    __syncthreads();   // everyone's; and chunk c - 1 is no longer read
+    if (c + 1 < nch) dma(c + 1);
 
-    // scores of this wave's 16 queries x 64 keys (4 column tiles)
-    pf32x4_t s[4];
+    // S^T of 64 keys (4 tiles) x this wave's 16 queries
+    float sv[4][4];
 #pragma unroll
     for (int ct = 0; ct < 4; ct++) {
+      pu32x4_t kf[KS];
+      const int row = 16 * ct + (lane & 15);
+#pragma unroll
+      for (int ks = 0; ks < KS; ks++) kf[ks] = lds_b128(kt + kv_slot<HD>(row, (lane >> 4) + 4 * ks));
+      lds_wait(kf);
       pf32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ks++) {
-        const uint4 raw = *(const uint4 *)&Ks[(16 * ct + (lane & 15)) * KP + 8 * (lane >> 4) + 32 * ks];
-        pf16x8_t b;
-        __builtin_memcpy(&b, &raw, 16);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qhi[ks], b, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(qlo[ks], b, acc, 0, 0, 0);
+        const pf16x8_t a = __builtin_bit_cast(pf16x8_t, kf[ks]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qhi[ks], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qlo[ks], acc, 0, 0, 0);
       }
-      const int key = 64 * c + 16 * ct + (lane & 15);
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float sc = acc[i] * s2scale;
-        // rows past n stay finite (discarded); past the causal limit: -inf
-        s[ct][i] = qrow[i] >= n ? 0.f : key > pos0 + qrow[i] ? -INFINITY : sc;
+        const int key = 64 * c + 16 * ct + g4 + i;
+        // queries past n stay finite (discarded); past the causal limit: -inf
+        sv[ct][i] = tq >= n ? 0.f : key > pos0 + tq ? -INFINITY : acc[i] * s2scale;
       }
     }
-    // online softmax per row (a row's 64 values: 4 tiles x 16 lanes)
+    // online softmax of query tq: its 64 scores are 16 per lane group
+    float mx = sv[0][0];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      float mx = fmaxf(fmaxf(s[0][i], s[1][i]), fmaxf(s[2][i], s[3][i]));
+    for (int ct = 0; ct < 4; ct++)
 #pragma unroll
-      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-      const float mnew = fmaxf(mrow[i], mx);
-      const float alpha = exp2f(mrow[i] - mnew);  // row 0 holds key 0: mnew is finite
-      float ps = 0.f;
-#pragma unroll
-      for (int ct = 0; ct < 4; ct++) {
-        const float p = exp2f(s[ct][i] - mnew);
-        s[ct][i] = p;
-        ps += p;
-      }
-#pragma unroll
-      for (int off = 1; off < 16; off <<= 1) ps += __shfl_xor(ps, off, 64);
-      lrow[i] = lrow[i] * alpha + ps;
-      mrow[i] = mnew;
-#pragma unroll
-      for (int d = 0; d < DT; d++) O[d][i] *= alpha;
-    }
-    // P (hi + lo f16) to LDS in [query][key] order for the A operands
+      for (int i = 0; i < 4; i++) mx = fmaxf(mx, sv[ct][i]);
+    mx = lane_groups_max(mx);
+    const float mnew = fmaxf(mrow, mx);  // key 0 is in every query's range: finite
+    const float alpha = exp2f(mrow - mnew);
+    float ps = 0.f;
 #pragma unroll
     for (int ct = 0; ct < 4; ct++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const int r = 4 * (lane >> 4) + i, kk = 16 * ct + (lane & 15);
-        const _Float16 hi = (_Float16)s[ct][i];
-        const _Float16 lo = (_Float16)(s[ct][i] - (float)hi);
-        Ph[wave][r * VP + kk] = __builtin_bit_cast(uint16_t, hi);
-        Pl[wave][r * VP + kk] = __builtin_bit_cast(uint16_t, lo);
+        sv[ct][i] = exp2f(sv[ct][i] - mnew);
+        ps += sv[ct][i];
       }
-    __syncthreads();
-    // O += P . V over the chunk's 64 keys (2 depth steps)
+    lrow = lrow * alpha + lane_groups_sum(ps);
+    mrow = mnew;
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-      const uint4 rh = *(const uint4 *)&Ph[wave][(lane & 15) * VP + 8 * (lane >> 4) + 32 * ks];
-      const uint4 rl = *(const uint4 *)&Pl[wave][(lane & 15) * VP + 8 * (lane >> 4) + 32 * ks];
-      pf16x8_t ah, al;
-      __builtin_memcpy(&ah, &rh, 16);
-      __builtin_memcpy(&al, &rl, 16);
+    for (int d = 0; d < DT; d++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) O[d][i] *= alpha;
+    // O^T += V^T . P^T over the chunk's keys, 2 depth steps of 32
+    const int r = lane & 15;
+#pragma unroll
+    for (int st = 0; st < 2; st++) {
+      const int t0 = 2 * st, t1 = 2 * st + 1;
+      pf16x8_t bh, bl;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const _Float16 h0 = (_Float16)sv[t0][i], h1 = (_Float16)sv[t1][i];
+        bh[i] = h0;
+        bh[4 + i] = h1;
+        bl[i] = (_Float16)(sv[t0][i] - (float)h0);
+        bl[4 + i] = (_Float16)(sv[t1][i] - (float)h1);
+      }
+      // lane r: rows k0 + r/4, 8 bytes at column 16 d + 4 (r % 4)
+      pu32x2_t vf[2 * DT];
+#pragma unroll
+      for (int d = 0; d < DT; d++)
+#pragma unroll
+        for (int tt = 0; tt < 2; tt++) {
+          const int row = 16 * (tt ? t1 : t0) + g4 + (r >> 2);
+          const int col = 16 * d + 4 * (r & 3);
+          vf[2 * d + tt] = lds_tr16(vt + kv_slot<HD>(row, col >> 3) + 2 * (col & 7));
+        }
+      lds_wait(vf);
 #pragma unroll
       for (int d = 0; d < DT; d++) {
-        const uint4 raw = *(const uint4 *)&Vt[(16 * d + (lane & 15)) * VP + 8 * (lane >> 4) + 32 * ks];
-        pf16x8_t b;
-        __builtin_memcpy(&b, &raw, 16);
-        O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, b, O[d], 0, 0, 0);
-        O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, b, O[d], 0, 0, 0);
+        const pu32x4_t a4 = {vf[2 * d].x, vf[2 * d].y, vf[2 * d + 1].x, vf[2 * d + 1].y};
+        const pf16x8_t a = __builtin_bit_cast(pf16x8_t, a4);
+        O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bh, O[d], 0, 0, 0);
+        O[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bl, O[d], 0, 0, 0);
       }
     }
   }
+  if (tq < n) {
+    float *dst = att + (long)tq * nh * HD + (long)h * HD + g4;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
-    if (qrow[i] >= n) continue;
-    float *dst = att + (long)qrow[i] * nh * HD + (long)h * HD + (lane & 15);
-#pragma unroll
-    for (int d = 0; d < DT; d++) dst[16 * d] = O[d][i] / lrow[i];
+    for (int d = 0; d < DT; d++)
+      *(float4 *)(dst + 16 * d) =
+          make_float4(O[d][0] / lrow, O[d][1] / lrow, O[d][2] / lrow, O[d][3] / lrow);
   }
 }
 
