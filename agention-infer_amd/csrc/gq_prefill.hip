@@ -235,8 +235,9 @@ __device__ __forceinline__ uint32_t kv_slot(int row, int blk) {
 // Causal attention of queries t = 0 .. n-1 (position pos0 + t, head h)
 // over cache rows 0 .. pos0 + t (attention_into, cpu_path.rs:141-194:
 // scores q.k / sqrt(hd), softmax, weighted sum of V), flash-style: block
-// (64-query tile, head h), 4 waves of 16 queries.  64-key chunks of K and
-// V go straight from memory to LDS (global_load_lds_dwordx4, no registers;
+// (64-query tile, head h), 8 waves: 4 of 16 queries for each half of the
+// 64-key chunks (even / odd), merged at the end.  K and V go straight
+// from memory to LDS (global_load_lds_dwordx4, no registers;
 // two buffers, the next chunk loading while this one is used), one
 // barrier per chunk.
 // Both products run transposed on v_mfma_f32_16x16x32_f16 so that no
@@ -256,16 +257,19 @@ __device__ __forceinline__ uint32_t kv_slot(int row, int blk) {
 // the probabilities are split into f16 hi + lo parts, so the products are
 // exact in fp32.  The softmax runs in base 2 (scores scaled by log2 e).
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint16_t *kc,
+__global__ __launch_bounds__(512) void k_attn_prefill(const float *q, const uint16_t *kc,
                                                       const uint16_t *vc, int pos0, int n, int nh,
                                                       int group, float *att) {
   constexpr int KS = HD / 32, DT = HD / 16;
   constexpr int NB = HD / 8;                 // 16-byte blocks per K/V row
   constexpr int TILE = 64 * HD * 2;          // bytes of one K or V tile
-  constexpr int NDMA = 64 * NB / 256;        // 16-byte loads per thread per tile
-  __shared__ __align__(16) uint8_t kvs[2][2][TILE];  // [buffer][K, V]
-  __shared__ float red[4];
+  constexpr int NDMA = 64 * NB / 256;        // 16-byte loads per thread per tile (4 waves)
+  // [key half][buffer][K, V]: waves 0-3 take the even chunks, waves 4-7
+  // the odd ones, each half with its own two buffers.
+  __shared__ __align__(16) uint8_t kvs[2][2][2][TILE];
+  __shared__ float red[8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g4 = 4 * (lane >> 4);
+  const int half = wave >> 2, wq = wave & 3;  // key half, query wave
   // Block b -> (query tile, query head): the group's heads of one (tile,
   // KV head) item G sit 8 blocks apart, i.e. on one XCD (consecutive blocks
   // go to consecutive XCDs), so they share the K/V chunks in one L2.
@@ -280,25 +284,26 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
   const int tlast = min(qt0 + PF_Q, n) - 1;
   const int kend = pos0 + tlast + 1;  // keys [0, kend)
   const int nch = (kend + 63) / 64;
-  // Chunk c's rows into buffer c & 1: load j of wave w fills the 64 slots
-  // s = 64 (NDMA w + j) + lane, slot s = row s / NB, stored block s % NB
-  // (global block (s % NB) ^ (row % NB)); rows past kend - 1 repeat it.
+  // Chunk c (of this wave's half, c % 2 == half) into buffer (c / 2) & 1:
+  // load j of query wave wq fills the 64 slots s = 64 (NDMA wq + j) + lane,
+  // slot s = row s / NB, stored block s % NB (global block (s % NB) ^
+  // (row % NB)); rows past kend - 1 repeat it.
   auto dma = [&](int c) {
-    uint8_t *kt = kvs[c & 1][0], *vt = kvs[c & 1][1];
+    uint8_t *kt = kvs[half][(c >> 1) & 1][0], *vt = kvs[half][(c >> 1) & 1][1];
 #pragma unroll
     for (int j = 0; j < NDMA; j++) {
-      const int sb = 64 * (NDMA * wave + j), sl = sb + lane;
+      const int sb = 64 * (NDMA * wq + j), sl = sb + lane;
       const int row = sl / NB, blk = (sl % NB) ^ (row & (NB - 1));
       const long r = min(64 * c + row, kend - 1);
       __builtin_amdgcn_global_load_lds(kbase + r * kvd + 8 * blk, (pf_lds_t *)(kt + 16 * sb), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(vbase + r * kvd + 8 * blk, (pf_lds_t *)(vt + 16 * sb), 16, 0, 0);
     }
   };
-  dma(0);
+  if (half < nch) dma(half);
 
-  // q fragments (the B operand of S^T): lane column = query qt0 + 16 wave
-  // + lane % 16, dims 8 (lane / 16) + 32 ks .. + 8.
-  const int tq = qt0 + 16 * wave + (lane & 15);
+  // q fragments (the B operand of S^T): lane column = query qt0 + 16 wq +
+  // lane % 16, dims 8 (lane / 16) + 32 ks .. + 8.
+  const int tq = qt0 + 16 * wq + (lane & 15);
   float qv[KS][8];
   float qm = 0.f;
 #pragma unroll
@@ -314,7 +319,9 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
   for (int off = 32; off > 0; off >>= 1) qm = fmaxf(qm, __shfl_xor(qm, off, 64));
   if (lane == 0) red[wave] = qm;
   __syncthreads();
-  qm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  qm = red[0];
+#pragma unroll
+  for (int w = 1; w < 8; w++) qm = fmaxf(qm, red[w]);
   int ex = 0;
   (void)frexpf(qm, &ex);
   const float qscale = qm > 0.f ? ldexpf(1.0f, 10 - ex) : 1.0f;
@@ -332,16 +339,18 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
       qlo[ks][e] = (_Float16)(x - (float)hi);
     }
 
-  float mrow = -INFINITY, lrow = 0.f;  // of query tq
+  float mrow = -INFINITY, lrow = 0.f;  // of query tq over this half's keys
   pf32x4_t O[DT];                      // O^T: dims 16 d + 4 (lane / 16) + i of query tq
 #pragma unroll
   for (int d = 0; d < DT; d++) O[d] = pf32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int c = 0; c < nch; c++) {
-    const uint32_t kt = lds_addr(kvs[c & 1][0]), vt = lds_addr(kvs[c & 1][1]);
+  for (int cp = 0; cp < nch; cp += 2) {  // chunk pairs: both halves meet at every barrier
+    const int c = cp + half;
+    const uint32_t kt = lds_addr(kvs[half][(c >> 1) & 1][0]), vt = lds_addr(kvs[half][(c >> 1) & 1][1]);
     vm_wait_all();     // this wave's loads of chunk c
-    __syncthreads();   // everyone's; and chunk c - 1 is no longer read
-    if (c + 1 < nch) dma(c + 1);
+    __syncthreads();   // everyone's; and the chunks before are no longer read
+    if (c + 2 < nch) dma(c + 2);
+    if (c >= nch) continue;
 
     // S^T of 64 keys (4 tiles) x this wave's 16 queries
     float sv[4][4];
@@ -373,14 +382,16 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
 #pragma unroll
       for (int i = 0; i < 4; i++) mx = fmaxf(mx, sv[ct][i]);
     mx = lane_groups_max(mx);
-    const float mnew = fmaxf(mrow, mx);  // key 0 is in every query's range: finite
-    const float alpha = exp2f(mrow - mnew);
+    // (a chunk wholly past a query's causal limit leaves mx = -inf: the
+    // state is unchanged; chunk 0 is in every query's range)
+    const float mnew = fmaxf(mrow, mx);
+    const float alpha = mnew == -INFINITY ? 1.f : exp2f(mrow - mnew);
     float ps = 0.f;
 #pragma unroll
     for (int ct = 0; ct < 4; ct++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        sv[ct][i] = exp2f(sv[ct][i] - mnew);
+        sv[ct][i] = mnew == -INFINITY ? 0.f : exp2f(sv[ct][i] - mnew);
         ps += sv[ct][i];
       }
     lrow = lrow * alpha + lane_groups_sum(ps);
@@ -423,12 +434,36 @@ __global__ __launch_bounds__(256) void k_attn_prefill(const float *q, const uint
       }
     }
   }
-  if (tq < n) {
-    float *dst = att + (long)tq * nh * HD + (long)h * HD + g4;
+  // Merge the odd half into the even one: M = max(m0, m1),
+  // O = O0 e^(m0 - M) + O1 e^(m1 - M), l likewise (the K/V buffers are free
+  // once every wave has passed the barrier).
+  __syncthreads();
+  float *xch = (float *)&kvs[0][0][0][0];  // [query wave][lane][2 + 4 DT]
+  constexpr int XW = 2 + 4 * DT;
+  if (half == 1) {
+    float *p = xch + (wq * 64 + lane) * XW;
+    p[0] = mrow;
+    p[1] = lrow;
 #pragma unroll
     for (int d = 0; d < DT; d++)
-      *(float4 *)(dst + 16 * d) =
-          make_float4(O[d][0] / lrow, O[d][1] / lrow, O[d][2] / lrow, O[d][3] / lrow);
+#pragma unroll
+      for (int i = 0; i < 4; i++) p[2 + 4 * d + i] = O[d][i];
+  }
+  __syncthreads();
+  if (half == 0 && tq < n) {
+    const float *p = xch + (wq * 64 + lane) * XW;
+    const float m1 = p[0], l1 = p[1];
+    const float M = fmaxf(mrow, m1);  // mrow is finite: chunk 0 is in this half
+    const float f0 = exp2f(mrow - M), f1 = m1 == -INFINITY ? 0.f : exp2f(m1 - M);
+    const float L = lrow * f0 + l1 * f1;
+    float *dst = att + (long)tq * nh * HD + (long)h * HD + g4;
+#pragma unroll
+    for (int d = 0; d < DT; d++) {
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) o[i] = (O[d][i] * f0 + p[2 + 4 * d + i] * f1) / L;
+      *(float4 *)(dst + 16 * d) = make_float4(o[0], o[1], o[2], o[3]);
+    }
   }
 }
 
@@ -491,9 +526,9 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
     const int items = (n + PF_Q - 1) / PF_Q * nkv;  // (query tile, KV head)
     const dim3 ag(8 * group * ((items + 7) / 8));
     if (hd == 128)
-      hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(256), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
+      hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(512), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
     else
-      hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(256), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
+      hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(512), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
     if ((e = launch_x_to_frag(b.att, n, qd, b.xb, s)) != hipSuccess) return e;
     float *xo[1] = {b.x};
     if ((e = launch_gemm_bf16(&m.wo[L], xo, 1, b.xb, n, b.part, true, num_cus, s)) != hipSuccess) return e;
