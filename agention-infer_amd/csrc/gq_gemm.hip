@@ -811,10 +811,21 @@ hipError_t launch_gemm_records(const gq_weight *w, uint8_t *out, hipStream_t st)
 }
 
 int gemm_ksplit(int tiles, int stages, int num_cus) {
-  // enough blocks for about one per CU, at least 4 stages per split
-  int ks = tiles >= num_cus ? 1 : (num_cus + tiles / 2) / tiles;
-  ks = std::min(ks, std::max(1, stages / 4));
-  return std::max(ks, 1);
+  // The split with the least time per unit of work, rounds / ks (a block
+  // per CU per round; 45 tiles x 6 = 270 blocks would run a second round
+  // of 14), the smaller on ties; at most 8, at least 4 stages per split.
+  if (tiles >= num_cus) return 1;
+  const int kmax = std::max(1, std::min(8, stages / 4));
+  int best = 1;
+  double best_t = 1.0;
+  for (int ks = 2; ks <= kmax; ks++) {
+    const double t = (double)((tiles * ks + num_cus - 1) / num_cus) / ks;
+    if (t < best_t - 1e-9) {
+      best_t = t;
+      best = ks;
+    }
+  }
+  return best;
 }
 
 namespace {
