@@ -390,26 +390,28 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
   }
 }
 
-// Merge of the chunk partials: block h (query head) of 1024 threads, thread
-// (qq, d) (qq < MQ = 1024 / HD) sums dim d over the chunks c = qq, qq + MQ,
-// ..., then the MQ partial sums are added in order:
+// Merge of the chunk partials: block (h, y) = query head h, dims
+// 32 y .. 32 y + 31, 256 threads; thread (qq, d) (qq < MQ = 8) sums dim d
+// over the chunks c = qq, qq + MQ, ..., then the MQ partial sums are added
+// in order (small blocks: a head's dims spread over HD / 32 of them):
 //   att[h][d] = sum_c o_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M),
 // M = max_c m_c over the chunks holding positions <= pos.  Every load of
 // the first 16 * MQ chunks (m, l and o: 8192 positions) is issued at the
-// start.
-constexpr int ATT_MERGE_THREADS = 1024;
+// start; every block of a head computes the head's M and L.
+constexpr int ATT_MERGE_THREADS = 256, ATT_MERGE_DIMS = 32;
 template <int HD>
 __global__ __launch_bounds__(ATT_MERGE_THREADS) void k_attn_merge(const DecodeState *st, int nchunk_grid,
                                                              const float *part, float *att) {
-  constexpr int NT = ATT_MERGE_THREADS, MQ = NT / HD, NWV = NT / 64, R = 16;
+  constexpr int NT = ATT_MERGE_THREADS, DB = ATT_MERGE_DIMS, MQ = NT / DB, NWV = NT / 64, R = 16;
+  static_assert(HD % DB == 0, "dims per block");
   __shared__ float fac[ATT_MAX_CTX / ATT_CHUNK];
   __shared__ float red[NWV];
-  __shared__ float osum[MQ][HD];
+  __shared__ float osum[MQ][DB];
   const int h = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // The first loads go out before the position is known: chunks of the
   // grid past the last one in use are read and then ignored.
   const float *ph = part + (long)h * nchunk_grid * (2 + HD);
-  const int qq = tid / HD, d = tid % HD;
+  const int qq = tid / DB, dl = tid % DB, d = DB * blockIdx.y + dl;
   const float *po = ph + 2 + d;
   float vals[R];
 #pragma unroll
@@ -468,12 +470,12 @@ __global__ __launch_bounds__(ATT_MERGE_THREADS) void k_attn_merge(const DecodeSt
       s4[j & 3] += c < nch ? vals[j] * fac[c] : 0.f;
     }
   }
-  osum[qq][d] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+  osum[qq][dl] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
   __syncthreads();
   if (qq == 0) {
-    float o = osum[0][d];
+    float o = osum[0][dl];
 #pragma unroll
-    for (int i = 1; i < MQ; i++) o += osum[i][d];
+    for (int i = 1; i < MQ; i++) o += osum[i][dl];
     att[(long)h * HD + d] = o / L;
   }
 }
@@ -621,10 +623,10 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
       hipLaunchKernelGGL((k_attn_gqa<64, false>), ag, at, 0, s, m.q, m.k, m.v, kc, vc, ksc, vsc, m.state,
                          group, kvd, m.rope_den, m.att_part);
     if (hd == 128)
-      hipLaunchKernelGGL(k_attn_merge<128>, dim3(m.n_heads), dim3(ATT_MERGE_THREADS), 0, s, m.state, m.att_chunks,
+      hipLaunchKernelGGL(k_attn_merge<128>, dim3(m.n_heads, 128 / ATT_MERGE_DIMS), dim3(ATT_MERGE_THREADS), 0, s, m.state, m.att_chunks,
                          m.att_part, m.att);
     else
-      hipLaunchKernelGGL(k_attn_merge<64>, dim3(m.n_heads), dim3(ATT_MERGE_THREADS), 0, s, m.state, m.att_chunks,
+      hipLaunchKernelGGL(k_attn_merge<64>, dim3(m.n_heads, 64 / ATT_MERGE_DIMS), dim3(ATT_MERGE_THREADS), 0, s, m.state, m.att_chunks,
                          m.att_part, m.att);
     MvIn ain;
     ain.x = m.att;
