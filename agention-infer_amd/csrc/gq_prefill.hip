@@ -112,12 +112,16 @@ __global__ __launch_bounds__(256) void k_norm_to_frag(const float *x, const floa
 }
 
 // Fragments of silu(g) * u (ffn_gate_up, cpu_path.rs:225-227), g and u
-// [n][F] (F % 8 == 0); zeros past n and F.  Block (token t, 2048 columns).
+// [n][F] (F % 8 == 0); zeros past n and F.  A wave writes one whole
+// fragment (16 tokens x 32 columns, 1 KiB contiguous): lane l converts
+// token 16 nt + l % 16, columns 32 ks + 8 (l / 16) .. + 8.
 __global__ __launch_bounds__(256) void k_swiglu_to_frag(const float *g, const float *u, int n, int F,
-                                                        int kpad, uint16_t *xb) {
-  const int t = blockIdx.y, ksteps = kpad / 32;
-  const int c = 8 * (blockIdx.x * 256 + threadIdx.x);
-  if (c >= kpad) return;
+                                                        int npad, int kpad, uint16_t *xb) {
+  const int ksteps = kpad / 32, lane = threadIdx.x & 63;
+  const long f = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (f >= (long)(npad / 16) * ksteps) return;
+  const int nt = (int)(f / ksteps), ks = (int)(f % ksteps);
+  const int t = 16 * nt + (lane & 15), c = 32 * ks + 8 * (lane >> 4);
   float v[8];
   if (t < n && c < F) {
     const float *gp = g + (long)t * F + c, *up = u + (long)t * F + c;
@@ -538,8 +542,8 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
     float *guo[2] = {b.g, b.u};
     if ((e = launch_gemm_bf16(gu, guo, 2, b.xb, n, b.part, false, num_cus, s)) != hipSuccess) return e;
     const int kpf = round_up(F, 256);
-    hipLaunchKernelGGL(k_swiglu_to_frag, dim3((kpf / 8 + 255) / 256, npad), dim3(256), 0, s, b.g, b.u, n, F,
-                       kpf, b.xb);
+    hipLaunchKernelGGL(k_swiglu_to_frag, dim3((int)(((long)npad / 16 * (kpf / 32) + 3) / 4)), dim3(256), 0,
+                       s, b.g, b.u, n, F, npad, kpf, b.xb);
     if ((e = launch_gemm_bf16(&m.wdown[L], xo, 1, b.xb, n, b.part, true, num_cus, s)) != hipSuccess) return e;
   }
   // logits of RMSNorm(x[n - 1]) (the decode head matvec)
