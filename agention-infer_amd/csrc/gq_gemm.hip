@@ -649,9 +649,25 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_ring(GemmArgs a) {
   }
 }
 
-// y[t][r] = (add ? y[t][r] : 0) + sum_s part[s][t][r], s in order.
-__global__ void k_gemm_reduce(const float *part, int ksplit, long count, float *y, int add) {
-  const long i = ((long)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+// y[t][r] = (add ? y[t][r] : 0) + sum_s part[s][t][r], s in order, for the
+// segments of one launch at once (segment i owns blocks blk0[i] ..
+// blk0[i + 1] - 1: one launch instead of one per matrix).
+struct ReduceSegs {
+  const float *part[GEMM_MAX_SEG];
+  float *y[GEMM_MAX_SEG];
+  long count[GEMM_MAX_SEG];
+  int blk0[GEMM_MAX_SEG + 1];
+  int nseg;
+};
+__global__ void k_gemm_reduce(ReduceSegs r, int ksplit, int add) {
+  int si = 0;
+#pragma unroll
+  for (int j = 1; j < GEMM_MAX_SEG; j++)
+    if (j < r.nseg && (int)blockIdx.x >= r.blk0[j]) si = j;
+  const float *part = r.part[si];
+  float *y = r.y[si];
+  const long count = r.count[si];
+  const long i = ((long)(blockIdx.x - r.blk0[si]) * blockDim.x + threadIdx.x) * 4;
   if (i >= count) return;
   if (i + 3 < count) {
     float4 s = add ? *(const float4 *)(y + i) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -914,11 +930,18 @@ hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int co
   hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(512), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ksplit == 1) return e;
+  ReduceSegs r{};
+  r.nseg = count;
+  int blocks = 0;
   for (int i = 0; i < count; i++) {
-    const long cnt = (long)n * a.seg[i].rows;
-    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((cnt / 4 + 255) / 256 + 1)), dim3(256), 0, st,
-                       a.seg[i].part, p.ksplit, cnt, a.seg[i].y, add ? 1 : 0);
+    r.part[i] = a.seg[i].part;
+    r.y[i] = a.seg[i].y;
+    r.count[i] = (long)n * a.seg[i].rows;
+    r.blk0[i] = blocks;
+    blocks += (int)((r.count[i] / 4 + 255) / 256 + 1);
   }
+  r.blk0[count] = blocks;
+  hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, r, p.ksplit, add ? 1 : 0);
   return hipGetLastError();
 }
 
