@@ -896,7 +896,7 @@ hipError_t launch_x_to_frag(const float *X, int n, int k, uint16_t *xb, hipStrea
 
 hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int count,
                             const uint16_t *xb, int n, float *part, bool add, int num_cus,
-                            hipStream_t st) {
+                            hipStream_t st, int *defer) {
   if (count < 1 || count > GEMM_MAX_SEG || n <= 0) return hipErrorInvalidValue;
   const int fmt = ws[0]->L.dtype;
   const GemmPlan p = gemm_plan(ws, count, n, num_cus, add);
@@ -930,6 +930,10 @@ hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int co
   hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(512), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || p.ksplit == 1) return e;
+  if (defer && add) {
+    *defer = p.ksplit;
+    return hipSuccess;
+  }
   ReduceSegs r{};
   r.nseg = count;
   int blocks = 0;

@@ -205,9 +205,11 @@ int gemm_ksplit(int tiles, int stages, int num_cus);
 // Q6_K) and in_dim, on X already in fragment form (xb, n tokens).  add: Y_i
 // += (else =; an accumulating launch always splits K and adds in the
 // reduction).  part: gemm_part_floats floats.
+// defer (accumulating launches only): the reduction is left to the
+// caller; *defer receives the K split whose partials part holds.
 hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int count,
                             const uint16_t *xb, int n, float *part, bool add, int num_cus,
-                            hipStream_t st);
+                            hipStream_t st, int *defer = nullptr);
 size_t gemm_part_floats(const gq_weight *const *ws, int count, int n, int num_cus, bool add);
 // X fp32 [n][k] -> bf16 fragments (kpad = k rounded up to 256, npad = n
 // rounded up to GEMM_NPAD, zero padding).

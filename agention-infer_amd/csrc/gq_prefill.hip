@@ -70,18 +70,34 @@ __global__ void k_embed_rows(const float *embd, const int *tokens, int H, float 
 // thread keeps its groups of 8 values in registers across the reduction
 // (H <= NORM_GROUPS * 8 * 256, H % 8 == 0 for the vector loads).
 constexpr int NORM_GROUPS = 4;
-__global__ __launch_bounds__(256) void k_norm_to_frag(const float *x, const float *w, int n, int H,
-                                                      int kpad, float eps, uint16_t *xb) {
+// With ksplit > 0 the preceding accumulating GEMM left its K-split
+// partials part[s][t][c] (s < ksplit) unreduced: x[t] += part[0][t] +
+// part[1][t] + ... (in that order, as k_gemm_reduce) is done here, and the
+// new row is stored back to x.
+__global__ __launch_bounds__(256) void k_norm_to_frag(float *x, const float *w, int n, int H,
+                                                      int kpad, float eps, uint16_t *xb,
+                                                      const float *part, int ksplit) {
   __shared__ float red[4];
   const int t = blockIdx.x, ksteps = kpad / 32;
-  const float *xt = x + (long)t * H;
+  float *xt = x + (long)t * H;
   float v[NORM_GROUPS][8];
   float ss = 0.f;
 #pragma unroll
   for (int j = 0; j < NORM_GROUPS; j++) {
     const int c = 8 * (threadIdx.x + 256 * j);
     if (t < n && c < H) {
-      const float4 a = *(const float4 *)(xt + c), b = *(const float4 *)(xt + c + 4);
+      float4 a = *(const float4 *)(xt + c), b = *(const float4 *)(xt + c + 4);
+      if (ksplit > 0) {
+        const long cnt = (long)n * H;
+        for (int k = 0; k < ksplit; k++) {
+          const float *pp = part + k * cnt + (long)t * H + c;
+          const float4 pa = *(const float4 *)pp, pb = *(const float4 *)(pp + 4);
+          a.x += pa.x; a.y += pa.y; a.z += pa.z; a.w += pa.w;
+          b.x += pb.x; b.y += pb.y; b.z += pb.z; b.w += pb.w;
+        }
+        *(float4 *)(xt + c) = a;
+        *(float4 *)(xt + c + 4) = b;
+      }
       v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
       v[j][4] = b.x; v[j][5] = b.y; v[j][6] = b.z; v[j][7] = b.w;
     } else {
@@ -504,9 +520,11 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
   const int npad = round_up(n, GEMM_NPAD);
   hipError_t e;
   hipLaunchKernelGGL(k_embed_rows, dim3(n), dim3(256), 0, s, m.embd, tokens_dev, H, b.x);
+  int pending = 0;  // K split of partials left for the next norm to add into x
   for (int L = 0; L < m.n_layers; L++) {
     hipLaunchKernelGGL(k_norm_to_frag, dim3(npad), dim3(256), 0, s, b.x, m.attn_norm[L], n, H,
-                       round_up(H, 256), m.eps, b.xb);
+                       round_up(H, 256), m.eps, b.xb, b.part, pending);
+    pending = 0;
     // q, k, v: one launch per distinct dtype (attn_v is Q6_K in some files)
     const gq_weight *qkv[3] = {m.wq[L], m.wk[L], m.wv[L]};
     float *outs[3] = {b.q, b.k, b.v};
@@ -535,16 +553,21 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
       hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(512), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
     if ((e = launch_x_to_frag(b.att, n, qd, b.xb, s)) != hipSuccess) return e;
     float *xo[1] = {b.x};
-    if ((e = launch_gemm_bf16(&m.wo[L], xo, 1, b.xb, n, b.part, true, num_cus, s)) != hipSuccess) return e;
+    if ((e = launch_gemm_bf16(&m.wo[L], xo, 1, b.xb, n, b.part, true, num_cus, s, &pending)) != hipSuccess)
+      return e;
     hipLaunchKernelGGL(k_norm_to_frag, dim3(npad), dim3(256), 0, s, b.x, m.ffn_norm[L], n, H,
-                       round_up(H, 256), m.eps, b.xb);
+                       round_up(H, 256), m.eps, b.xb, b.part, pending);
+    pending = 0;
     const gq_weight *gu[2] = {m.wgate[L], m.wup[L]};
     float *guo[2] = {b.g, b.u};
     if ((e = launch_gemm_bf16(gu, guo, 2, b.xb, n, b.part, false, num_cus, s)) != hipSuccess) return e;
     const int kpf = round_up(F, 256);
     hipLaunchKernelGGL(k_swiglu_to_frag, dim3((int)(((long)npad / 16 * (kpf / 32) + 3) / 4)), dim3(256), 0,
                        s, b.g, b.u, n, F, npad, kpf, b.xb);
-    if ((e = launch_gemm_bf16(&m.wdown[L], xo, 1, b.xb, n, b.part, true, num_cus, s)) != hipSuccess) return e;
+    // (the next layer's norm does the reduction; the head reads x itself)
+    if ((e = launch_gemm_bf16(&m.wdown[L], xo, 1, b.xb, n, b.part, true, num_cus, s,
+                              L + 1 < m.n_layers ? &pending : nullptr)) != hipSuccess)
+      return e;
   }
   // logits of RMSNorm(x[n - 1]) (the decode head matvec)
   MvIn hin;
