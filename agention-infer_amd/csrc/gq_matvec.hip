@@ -236,6 +236,9 @@ __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u
 // pairs (2m, 2m+1), whose e0 differ by 16.  All threads execute the
 // shuffles.
 template <bool Q6>
+__device__ __forceinline__ void put_aux(const Smem &S, int e0, float sx, float sum32, int xs);
+
+template <bool Q6>
 __device__ __forceinline__ void stage_x(int kpad, int e0, const float (&xv)[16], const Smem &S) {
   float amax = 0.f, sum = 0.f;
 #pragma unroll

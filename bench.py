@@ -295,7 +295,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "see DESIGN.md for how the path would shard.", file=sys.stderr)
+              "multi-GPU sharding of the path is not built.", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
