@@ -7,7 +7,8 @@
 //   xn = RMSNorm(x) * attn_norm      -> bf16 MFMA fragments (k_norm_to_frag)
 //   q, k, v = xn . Wq/Wk/Wv          (one GEMM launch, K split)
 //   RoPE of q and k, f16 K/V rows into the cache (k_rope_kv)
-//   att = causal attention of every query over the cache (k_attn_prefill)
+//   att = causal attention of every query over the cache (k_attn_prefill,
+//         written as the o GEMM's bf16 X fragments)
 //   x += att . Wo                    (GEMM, K split, accumulating reduction)
 //   xn = RMSNorm(x) * ffn_norm; g, u = xn . Wgate/Wup
 //   x += (silu(g) * u) . Wdown       (k_swiglu_to_frag, GEMM)
@@ -279,7 +280,7 @@ __device__ __forceinline__ uint32_t kv_slot(int row, int blk) {
 template <int HD>
 __global__ __launch_bounds__(512) void k_attn_prefill(const float *q, const uint16_t *kc,
                                                       const uint16_t *vc, int pos0, int n, int nh,
-                                                      int group, float *att) {
+                                                      int group, uint16_t *xb) {
   constexpr int KS = HD / 32, DT = HD / 16;
   constexpr int NB = HD / 8;                 // 16-byte blocks per K/V row
   constexpr int TILE = 64 * HD * 2;          // bytes of one K or V tile
@@ -470,19 +471,28 @@ __global__ __launch_bounds__(512) void k_attn_prefill(const float *q, const uint
       for (int i = 0; i < 4; i++) p[2 + 4 * d + i] = O[d][i];
   }
   __syncthreads();
-  if (half == 0 && tq < n) {
+  // The output goes straight into the o GEMM's bf16 X fragments (row tq,
+  // columns h HD + 16 d + 4 (lane / 16) + i): lane groups 0 and 2 take the
+  // 4 values of groups 1 and 3 (lane swap) and store 8 columns each.
+  if (half == 0) {
     const float *p = xch + (wq * 64 + lane) * XW;
     const float m1 = p[0], l1 = p[1];
     const float M = fmaxf(mrow, m1);  // mrow is finite: chunk 0 is in this half
     const float f0 = exp2f(mrow - M), f1 = m1 == -INFINITY ? 0.f : exp2f(m1 - M);
     const float L = lrow * f0 + l1 * f1;
-    float *dst = att + (long)tq * nh * HD + (long)h * HD + g4;
+    const int ksteps = nh * HD / 32;
 #pragma unroll
     for (int d = 0; d < DT; d++) {
-      float o[4];
+      float v[8];
 #pragma unroll
-      for (int i = 0; i < 4; i++) o[i] = (O[d][i] * f0 + p[2 + 4 * d + i] * f1) / L;
-      *(float4 *)(dst + 16 * d) = make_float4(o[0], o[1], o[2], o[3]);
+      for (int i = 0; i < 4; i++) {
+        const float o = (O[d][i] * f0 + p[2 + 4 * d + i] * f1) / L;
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(o), __float_as_uint(o), false, false);
+        v[i] = __uint_as_float(r[0]);      // this group's (even) value
+        v[4 + i] = __uint_as_float(r[1]);  // the odd group's
+      }
+      if (((lane >> 4) & 1) == 0 && tq < n)
+        put_frag8(xb, frag_slot(tq, h * HD + 16 * d + 8 * (lane >> 5), ksteps), v);
     }
   }
 }
@@ -548,10 +558,9 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
     const int items = (n + PF_Q - 1) / PF_Q * nkv;  // (query tile, KV head)
     const dim3 ag(8 * group * ((items + 7) / 8));
     if (hd == 128)
-      hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(512), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
+      hipLaunchKernelGGL(k_attn_prefill<128>, ag, dim3(512), 0, s, b.q, kc, vc, pos0, n, nh, group, b.xb);
     else
-      hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(512), 0, s, b.q, kc, vc, pos0, n, nh, group, b.att);
-    if ((e = launch_x_to_frag(b.att, n, qd, b.xb, s)) != hipSuccess) return e;
+      hipLaunchKernelGGL(k_attn_prefill<64>, ag, dim3(512), 0, s, b.q, kc, vc, pos0, n, nh, group, b.xb);
     float *xo[1] = {b.x};
     if ((e = launch_gemm_bf16(&m.wo[L], xo, 1, b.xb, n, b.part, true, num_cus, s, &pending)) != hipSuccess)
       return e;
