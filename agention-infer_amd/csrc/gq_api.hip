@@ -836,7 +836,6 @@ int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float 
     if (!rc) rc = dalloc(m, &m->pf.q, np * qd);
     if (!rc) rc = dalloc(m, &m->pf.k, np * kvd);
     if (!rc) rc = dalloc(m, &m->pf.v, np * kvd);
-    if (!rc) rc = dalloc(m, &m->pf.att, np * qd);
     if (!rc) rc = dalloc(m, &m->pf.g, np * L.ffn);
     if (!rc) rc = dalloc(m, &m->pf.u, np * L.ffn);
     if (!rc) rc = dalloc(m, &m->pf.part, std::max<size_t>(1, gq::prefill_part_floats(L, gq::PREFILL_MAX, g_dev.num_cus)));

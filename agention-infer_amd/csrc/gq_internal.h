@@ -138,7 +138,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s);
 constexpr int PREFILL_MAX = 512;
 struct PrefillBufs {
   float *x;        // [n][hidden] residual stream
-  float *q, *k, *v, *att, *g, *u;
+  float *q, *k, *v, *g, *u;
   float *part;     // GEMM K-split partials (prefill_part_floats)
   uint16_t *xb;    // GEMM X fragments [512][max(hidden, ffn, q_dim) rounded to 256] bf16
   int *tokens;     // [PREFILL_MAX]
