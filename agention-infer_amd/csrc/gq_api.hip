@@ -46,6 +46,10 @@ struct DeviceState {
   int num_cus = 0;
   uint32_t *grid = nullptr;  // IQ3_XXS codebook, 256 u32 on the device
   uint32_t grid_host[256];
+  // IQ3_XXS weights are accepted only once a codebook has been installed
+  // with gq_set_iq3xxs_grid: the library does not ship ggml's iq3xxs_grid,
+  // and a real IQ3_XXS tensor decoded with any other table is garbage.
+  bool grid_installed = false;
 };
 
 std::mutex g_mu;
@@ -79,7 +83,7 @@ int init_locked(int device) {
                 p.gcnArchName);
   g_dev.device = device;
   g_dev.num_cus = p.multiProcessorCount;
-  default_grid(g_dev.grid_host);
+  if (!g_dev.grid_installed) default_grid(g_dev.grid_host);
   if (!g_dev.grid) HIP_TRY(hipMalloc(&g_dev.grid, 1024));
   HIP_TRY(hipMemcpy(g_dev.grid, g_dev.grid_host, 1024, hipMemcpyHostToDevice));
   g_dev.ready = true;
@@ -142,6 +146,10 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   if (rc) return rc;
   if (!supported(dtype))
     return fail(GQ_EDTYPE, "matmul_dequant: unsupported dtype %s", type_name(dtype));
+  if (dtype == gq::T_IQ3_XXS && !g_dev.grid_installed)
+    return fail(GQ_EDTYPE,
+                "IQ3_XXS: no codebook installed; call gq_set_iq3xxs_grid with ggml's iq3xxs_grid "
+                "(or NULL for the built-in test codebook) before uploading IQ3_XXS tensors");
   if (in_dim <= 0 || out_dim < 0) return fail(GQ_EINVAL, "bad shape %d x %d", out_dim, in_dim);
   const int be = gq::block_elems(dtype);
   const int nb = (in_dim + be - 1) / be;
@@ -350,8 +358,13 @@ int gq_weight_shape(const gq_weight *w, int *dtype, int *in_dim, int *out_dim) {
 
 size_t gq_weight_bytes(const gq_weight *w) { return w ? w->ggml_bytes : 0; }
 
-int gq_matvec_multi(const gq_weight *const *ws, int count, const float *x_dev,
-                    float *const *y_dev, void *stream) {
+}  // extern "C"
+
+namespace {
+// y_i = W_i . x for weights sharing dtype and in_dim; q8k selects the
+// Q8_K route for Q5_K weights.
+int matvec_multi(const gq_weight *const *ws, int count, const float *x_dev, float *const *y_dev,
+                 void *stream, bool q8k) {
   int rc = ensure_init();
   if (rc) return rc;
   if (count <= 0 || !ws || !y_dev) return fail(GQ_EINVAL, "empty weight list");
@@ -364,15 +377,23 @@ int gq_matvec_multi(const gq_weight *const *ws, int count, const float *x_dev,
   if (!x_dev) return fail(GQ_EINVAL, "null x");
   gq::MvIn in;
   in.x = x_dev;
+  in.q8k = q8k;
   hipError_t e = gq::matvec_launch(ws, count, in, y_dev, (hipStream_t)stream);
   if (e != hipSuccess) return fail(GQ_EHIP, "matvec launch failed: %s", hipGetErrorString(e));
   return GQ_OK;
+}
+}  // namespace
+
+extern "C" {
+int gq_matvec_multi(const gq_weight *const *ws, int count, const float *x_dev,
+                    float *const *y_dev, void *stream) {
+  return matvec_multi(ws, count, x_dev, y_dev, stream, true);
 }
 
 int gq_matvec(const gq_weight *w, const float *x_dev, float *y_dev, void *stream) {
   const gq_weight *ws[1] = {w};
   float *ys[1] = {y_dev};
-  return gq_matvec_multi(ws, 1, x_dev, ys, stream);
+  return matvec_multi(ws, 1, x_dev, ys, stream, true);
 }
 
 int gq_matmul_dequant_preloaded(const gq_weight *w, const float *x_host, float *out_host) {
@@ -389,7 +410,12 @@ int gq_matmul_dequant_preloaded(const gq_weight *w, const float *x_host, float *
   }
   hipError_t e = hipMemcpy(xd, x_host, (size_t)w->L.k * 4, hipMemcpyHostToDevice);
   if (e == hipSuccess) {
-    rc = gq_matvec(w, xd, yd, nullptr);
+    // the float dot of every type, Q5_K included (matmul_dequant_preloaded
+    // runs the per-format dequant-dot kernels, wgpu_backend/mod.rs:642-696,
+    // like CpuBackend::matmul_dequant's dot_row)
+    const gq_weight *ws[1] = {w};
+    float *ys[1] = {yd};
+    rc = matvec_multi(ws, 1, xd, ys, nullptr, false);
     if (!rc) e = hipMemcpy(out_host, yd, (size_t)w->L.rows * 4, hipMemcpyDeviceToHost);
   }
   (void)hipFree(xd);
@@ -462,6 +488,18 @@ int gq_quantize_q8_32(const float *x_dev, int n, uint16_t *scale_dev, int8_t *q_
   return GQ_OK;
 }
 
+int gq_quantize_row_q8k(const float *x_dev, int n, float *d_dev, int8_t *qs_dev,
+                        int16_t *bsums_dev, void *stream) {
+  int rc = ensure_init();
+  if (rc) return rc;
+  if (n < 0) return fail(GQ_EINVAL, "negative length %d", n);
+  if (n == 0) return GQ_OK;
+  if (!x_dev || !d_dev || !qs_dev || !bsums_dev) return fail(GQ_EINVAL, "null Q8_K buffer");
+  hipError_t e = gq::launch_quantize_row_q8k(x_dev, n, d_dev, qs_dev, bsums_dev, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(GQ_EHIP, "quantize launch failed: %s", hipGetErrorString(e));
+  return GQ_OK;
+}
+
 int gq_set_iq3xxs_grid(const uint32_t *grid_host) {
   int rc = ensure_init();
   if (rc) return rc;
@@ -479,6 +517,7 @@ int gq_set_iq3xxs_grid(const uint32_t *grid_host) {
   }
   else default_grid(g_dev.grid_host);
   HIP_TRY(hipMemcpy(g_dev.grid, g_dev.grid_host, 1024, hipMemcpyHostToDevice));
+  g_dev.grid_installed = true;
   return GQ_OK;
 }
 
@@ -855,10 +894,14 @@ int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float 
     std::vector<float> lg((size_t)L.vocab);
     HIP_TRY(hipMemcpy(lg.data(), L.logits, lg.size() * 4, hipMemcpyDeviceToHost));
     if (logits_host) memcpy(logits_host, lg.data(), lg.size() * 4);
-    if (next_token) {  // first maximum (sampler.rs:120-131)
+    if (next_token) {  // first maximum from -inf, NaN never wins (sampler.rs:120-131)
       int best = 0;
-      for (int i = 1; i < L.vocab; i++)
-        if (lg[i] > lg[best]) best = i;
+      float bv = -INFINITY;
+      for (int i = 0; i < L.vocab; i++)
+        if (lg[i] > bv) {
+          bv = lg[i];
+          best = i;
+        }
       *next_token = best;
     }
   }

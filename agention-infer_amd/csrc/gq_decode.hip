@@ -583,6 +583,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     in.nw = m.attn_norm[L];
     in.xo = m.xb;
     in.eps = m.eps;
+    in.q8k = true;  // matmul_qkv_into -> matmul_into (cpu_path.rs:319-321)
     // One launch per distinct dtype among q/k/v (GGUF Q4_K_M files carry
     // attn_v in Q6_K on some layers); each launch recomputes the norm and
     // stores the same x_b.
@@ -630,6 +631,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
                          m.att_part, m.att);
     MvIn ain;
     ain.x = m.att;
+    ain.q8k = true;  // matmul_into (cpu_path.rs:757)
     const gq_weight *wo[1] = {m.wo[L]};
     float *proj[1] = {m.proj};
     if ((e = matvec_launch(wo, 1, ain, proj, s)) != hipSuccess) return e;
@@ -646,6 +648,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     if ((e = matvec_launch(gu, 2, fin, hout, s, true)) != hipSuccess) return e;
     MvIn din;
     din.x = m.h;
+    din.q8k = true;  // matmul_ffn_into's down: matmul_into (cpu_path.rs:383)
     const gq_weight *wd[1] = {m.wdown[L]};
     if ((e = matvec_launch(wd, 1, din, proj, s)) != hipSuccess) return e;
   }
@@ -656,6 +659,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
   hin.r = m.proj;
   hin.nw = m.output_norm;
   hin.eps = m.eps;
+  hin.q8k = true;  // the head: matmul_into (cpu_path.rs:815)
   const gq_weight *hw[1] = {m.lm_head};
   float *lo[1] = {m.logits};
   if ((e = matvec_launch(hw, 1, hin, lo, s)) != hipSuccess) return e;

@@ -158,4 +158,33 @@ hipError_t launch_quantize_q8_32(const float *x, long n, uint16_t *scale, int8_t
   return hipGetLastError();
 }
 
+// ------------------------------------------------------ Q8_K quantizer
+// quantize_row_q8_k (src/quant/q8_k.rs:49-91) of x[n]: 16 lanes per
+// 256-element block (16 elements each, zero past n), q8k_quant16 per block;
+// qs [nb*256] (zero padded), d [nb], bsums [nb*16].
+__global__ __launch_bounds__(256) void k_quantize_row_q8k(const float *x, long n, long nb, float *d,
+                                                          int8_t *qs, int16_t *bsums) {
+  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const long b = gid >> 4;
+  const int g = (int)(gid & 15);
+  const long e0 = b * 256 + 16 * g;
+  float xv[16];
+#pragma unroll
+  for (int i = 0; i < 16; i++) xv[i] = (b < nb && e0 + i < n) ? x[e0 + i] : 0.f;
+  const Q8K16 r = q8k_quant16(xv, 16 * g);
+  if (b >= nb) return;
+  *(uint4 *)(qs + e0) = make_uint4(r.q[0], r.q[1], r.q[2], r.q[3]);
+  bsums[b * 16 + g] = (int16_t)r.bsum;
+  if (g == 0) d[b] = r.d;
+}
+
+hipError_t launch_quantize_row_q8k(const float *x, long n, float *d, int8_t *qs, int16_t *bsums,
+                                   hipStream_t st) {
+  const long nb = (n + 255) / 256;
+  if (nb == 0) return hipSuccess;
+  hipLaunchKernelGGL(k_quantize_row_q8k, dim3((unsigned)((nb * 16 + 255) / 256)), dim3(256), 0, st,
+                     x, n, nb, d, qs, bsums);
+  return hipGetLastError();
+}
+
 }  // namespace gq

@@ -26,6 +26,10 @@
 namespace gq {
 
 enum : int { T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_IQ3_XXS = 18 };
+// Kernel-side id (not a ggml type) of Q5_K weights dotted against an input
+// quantized to Q8_K, the route WeightMap::matmul_into takes for Q5_K
+// (src/model/mod.rs:381-394).
+enum : int { T_Q5_K8 = 113 };
 
 // Device body bytes per block for each layout.
 __host__ __device__ constexpr int body_block_bytes(int t) {
@@ -86,6 +90,59 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
 // ksigns_iq2xs[i]: 7 sign bits plus an even-parity 8th bit.
 __device__ __forceinline__ uint32_t ksign7(uint32_t i) {
   return i | ((uint32_t)(__popc(i) & 1) << 7);
+}
+
+// quantize_row_q8_k (src/quant/q8_k.rs:49-91) of one 256-element block held
+// by 16 aligned lanes, 16 consecutive elements each (idx0 = index of this
+// lane's first element in the block).  The block's pivot is the first
+// element of largest magnitude (the reference's sequential `av > amax`
+// scan: lexicographic (magnitude, lowest index) across lanes), iscale =
+// -127 / pivot, q = min(round(iscale * x), 127) (round half away from zero),
+// d = 1 / iscale; an all-zero block has d = 0 and q = 0.  Returns the
+// lane's 16 codes as 4 dwords, their sum (the lane's bsums entry) and d.
+struct Q8K16 {
+  uint32_t q[4];
+  int bsum;
+  float d;
+};
+__device__ __forceinline__ Q8K16 q8k_quant16(const float (&xv)[16], int idx0) {
+  float amax = 0.f, mx = 0.f;
+  int ia = 0x7fffffff;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const float av = fabsf(xv[i]);
+    if (av > amax) {
+      amax = av;
+      mx = xv[i];
+      ia = idx0 + i;
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < 16; off <<= 1) {
+    const float oa = __shfl_xor(amax, off, 64), om = __shfl_xor(mx, off, 64);
+    const int oi = __shfl_xor(ia, off, 64);
+    if (oa > amax || (oa == amax && oi < ia)) {
+      amax = oa;
+      mx = om;
+      ia = oi;
+    }
+  }
+  Q8K16 r;
+  r.bsum = 0;
+  r.d = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; k++) r.q[k] = 0;
+  if (amax > 0.f) {
+    const float iscale = -127.0f / mx;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const int v = min((int)roundf(iscale * xv[i]), 127);
+      r.bsum += v;
+      r.q[i >> 2] |= ((uint32_t)v & 0xffu) << (8 * (i & 3));
+    }
+    r.d = 1.0f / iscale;
+  }
+  return r;
 }
 
 // Unsigned byte k of w as float (lowers to v_cvt_f32_ubyte{k}).

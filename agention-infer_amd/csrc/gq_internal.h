@@ -37,7 +37,7 @@ struct MvSeg {
 // (bytes in flight set the HBM throughput): 4 per SIMD for IQ3_XXS, 3 for
 // Q4_K/Q5_K, 2 for the others.
 __host__ __device__ constexpr int mv_threads(int fmt) {
-  return fmt == 18 ? 1024 : fmt == 12 || fmt == 13 ? 768 : 512;
+  return fmt == 18 ? 1024 : fmt == 12 || fmt == 13 || fmt == 113 ? 768 : 512;
 }
 constexpr int MV_BLOCKS_PER_CU = 1;
 
@@ -57,6 +57,10 @@ struct MvIn {
   float *xo = nullptr;        // MV_NORM: x + r written here (may be null)
   const int *tok = nullptr;   // MV_NORM: if set, x is row *tok of the table x
   float eps = 0.f;
+  // Q5_K weights: dot against the input quantized to Q8_K (matmul_into's
+  // route, src/model/mod.rs:381-394) instead of the float dot (dot_row,
+  // the route of CpuBackend::matmul_dequant and ffn_gate_up).
+  bool q8k = false;
 };
 
 struct MvArgs {
@@ -171,6 +175,10 @@ hipError_t launch_dequant(const gq_weight *w, const uint32_t *grid, int row0, in
 // Per-32 Q8 activation pack (KvDtype::Q8_0::pack).
 hipError_t launch_quantize_q8_32(const float *x, long n, uint16_t *scale, int8_t *q,
                                  hipStream_t st);
+
+// quantize_row_q8_k of x[n] (bit-identical to the reference).
+hipError_t launch_quantize_row_q8k(const float *x, long n, float *d, int8_t *qs, int16_t *bsums,
+                                   hipStream_t st);
 
 // Prefill GEMM.
 hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int mode,

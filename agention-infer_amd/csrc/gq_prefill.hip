@@ -584,6 +584,7 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
   hin.x = b.x + (long)(n - 1) * H;
   hin.nw = m.output_norm;
   hin.eps = m.eps;
+  hin.q8k = true;  // the head: matmul_into (cpu_path.rs:815)
   float *lo[1] = {m.logits};
   return matvec_launch(&m.lm_head, 1, hin, lo, s);
 }

@@ -50,6 +50,7 @@ SIGNATURES = {
     "gq_dequant_rows_host": (_I, [_P, _I, _I, _P]),
     "gq_gemm": (_I, [_P, _P, _I, _P, _I, _P]),
     "gq_quantize_q8_32": (_I, [_P, _I, _P, _P, _P]),
+    "gq_quantize_row_q8k": (_I, [_P, _I, _P, _P, _P, _P]),
     "gq_set_iq3xxs_grid": (_I, [_P]),
     "gq_get_iq3xxs_grid": (_I, [_P]),
     "gq_sync": (_I, [_P]),
@@ -293,6 +294,19 @@ class HipBackend:
         q = torch.empty(n, dtype=torch.int8, device=x_dev.device)
         _check(lib().gq_quantize_q8_32(_ptr(x_dev), n, _ptr(scale), _ptr(q), _stream(stream)))
         return scale, q
+
+    def quantize_row_q8_k(self, x_dev, stream=None):
+        """quantize_row_q8_k (q8_k.rs:49-91): (d f32[nb], qs int8[nb*256],
+        bsums int16[nb*16]) on the device."""
+        import torch
+        n = x_dev.numel()
+        nb = (n + 255) // 256
+        d = torch.empty(nb, dtype=torch.float32, device=x_dev.device)
+        qs = torch.empty(nb * 256, dtype=torch.int8, device=x_dev.device)
+        bs = torch.empty(nb * 16, dtype=torch.int16, device=x_dev.device)
+        _check(lib().gq_quantize_row_q8k(_ptr(x_dev), n, _ptr(d), _ptr(qs), _ptr(bs),
+                                         _stream(stream)))
+        return d, qs, bs
 
     def upload_experts(self, dtype, w, in_dim, rows_per_expert, n_experts):
         """A stacked expert tensor [n_experts][rows_per_expert][in_dim]."""

@@ -208,8 +208,11 @@ std::string MetadataValue::display_value() const {
 }
 
 size_t TensorInfo::n_elements() const {
+  // parse() rejects shapes whose product overflows; saturate for tensors
+  // built by other means
   size_t n = 1;
-  for (uint64_t d : dims) n *= (size_t)d;
+  for (uint64_t d : dims)
+    if (__builtin_mul_overflow(n, (size_t)d, &n)) return SIZE_MAX;
   return n;
 }
 std::string TensorInfo::shape_str() const {
@@ -295,7 +298,19 @@ GgufFile parse(const uint8_t *data, size_t len) {
     if (t.n_dims > (len - r.pos()) / 8)  // each dim is 8 bytes
       throw GgufError(GgufError::Kind::UnexpectedEof,
                       fmt("unexpected end of input at byte %llu", r.pos()), r.pos());
-    for (uint32_t d = 0; d < t.n_dims; d++) t.dims.push_back(r.le<uint64_t>());
+    uint64_t prod = 1;
+    bool wraps = false;
+    for (uint32_t d = 0; d < t.n_dims; d++) {
+      t.dims.push_back(r.le<uint64_t>());
+      wraps |= __builtin_mul_overflow(prod, t.dims.back(), &prod);
+    }
+    // An element count past 2^64 cannot be backed by the input (the
+    // reference's dims.product() would wrap and index the wrong bytes).
+    if (wraps)
+      throw GgufError(GgufError::Kind::UnexpectedEof,
+                      fmt("unexpected end of input at byte %llu", r.pos()) + " (tensor " + t.name +
+                          ": element count overflows)",
+                      r.pos());
     t.ggml_type = ggml_type_from_u32(r.le<uint32_t>());
     t.byte_offset = r.le<uint64_t>();
     f.tensors.push_back(std::move(t));

@@ -1,4 +1,5 @@
 // hip_backend.cpp -- see hip_backend.h.
+#include <climits>
 #include "hip_backend.h"
 
 namespace gqh {
@@ -61,6 +62,10 @@ GpuWeight HipBackend::upload_weight(GgmlType dtype, const uint8_t *w, size_t w_l
     throw GgufError(GgufError::Kind::BackendError,
                     "backend error: upload_weight: " + std::to_string(w_len) +
                         " bytes is not a whole number of rows of " + std::to_string(row));
+  if (in_dim > (size_t)INT_MAX || out_dim > (size_t)INT_MAX)
+    throw GgufError(GgufError::Kind::BackendError,
+                    "backend error: upload_weight: shape " + std::to_string(out_dim) + " x " +
+                        std::to_string(in_dim) + " exceeds the backend's 2^31-1 rows/columns");
   gq_weight *h = nullptr;
   check(gq_upload((int)dtype, w, w_len, (int)in_dim, (int)out_dim, &h));
   return GpuWeight(h);

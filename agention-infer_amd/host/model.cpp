@@ -1,4 +1,5 @@
 // model.cpp -- see model.h.
+#include <climits>
 #include "model.h"
 
 #include <algorithm>
@@ -102,6 +103,10 @@ std::vector<float> dequant_tensor(const TensorInfo &t, const uint8_t *bytes) {
   } else if (gpu_dequant_type(t.ggml_type)) {
     const size_t in_dim = t.dims.empty() ? 0 : t.dims[0], rows = outer(t);
     if (!n) return out;
+    if (in_dim > (size_t)INT_MAX || rows > (size_t)INT_MAX)
+      throw GgufError(GgufError::Kind::BackendError,
+                      "backend error: dequant: tensor " + t.name + " shape " + t.shape_str() +
+                          " exceeds the backend's 2^31-1 rows/columns");
     gq_weight *w = nullptr;
     check(gq_upload((int)t.ggml_type, bytes, t.byte_size(), (int)in_dim, (int)rows, &w));
     GpuWeight hold(w);

@@ -128,6 +128,7 @@ def moe_leg(be, gq, syn, torch, cpu):
     GB/s counts the weight bytes of the distinct experts a call touches."""
     E, H, F, K = 256, 3072, 1536, 8
     IQ3 = 18
+    be.set_iq3xxs_grid(None)  # the library's test codebook (synthetic weights)
     gw = syn.make_blocks(IQ3, E * F, H, seed=41)
     uw = syn.make_blocks(IQ3, E * F, H, seed=42)
     dw = syn.make_blocks(IQ3, E * H, F, seed=43)

@@ -76,8 +76,11 @@ int gq_weight_shape(const gq_weight *w, int *dtype, int *in_dim, int *out_dim);
 /* Device bytes held by the handle (equals the ggml tensor size). */
 size_t gq_weight_bytes(const gq_weight *w);
 
-/* launch_only / launch_only_f32out (src/ops/wgpu_backend/resident.rs:13-69):
- * y_dev[out_dim] = W . x_dev[in_dim], fp32 in and out, no readback. */
+/* launch_only / launch_only_f32out (src/ops/wgpu_backend/resident.rs:13-69)
+ * with the arithmetic of WeightMap::matmul_into (src/model/mod.rs:362-403):
+ * y_dev[out_dim] = W . x_dev[in_dim], fp32 in and out, no readback.  Q5_K
+ * weights take matmul_into's route: x quantized to Q8_K, then
+ * dot_q5_k_q8k per row (mod.rs:381-394); every other type the float dot. */
 int gq_matvec(const gq_weight *w, const float *x_dev, float *y_dev, void *stream);
 
 /* matmul_dequant_qkv / _multi / _ffn (src/ops/wgpu_backend/mod.rs:702-854):
@@ -87,12 +90,14 @@ int gq_matvec_multi(const gq_weight *const *w, int count, const float *x_dev,
                     float *const *y_dev, void *stream);
 
 /* matmul_dequant_preloaded (src/ops/wgpu_backend/mod.rs:642-696):
- * host x in, host out, synchronous. */
+ * host x in, host out, synchronous.  The float dot of every type, Q5_K
+ * included (Backend::matmul_dequant's dot_row). */
 int gq_matmul_dequant_preloaded(const gq_weight *w, const float *x_host, float *out_host);
 
 /* Backend::matmul_dequant (src/ops/mod.rs:105, cpu_backend.rs:38-65):
  * w_host is the whole tensor (out_dim rows of type_size(in_dim) bytes);
- * out_host[out_dim] is overwritten.  Uploads, runs, reads back. */
+ * out_host[out_dim] is overwritten.  Uploads, runs, reads back.  The float
+ * dot (dot_row) of every type, Q5_K included. */
 int gq_matmul_dequant_host(int dtype, const void *w_host, size_t nbytes, const float *x_host,
                            size_t in_dim, float *out_host, size_t out_dim);
 
@@ -117,9 +122,19 @@ int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mod
 int gq_quantize_q8_32(const float *x_dev, int n, uint16_t *scale_dev, int8_t *q_dev,
                       void *stream);
 
+/* quantize_row_q8_k (src/quant/q8_k.rs:49-91) of x_dev[n]: per 256-element
+ * block d_dev[nb] (f32), qs_dev[nb*256] (int8, zero past n) and
+ * bsums_dev[nb*16] (int16), nb = ceil(n / 256); bit-identical to the
+ * reference.  This is the input quantization gq_matvec applies for Q5_K. */
+int gq_quantize_row_q8k(const float *x_dev, int n, float *d_dev, int8_t *qs_dev,
+                        int16_t *bsums_dev, void *stream);
+
 /* IQ3_XXS codebook (256 entries, 4 magnitude bytes each).  The reference
- * has no IQ3_XXS implementation (src/quant/mod.rs:7,38-41); the default is
- * a placeholder until the caller installs ggml's iq3xxs_grid. */
+ * has no IQ3_XXS implementation (src/quant/mod.rs:7,38-41) and the library
+ * does not ship ggml's iq3xxs_grid: IQ3_XXS uploads fail with GQ_EDTYPE
+ * until the caller installs a codebook.  NULL installs a built-in test
+ * codebook (a fixed hash over ggml's magnitude alphabet) for synthetic
+ * weights; it cannot decode a real IQ3_XXS tensor. */
 int gq_set_iq3xxs_grid(const uint32_t *grid_host);
 int gq_get_iq3xxs_grid(uint32_t *grid_host);
 

@@ -598,13 +598,73 @@ static int run_jobs(job_t *proto, size_t rows, int nthreads, void *(*fn)(void *)
     return rc;
 }
 
-/* model/mod.rs:362-403 */
-int gqo_matmul_into(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
+/* Rows through the per-format float dot (quant::dot_row), row-parallel:
+ * the non-Q5_K branch of WeightMap::matmul_into (model/mod.rs:396-402) and
+ * the per-row dots of ffn_gate_up (cpu_path.rs:222-229). */
+int gqo_matmul_rows(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
                     float *out, size_t out_dim, int nthreads) {
     if (!gqo_block_size(dtype) || dtype == GQO_F32 || dtype == GQO_F16 || dtype == GQO_BF16)
         return GQO_EDTYPE;
     job_t p = {dtype, w, nbytes, in_dim, 0, 0, 0, x, out, 0};
     return run_jobs(&p, out_dim, nthreads, matvec_job);
+}
+
+typedef struct {
+    const uint8_t *w;
+    size_t nbytes, in_dim, r0, r1;
+    const float *d8;
+    const int8_t *q8;
+    const int16_t *bs;
+    float *out;
+    int rc;
+} q8k_job;
+
+static void *q8k_rows_job(void *p) {
+    q8k_job *j = (q8k_job *)p;
+    size_t rb = gqo_type_size(GQO_Q5_K, j->in_dim);
+    for (size_t r = j->r0; r < j->r1 && !j->rc; r++) {
+        size_t off = r * rb;
+        if (off + rb > j->nbytes) { j->rc = GQO_ESHORT; break; }
+        j->rc = gqo_dot_q5_k_q8k(j->w + off, j->nbytes - off, j->in_dim, j->d8, j->q8, j->bs,
+                                 &j->out[r]);
+    }
+    return NULL;
+}
+
+/* model/mod.rs:362-403: Q5_K quantizes x to Q8_K once (q8_k.rs:49-91) and
+ * runs dot_q5_k_q8k (q5_k.rs:126-184) per row (model/mod.rs:381-394);
+ * every other type takes quant::dot_row. */
+int gqo_matmul_into(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
+                    float *out, size_t out_dim, int nthreads) {
+    if (dtype != GQO_Q5_K) return gqo_matmul_rows(dtype, w, nbytes, x, in_dim, out, out_dim, nthreads);
+    size_t nb = (in_dim + 255) / 256;
+    float *d8 = (float *)malloc(sizeof(float) * (nb ? nb : 1));
+    int8_t *q8 = (int8_t *)malloc(nb ? nb * 256 : 1);
+    int16_t *bs = (int16_t *)malloc(sizeof(int16_t) * (nb ? nb * 16 : 1));
+    gqo_quantize_row_q8_k(x, in_dim, d8, q8, bs);
+    int nt = hw_threads(nthreads);
+    if ((size_t)nt > out_dim) nt = out_dim ? (int)out_dim : 1;
+    if (nt > 256) nt = 256;
+    pthread_t th[256];
+    q8k_job jobs[256];
+    size_t per = (out_dim + nt - 1) / nt;
+    for (int t = 0; t < nt; t++) {
+        size_t r0 = (size_t)t * per < out_dim ? (size_t)t * per : out_dim;
+        size_t r1 = r0 + per < out_dim ? r0 + per : out_dim;
+        q8k_job j = {w, nbytes, in_dim, r0, r1, d8, q8, bs, out, 0};
+        jobs[t] = j;
+        if (nt == 1) q8k_rows_job(&jobs[t]);
+        else pthread_create(&th[t], NULL, q8k_rows_job, &jobs[t]);
+    }
+    int rc = 0;
+    for (int t = 0; t < nt; t++) {
+        if (nt > 1) pthread_join(th[t], NULL);
+        if (jobs[t].rc && !rc) rc = jobs[t].rc;
+    }
+    free(d8);
+    free(q8);
+    free(bs);
+    return rc;
 }
 
 /* cpu_backend.rs:38-65 */
@@ -882,8 +942,10 @@ int gqo_decode_step(const gqo_model *m, int token, int pos, float *logits, int n
         rc |= gqo_matmul_into(to, m->wo[L], gqo_type_size(to, nh * hd) * H, att, nh * hd, proj, H, nthreads);
         for (int i = 0; i < H; i++) x[i] += proj[i];
         rms_norm(x, m->ffn_norm[L], H, m->eps, xn);
-        rc |= gqo_matmul_into(tg, m->wgate[L], gqo_type_size(tg, H) * F, xn, H, g, F, nthreads);
-        rc |= gqo_matmul_into(tu, m->wup[L], gqo_type_size(tu, H) * F, xn, H, u, F, nthreads);
+        /* ffn_gate_up (cpu_path.rs:200-232): quant::dot_row per row for
+         * every type (no Q8_K branch, unlike matmul_into) */
+        rc |= gqo_matmul_rows(tg, m->wgate[L], gqo_type_size(tg, H) * F, xn, H, g, F, nthreads);
+        rc |= gqo_matmul_rows(tu, m->wup[L], gqo_type_size(tu, H) * F, xn, H, u, F, nthreads);
         for (int i = 0; i < F; i++) act[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
         rc |= gqo_matmul_into(td, m->wdown[L], gqo_type_size(td, F) * H, act, F, proj, H, nthreads);
         for (int i = 0; i < H; i++) x[i] += proj[i];

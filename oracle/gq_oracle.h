@@ -70,8 +70,14 @@ void gqo_set_iq3xxs_grid(const uint32_t *grid);
 void gqo_get_iq3xxs_grid(uint32_t *grid);
 
 /* WeightMap::matmul_into (model/mod.rs:362-403): out[r] = dot_row(W, r, x),
- * rows partitioned over nthreads (0 = hardware concurrency). */
+ * rows partitioned over nthreads (0 = hardware concurrency); for Q5_K x is
+ * quantized to Q8_K once and every row runs dot_q5_k_q8k (mod.rs:381-394). */
 int gqo_matmul_into(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
+                    float *out, size_t out_dim, int nthreads);
+
+/* out[r] = quant::dot_row(W, r, x) for every type (the float dot, also for
+ * Q5_K), row-parallel: ffn_gate_up's per-row dots (cpu_path.rs:222-229). */
+int gqo_matmul_rows(int dtype, const uint8_t *w, size_t nbytes, const float *x, size_t in_dim,
                     float *out, size_t out_dim, int nthreads);
 
 /* CpuBackend::matmul_dequant (cpu_backend.rs:38-65): serial row loop. */

@@ -41,6 +41,7 @@ def lib():
             "gqo_set_iq3xxs_grid": (None, [_P]),
             "gqo_get_iq3xxs_grid": (None, [_P]),
             "gqo_matmul_into": (_I, [_I, _P, _SZ, _P, _SZ, _P, _SZ, _I]),
+            "gqo_matmul_rows": (_I, [_I, _P, _SZ, _P, _SZ, _P, _SZ, _I]),
             "gqo_matmul_dequant": (_I, [_I, _P, _SZ, _P, _SZ, _P, _SZ]),
             "gqo_matmul_batch_into": (_I, [_I, _P, _SZ, _P, _SZ, _SZ, _P, _SZ, _I]),
             "gqo_argmax": (_SZ, [_P, _SZ]),
@@ -150,11 +151,22 @@ def get_iq3xxs_grid():
 
 
 def matmul_into(dtype, w, x, out_dim, nthreads=0):
-    """WeightMap::matmul_into: threaded row-parallel fused dot."""
+    """WeightMap::matmul_into: threaded row-parallel fused dot (Q5_K: x to
+    Q8_K once, then dot_q5_k_q8k per row, model/mod.rs:381-394)."""
     w = np.ascontiguousarray(w, np.uint8)
     x = np.ascontiguousarray(x, np.float32)
     out = np.zeros(out_dim, np.float32)
     _chk(lib().gqo_matmul_into(dtype, _p(w), w.nbytes, _p(x), x.size, _p(out), out_dim, nthreads))
+    return out
+
+
+def matmul_rows(dtype, w, x, out_dim, nthreads=0):
+    """quant::dot_row per row for every type (ffn_gate_up's float dots; for
+    Q5_K this differs from matmul_into, which takes the Q8_K int dot)."""
+    w = np.ascontiguousarray(w, np.uint8)
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros(out_dim, np.float32)
+    _chk(lib().gqo_matmul_rows(dtype, _p(w), w.nbytes, _p(x), x.size, _p(out), out_dim, nthreads))
     return out
 
 

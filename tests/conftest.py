@@ -23,4 +23,9 @@ def orc():
 @pytest.fixture(scope="session")
 def backend():
     import gq
-    return gq.create_backend("hip")
+    be = gq.create_backend("hip")
+    # IQ3_XXS weights need a codebook installed first: the synthetic
+    # weights of the tests use the library's built-in test codebook (the
+    # oracle's default table).
+    be.set_iq3xxs_grid(None)
+    return be

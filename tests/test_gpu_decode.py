@@ -104,34 +104,52 @@ def test_generate_edges(backend):
         gm.decode(1, cfg["ctx"])
 
 
-@pytest.mark.timeout(900)
+@pytest.mark.timeout(1200)
 def test_generate_qwen25_7b_shape(backend):
-    """the 7B Q4_K_M shape, 4096 prefilled KV rows.
-    With the specified N(0, 1) embedding the greedy token is the same at
-    every step (the layers' per-block weight biases dominate), so a second
-    model over the same uploaded weights, with the embedding scaled by 1e5,
-    checks a varying token stream as well; both must match the oracle's
-    greedy tokens, and the first step's logits agree to LOGIT_TOL."""
+    """the 7B Q4_K_M shape, 4096 cached positions, 128
+    greedy steps.  The embedding is scaled by 1e5 so the token stream
+    varies (with the specified N(0, 1) embedding the layers' per-block
+    weight biases dominate and the greedy token is the same at every step;
+    that stream is checked for 24 steps).  Two caches:
+      * 4096 random f16 rows uploaded (KvCache::write_range);
+      * the cache gq_model_prefill writes for 4096 random token ids, read
+        back and given to the oracle as its prefilled context.
+    Both streams must equal the oracle's greedy tokens for all 128 steps,
+    and each first step's logits agree to LOGIT_TOL."""
     import gq
-    cfg = dict(syn.QWEN25_7B, ctx=4096 + 64)
+    cfg = dict(syn.QWEN25_7B, ctx=4096 + 160)
     w = syn.make_decoder(cfg, 11)
     kv = syn.make_kv(cfg, 4096, 12)
     hw = syn.upload_decoder(backend, cfg, w)
-    for scale, n_steps in ((1.0, 24), (1e5, 16)):
+    for scale, n_steps, prefill in ((1.0, 24, False), (1e5, 128, False), (1e5, 128, True)):
+        print(f"7b stream: embedding x{scale:g}, {n_steps} steps, "
+              f"{'prefilled by gq_model_prefill' if prefill else 'uploaded KV'}", flush=True)
         ws = dict(w, embd=w["embd"] * np.float32(scale)) if scale != 1.0 else w
-        gm = gq.DecodeModel(dict(cfg, max_tokens=64), dict(hw, embd=ws["embd"]))
-        for l in range(cfg["n_layers"]):
-            gm.kv_upload(l, kv[0][l], kv[1][l])
-        om = oracle.DecoderModel(cfg, ws, kv)
-        ref0 = om.step(1234, 4096)
-        nxt, got0 = gm.decode(1234, 4096)
+        gm = gq.DecodeModel(dict(cfg, max_tokens=160), dict(hw, embd=ws["embd"]))
+        if prefill:
+            toks = np.random.default_rng(13).integers(0, cfg["vocab"], 4096).astype(np.int32)
+            first, _ = gm.prefill(toks, 0, want_logits=False)
+            cache = [[], []]
+            for l in range(cfg["n_layers"]):
+                k, v = gm.kv_download(l, 4096)
+                cache[0].append(k)
+                cache[1].append(v)
+            ckv = (np.stack(cache[0]), np.stack(cache[1]))
+        else:
+            first = 1234
+            for l in range(cfg["n_layers"]):
+                gm.kv_upload(l, kv[0][l], kv[1][l])
+            ckv = kv
+        om = oracle.DecoderModel(cfg, ws, ckv)
+        ref0 = om.step(int(first), 4096)
+        nxt, got0 = gm.decode(int(first), 4096)
         assert np.abs(got0 - ref0).max() <= LOGIT_TOL * np.abs(ref0).max()
         assert nxt == oracle.argmax(ref0)
         ref = [nxt] + list(_oracle_greedy(om, nxt, 4097, n_steps - 1))
-        got = gm.generate(1234, 4096, n_steps)
+        got = gm.generate(int(first), 4096, n_steps)
         np.testing.assert_array_equal(got, np.array(ref, np.int32))
         if scale != 1.0:
-            assert len(set(ref)) > 1, "token stream should vary"
+            assert len(set(ref)) > 8, "token stream should vary"
         del gm, om
 
 

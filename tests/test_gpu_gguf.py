@@ -118,8 +118,14 @@ def test_gguf_upload_tensor_matvec(backend, tmp_path, dtype):
     assert h.shape() == (dtype, cols) and h.out_dim() == rows
     x = np.random.default_rng(dtype).standard_normal(cols).astype(np.float32)
     out = np.zeros(rows, np.float32)
+    # Backend::matmul_dequant_preloaded: the float dot of every type
     backend.matmul_dequant_preloaded(h, x, out)
-    ref = oracle.matmul_into(dtype, wb, x, rows)
+    ref = oracle.matmul_dequant(dtype, wb, x, rows)
     assert np.abs(out - ref).max() <= 1e-4 * np.abs(ref).max()
+    # launch_only follows matmul_into (Q5_K: the Q8_K route)
+    import torch
+    y = h.launch_only(torch.from_numpy(x).cuda()).cpu().numpy()
+    ref = oracle.matmul_into(dtype, wb, x, rows)
+    assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max()
     with pytest.raises(gq.GgufError):
         f.upload("norm")  # 1-D F32: not a weight the backend multiplies

@@ -150,3 +150,26 @@ def test_prefill_errors(backend):
     gq8 = _build(backend, q8, seed=4, n_ctx=0)[0]
     with pytest.raises(gq.GqError, match="Q4_K or Q6_K"):
         gq8.prefill(np.zeros(4, np.int32), 0)
+
+
+def test_prefill_next_token_skips_nan(backend):
+    """A NaN logit at index 0 (the head's row 0 has a NaN scale) never wins
+    the greedy pick: prefill's next token, decode's and the sampler's
+    first-maximum rule from -inf (sampler.rs:120-131) agree."""
+    import gq
+    cfg = SMALL
+    w = syn.make_decoder(cfg, 41, embd_scale=1e4)
+    head = w["lm_head"].copy()
+    head[0, 208:210] = np.array([0x7E00], np.uint16).view(np.uint8)  # Q6_K d of row 0, block 0
+    w["lm_head"] = head
+    hw = syn.upload_decoder(backend, cfg, w)
+    gm = gq.DecodeModel(dict(cfg, max_tokens=64), hw)
+    toks = np.array([3, 14, 15, 92], np.int32)
+    nxt, lg = gm.prefill(toks, 0)
+    assert np.isnan(lg[0]) and not np.isnan(lg[1:]).any()
+    assert nxt == int(np.nanargmax(lg)) == oracle.argmax(lg)
+    gm2 = gq.DecodeModel(dict(cfg, max_tokens=64), hw)
+    for pos, t in enumerate(toks[:-1]):
+        gm2.decode(int(t), pos, want_logits=False)
+    nxt2, lg2 = gm2.decode(int(toks[-1]), len(toks) - 1)
+    assert np.isnan(lg2[0]) and nxt2 == oracle.argmax(lg2)

@@ -256,3 +256,14 @@ def test_model_load_missing_head_count(tmp_path):
     with pytest.raises(gq.GgufError) as e:
         g.load_model()
     assert _code(e) == -107 and "attention.head_count" in str(e.value)
+
+
+def test_tensor_dims_overflow_rejected():
+    """A tensor whose element count overflows 64 bits cannot be backed by
+    the file: parse fails (UnexpectedEof) instead of wrapping the count."""
+    data, _ = gw.build_file(tensors=[("w", [1 << 33, 1 << 33], 12, b"")])
+    with pytest.raises(gq.GgufError, match="overflows"):
+        _gguf(data)
+    # the largest product that fits is parsed (its data is checked on access)
+    data, _ = gw.build_file(tensors=[("w", [1 << 31, 1 << 32], 12, b"")])
+    assert _gguf(data).tensors[0].dims == [1 << 31, 1 << 32]

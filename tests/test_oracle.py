@@ -303,6 +303,53 @@ def test_iq3_grid_install(orc):
     assert np.array_equal(orc.get_iq3xxs_grid(), g0)
 
 
+def test_iq3_one_hot_fields(orc):
+    """Scale nibbles, sign indices and grid slots of the oracle's IQ3_XXS
+    dequant against closed forms (tests/iq3_onehot.py)."""
+    import iq3_onehot as oh
+    g0 = orc.get_iq3xxs_grid()
+    orc.set_iq3xxs_grid(oh.IDENT_GRID)
+    try:
+        b, exp = oh.scale_blocks(oh.IDENT_GRID)
+        y = orc.dequant(IQ3, b.reshape(-1), 16 * 256).reshape(16, 256)
+        assert np.array_equal(y.astype(np.float64), exp)
+        b, mags, idx = oh.sign_blocks(oh.IDENT_GRID)
+        oh.check_signs(orc.dequant(IQ3, b.reshape(-1), 4 * 256).reshape(4, 256), mags, idx)
+        b, exp = oh.grid_blocks(oh.IDENT_GRID)
+        y = orc.dequant(IQ3, b.reshape(-1), 4 * 256).reshape(4, 256)
+        assert np.array_equal(y.astype(np.float64), exp)
+    finally:
+        orc.set_iq3xxs_grid(g0)
+
+
+def test_matmul_into_q5_k_takes_the_q8_k_route(orc):
+    """model/mod.rs:381-394: for Q5_K, matmul_into quantizes x to Q8_K once
+    and runs dot_q5_k_q8k per row; CpuBackend::matmul_dequant and
+    ffn_gate_up run the float dot_row.  The two routes differ by the Q8_K
+    rounding of x (about 1/254 of a block's max per element)."""
+    rows, n = 40, 1024
+    w = syn.make_blocks(Q5_K, rows, n, seed=31)
+    x = syn.make_x(n, seed=32)
+    y = orc.matmul_into(Q5_K, w, x, rows, nthreads=3)
+    d, qs, bs = orc.quantize_row_q8_k(x)
+    assert np.array_equal(y, np.array([orc.dot_q5_k_q8k(w[r], n, d, qs, bs) for r in range(rows)],
+                                      np.float32))
+    yf = orc.matmul_rows(Q5_K, w, x, rows)
+    assert np.array_equal(yf, orc.matmul_dequant(Q5_K, w, x, rows))
+    assert np.array_equal(yf, np.array([orc.dot_row(Q5_K, w[r], x) for r in range(rows)], np.float32))
+    gap = np.abs(y - yf).max() / np.abs(yf).max()
+    assert 1e-4 < gap < 2e-2, gap
+    # Q8_K x against the exact float dot: the quantized-x product in fp64
+    xq = (np.repeat(d, 256) * qs.astype(np.float32)).astype(np.float64)[:n]
+    W = np.stack([npref.dequant_k4(w[r], n, q5=True) for r in range(rows)]).astype(np.float64)
+    ref = W @ xq
+    assert np.abs(y - ref).max() <= 1e-5 * np.abs(ref).max()
+    # the other types: matmul_into == matmul_rows
+    w4 = syn.make_blocks(Q4_K, 8, 512, seed=2)
+    x4 = syn.make_x(512, seed=3)
+    assert np.array_equal(orc.matmul_into(Q4_K, w4, x4, 8), orc.matmul_rows(Q4_K, w4, x4, 8))
+
+
 def test_argmax_first_max_wins(orc):
     # sampler.rs:120-131
     assert orc.argmax(np.array([1, 3, 3, 2], np.float32)) == 1
