@@ -126,6 +126,11 @@ size_t matvec_block_lds(const gq_weight *w, bool pair) {
   a.pair = pair;
   a.nseg = 1;
   a.seg[0].rows = std::max(w->L.rows, 1);
+  if (w->L.quad) {
+    a.nseg = pair ? 2 : 1;
+    a.seg[1].rows = a.seg[0].rows;
+    return gq::mvq_plan(a, g_dev.num_cus);
+  }
   return gq::matvec_plan(a, g_dev.num_cus);
 }
 
@@ -166,6 +171,9 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   w->L.units = (in_dim + 255) / 256;
   w->L.chunks = gq::unit_chunks(dtype);
   w->L.rt = std::max(out_dim, 1);  // one tile: the whole matrix
+  // Dense Q4_K / Q5_K / Q6_K / Q8_0 matrices take the quad layout of the
+  // MFMA matvec; IQ3_XXS and stacked expert tensors the wave-tiled one.
+  w->L.quad = rows_per_group == 0 && dtype != gq::T_IQ3_XXS;
   // Stacked expert tensors: one tile per expert.
   if (rows_per_group > 0) w->L.rt = rows_per_group;
   w->ggml_bytes = need;
@@ -225,6 +233,7 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
     a.nseg = 2;
     a.seg[0] = MvSeg{w0->body, w0->d, ys[0], w0->L.rows, 0, 0};
     a.seg[1] = MvSeg{ws[1]->body, ws[1]->d, nullptr, ws[1]->L.rows, 0, 0};
+    if (w0->L.quad) return launch_mvq(a, mvq_plan(a, g_dev.num_cus), st);
     matvec_plan(a, g_dev.num_cus);
     return launch_matvec(a, w0->L.dtype, st);
   }
@@ -244,8 +253,13 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
     }
     if (ns == 0) continue;
     a.nseg = ns;
-    matvec_plan(a, g_dev.num_cus);
-    hipError_t e = launch_matvec(a, w0->L.dtype, st);
+    hipError_t e;
+    if (w0->L.quad) {
+      e = launch_mvq(a, mvq_plan(a, g_dev.num_cus), st);
+    } else {
+      matvec_plan(a, g_dev.num_cus);
+      e = launch_matvec(a, w0->L.dtype, st);
+    }
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

@@ -64,6 +64,14 @@ __device__ __forceinline__ uint32_t ldh(const uint16_t *p) {
   return __builtin_nontemporal_load(p);
 }
 
+// Dword k of an array of 16-byte chunks (k a compile-time constant after
+// unrolling, so this is a register pick).
+__device__ __forceinline__ uint32_t dw(const uint4 *ch, int k) {
+  const uint4 c = ch[k >> 2];
+  const int m = k & 3;
+  return m == 0 ? c.x : m == 1 ? c.y : m == 2 ? c.z : c.w;
+}
+
 // IEEE binary16 -> binary32 (exact; v_cvt_f32_f16 keeps f16 subnormals).
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));

@@ -71,6 +71,8 @@ struct MvArgs {
   int blocks;
   int pair;              // 1: seg[0] = gate, seg[1] = up (same shape); y0 = silu(g) * u
   int nseg;
+  int groups;            // quad layout: 16-row groups of all segments (seg[i].blk_begin
+                         // is then the first of segment i)
   MvSeg seg[MV_MAX_SEG];
 };
 
@@ -106,6 +108,10 @@ size_t matvec_lds_bytes(int dtype, int units, int part_total);
 // size the partial-sum region; returns the LDS bytes a block needs.
 size_t matvec_plan(MvArgs &a, int num_cus);
 hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st);
+// The MFMA matvec over quad-layout weights (Q4_K, Q5_K, Q6_K, Q8_0): plan
+// (returns the LDS bytes of a block) and launch.
+size_t mvq_plan(MvArgs &a, int num_cus);
+hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st);
 
 // Decode step state in device memory (advanced by the argmax kernel).
 struct DecodeState {

@@ -19,6 +19,16 @@
 //   IQ3_XXS bytes 2..97 (qs, signs/scales); d separately   C = 6
 //   Q8_0    qs of blocks 0..7 (8 x 32 B), then their 8 f16 d  C = 17
 // "d separately": one f16 per unit at index (tile * RT * U + j).
+//
+// Quad layout (quad = 1; dense Q4_K / Q5_K / Q6_K / Q8_0 matrices, for the
+// MFMA matvec): rows in groups of 16 (the last group has nr = R % 16 rows
+// if that is not 0), units in quads of 4 (the last quad of a row has
+// nq = U % 4 units if that is not 0).  An item is (row group g, quad t):
+// its nv = nr * nq units sit in lanes nr * q + r (row 16g + r, unit
+// 4t + q), and memory holds chunk 0 of the item's nv units (16 B each),
+// then chunk 1, ...; items follow each other row group by row group, quad
+// by quad.  A full item is one wave-wide 1 KiB load per chunk.  No padding;
+// the d array (Q6_K) holds the units in the same item / lane order.
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -34,7 +44,18 @@ struct Layout {
   int rt;      // rows per tile: all rows (one tile) for matvec weights; a
                // power of two <= 64 dividing the rows per expert for stacked
                // expert tensors
+  int quad;    // 1: the quad layout (one tile, rt = rows)
 };
+
+constexpr int QROWS = 16;  // rows per row group of the quad layout
+
+// Quad layout: first unit index (in the item / lane order of the body and
+// d array) of item (g, t), its row count nr and unit count nq.
+__host__ __device__ inline long quad_item_unit(const Layout &L, int g, int t, int &nr, int &nq) {
+  nr = min(QROWS, L.rows - QROWS * g);
+  nq = min(4, L.units - 4 * t);
+  return (long)g * QROWS * L.units + (long)t * 4 * nr;
+}
 
 __host__ __device__ constexpr int unit_chunks(int t) {
   return t == 12 ? 9 : t == 13 ? 11 : t == 14 ? 13 : t == 18 ? 6 : t == 8 ? 17 : 0;
@@ -42,6 +63,12 @@ __host__ __device__ constexpr int unit_chunks(int t) {
 
 // Byte offset of chunk c of unit j (0 <= j < units in tile) of tile t.
 __host__ __device__ inline long chunk_offset(const Layout &L, int t, int j, int c) {
+  if (L.quad) {  // one tile; j = row * U + unit
+    const int row = j / L.units, u = j - row * L.units;
+    int nr, nq;
+    const long base = quad_item_unit(L, row / QROWS, u >> 2, nr, nq);
+    return (base * L.chunks + (long)c * nr * nq + (long)nr * (u & 3) + row % QROWS) * 16;
+  }
   const long tile_units = (long)L.rt * L.units;
   const int rows_here = min(L.rt, L.rows - t * L.rt);
   const int uit = rows_here * L.units;  // units in this tile
@@ -54,6 +81,11 @@ __host__ __device__ inline long chunk_offset(const Layout &L, int t, int j, int 
 }
 
 __host__ __device__ inline long unit_index(const Layout &L, int t, int j) {
+  if (L.quad) {
+    const int row = j / L.units, u = j - row * L.units;
+    int nr, nq;
+    return quad_item_unit(L, row / QROWS, u >> 2, nr, nq) + (long)nr * (u & 3) + row % QROWS;
+  }
   return (long)t * L.rt * L.units + j;
 }
 

@@ -1,0 +1,571 @@
+// gq_mvq.hip -- batch-1 decode matvec y = W . x on int8 MFMA for dense
+// Q4_K, Q5_K, Q6_K and Q8_0 weights (gfx950, wave64).
+//
+// Replaces the reference's per-row dot kernels (src/quant/q8_0.rs:58-90,
+// q4_k.rs:95-212, q5_k.rs:126-184 and 189-317, q6_k.rs:82-131) driven
+// row-parallel by WeightMap::matmul_into (src/model/mod.rs:362-403).
+//
+// Weights are in the quad layout (gq_layout.h): a wave-wide load of one
+// chunk of an item (16 rows x 4 units) is 1 KiB of contiguous HBM, and lane
+// l = 16q + r holds the whole unit (row r, unit q) -- every weight byte is
+// read once, by one lane.
+//
+// x is staged once per block in LDS as three int8 limbs per element: per
+// 256-element unit, s = max|x| / (127 * 2^16) and X = rint(x / s) =
+// x2 * 2^16 + x1 * 2^8 + x0 (signed bytes), so |x - s * X| <= s / 2 (6e-8
+// of the unit's max).
+//
+// The products run on v_mfma_i32_16x16x64_i8, D = A * B:
+//   * B = 16 weight codes of each lane's unit (col r = row r of the group,
+//     k-group q = unit q);
+//   * A = block-diagonal x: row 4q + i holds limb i of unit q's 16 inputs in
+//     k-group q and zero elsewhere (lanes 20q + i read 16 limb bytes from
+//     LDS, all other lanes read a zero region).
+// Lane 16q + r then holds D[4q + i][r] = sum(codes of (r, q) * limb i of
+// unit q): every sum of a lane is its own unit's, so the sub-block scales
+// apply in the lane, in exact integer arithmetic where the format allows:
+//   Q4_K/Q5_K  acc_i = sum_sb sc_sb * D_sb,i  (i32)
+//              y += d * s * (acc_2 2^16 + acc_1 2^8 + acc_0) - dmin * sum_sb m_sb * sum(x_sb)
+//   Q6_K       acc_i = sum_run sc_run * D_run,i (codes q in 0..63), and
+//              -32 * sum_run sc_run * sum(X_run) for the code offset
+//   Q8_0       y += s * sum_b d_b * (D_b,2 2^16 + D_b,1 2^8 + D_b,0)
+//   Q5_K x Q8_K (matmul_into's route): A holds the Q8_K codes (one limb)
+//              and the block term dx * (d * acc_pos - dmin * acc_min) is
+//              the reference's, exactly.
+// The four lanes of a row add their units (lane swaps), waves write per-row
+// partial sums to LDS, and the block adds them per row in a fixed order
+// (deterministic results).
+//
+// Work split: block b owns the row groups [G b / B, G (b + 1) / B) of the
+// launch (all segments' groups in a row); its items (group, matrix, quad)
+// are split into NW equal contiguous ranges, one per wave.  Each lane keeps
+// its next item in flight while it computes the current one.
+#include <algorithm>
+#include <cmath>
+#include <cstdlib>
+#include <type_traits>
+
+#include "gq_device.h"
+#include "gq_internal.h"
+#include "gq_xsrc.h"
+
+namespace gq {
+
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int QL_STRIDE = 272;  // LDS bytes per unit of one limb (16 B pad: bank spread)
+constexpr int QZERO = 256;      // bytes of zeros the A operand's idle lanes read
+
+// Waves per block, and items per lane in registers at once (the current
+// one and DEPTH - 1 in flight): 8 waves (two per SIMD, 256 registers per
+// lane) keep 3 items of Q4_K / Q5_K / Q6_K (2 of Q8_0) per lane.
+__host__ __device__ constexpr int mvq_waves(int) { return 8; }
+__host__ __device__ constexpr int mvq_depth(int fmt) { return fmt == T_Q8_0 ? 2 : 3; }
+
+template <int FMT> struct QF;
+template <> struct QF<T_Q4_K> { static constexpr int C = 9, AUX = 8; };
+template <> struct QF<T_Q5_K> { static constexpr int C = 11, AUX = 8; };
+template <> struct QF<T_Q5_K8> { static constexpr int C = 11, AUX = 16; };
+template <> struct QF<T_Q6_K> { static constexpr int C = 13, AUX = 16; };
+template <> struct QF<T_Q8_0> { static constexpr int C = 17, AUX = 0; };
+
+// LDS: limbs [3][units][QL_STRIDE] (Q5_K8: the Q8_K codes in limb 0),
+// zeros [QZERO], per-unit scale s [units] (Q5_K8: the Q8_K d), per-unit aux
+// [units][AUX] (Q4_K/Q5_K: fp32 sums of the 8 sub-blocks; Q6_K: int sums of
+// the 16 runs of X; Q5_K8: bsums as int), per-row wave partials
+// [nt][rows][NW], 16 floats of reduction scratch.
+struct QSmem {
+  uint8_t *limb;
+  uint32_t zero_off;
+  float *us;
+  int *aux;
+  float *part;
+  float *red;
+};
+
+__host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int part_floats,
+                                               QSmem *s, char *base) {
+  size_t o = 0;
+  auto take = [&](size_t n) { size_t r = o; o += (n + 15) & ~(size_t)15; return r; };
+  const int upad = (units + 3) & ~3;  // the last quad's missing units stay in bounds
+  const size_t ol = take((size_t)3 * upad * QL_STRIDE);
+  const size_t oz = take(QZERO);
+  const size_t ou = take((size_t)upad * 4);
+  const size_t oa = take((size_t)upad * aux_per_unit * 4);
+  const size_t op = take((size_t)part_floats * 4);
+  const size_t orr = take(64);
+  if (s) {
+    s->limb = (uint8_t *)(base + ol);
+    s->zero_off = (uint32_t)oz;
+    s->us = (float *)(base + ou);
+    s->aux = (int *)(base + oa);
+    s->part = (float *)(base + op);
+    s->red = (float *)(base + orr);
+  }
+  return o;
+}
+
+__device__ __forceinline__ i32x4 lds16(const char *smem, uint32_t off) {
+  return *(const i32x4 *)(smem + off);
+}
+
+__device__ __forceinline__ i32x4 mfma(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ i32x4 v4(uint4 q) { return i32x4{(int)q.x, (int)q.y, (int)q.z, (int)q.w}; }
+
+__device__ __forceinline__ float combine(int a2, int a1, int a0) {
+  return fmaf((float)a2, 65536.f, fmaf((float)a1, 256.f, (float)a0));
+}
+
+// -------------------------------------------------------------- staging
+// Thread t converts elements [16t, 16t + 16) of a pass; the 16 threads of a
+// unit are aligned lanes of one wave (xor shuffles 1..8).
+template <int FMT>
+__device__ __forceinline__ void stage16(int kpad, int e0, const float (&xv)[16], const QSmem &S,
+                                        int upad) {
+  const int u = e0 >> 8, w16 = (e0 & 255) >> 4;
+  if constexpr (FMT == T_Q5_K8) {
+    const Q8K16 r = q8k_quant16(xv, e0 & 255);
+    if (e0 >= kpad) return;
+    *(uint4 *)(S.limb + u * QL_STRIDE + (e0 & 255)) = make_uint4(r.q[0], r.q[1], r.q[2], r.q[3]);
+    S.aux[u * 16 + w16] = r.bsum;
+    if (w16 == 0) S.us[u] = r.d;
+  } else {
+    float amax = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(xv[i]));
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 64));
+    float sum = 0.f;
+    if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+#pragma unroll
+      for (int i = 0; i < 16; i++) sum += xv[i];
+    }
+    const float sum32 = sum + __shfl_xor(sum, 1, 64);
+    if (e0 >= kpad) return;
+    const float inv = amax > 0.f ? LIMB_RANGE / amax : 0.f;
+    uint32_t w2[4], w1[4], w0[4];
+    int xs = 0;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      uint32_t V[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int X = (int)rintf(xv[4 * q + r] * inv);
+        xs += X;
+        V[r] = ((uint32_t)X + 0x808080u) ^ 0x808080u;  // signed base-256 digits
+      }
+      const uint32_t l01 = __builtin_amdgcn_perm(V[1], V[0], 0x05010400u);
+      const uint32_t l23 = __builtin_amdgcn_perm(V[3], V[2], 0x05010400u);
+      const uint32_t h01 = __builtin_amdgcn_perm(V[1], V[0], 0x0c0c0602u);
+      const uint32_t h23 = __builtin_amdgcn_perm(V[3], V[2], 0x0c0c0602u);
+      w0[q] = __builtin_amdgcn_perm(l23, l01, 0x05040100u);
+      w1[q] = __builtin_amdgcn_perm(l23, l01, 0x07060302u);
+      w2[q] = __builtin_amdgcn_perm(h23, h01, 0x05040100u);
+    }
+    const int lo = u * QL_STRIDE + (e0 & 255);
+    const int lstride = upad * QL_STRIDE;
+    *(uint4 *)(S.limb + lo) = make_uint4(w2[0], w2[1], w2[2], w2[3]);
+    *(uint4 *)(S.limb + lstride + lo) = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+    *(uint4 *)(S.limb + 2 * lstride + lo) = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+    if (w16 == 0) S.us[u] = amax / LIMB_RANGE;
+    if constexpr (FMT == T_Q4_K || FMT == T_Q5_K) {
+      if (!(w16 & 1)) ((float *)S.aux)[u * 8 + (w16 >> 1)] = sum32;
+    } else if constexpr (FMT == T_Q6_K) {
+      S.aux[u * 16 + w16] = xs;
+    }
+  }
+}
+
+// ------------------------------------------------------------ item math
+// One unit per lane.  ch: the unit's chunks, a: this lane's A-operand LDS
+// byte offset for the unit's quad (idle lanes: the zero region), u: the
+// lane's unit (column index in x units), S: staged x.
+template <int FMT>
+__device__ __forceinline__ float item_dot(const uint4 *ch, uint32_t dbits, const char *smem,
+                                          uint32_t a, int u, const QSmem &S) {
+  if constexpr (FMT == T_Q4_K || FMT == T_Q5_K || FMT == T_Q5_K8) {
+    constexpr bool Q5 = FMT != T_Q4_K;
+    constexpr int QS = Q5 ? 3 : 1;  // first qs chunk
+    const uint4 hd = ch[0];
+    const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+    int acc2 = 0, acc1 = 0, acc0 = 0, amin = 0;
+    float mt = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      uint32_t sc0, m0, sc1, m1;
+      scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
+      scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
+      i32x4 dlo = {0, 0, 0, 0}, dhi = {0, 0, 0, 0};
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const uint4 q = ch[QS + 2 * j + h];
+        uint4 lo = make_uint4(q.x & 0x0F0F0F0Fu, q.y & 0x0F0F0F0Fu, q.z & 0x0F0F0F0Fu, q.w & 0x0F0F0F0Fu);
+        uint4 hi = make_uint4((q.x >> 4) & 0x0F0F0F0Fu, (q.y >> 4) & 0x0F0F0F0Fu,
+                              (q.z >> 4) & 0x0F0F0F0Fu, (q.w >> 4) & 0x0F0F0F0Fu);
+        if constexpr (Q5) {  // qh bytes 16h..16h+15: bit 2j -> low, 2j+1 -> high
+          const uint4 qh = ch[1 + h];
+          lo.x |= ((qh.x >> (2 * j)) & 0x01010101u) << 4;
+          lo.y |= ((qh.y >> (2 * j)) & 0x01010101u) << 4;
+          lo.z |= ((qh.z >> (2 * j)) & 0x01010101u) << 4;
+          lo.w |= ((qh.w >> (2 * j)) & 0x01010101u) << 4;
+          hi.x |= ((qh.x >> (2 * j + 1)) & 0x01010101u) << 4;
+          hi.y |= ((qh.y >> (2 * j + 1)) & 0x01010101u) << 4;
+          hi.z |= ((qh.z >> (2 * j + 1)) & 0x01010101u) << 4;
+          hi.w |= ((qh.w >> (2 * j + 1)) & 0x01010101u) << 4;
+        }
+        dlo = mfma(lds16(smem, a + 64 * j + 16 * h), v4(lo), dlo);
+        dhi = mfma(lds16(smem, a + 64 * j + 32 + 16 * h), v4(hi), dhi);
+      }
+      if constexpr (FMT == T_Q5_K8) {
+        acc0 += __mul24((int)sc0, dlo[0]) + __mul24((int)sc1, dhi[0]);
+        const int4 bs = *(const int4 *)(S.aux + u * 16 + 4 * j);
+        amin += __mul24((int)m0, bs.x + bs.y) + __mul24((int)m1, bs.z + bs.w);
+      } else {
+        acc2 += __mul24((int)sc0, dlo[0]) + __mul24((int)sc1, dhi[0]);
+        acc1 += __mul24((int)sc0, dlo[1]) + __mul24((int)sc1, dhi[1]);
+        acc0 += __mul24((int)sc0, dlo[2]) + __mul24((int)sc1, dhi[2]);
+        const float2 sx = *(const float2 *)((const float *)S.aux + u * 8 + 2 * j);
+        mt = fmaf((float)m0, sx.x, mt);
+        mt = fmaf((float)m1, sx.y, mt);
+      }
+    }
+    if constexpr (FMT == T_Q5_K8) return S.us[u] * (d * (float)acc0 - dmin * (float)amin);
+    return d * S.us[u] * combine(acc2, acc1, acc0) - dmin * mt;
+  } else if constexpr (FMT == T_Q6_K) {
+    // ch[0..7] ql, ch[8..11] qh, ch[12] scales; run s = elements 16s.. uses scale s
+    int acc2 = 0, acc1 = 0, acc0 = 0;
+    float corr = 0.f;
+#pragma unroll
+    for (int hh = 0; hh < 2; hh++) {
+#pragma unroll
+      for (int half = 0; half < 2; half++) {
+        uint32_t q[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int ii = 4 * half + i;
+          const uint32_t A = dw(ch, 16 * hh + ii), B = dw(ch, 16 * hh + 8 + ii);
+          const uint32_t H = dw(ch + 8, 8 * hh + ii);
+          q[0][i] = (A & 0x0F0F0F0Fu) | ((H << 4) & 0x30303030u);
+          q[1][i] = (B & 0x0F0F0F0Fu) | ((H << 2) & 0x30303030u);
+          q[2][i] = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
+          q[3][i] = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          const int s = 8 * hh + 2 * t + half;
+          const int sc = (int)(int8_t)(dw(ch + 12, s >> 2) >> (8 * (s & 3)));
+          const i32x4 z = {0, 0, 0, 0};
+          const i32x4 dd = mfma(lds16(smem, a + 16 * s),
+                                i32x4{(int)q[t][0], (int)q[t][1], (int)q[t][2], (int)q[t][3]}, z);
+          acc2 += __mul24(sc, dd[0]);
+          acc1 += __mul24(sc, dd[1]);
+          acc0 += __mul24(sc, dd[2]);
+          corr = fmaf((float)sc, (float)S.aux[u * 16 + s], corr);
+        }
+      }
+    }
+    return h2f(dbits) * S.us[u] * (combine(acc2, acc1, acc0) - 32.f * corr);
+  } else {  // Q8_0: ch[0..15] qs of 8 blocks, ch[16] their f16 d
+    float acc = 0.f;
+#pragma unroll
+    for (int b = 0; b < 8; b++) {
+      const i32x4 z = {0, 0, 0, 0};
+      i32x4 dd = mfma(lds16(smem, a + 32 * b), v4(ch[2 * b]), z);
+      dd = mfma(lds16(smem, a + 32 * b + 16), v4(ch[2 * b + 1]), dd);
+      const float db = h2f(dw(ch + 16, b >> 1) >> (16 * (b & 1)));
+      acc = fmaf(db, combine(dd[0], dd[1], dd[2]), acc);
+    }
+    return S.us[u] * acc;
+  }
+}
+
+template <int FMT>
+struct QItem {
+  uint4 ch[QF<FMT>::C];
+  uint32_t d;
+};
+
+
+template <int FMT, bool K4, int SRC, int NT>
+__global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
+  extern __shared__ __align__(16) char smem[];
+  constexpr int NW = mvq_waves(FMT), NTH = 64 * NW, C = QF<FMT>::C;
+  constexpr bool HAS_D = FMT == T_Q6_K;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int U = a.units, T = (U + 3) >> 2, upad = 4 * T;
+  // This block's row groups [fg0, fg1) and items (group, matrix, quad).
+  const int G = a.groups;  // flat row groups of the launch
+  const int fg0 = (int)((long)G * blockIdx.x / a.blocks);
+  const int fg1 = (int)((long)G * (blockIdx.x + 1) / a.blocks);
+  const int nitems = (fg1 - fg0) * NT * T;
+  const int i0 = (int)((long)nitems * wave / NW), i1 = (int)((long)nitems * (wave + 1) / NW);
+  const int rows_blk = (fg1 - fg0) * QROWS;
+  QSmem S;
+  qsmem_layout(QF<FMT>::AUX, U, NT * rows_blk * NW, &S, smem);
+
+  // Item cursors (wave-uniform): flat group, matrix, quad and segment.
+  struct Cur {
+    int fg, m, t, seg;
+  };
+  auto cur_at = [&](int it) {
+    Cur c;
+    const int per = NT * T, gi = it / per, rem = it - gi * per;
+    c.fg = fg0 + gi;
+    c.m = rem / T;
+    c.t = rem - c.m * T;
+    c.seg = 0;
+    if constexpr (NT == 1) {
+#pragma unroll
+      for (int i = 1; i < MV_MAX_SEG; i++)
+        if (i < a.nseg && c.fg >= a.seg[i].blk_begin) c.seg = i;
+    }
+    return c;
+  };
+  auto advance = [&](Cur &c) {
+    if (++c.t == T) {
+      c.t = 0;
+      if (++c.m == NT) {
+        c.m = 0;
+        ++c.fg;
+        if constexpr (NT == 1)
+          while (c.seg + 1 < a.nseg && c.fg >= a.seg[c.seg + 1].blk_begin) c.seg++;
+      }
+    }
+  };
+  const int q = lane >> 4, r = lane & 15;
+  Cur lc = cur_at(i0), cc = lc;
+  auto load = [&](QItem<FMT> &dst) {
+    const MvSeg &sg = a.seg[NT == 2 ? lc.m : lc.seg];
+    const int g = lc.fg - a.seg[lc.seg].blk_begin;
+    const int nr = min(QROWS, sg.rows - QROWS * g), nq = min(4, U - 4 * lc.t);
+    const long base = (long)g * QROWS * U + (long)lc.t * 4 * nr;  // quad_item_unit
+    const bool live = r < nr && q < nq;
+    const int l = live ? nr * q + r : 0;  // idle lanes re-read lane 0 (same lines)
+    const uint8_t *bp = sg.body + base * (C * 16);
+    const int cs = 16 * nr * nq;
+#pragma unroll
+    for (int c = 0; c < C; c++) dst.ch[c] = ldw4(bp + (uint32_t)(c * cs + 16 * l));
+    if constexpr (HAS_D) dst.d = ldh(sg.d + base + l);
+    advance(lc);
+  };
+
+  constexpr int DEPTH = mvq_depth(FMT);
+  QItem<FMT> R0, R1, R2;
+  // The first items' loads go out right after the x loads of the staging
+  // (not before them: a wave's loads complete in order, so x would wait
+  // behind the weights).
+  auto first_loads = [&] {
+    if (i0 < i1) load(R0);
+    if (DEPTH == 3 && i0 + 1 < i1) load(R1);
+  };
+
+  // ---- stage x (and clear the partial-sum slots)
+  for (int i = tid; i < NT * rows_blk * NW; i += NTH) S.part[i] = 0.f;
+  if (tid < QZERO / 16) *(uint4 *)(smem + S.zero_off + 16 * tid) = make_uint4(0, 0, 0, 0);
+  float rscale = 1.f;
+  const int kpad = U * 256;
+  auto stage_all = [&](auto &xsrc) {
+    const int passes = (kpad + 16 * NTH - 1) / (16 * NTH);
+    using XS = std::remove_reference_t<decltype(xsrc)>;
+    if constexpr (IsExact<XS>::value) {
+      for (int p = 0; p < passes; p++) {
+        typename XS::Raw r0;
+        xsrc.issue(16 * NTH * p + 16 * tid, r0);
+        xsrc.accum_ss(r0);
+      }
+      xsrc.pre_barrier(S.red);
+      __syncthreads();
+      xsrc.set_rms(S.red);
+      __syncthreads();
+    }
+    // the x loads of the first NP passes, then the first items' loads, then
+    // the conversion (later passes one by one)
+    constexpr int NP = sizeof(typename XS::Raw) <= 64 ? 3 : 2;
+    typename XS::Raw raw[NP];
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+      if (k < passes) xsrc.issue(16 * NTH * k + 16 * tid, raw[k]);
+    float xv[NP][16];
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+      if (k < passes) xsrc.make(raw[k], 16 * NTH * k + 16 * tid, xv[k]);
+    __builtin_amdgcn_sched_barrier(0);
+    first_loads();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < NP; k++)
+      if (k < passes) stage16<FMT>(kpad, 16 * NTH * k + 16 * tid, xv[k], S, upad);
+    for (int p = NP; p < passes; p++) {
+      typename XS::Raw r1;
+      const int e0 = 16 * NTH * p + 16 * tid;
+      xsrc.issue(e0, r1);
+      float xv[16];
+      xsrc.make(r1, e0, xv);
+      stage16<FMT>(kpad, e0, xv, S, upad);
+    }
+    if constexpr (!IsExact<XS>::value) xsrc.pre_barrier(S.red);
+    __syncthreads();
+    rscale = xsrc.scale(S.red);
+  };
+  if constexpr (SRC == MV_NORM) {
+    const float *x = a.in.tok ? a.in.x + (long)(*a.in.tok) * a.k : a.in.x;
+    XNorm<K4, FMT == T_Q5_K8> xs{x, a.in.r, a.in.nw, blockIdx.x == 0 ? a.in.xo : nullptr, a.k, a.in.eps};
+    stage_all(xs);
+  } else if constexpr (SRC == MV_SWIGLU) {
+    XSwiGLU<K4> xs{a.in.xg, a.in.xu, a.k};
+    stage_all(xs);
+  } else {
+    XPlain<K4> xs{a.in.x, a.k};
+    stage_all(xs);
+  }
+
+  // ---- stream this wave's items
+  // A operand: lanes 20q' + i (i < 3) read limb i of unit q' of the quad
+  // (Q5_K8: limb 0 only), every other lane the zero region.
+  const int aq = lane >> 4, ai = lane & 15;
+  const bool alive = (ai >> 2) == aq && (ai & 3) < (FMT == T_Q5_K8 ? 1 : 3);
+  const uint32_t limb_off = (uint32_t)((ai & 3) * upad * QL_STRIDE);
+  float racc = 0.f;
+  int cur = -1;  // flat group * NT + matrix of racc
+  auto flush = [&]() {
+    float v = racc;
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (cur >= 0 && q == 0) {
+      const int fgm = cur, m = fgm % NT, lrow = (fgm / NT - fg0) * QROWS + r;
+      S.part[(m * rows_blk + lrow) * NW + wave] = v;
+    }
+    racc = 0.f;
+  };
+  auto consume = [&](const QItem<FMT> &src) {
+    const int key = cc.fg * NT + cc.m;
+    if (key != cur) {
+      flush();
+      cur = key;
+    }
+    const int u = 4 * cc.t + q;  // this lane's unit
+    const uint32_t aoff = alive ? limb_off + (uint32_t)(4 * cc.t + aq) * QL_STRIDE : S.zero_off;
+    const float v = item_dot<FMT>(src.ch, src.d, smem, aoff, min(u, upad - 1), S);
+    const MvSeg &sg = a.seg[NT == 2 ? cc.m : cc.seg];
+    const int g = cc.fg - a.seg[cc.seg].blk_begin;
+    if (u < U && QROWS * g + r < sg.rows) racc += v;
+    advance(cc);
+  };
+  if constexpr (DEPTH == 3) {
+    for (int it = i0; it < i1; it += 3) {
+      if (it + 2 < i1) load(R2);
+      consume(R0);
+      if (it + 3 < i1) load(R0);
+      if (it + 1 < i1) consume(R1);
+      if (it + 4 < i1) load(R1);
+      if (it + 2 < i1) consume(R2);
+    }
+  } else {
+    for (int it = i0; it < i1; it += 2) {
+      if (it + 1 < i1) load(R1);
+      consume(R0);
+      if (it + 2 < i1) load(R0);
+      if (it + 1 < i1) consume(R1);
+    }
+  }
+  flush();
+  __syncthreads();
+
+  // ---- per-row sums over the waves, in wave order
+  for (int lr = tid; lr < rows_blk; lr += NTH) {
+    const int fg = fg0 + lr / QROWS;
+    int sgi = 0;
+    if constexpr (NT == 1) {
+#pragma unroll
+      for (int i = 1; i < MV_MAX_SEG; i++)
+        if (i < a.nseg && fg >= a.seg[i].blk_begin) sgi = i;
+    }
+    const MvSeg &sg = a.seg[sgi];
+    const int row = (fg - sg.blk_begin) * QROWS + (lr % QROWS);
+    if (row >= sg.rows) continue;
+    float v[NT];
+#pragma unroll
+    for (int m = 0; m < NT; m++) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) s += S.part[(m * rows_blk + lr) * NW + w];
+      v[m] = s * rscale;
+    }
+    float out = v[0];
+    if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
+    sg.y[row] = out;
+  }
+}
+
+template <int FMT, bool K4, int SRC, int NT>
+hipError_t mvq_launch_t(const MvArgs &a, size_t lds, hipStream_t st) {
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute((const void *)k_mvq<FMT, K4, SRC, NT>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipLaunchKernelGGL((k_mvq<FMT, K4, SRC, NT>), dim3(a.blocks), dim3(64 * mvq_waves(FMT)), lds, st, a);
+  return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t mvq_launch_f(const MvArgs &a, size_t lds, hipStream_t st) {
+  const bool k4 = a.k % 4 == 0;
+  switch (a.in.src) {
+  case MV_NORM:
+    if (!k4) return hipErrorInvalidValue;
+    return a.pair ? mvq_launch_t<FMT, true, MV_NORM, 2>(a, lds, st) : mvq_launch_t<FMT, true, MV_NORM, 1>(a, lds, st);
+  case MV_SWIGLU:
+    if (a.pair) return hipErrorInvalidValue;
+    return k4 ? mvq_launch_t<FMT, true, MV_SWIGLU, 1>(a, lds, st) : mvq_launch_t<FMT, false, MV_SWIGLU, 1>(a, lds, st);
+  default:
+    if (a.pair) return hipErrorInvalidValue;
+    return k4 ? mvq_launch_t<FMT, true, MV_X, 1>(a, lds, st) : mvq_launch_t<FMT, false, MV_X, 1>(a, lds, st);
+  }
+}
+
+int aux_per_unit(int fmt) {
+  return fmt == T_Q4_K || fmt == T_Q5_K ? 8 : fmt == T_Q8_0 ? 0 : 16;
+}
+
+}  // namespace
+
+// Groups and blocks of a quad-layout launch; returns the LDS bytes a block
+// needs.  The launch's flat row-group count goes to groups, segment i's
+// first flat group to seg[i].blk_begin.
+size_t mvq_plan(MvArgs &a, int num_cus) {
+  const int nt = a.pair ? 2 : 1, nseg = a.pair ? 1 : a.nseg;
+  int G = 0;
+  for (int i = 0; i < nseg; i++) {
+    a.seg[i].blk_begin = G;
+    a.seg[i].nblk = 0;
+    G += (a.seg[i].rows + QROWS - 1) / QROWS;
+  }
+  if (a.pair) a.seg[1].blk_begin = 0;
+  a.groups = G;
+  static const int bpc = [] {
+    const char *e = getenv("GQ_MVQ_BLOCKS_PER_CU");  // tuning override
+    return e && atoi(e) > 0 ? atoi(e) : 1;
+  }();
+  a.blocks = std::max(1, std::min(G, num_cus * bpc));
+  const int fmt = a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt;
+  const int rows_blk = QROWS * ((G + a.blocks - 1) / a.blocks);
+  return qsmem_layout(aux_per_unit(fmt), a.units, nt * rows_blk * mvq_waves(fmt), nullptr, nullptr);
+}
+
+hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {
+  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  switch (a.fmt) {
+  case T_Q4_K: return mvq_launch_f<T_Q4_K>(a, lds, st);
+  case T_Q5_K: return a.in.q8k && !a.pair ? mvq_launch_f<T_Q5_K8>(a, lds, st) : mvq_launch_f<T_Q5_K>(a, lds, st);
+  case T_Q6_K: return mvq_launch_f<T_Q6_K>(a, lds, st);
+  case T_Q8_0: return mvq_launch_f<T_Q8_0>(a, lds, st);
+  default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace gq

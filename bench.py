@@ -38,6 +38,9 @@ MATS = [  # name, dtype, out_dim, in_dim
 # uses of a copy the step streams > 1 GB (the head alone is 447 MB), far
 # more than the 256 MB Infinity Cache, so every launch reads cold HBM.
 NCOPY = 2
+# Per-launch timings cycle through at least this many bytes of weight copies
+# (over the 256 MB Infinity Cache).
+COLD_BYTES = 320 << 20
 
 
 def measured_traffic():
@@ -56,24 +59,44 @@ def algo_bytes(gq, dtype, out_dim, in_dim):
     return gq.type_size(dtype, in_dim) * out_dim + 4 * in_dim + 4 * out_dim
 
 
-def cpu_baseline(mats, host, xs, nthreads, budget_s=15.0):
-    """The oracle's WeightMap::matmul_into restatement on the host cores."""
-    sys.path.insert(0, os.path.join(ROOT, "oracle"))
-    import oracle
-    total_bytes = sum(b for *_, b in mats)
-    oracle.matmul_into(Q4_K, host["Wq"], xs[HID], HID, nthreads)  # warm
+# Host threads for the CPU legs: every core this process may use, capped at
+# the GPU box's CPU share for one GPU (16 threads).
+BOX_CPU_SHARE = 16
+
+
+def host_threads():
+    return min(len(os.sched_getaffinity(0)), BOX_CPU_SHARE)
+
+
+def _cpu_steps(oracle, mats, host, xs, nthreads, budget_s, max_steps=50):
     steps, t0 = 0, time.perf_counter()
     while True:
         for name, dtype, out_dim, in_dim, _ in mats:
             oracle.matmul_into(dtype, host[name], xs[in_dim], out_dim, nthreads)
         steps += 1
         el = time.perf_counter() - t0
-        if el > budget_s or steps >= 50:
-            break
+        if el > budget_s or steps >= max_steps:
+            return steps, el
+
+
+def cpu_baseline(mats, host, xs, nthreads, budget_s=15.0):
+    """The oracle's WeightMap::matmul_into restatement (row-parallel like
+    the reference's rayon par_iter_mut, model/mod.rs:362-403) on the host
+    cores: nthreads threads (all usable cores up to the box's share), and a
+    1-thread sample of the same step."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    total_bytes = sum(b for *_, b in mats)
+    oracle.matmul_into(Q4_K, host["Wq"], xs[HID], HID, nthreads)  # warm
+    steps, el = _cpu_steps(oracle, mats, host, xs, nthreads, budget_s)
+    s1, el1 = _cpu_steps(oracle, mats, host, xs, 1, budget_s / 3, max_steps=3)
     return {"value": round(total_bytes * steps / el / 1e9, 3), "unit": "GB/s",
             "cores": nthreads, "kind": "port",
+            "single_thread_value": round(total_bytes * s1 / el1 / 1e9, 3),
+            "host_cpus": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0)),
             "sample": f"{steps} full steps (all 8 matvecs, {total_bytes / 1e6:.0f} MB each) "
-                      f"through oracle matmul_into, {el:.1f} s"}
+                      f"through oracle matmul_into on {nthreads} threads, {el:.1f} s; "
+                      f"1 thread: {s1} steps, {el1:.1f} s"}
 
 
 DECODE_PREFILL, DECODE_STEPS = 4096, 128
@@ -112,7 +135,7 @@ def gemm_leg(be, gq, syn, torch, cpu):
     if cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle
-        nthreads = min(len(os.sched_getaffinity(0)), 16)
+        nthreads = host_threads()
         xs = X[:32].cpu().numpy()
         t0 = time.perf_counter()
         oracle.matmul_batch_into(Q4_K, w, xs, rows, nthreads)
@@ -120,6 +143,54 @@ def gemm_leg(be, gq, syn, torch, cpu):
         out["cpu_gflops"] = round(2.0 * rows * k * 32 / el / 1e9, 2)
         out["cpu_sample"] = f"oracle matmul_batch_into, 32 of the 512 tokens, {nthreads} threads"
     return out
+
+
+def q8_0_leg(be, gq, syn, torch, cpu):
+    """Q8_0 matvec at the Llama-3.2-1B FFN-up shape,
+    W 8192x2048, batch 1.  The matrix is 17.8 MB, so Q8_COPIES device copies
+    (356 MB, over the 256 MB Infinity Cache) are cycled to read cold HBM;
+    one graph of Q8_COPIES launches, timed with events on its stream."""
+    Q8_0, rows, k = 8, 8192, 2048
+    w = syn.make_blocks(Q8_0, rows, k, seed=21)
+    dev = torch.from_numpy(w.reshape(-1)).cuda()
+    hs = [be.upload_weight(Q8_0, dev, k, rows) for _ in range(Q8_COPIES)]
+    del dev
+    x = syn.make_x(k, seed=22)
+    xd = torch.from_numpy(x).cuda()
+    y = torch.empty(rows, device="cuda")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for h in hs:
+            h.launch_only(xd, y)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(3):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (3 * Q8_COPIES)
+    nb = algo_bytes(gq, Q8_0, rows, k)
+    gbs = nb / (us * 1e-6) / 1e9
+    out = {"shape": f"W {rows}x{k} Q8_0", "algo_bytes": nb, "us": round(us, 2),
+           "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+    if cpu:
+        sys.path.insert(0, os.path.join(ROOT, "oracle"))
+        import oracle
+        nthreads = host_threads()
+        oracle.matmul_into(Q8_0, w, x, rows, nthreads)
+        reps, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 2.0:
+            oracle.matmul_into(Q8_0, w, x, rows, nthreads)
+            reps += 1
+        el = time.perf_counter() - t0
+        out["cpu_GB_s"] = round(nb * reps / el / 1e9, 3)
+        out["cpu_sample"] = f"oracle matmul_into, {reps} calls, {nthreads} threads"
+    return out
+
+
+Q8_COPIES = 20
 
 
 def moe_leg(be, gq, syn, torch, cpu):
@@ -288,7 +359,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-decode", action="store_true", help="skip the 7B decode leg")
-    ap.add_argument("--only", choices=["matvec", "decode", "gemm", "moe"],
+    ap.add_argument("--only", choices=["matvec", "decode", "gemm", "moe", "q8_0"],
                     help="run only this leg and print its figures (for profiling)")
     ap.add_argument("--cpu-decode-steps", type=int, default=3)
     ap.add_argument("--calib-copy", action="store_true",
@@ -311,12 +382,13 @@ def main():
         print(json.dumps({"decode": decode_leg(be, gq, syn, torch, 0 if args.no_cpu else
                                                args.cpu_decode_steps)}), flush=True)
         return
-    if args.only in ("gemm", "moe"):
-        leg = gemm_leg if args.only == "gemm" else moe_leg
+    if args.only in ("gemm", "moe", "q8_0"):
+        leg = {"gemm": gemm_leg, "moe": moe_leg, "q8_0": q8_0_leg}[args.only]
         print(json.dumps({args.only: leg(be, gq, syn, torch, not args.no_cpu)}), flush=True)
         return
 
-    host, xs, mats, copies = {}, {}, [], {}
+    host, xs, mats, copies, dev_of, rows_of = {}, {}, [], {}, {}, {}
+    dtype_of = {m[0]: m[1] for m in MATS}
     for i, (name, dtype, out_dim, in_dim) in enumerate(MATS):
         w = syn.make_blocks(dtype, out_dim, in_dim, seed=100 + i)
         host[name] = w
@@ -324,7 +396,8 @@ def main():
         mats.append((name, dtype, out_dim, in_dim, nb))
         dev = torch.from_numpy(w.reshape(-1)).cuda()
         copies[name] = [be.upload_weight(dtype, dev, in_dim, out_dim) for _ in range(NCOPY)]
-        del dev
+        dev_of[name] = dev
+        rows_of[name] = out_dim
     for d in (HID, FFN):
         xs[d] = syn.make_x(d, seed=d)
     xd = {d: torch.from_numpy(v).cuda() for d, v in xs.items()}
@@ -378,15 +451,21 @@ def main():
     ms_step = ms_total / args.steps
     value = step_bytes / (ms_step * 1e-3) / 1e9
 
-    # Per-launch kernel time: a graph of REPS launches of one group,
-    # alternating the copies, bracketed by events on the replay stream.
-    per = {}
-    REPS = 20
+    # Per-launch kernel time: a graph of REPS launches of one group, cycling
+    # through enough device copies of the group (over COLD_BYTES in all) that
+    # every launch reads cold HBM, bracketed by events on the replay stream.
+    per, cold_keep = {}, []
+    REPS = 40
     for grp in GROUPS:
+        gb = group_bytes(grp)
+        ncold = min(REPS, max(NCOPY, -(-COLD_BYTES // gb) + 1))
+        extra = {n: [be.upload_weight(dtype_of[n], dev_of[n], dims[n], rows_of[n])
+                     for _ in range(ncold - NCOPY)] for n in grp}
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for r in range(REPS):
-                hs = [copies[n][r % NCOPY] for n in grp]
+                c = r % ncold
+                hs = [copies[n][c] if c < NCOPY else extra[n][c - NCOPY] for n in grp]
                 if len(grp) == 1:
                     hs[0].launch_only(xd[dims[grp[0]]], yd[grp[0]])
                 else:
@@ -399,8 +478,13 @@ def main():
         e1.record()
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / REPS
-        nb = group_bytes(grp)
-        per["+".join(grp)] = {"us": round(us, 2), "GB/s": round(nb / (us * 1e-6) / 1e9, 1)}
+        per["+".join(grp)] = {"us": round(us, 2), "GB/s": round(gb / (us * 1e-6) / 1e9, 1),
+                              "copies": ncold}
+        # (freed after the last capture: a handle released during a capture
+        # would hipFree inside it)
+        cold_keep.append((g, extra))
+    del cold_keep, hs
+    torch.cuda.synchronize()
     head_bytes = [b for n, *_, b in mats if n == "head"][0]
     head_us = per["head"]["us"]
     achieved = head_bytes / (head_us * 1e-6) / 1e9
@@ -435,15 +519,15 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
     if not args.no_cpu:
-        nthreads = min(len(os.sched_getaffinity(0)), 16)
-        out["cpu_baseline"] = cpu_baseline(mats, host, xs, nthreads, args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline(mats, host, xs, host_threads(), args.cpu_seconds)
     if args.only == "matvec":
         print(json.dumps(out), flush=True)
         return
+    out["q8_0"] = q8_0_leg(be, gq, syn, torch, not args.no_cpu)
     out["gemm"] = gemm_leg(be, gq, syn, torch, not args.no_cpu)
     out["moe"] = moe_leg(be, gq, syn, torch, not args.no_cpu)
     if not args.no_decode:
-        del copies, host
+        del copies, host, dev_of
         torch.cuda.empty_cache()
         out["decode"] = decode_leg(be, gq, syn, torch, 0 if args.no_cpu else args.cpu_decode_steps)
     print(json.dumps(out), flush=True)

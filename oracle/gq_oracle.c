@@ -25,6 +25,7 @@
  *                    ggml's published dequantize_row_iq3_xxs; its codebook is
  *                    a placeholder unless the caller installs the real one.
  */
+#define _GNU_SOURCE  /* sched_getaffinity */
 #include "gq_oracle.h"
 
 #include <math.h>
@@ -569,10 +570,16 @@ static void *matvec_job(void *p) {
     return NULL;
 }
 
+/* nthreads 0: the cores this process may run on (rayon's default pool),
+ * capped by GQO_MAX_THREADS (default 16, the GPU box's CPU share). */
 static int hw_threads(int n) {
     if (n > 0) return n;
-    long c = sysconf(_SC_NPROCESSORS_ONLN);
-    return c > 0 ? (int)c : 1;
+    cpu_set_t set;
+    int c = sched_getaffinity(0, sizeof set, &set) == 0 ? CPU_COUNT(&set) : (int)sysconf(_SC_NPROCESSORS_ONLN);
+    const char *e = getenv("GQO_MAX_THREADS");
+    int cap = e && atoi(e) > 0 ? atoi(e) : 16;
+    if (c > cap) c = cap;
+    return c > 0 ? c : 1;
 }
 
 static int run_jobs(job_t *proto, size_t rows, int nthreads, void *(*fn)(void *)) {
