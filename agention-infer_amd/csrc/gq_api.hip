@@ -55,6 +55,14 @@ struct DeviceState {
 std::mutex g_mu;
 DeviceState g_dev;
 
+// Workspace of gq_moe_ffn_noalloc: a file-scope device array (each GPU holds
+// its own copy for the life of the process).  Host code never uses the
+// array's name as an address: init_locked fetches the device address with
+// hipGetSymbolAddress, once per device, into g_scratch_dev.
+constexpr int MAX_DEVICES = 64;
+static __device__ __align__(256) unsigned char scratch[GQ_MOE_NOALLOC_MAX_BYTES];
+void *g_scratch_dev[MAX_DEVICES] = {};
+
 // Placeholder IQ3_XXS codebook: ggml's magnitude alphabet
 // {4,12,20,28,36,44,52,62}, four magnitudes per entry chosen by a fixed
 // integer hash of the entry index.  Replaced by gq_set_iq3xxs_grid.
@@ -81,6 +89,11 @@ int init_locked(int device) {
   if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
     return fail(GQ_ENODEV, "device %d is %s, this library is built for gfx950", device,
                 p.gcnArchName);
+  if (device < MAX_DEVICES && !g_scratch_dev[device]) {
+    void *ptr = nullptr;
+    HIP_TRY(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    g_scratch_dev[device] = ptr;
+  }
   g_dev.device = device;
   g_dev.num_cus = p.multiProcessorCount;
   if (!g_dev.grid_installed) default_grid(g_dev.grid_host);
@@ -304,9 +317,15 @@ int gq_upload_experts(int dtype, const void *w_host, size_t nbytes, int in_dim,
                        rows_per_expert);
 }
 
-int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, int n_experts,
-               const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
-               int *ids_dev, float *w_dev, void *stream) {
+}  // extern "C"
+
+namespace {
+// gq_moe_ffn and its no-allocation variant: with noalloc the workspace is
+// the device's scratch array (sizes above GQ_MOE_NOALLOC_MAX_BYTES are
+// refused), otherwise a stream-ordered allocation freed after the launch.
+int moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, int n_experts,
+            const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
+            int *ids_dev, float *w_dev, void *stream, bool noalloc) {
   int rc = ensure_init();
   if (rc) return rc;
   if (!gate || !up || !down) return fail(GQ_EINVAL, "null expert weight handle");
@@ -329,7 +348,18 @@ int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down
   const int pairs = T * top_k;
   const size_t ws = (size_t)pairs * (size_t)f * 4 + (size_t)pairs * 8 + 1024;
   char *wsp = nullptr;
-  HIP_TRY(hipMallocAsync((void **)&wsp, ws, (hipStream_t)stream));
+  if (noalloc) {
+    if (ws > GQ_MOE_NOALLOC_MAX_BYTES)
+      return fail(GQ_EINVAL,
+                  "gq_moe_ffn_noalloc: workspace of %zu bytes (T=%d top_k=%d f=%d) exceeds the %d-byte "
+                  "scratch; use gq_moe_ffn",
+                  ws, T, top_k, f, GQ_MOE_NOALLOC_MAX_BYTES);
+    if (g_dev.device < 0 || g_dev.device >= MAX_DEVICES || !g_scratch_dev[g_dev.device])
+      return fail(GQ_ENODEV, "gq_moe_ffn_noalloc: no scratch on device %d", g_dev.device);
+    wsp = (char *)g_scratch_dev[g_dev.device];
+  } else {
+    HIP_TRY(hipMallocAsync((void **)&wsp, ws, (hipStream_t)stream));
+  }
   gq::MoeArgs a{};
   a.fmt = gate->L.dtype;
   a.n_experts = n_experts;
@@ -349,9 +379,25 @@ int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down
   a.w = w_dev ? w_dev : (float *)((int *)(a.hbuf + (size_t)pairs * f) + pairs);
   a.out = out_dev;
   hipError_t e = gq::launch_moe(a, T, (hipStream_t)stream);
-  (void)hipFreeAsync(wsp, (hipStream_t)stream);
+  if (!noalloc) (void)hipFreeAsync(wsp, (hipStream_t)stream);
   if (e != hipSuccess) return fail(GQ_EHIP, "MoE launch failed: %s", hipGetErrorString(e));
   return GQ_OK;
+}
+}  // namespace
+
+extern "C" {
+int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, int n_experts,
+               const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
+               int *ids_dev, float *w_dev, void *stream) {
+  return moe_ffn(gate, up, down, n_experts, logits_dev, T, top_k, x_dev, out_dev, ids_dev, w_dev,
+                 stream, false);
+}
+
+int gq_moe_ffn_noalloc(const gq_weight *gate, const gq_weight *up, const gq_weight *down,
+                       int n_experts, const float *logits_dev, int T, int top_k, const float *x_dev,
+                       float *out_dev, int *ids_dev, float *w_dev, void *stream) {
+  return moe_ffn(gate, up, down, n_experts, logits_dev, T, top_k, x_dev, out_dev, ids_dev, w_dev,
+                 stream, true);
 }
 
 int gq_weight_free(gq_weight *w) {

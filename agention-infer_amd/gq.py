@@ -63,6 +63,7 @@ SIGNATURES = {
     "gq_model_generate": (_I, [_P, _I, _I, _I, _P, _P]),
     "gq_model_prefill": (_I, [_P, _P, _I, _I, _P, ctypes.POINTER(_I), _P]),
     "gq_moe_ffn": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _P]),
+    "gq_moe_ffn_noalloc": (_I, [_P, _P, _P, _I, _P, _I, _I, _P, _P, _P, _P, _P]),
 }
 
 
@@ -317,16 +318,19 @@ class HipBackend:
         return GpuWeightHandle(h.value, dtype, in_dim, rows_per_expert * n_experts)
 
     def moe_ffn(self, gate, up, down, n_experts, logits_dev, x_dev, top_k, out_dev=None,
-                want_routing=False, stream=None):
-        """MoE expert FFN for T tokens; returns out [T][h] (and ids, w)."""
+                want_routing=False, stream=None, noalloc=False):
+        """MoE expert FFN for T tokens; returns out [T][h] (and ids, w).
+        noalloc: gq_moe_ffn_noalloc (workspace in the library's static device
+        scratch, no allocation)."""
         import torch
         T, h = x_dev.shape
         if out_dev is None:
             out_dev = torch.empty((T, h), dtype=torch.float32, device=x_dev.device)
         ids = torch.empty((T, top_k), dtype=torch.int32, device=x_dev.device) if want_routing else None
         w = torch.empty((T, top_k), dtype=torch.float32, device=x_dev.device) if want_routing else None
-        _check(lib().gq_moe_ffn(gate._h, up._h, down._h, n_experts, _ptr(logits_dev), T, top_k,
-                                _ptr(x_dev), _ptr(out_dev), _ptr(ids), _ptr(w), _stream(stream)))
+        fn = lib().gq_moe_ffn_noalloc if noalloc else lib().gq_moe_ffn
+        _check(fn(gate._h, up._h, down._h, n_experts, _ptr(logits_dev), T, top_k,
+                  _ptr(x_dev), _ptr(out_dev), _ptr(ids), _ptr(w), _stream(stream)))
         return (out_dev, ids, w) if want_routing else out_dev
 
     def set_iq3xxs_grid(self, grid=None):

@@ -157,6 +157,18 @@ int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down
                const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
                int *ids_dev, float *w_dev, void *stream);
 
+/* gq_moe_ffn without any allocation: no counterpart in the reference; for
+ * callers that cannot allocate (code under HIP graph capture, serving
+ * loops).  The workspace (T * top_k * (4 * f + 8) + 1024 bytes) lives in a
+ * static device array of GQ_MOE_NOALLOC_MAX_BYTES per GPU, held until the
+ * process ends; larger shapes fail with GQ_EINVAL.  Every call on a GPU
+ * shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other threads) race.  Results equal gq_moe_ffn's. */
+#define GQ_MOE_NOALLOC_MAX_BYTES (4 << 20)
+int gq_moe_ffn_noalloc(const gq_weight *gate, const gq_weight *up, const gq_weight *down,
+                       int n_experts, const float *logits_dev, int T, int top_k, const float *x_dev,
+                       float *out_dev, int *ids_dev, float *w_dev, void *stream);
+
 /* ---- GPU-resident decode of a dense Llama/Qwen2-style decoder ----------
  * The reference's run_gpu_resident (src/model/llama/gpu_resident.rs:427-697)
  * with the arithmetic of LlamaModel::run (src/model/llama/cpu_path.rs:
