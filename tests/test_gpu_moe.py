@@ -63,11 +63,11 @@ def test_moe_small(backend, orc, E, H, F, T, k):
 
 def test_moe_full_config(backend, orc):
     """config 4: 256 experts, hidden 3072, expert intermediate 1536, top-8,
-    T = 1, 4, 16 (T = 16 checked on 3 of its tokens; routing on all)."""
+    T = 1, 4, 16, every token's output and routing checked."""
     E, H, F, k = 256, 3072, 1536, 8
     say("moe full config: generating 1.39 GB of IQ3_XXS experts")
     weights = make(E, H, F, seed=100)
-    for T, toks in ((1, None), (4, None), (16, [0, 7, 15])):
+    for T, toks in ((1, None), (4, None), (16, None)):
         say(f"moe full T={T}")
         run(backend, orc, E, H, F, T, k, seed=200 + T, check_tokens=toks, weights=weights)
 
