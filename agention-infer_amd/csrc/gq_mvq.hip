@@ -299,24 +299,28 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int U = a.units, T = (U + 3) >> 2, upad = 4 * T;
-  // This block's row groups [fg0, fg1) and items (group, matrix, quad).
+  // This block's row groups: flat groups b, b + B, b + 2B, ... (local
+  // group lg is flat group b + lg B: at any time the blocks stream
+  // neighbouring groups, spreading the traffic evenly over the memory
+  // channels), and their items (group, matrix, quad).
   const int G = a.groups;  // flat row groups of the launch
-  const int fg0 = (int)((long)G * blockIdx.x / a.blocks);
-  const int fg1 = (int)((long)G * (blockIdx.x + 1) / a.blocks);
-  const int nitems = (fg1 - fg0) * NT * T;
+  const int B = a.blocks, b = blockIdx.x;
+  const int ngb = (G - b + B - 1) / B;
+  const int nitems = ngb * NT * T;
   const int i0 = (int)((long)nitems * wave / NW), i1 = (int)((long)nitems * (wave + 1) / NW);
-  const int rows_blk = (fg1 - fg0) * QROWS;
+  const int rows_blk = ngb * QROWS;
   QSmem S;
   qsmem_layout(QF<FMT>::AUX, U, NT * rows_blk * NW, &S, smem);
 
   // Item cursors (wave-uniform): flat group, matrix, quad and segment.
   struct Cur {
-    int fg, m, t, seg;
+    int lg, fg, m, t, seg;
   };
   auto cur_at = [&](int it) {
     Cur c;
     const int per = NT * T, gi = it / per, rem = it - gi * per;
-    c.fg = fg0 + gi;
+    c.lg = gi;
+    c.fg = b + gi * B;
     c.m = rem / T;
     c.t = rem - c.m * T;
     c.seg = 0;
@@ -332,7 +336,8 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
       c.t = 0;
       if (++c.m == NT) {
         c.m = 0;
-        ++c.fg;
+        ++c.lg;
+        c.fg += B;
         if constexpr (NT == 1)
           while (c.seg + 1 < a.nseg && c.fg >= a.seg[c.seg + 1].blk_begin) c.seg++;
       }
@@ -438,13 +443,13 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
     if (cur >= 0 && q == 0) {
-      const int fgm = cur, m = fgm % NT, lrow = (fgm / NT - fg0) * QROWS + r;
+      const int fgm = cur, m = fgm % NT, lrow = (fgm / NT) * QROWS + r;
       S.part[(m * rows_blk + lrow) * NW + wave] = v;
     }
     racc = 0.f;
   };
   auto consume = [&](const QItem<FMT> &src) {
-    const int key = cc.fg * NT + cc.m;
+    const int key = cc.lg * NT + cc.m;
     if (key != cur) {
       flush();
       cur = key;
@@ -479,7 +484,7 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
 
   // ---- per-row sums over the waves, in wave order
   for (int lr = tid; lr < rows_blk; lr += NTH) {
-    const int fg = fg0 + lr / QROWS;
+    const int fg = b + (lr / QROWS) * B;
     int sgi = 0;
     if constexpr (NT == 1) {
 #pragma unroll
