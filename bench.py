@@ -506,7 +506,7 @@ def main():
                                "(Wq,Wk,Wv,Wo,Wgate,Wup Q4_K; Wdown,head Q6_K), cold HBM",
                    "step_bytes": step_bytes, "timing": "HIP graph per step", "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1),
                    "wall_s": round(wall, 4)},
-        "roofline": {"bound": "hbm", "kernel": "k_matvec<Q6_K> (output head 152064x3584)",
+        "roofline": {"bound": "hbm", "kernel": "k_mvq<Q6_K> (output head 152064x3584)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                      "launch_us": head_us, "algo_bytes": head_bytes},
