@@ -19,10 +19,11 @@
 //                dot); its result is scaled by (d*sc)*xs and the min term
 //                dmin*m*xs*sum(q) is subtracted in fp32.
 //
-// Tiling (bf16): a block computes 80 weight rows x 512 tokens when the
-// batch is longer than 256 tokens (18944 rows x 512 tokens -> 237 blocks:
-// one round on 256 CUs, every weight element dequantized once), else 160
-// rows x 256 tokens.  K advances 64 elements (one Q4_K group) per stage.
+// Tiling (bf16): a block computes 160 weight rows x 256 tokens (18944 rows
+// x 512 tokens -> 238 blocks, one round on 256 CUs).  K advances 64
+// elements (one Q4_K group) per stage.  Batches longer than 128 tokens take
+// the direct-X kernel (X fragments straight from L2 into the multiply
+// waves' registers), shorter ones the ring kernel (X through LDS).
 // int8: 160 rows x 128 tokens.
 #include <type_traits>
 
@@ -649,6 +650,235 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_ring(GemmArgs a) {
   }
 }
 
+// ----------------------------------------------------------- bf16 kernel, direct X
+// Block tile 160 rows x 256 tokens, 512 threads, K-steps ("stages") of 64.
+// Waves 0-3 multiply: wave w owns all 160 rows x tokens 64w .. 64w + 63 of
+// the tile, so no X fragment is needed by two waves and X never passes
+// through LDS: each multiply wave loads its B fragments (bf16, written in
+// fragment order by a pre-pass) from global memory (L2) straight into
+// registers, one stage ahead.  The only LDS operand is the dequantized W
+// tile (fragment-major, two slots), read once per 4 MFMAs.  Waves 4-7
+// produce it as in the ring kernel: each fetches its 40 rows' stage records
+// two stages ahead into a ring private to the wave (straight to LDS) and
+// dequantizes them to bf16.  One barrier per stage.
+// LDS traffic per stage: 20 KiB of A written, 4 x 20 KiB read (the ring
+// kernel also moved 2 x 64 KiB of X); load path per stage: 32 KiB of X plus
+// the W records.
+template <int FMT>
+struct Direct {
+  static constexpr int TBM = 160, TBN = 256;
+  static constexpr int AT_ = TBM / 16;         // row tiles (10)
+  static constexpr int A_FR_ = 2 * AT_;        // A fragments per stage
+  static constexpr int C = GemmFmt<FMT>::C;
+  static constexpr int PROWS = TBM / 4;        // rows per producer wave (40)
+  static constexpr int WSLOTS = C * PROWS;
+  static constexpr int WINS = (WSLOTS + 63) / 64;
+  static constexpr int TASKS = 4 * PROWS;      // 16-element dequant tasks per producer wave
+  static constexpr int ROUNDS = (TASKS + 63) / 64;
+  static_assert(ROUNDS == 3, "3 dequant rounds");
+  static constexpr int WR = 3;
+};
+
+template <int FMT>
+__global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
+  using R = Direct<FMT>;
+  constexpr int AT_ = R::AT_, PROWS = R::PROWS, WSLOTS = R::WSLOTS, C = R::C;
+  constexpr int WINS = R::WINS, WR = R::WR, TBM = R::TBM, TBN = R::TBN;
+  __shared__ __align__(16) uint16_t As[2][R::A_FR_ * FR16];
+  __shared__ __align__(16) uint8_t Wg[4][WR][WSLOTS * 16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int b = blockIdx.x, split = b % a.ksplit, rest = b / a.ksplit;
+  const int ntile = rest % a.ntiles, tile = rest / a.ntiles;
+  GemmSeg sg = a.seg[0];
+#pragma unroll
+  for (int i = 1; i < GEMM_MAX_SEG; i++)
+    if (i < a.nseg && tile >= a.seg[i].tile_begin) sg = a.seg[i];
+  const int m0 = (tile - sg.tile_begin) * TBM, n0 = ntile * TBN, rows = sg.rows;
+  const int stages_all = a.kpad / BK;
+  const int s0 = (int)((long)stages_all * split / a.ksplit);
+  const int stages = (int)((long)stages_all * (split + 1) / a.ksplit) - s0, last = stages - 1;
+  const long row_stride = (long)(stages_all / 4) * gemm_unit_bytes(FMT);
+
+  if (wave >= 4) {
+    const int pw = wave - 4;
+    // W chunk slots of this wave: q = 64 i + lane (q < WSLOTS): row
+    // PROWS * pw + q / C, chunk q % C of the stage record.
+    const uint8_t *wsrc[WINS];
+    int wc[WINS];
+#pragma unroll
+    for (int i = 0; i < WINS; i++) {
+      const int q = min(64 * i + lane, WSLOTS - 1);
+      const int row = min(m0 + PROWS * pw + q / C, rows - 1);
+      wsrc[i] = sg.rec + (long)row * row_stride;
+      wc[i] = q % C;
+    }
+    auto issue_w = [&](int s) {  // this wave's rows of local stage s (clamped) into slot s % WR
+      const int sg_ = s0 + min(s, last);
+#pragma unroll
+      for (int i = 0; i < WINS; i++)
+        if (64 * i + lane < WSLOTS)
+          dma16(wsrc[i] + gemm_chunk_off<FMT>(sg_, wc[i]), &Wg[pw][s % WR][1024 * i]);
+    };
+    // Dequantize local stage s of this wave's rows: task t = 4 rr + 2 h + qq
+    // (row rr, half h of the 64 elements, 16-element quarter qq of the half),
+    // t = lane + 64 round.
+    auto dequant = [&](int s) {
+      const int j = (s0 + s) & 3;  // group of the unit (Q4_K scale pick)
+      const uint8_t *wg = Wg[pw][s % WR];
+      uint4 hd[3], qs[3], qh[3];
+      {
+        uint32_t ad[3 * 3];
+#pragma unroll
+        for (int round = 0; round < 3; round++) {
+          const int t = min(lane + 64 * round, R::TASKS - 1);
+          const int rr = t >> 2, qq = t & 1;
+          ad[3 * round] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr);
+          ad[3 * round + 1] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr + 16 + 16 * qq);
+          ad[3 * round + 2] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr + 48);
+        }
+        if constexpr (FMT == T_Q4_K) {
+          const uint32_t a6[6] = {ad[0], ad[1], ad[3], ad[4], ad[6], ad[7]};
+          uint4 v[6];
+          lds_read6(a6, v);
+          hd[0] = v[0]; qs[0] = v[1]; hd[1] = v[2]; qs[1] = v[3]; hd[2] = v[4]; qs[2] = v[5];
+        } else {
+          const uint32_t a6[6] = {ad[0], ad[1], ad[2], ad[3], ad[4], ad[5]};
+          uint4 v[6];
+          lds_read6(a6, v);
+          hd[0] = v[0]; qs[0] = v[1]; qh[0] = v[2]; hd[1] = v[3]; qs[1] = v[4]; qh[1] = v[5];
+          const uint32_t a2[2] = {ad[6], ad[7]};
+          uint4 w[2];
+          lds_read2_a(a2, w);
+          hd[2] = w[0]; qs[2] = w[1];
+          const uint32_t a1[2] = {ad[8], ad[8]};
+          lds_read2_a(a1, w);
+          qh[2] = w[0];
+        }
+      }
+#pragma unroll
+      for (int round = 0; round < R::ROUNDS; round++) {
+        const int t = lane + 64 * round;
+        if (round < R::ROUNDS - 1 || t < R::TASKS) {
+          const int rr = t >> 2, h = (t >> 1) & 1, qq = t & 1;
+          const int r = PROWS * pw + rr;
+          const bool ok = m0 + r < rows;
+          const uint32_t qw[4] = {qs[round].x, qs[round].y, qs[round].z, qs[round].w};
+          const uint32_t sh = 4u * (uint32_t)h;
+          uint32_t o[8];
+          if constexpr (FMT == T_Q4_K) {
+            uint32_t sc, mn;
+            scale_min_k4_sel(2 * j + h, hd[round].y, hd[round].z, hd[round].w, sc, mn);
+            const float ds = ok ? h2f(hd[round].x) * (float)sc : 0.f;
+            const float nm = ok ? -(h2f(hd[round].x >> 16) * (float)mn) : 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const uint32_t qv = (qw[i] >> sh) & 0x0F0F0F0Fu;
+              o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(qv), nm), fmaf(ds, cvt_ubyte<1>(qv), nm));
+              o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(qv), nm), fmaf(ds, cvt_ubyte<3>(qv), nm));
+            }
+          } else {
+            // dequant_q6_k: (d * sc) * (q - 32), one rounding: fma(ds, q, -32 ds)
+            const int g = 2 * h + qq;
+            const int sc8 = (int)(int8_t)(hd[round].x >> (8 * g));
+            const float ds = ok ? h2f(hd[round].y) * (float)sc8 : 0.f;
+            const float nm = -32.0f * ds;
+            const uint32_t hw = g == 0 ? qh[round].x : g == 1 ? qh[round].y : g == 2 ? qh[round].z : qh[round].w;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const uint32_t b2 = (hw >> (8 * i)) & 0xFFu;
+              const uint32_t hi = (b2 | (b2 << 6) | (b2 << 12) | (b2 << 18)) & 0x03030303u;
+              const uint32_t qv = ((qw[i] >> sh) & 0x0F0F0F0Fu) | (hi << 4);
+              o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(qv), nm), fmaf(ds, cvt_ubyte<1>(qv), nm));
+              o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(qv), nm), fmaf(ds, cvt_ubyte<3>(qv), nm));
+            }
+          }
+          uint16_t *dst = &As[s & 1][((h * AT_ + (r >> 4)) * 64 + (r & 15) + 32 * qq) * 8];
+          *(uint4 *)dst = make_uint4(o[0], o[1], o[2], o[3]);
+          *(uint4 *)(dst + 128) = make_uint4(o[4], o[5], o[6], o[7]);
+        }
+      }
+    };
+    issue_w(0);
+    issue_w(1);
+    wait_vm<WINS>();  // W of stage 0
+    dequant(0);
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    for (int kt = 0; kt < stages; kt++) {
+      issue_w(kt + 2);
+      wait_vm<WINS>();  // W of stage kt + 1
+      if (kt + 1 < stages) dequant(kt + 1);
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+    }
+    wait_vm<0>();  // drain the clamped loads before the block ends
+    return;
+  }
+
+  // ---- multiply waves: 160 rows x 64 tokens each
+  const int ksteps = a.kpad / 32;
+  // fragment (token tile 4 * wave + jn of the block, k-step ks):
+  // xp + (jn * ksteps + ks) * 512
+  const uint16_t *xp = a.xb + ((long)((n0 >> 4) + 4 * wave) * ksteps * 64 + lane) * 8;
+  // B fragments of the current stage, per 32-k half; a half is reloaded
+  // with the next stage's as soon as its MFMAs are issued (half a stage of
+  // lead for the L2 latency, 32 registers).
+  bf16x8_t bv[2][4];
+  auto load_b = [&](int s, int ks) {
+    const int kk = 2 * (s0 + s) + ks;
+#pragma unroll
+    for (int jn = 0; jn < 4; jn++) bv[ks][jn] = *(const bf16x8_t *)(xp + ((long)jn * ksteps + kk) * 512);
+  };
+  f32x4_t acc[AT_][4];
+#pragma unroll
+  for (int i = 0; i < AT_; i++)
+#pragma unroll
+    for (int jn = 0; jn < 4; jn++) acc[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  load_b(0, 0);
+  load_b(0, 1);
+  __builtin_amdgcn_s_barrier();  // stage 0 in LDS
+  for (int kt = 0; kt < stages; kt++) {
+    const uint16_t *A = As[kt & 1];
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+      // A fragments one ahead: the read of i + 1 is in flight during the
+      // 4 MFMAs of i (the scheduler may not hoist more: registers).
+      bf16x8_t av[2];
+      av[0] = *(const bf16x8_t *)(A + ((ks * AT_) * 64 + lane) * 8);
+#pragma unroll
+      for (int i = 0; i < AT_; i++) {
+        if (i + 1 < AT_) av[(i + 1) & 1] = *(const bf16x8_t *)(A + ((ks * AT_ + i + 1) * 64 + lane) * 8);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int jn = 0; jn < 4; jn++)
+          acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[i & 1], bv[ks][jn], acc[i][jn], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (kt + 1 < stages) load_b(kt + 1, ks);
+    }
+    __builtin_amdgcn_s_barrier();
+  }
+  // D layout: lane holds rows 4*(lane/16)+r (weight rows) of column lane%16 (token).
+  float *Y = a.ksplit > 1 ? sg.part + (long)split * a.n * rows : sg.y;
+#pragma unroll
+  for (int i = 0; i < AT_; i++) {
+    const int m = m0 + 16 * i + 4 * (lane >> 4);
+#pragma unroll
+    for (int jn = 0; jn < 4; jn++) {
+      const int t = n0 + 64 * wave + 16 * jn + (lane & 15);
+      if (t >= a.n) continue;
+      float *yp = Y + (long)t * rows + m;
+      if (m + 3 < rows && (rows & 3) == 0) {
+        *(float4 *)yp = make_float4(acc[i][jn][0], acc[i][jn][1], acc[i][jn][2], acc[i][jn][3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (m + r < rows) yp[r] = acc[i][jn][r];
+      }
+    }
+  }
+}
+
 // y[t][r] = (add ? y[t][r] : 0) + sum_s part[s][t][r], s in order, for the
 // segments of one launch at once (segment i owns blocks blk0[i] ..
 // blk0[i + 1] - 1: one launch instead of one per matrix).
@@ -846,14 +1076,17 @@ int gemm_ksplit(int tiles, int stages, int num_cus) {
 
 namespace {
 struct GemmPlan {
-  bool wide;
+  bool direct;
   int tbm, tbn, ntiles, tiles, ksplit;
 };
+// Kernel choice: the direct-X kernel (160 x 256 tiles, X fragments loaded
+// straight into the multiply waves' registers) for batches longer than 128
+// tokens; the ring kernel (160 x 256 tiles, X through LDS) for shorter ones.
 GemmPlan gemm_plan(const gq_weight *const *ws, int count, int n, int num_cus, bool add) {
   GemmPlan p;
-  p.wide = n > BN;
-  p.tbm = p.wide ? 80 : BM;
-  p.tbn = p.wide ? 512 : BN;
+  p.direct = n > 128;
+  p.tbm = BM;
+  p.tbn = BN;
   p.ntiles = (n + p.tbn - 1) / p.tbn;
   int mt = 0;
   for (int i = 0; i < count; i++) mt += (ws[i]->L.rows + p.tbm - 1) / p.tbm;
@@ -924,8 +1157,9 @@ hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int co
   const long nb = (long)tb * p.ntiles * p.ksplit;
   if (nb > 0x7fffffffL) return hipErrorInvalidValue;
   void (*kern)(GemmArgs);
-  if (fmt == T_Q4_K) kern = p.wide ? k_gemm_bf16_ring<80, 512, 2, T_Q4_K> : k_gemm_bf16_ring<160, 256, 3, T_Q4_K>;
-  else if (fmt == T_Q6_K) kern = p.wide ? k_gemm_bf16_ring<80, 512, 2, T_Q6_K> : k_gemm_bf16_ring<160, 256, 3, T_Q6_K>;
+  if (p.direct) kern = fmt == T_Q4_K ? k_gemm_bf16_direct<T_Q4_K> : k_gemm_bf16_direct<T_Q6_K>;
+  else if (fmt == T_Q4_K) kern = k_gemm_bf16_ring<160, 256, 3, T_Q4_K>;
+  else if (fmt == T_Q6_K) kern = k_gemm_bf16_ring<160, 256, 3, T_Q6_K>;
   else return hipErrorInvalidValue;
   hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(512), 0, st, a);
   hipError_t e = hipGetLastError();

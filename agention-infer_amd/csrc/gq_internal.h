@@ -210,8 +210,8 @@ struct GemmArgs {
   int nseg, ntiles, ksplit, n, kpad;
   const uint16_t *xb;  // X as bf16 MFMA fragments [npad/16][kpad/32][64 lanes][8]
 };
-// Token tiles are 512 wide when n > 256 (else 256): X fragments must cover
-// n rounded up to GEMM_NPAD.
+// X fragments must cover n rounded up to GEMM_NPAD (a multiple of the
+// 256-token tile).
 constexpr int GEMM_NPAD = 512;
 // K split of a launch with this many row x token tiles and stages.
 int gemm_ksplit(int tiles, int stages, int num_cus);
