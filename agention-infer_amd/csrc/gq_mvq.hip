@@ -362,13 +362,10 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
 
   constexpr int DEPTH = mvq_depth(FMT);
   QItem<FMT> R0, R1, R2;
-  // The first items' loads go out right after the x loads of the staging
-  // (not before them: a wave's loads complete in order, so x would wait
-  // behind the weights).
-  auto first_loads = [&] {
-    if (i0 < i1) load(R0);
-    if (DEPTH == 3 && i0 + 1 < i1) load(R1);
-  };
+  // The first item's loads go out once the staging's x has arrived (not
+  // before: a wave's loads complete in order, so x would wait behind the
+  // weights), the second one's after the x conversion (issuing both first
+  // holds the conversion back while the memory pipeline takes them).
 
   // ---- stage x (and clear the partial-sum slots)
   for (int i = tid; i < NT * rows_blk * NW; i += NTH) S.part[i] = 0.f;
@@ -401,11 +398,14 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
     for (int k = 0; k < NP; k++)
       if (k < passes) xsrc.make(raw[k], 16 * NTH * k + 16 * tid, xv[k]);
     __builtin_amdgcn_sched_barrier(0);
-    first_loads();
+    if (i0 < i1) load(R0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < NP; k++)
       if (k < passes) stage16<FMT>(kpad, 16 * NTH * k + 16 * tid, xv[k], S, upad);
+    __builtin_amdgcn_sched_barrier(0);
+    if (DEPTH == 3 && i0 + 1 < i1) load(R1);
+    __builtin_amdgcn_sched_barrier(0);
     for (int p = NP; p < passes; p++) {
       typename XS::Raw r1;
       const int e0 = 16 * NTH * p + 16 * tid;
@@ -574,3 +574,4 @@ hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {
 }
 
 }  // namespace gq
+
