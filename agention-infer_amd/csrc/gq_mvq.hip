@@ -74,8 +74,8 @@ template <> struct QF<T_Q8_0> { static constexpr int C = 17, AUX = 0; };
 // LDS: limbs [3][units][QL_STRIDE] (Q5_K8: the Q8_K codes in limb 0),
 // zeros [QZERO], per-unit scale s [units] (Q5_K8: the Q8_K d), per-unit aux
 // [units][AUX] (Q4_K/Q5_K: fp32 sums of the 8 sub-blocks; Q6_K: int sums of
-// the 16 runs of X; Q5_K8: bsums as int), per-row wave partials
-// [nt][rows][NW], 16 floats of reduction scratch.
+// the 16 runs of X; Q5_K8: bsums as int), per-item row sums [items][16],
+// 16 floats of reduction scratch, the item counter.
 struct QSmem {
   uint8_t *limb;
   uint32_t zero_off;
@@ -83,6 +83,7 @@ struct QSmem {
   int *aux;
   float *part;
   float *red;
+  int *ctr;
 };
 
 __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int part_floats,
@@ -96,6 +97,7 @@ __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int 
   const size_t oa = take((size_t)upad * aux_per_unit * 4);
   const size_t op = take((size_t)part_floats * 4);
   const size_t orr = take(64);
+  const size_t oc = take(16);
   if (s) {
     s->limb = (uint8_t *)(base + ol);
     s->zero_off = (uint32_t)oz;
@@ -103,6 +105,7 @@ __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int 
     s->aux = (int *)(base + oa);
     s->part = (float *)(base + op);
     s->red = (float *)(base + orr);
+    s->ctr = (int *)(base + oc);
   }
   return o;
 }
@@ -302,17 +305,21 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   // This block's row groups: flat groups b, b + B, b + 2B, ... (local
   // group lg is flat group b + lg B: at any time the blocks stream
   // neighbouring groups, spreading the traffic evenly over the memory
-  // channels), and their items (group, matrix, quad).
+  // channels), and their items (group, matrix, quad), numbered
+  // it = (lg NT + m) T + t.  The waves take items in turn: wave w starts
+  // with items w and w + NW, and each further item comes from an LDS
+  // counter, so the waves finish within about one item of each other.
+  // Each item's 16 row sums go to their own LDS slot and a row adds its
+  // items in item order, so results do not depend on which wave took what.
   const int G = a.groups;  // flat row groups of the launch
   const int B = a.blocks, b = blockIdx.x;
   const int ngb = (G - b + B - 1) / B;
   const int nitems = ngb * NT * T;
-  const int i0 = (int)((long)nitems * wave / NW), i1 = (int)((long)nitems * (wave + 1) / NW);
   const int rows_blk = ngb * QROWS;
   QSmem S;
-  qsmem_layout(QF<FMT>::AUX, U, NT * rows_blk * NW, &S, smem);
+  qsmem_layout(QF<FMT>::AUX, U, nitems * QROWS, &S, smem);
 
-  // Item cursors (wave-uniform): flat group, matrix, quad and segment.
+  // Item cursor (wave-uniform): local and flat group, matrix, quad, segment.
   struct Cur {
     int lg, fg, m, t, seg;
   };
@@ -331,21 +338,14 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
     }
     return c;
   };
-  auto advance = [&](Cur &c) {
-    if (++c.t == T) {
-      c.t = 0;
-      if (++c.m == NT) {
-        c.m = 0;
-        ++c.lg;
-        c.fg += B;
-        if constexpr (NT == 1)
-          while (c.seg + 1 < a.nseg && c.fg >= a.seg[c.seg + 1].blk_begin) c.seg++;
-      }
-    }
+  auto grab = [&]() {
+    int v = 0;
+    if (lane == 0) v = atomicAdd(S.ctr, 1);
+    return __builtin_amdgcn_readfirstlane(v);
   };
   const int q = lane >> 4, r = lane & 15;
-  Cur lc = cur_at(i0), cc = lc;
-  auto load = [&](QItem<FMT> &dst) {
+  auto load = [&](QItem<FMT> &dst, int it) {
+    const Cur lc = cur_at(it);
     const MvSeg &sg = a.seg[NT == 2 ? lc.m : lc.seg];
     const int g = lc.fg - a.seg[lc.seg].blk_begin;
     const int nr = min(QROWS, sg.rows - QROWS * g), nq = min(4, U - 4 * lc.t);
@@ -357,7 +357,6 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
 #pragma unroll
     for (int c = 0; c < C; c++) dst.ch[c] = ldw4(bp + (uint32_t)(c * cs + 16 * l));
     if constexpr (HAS_D) dst.d = ldh(sg.d + base + l);
-    advance(lc);
   };
 
   constexpr int DEPTH = mvq_depth(FMT);
@@ -367,8 +366,9 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   // weights), the second one's after the x conversion (issuing both first
   // holds the conversion back while the memory pipeline takes them).
 
-  // ---- stage x (and clear the partial-sum slots)
-  for (int i = tid; i < NT * rows_blk * NW; i += NTH) S.part[i] = 0.f;
+  // ---- stage x (and set the item counter)
+  if (tid == 0) *S.ctr = (DEPTH - 1) * NW;
+  int c0 = wave, c1 = wave + NW, c2 = nitems;  // items held by R0, R1, R2
   if (tid < QZERO / 16) *(uint4 *)(smem + S.zero_off + 16 * tid) = make_uint4(0, 0, 0, 0);
   float rscale = 1.f;
   const int kpad = U * 256;
@@ -398,13 +398,13 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
     for (int k = 0; k < NP; k++)
       if (k < passes) xsrc.make(raw[k], 16 * NTH * k + 16 * tid, xv[k]);
     __builtin_amdgcn_sched_barrier(0);
-    if (i0 < i1) load(R0);
+    if (c0 < nitems) load(R0, c0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < NP; k++)
       if (k < passes) stage16<FMT>(kpad, 16 * NTH * k + 16 * tid, xv[k], S, upad);
     __builtin_amdgcn_sched_barrier(0);
-    if (DEPTH == 3 && i0 + 1 < i1) load(R1);
+    if (DEPTH == 3 && c1 < nitems) load(R1, c1);
     __builtin_amdgcn_sched_barrier(0);
     for (int p = NP; p < passes; p++) {
       typename XS::Raw r1;
@@ -436,55 +436,51 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   const int aq = lane >> 4, ai = lane & 15;
   const bool alive = (ai >> 2) == aq && (ai & 3) < (FMT == T_Q5_K8 ? 1 : 3);
   const uint32_t limb_off = (uint32_t)((ai & 3) * upad * QL_STRIDE);
-  float racc = 0.f;
-  int cur = -1;  // flat group * NT + matrix of racc
-  auto flush = [&]() {
-    float v = racc;
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    if (cur >= 0 && q == 0) {
-      const int fgm = cur, m = fgm % NT, lrow = (fgm / NT) * QROWS + r;
-      S.part[(m * rows_blk + lrow) * NW + wave] = v;
-    }
-    racc = 0.f;
-  };
-  auto consume = [&](const QItem<FMT> &src) {
-    const int key = cc.lg * NT + cc.m;
-    if (key != cur) {
-      flush();
-      cur = key;
-    }
+  auto consume = [&](const QItem<FMT> &src, int it) {
+    const Cur cc = cur_at(it);
     const int u = 4 * cc.t + q;  // this lane's unit
     const uint32_t aoff = alive ? limb_off + (uint32_t)(4 * cc.t + aq) * QL_STRIDE : S.zero_off;
-    const float v = item_dot<FMT>(src.ch, src.d, smem, aoff, min(u, upad - 1), S);
+    float v = item_dot<FMT>(src.ch, src.d, smem, aoff, min(u, upad - 1), S);
     const MvSeg &sg = a.seg[NT == 2 ? cc.m : cc.seg];
     const int g = cc.fg - a.seg[cc.seg].blk_begin;
-    if (u < U && QROWS * g + r < sg.rows) racc += v;
-    advance(cc);
+    if (!(u < U && QROWS * g + r < sg.rows)) v = 0.f;
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    if (q == 0) S.part[it * QROWS + r] = v;
   };
   if constexpr (DEPTH == 3) {
-    for (int it = i0; it < i1; it += 3) {
-      if (it + 2 < i1) load(R2);
-      consume(R0);
-      if (it + 3 < i1) load(R0);
-      if (it + 1 < i1) consume(R1);
-      if (it + 4 < i1) load(R1);
-      if (it + 2 < i1) consume(R2);
+    for (;;) {
+      if (c0 >= nitems) break;
+      c2 = grab();
+      if (c2 < nitems) load(R2, c2);
+      consume(R0, c0);
+      if (c1 >= nitems) break;
+      c0 = grab();
+      if (c0 < nitems) load(R0, c0);
+      consume(R1, c1);
+      if (c2 >= nitems) break;
+      c1 = grab();
+      if (c1 < nitems) load(R1, c1);
+      consume(R2, c2);
     }
   } else {
-    for (int it = i0; it < i1; it += 2) {
-      if (it + 1 < i1) load(R1);
-      consume(R0);
-      if (it + 2 < i1) load(R0);
-      if (it + 1 < i1) consume(R1);
+    for (;;) {
+      if (c0 >= nitems) break;
+      c1 = grab();
+      if (c1 < nitems) load(R1, c1);
+      consume(R0, c0);
+      if (c1 >= nitems) break;
+      c0 = grab();
+      if (c0 < nitems) load(R0, c0);
+      consume(R1, c1);
     }
   }
-  flush();
   __syncthreads();
 
-  // ---- per-row sums over the waves, in wave order
+  // ---- per-row sums over the items, in item order
   for (int lr = tid; lr < rows_blk; lr += NTH) {
-    const int fg = b + (lr / QROWS) * B;
+    const int lg = lr / QROWS, rr = lr % QROWS;
+    const int fg = b + lg * B;
     int sgi = 0;
     if constexpr (NT == 1) {
 #pragma unroll
@@ -492,14 +488,14 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
         if (i < a.nseg && fg >= a.seg[i].blk_begin) sgi = i;
     }
     const MvSeg &sg = a.seg[sgi];
-    const int row = (fg - sg.blk_begin) * QROWS + (lr % QROWS);
+    const int row = (fg - sg.blk_begin) * QROWS + rr;
     if (row >= sg.rows) continue;
     float v[NT];
 #pragma unroll
     for (int m = 0; m < NT; m++) {
       float s = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; w++) s += S.part[(m * rows_blk + lr) * NW + w];
+      const float *pp = S.part + ((lg * NT + m) * T) * QROWS + rr;
+      for (int t = 0; t < T; t++) s += pp[t * QROWS];
       v[m] = s * rscale;
     }
     float out = v[0];
@@ -558,8 +554,8 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
   }();
   a.blocks = std::max(1, std::min(G, num_cus * bpc));
   const int fmt = a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt;
-  const int rows_blk = QROWS * ((G + a.blocks - 1) / a.blocks);
-  return qsmem_layout(aux_per_unit(fmt), a.units, nt * rows_blk * mvq_waves(fmt), nullptr, nullptr);
+  const int ngb = (G + a.blocks - 1) / a.blocks, T = (a.units + 3) / 4;
+  return qsmem_layout(aux_per_unit(fmt), a.units, ngb * nt * T * QROWS, nullptr, nullptr);
 }
 
 hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {
