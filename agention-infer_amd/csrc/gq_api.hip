@@ -621,8 +621,8 @@ int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mod
   if (ws == (size_t)-1)
     return fail(GQ_EDTYPE, "gq_gemm: %s weights not supported in %s mode", type_name(w->L.dtype),
                 mode == GQ_GEMM_BF16 ? "bf16" : "int8");
-  if (mode == GQ_GEMM_BF16) {
-    int rc2 = gq_ensure_gemm_records(w, (hipStream_t)stream);
+  {
+    int rc2 = gq_ensure_gemm_records(w, (hipStream_t)stream);  // both modes read the ggml-order copy
     if (rc2) return rc2;
   }
   void *wsp = nullptr;

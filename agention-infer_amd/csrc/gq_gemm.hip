@@ -24,7 +24,8 @@
 // elements (one Q4_K group) per stage.  Batches longer than 128 tokens take
 // the direct-X kernel (X fragments straight from L2 into the multiply
 // waves' registers), shorter ones the ring kernel (X through LDS).
-// int8: 160 rows x 128 tokens.
+// int8 (k_gemm_i8_direct): 160 rows x 256 tokens, W nibbles straight to
+// int8 MFMA, per-32 scaling on the VALU.
 #include <type_traits>
 
 #include "gq_device.h"
@@ -85,77 +86,6 @@ __global__ void k_x_to_bf16_frag(const float *X, int n, int npad, int k, int kpa
   *(uint4 *)(out + 8 * i) = make_uint4(o[0], o[1], o[2], o[3]);
 }
 
-// X fp32 [n][k] -> per-32 Q8 (KvDtype::Q8_0::pack): q [n][kpad] int8,
-// scale [n][kpad/32] f32 (the f16-rounded scale, widened), qsum [n][kpad/32]
-// int (sum of the 32 quants).  One 32-lane group per block of 32.
-__global__ void k_x_to_q8(const float *X, int n, int k, int kpad, int8_t *q, float *scale,
-                          int *qsum) {
-  const long gid = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long b = gid >> 5;
-  const long nblk = (long)n * (kpad / 32);
-  const int l = threadIdx.x & 31;
-  const int t = (int)(b / (kpad / 32)), c = (int)(b % (kpad / 32)) * 32 + l;
-  const float v = (b < nblk && c < k) ? X[(long)t * k + c] : 0.f;
-  float amax = fabsf(v);
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
-  const float s = amax > 0.f ? amax / 127.0f : 1.0f;
-  float r = roundf(v / s);
-  r = fminf(fmaxf(r, -127.f), 127.f);
-  int qi = (int)r;
-  int sum = qi;
-#pragma unroll
-  for (int off = 16; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 32);
-  if (b >= nblk) return;
-  q[(long)t * kpad + c] = (int8_t)qi;
-  if (l == 0) {
-    scale[b] = __half2float(__float2half_rn(s));
-    qsum[b] = sum;
-  }
-}
-
-// ----------------------------------------------------------- W loading
-struct WRegs {
-  uint4 hd, q0, q1;  // header and the 32 qs bytes of group j
-  bool ok;
-};
-
-__device__ __forceinline__ WRegs load_w(const Layout &L, const uint8_t *body, int r, int u,
-                                        int j) {
-  WRegs w;
-  w.ok = r < L.rows;
-  const int rc = w.ok ? r : L.rows - 1;
-  const int t = rc / L.rt, jj = (rc % L.rt) * L.units + u;
-  w.hd = *(const uint4 *)(body + chunk_offset(L, t, jj, 0));
-  w.q0 = *(const uint4 *)(body + chunk_offset(L, t, jj, 1 + 2 * j));
-  w.q1 = *(const uint4 *)(body + chunk_offset(L, t, jj, 2 + 2 * j));
-  return w;
-}
-
-// int8 mode: 64 nibbles as int8 (k order as above), plus per sub-block
-// (d*sc, dmin*m) for the two sub-blocks of group j.
-__device__ __forceinline__ void store_w_i8(const WRegs &w, int j, uint8_t *dst, float *wsc) {
-  const uint32_t qw[8] = {w.q0.x, w.q0.y, w.q0.z, w.q0.w, w.q1.x, w.q1.y, w.q1.z, w.q1.w};
-  uint32_t lo[8], hi[8];
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    lo[i] = w.ok ? (qw[i] & 0x0F0F0F0Fu) : 0u;
-    hi[i] = w.ok ? ((qw[i] >> 4) & 0x0F0F0F0Fu) : 0u;
-  }
-  *(uint4 *)(dst + 0) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-  *(uint4 *)(dst + 16) = make_uint4(lo[4], lo[5], lo[6], lo[7]);
-  *(uint4 *)(dst + 32) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
-  *(uint4 *)(dst + 48) = make_uint4(hi[4], hi[5], hi[6], hi[7]);
-  uint32_t sc0, m0, sc1, m1;
-  scale_min_k4(2 * j, w.hd.y, w.hd.z, w.hd.w, sc0, m0);
-  scale_min_k4(2 * j + 1, w.hd.y, w.hd.z, w.hd.w, sc1, m1);
-  const float d = h2f(w.hd.x), dmin = h2f(w.hd.x >> 16);
-  wsc[0] = w.ok ? d * (float)sc0 : 0.f;
-  wsc[1] = w.ok ? dmin * (float)m0 : 0.f;
-  wsc[2] = w.ok ? d * (float)sc1 : 0.f;
-  wsc[3] = w.ok ? dmin * (float)m1 : 0.f;
-}
-
 // ----------------------------------------------------------- bf16 kernel
 // Producer / consumer: 512 threads.  Waves 0-3 only multiply: each owns an
 // 80-row x 128-token tile (5 x 8 MFMA tiles) of the 160 x 256 block tile.
@@ -173,8 +103,6 @@ __device__ __forceinline__ void store_w_i8(const WRegs &w, int j, uint8_t *dst, 
 // barrier per stage.  A wave's waits count only its own loads (in issue
 // order), so the long-lived unit loads are issued after each stage's X
 // loads and only waves 4-5 carry them.
-constexpr int AT = BM / 16, BT = BN / 16;     // 10 row tiles, 16 token tiles
-constexpr int A_FR = 2 * AT, B_FR = 2 * BT;   // fragments per stage
 constexpr int FR16 = 512;                     // bf16 per 1 KiB fragment
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -916,127 +844,198 @@ __global__ void k_gemm_reduce(ReduceSegs r, int ksplit, int add) {
 }
 
 // ----------------------------------------------------------- int8 kernel
-// LDS: W int8 [BM][64+16], X int8 [BN][64+16] (16 B pad); per-row scale
-// pairs for the stage's two sub-blocks; per-token (xs, xs*sum(q)) for them.
-constexpr int LDQ = BK + 16;
-// int8 mode keeps its fp32 accumulators in VGPRs (each sub-block's integer
-// result is scaled on the VALU), so its tile is half as wide in tokens.
-constexpr int BN8 = 128, WN8 = 64, TN8 = WN8 / 16;
-
-__global__ __launch_bounds__(256) void k_gemm_i8(Layout L, const uint8_t *body, const int8_t *Xq,
-                                                 const float *Xs, const int *Xsum, int n,
-                                                 int kpad, float *Y) {
-  __shared__ __align__(16) uint8_t As[2][BM * LDQ];
-  __shared__ __align__(16) uint8_t Bs[2][BN8 * LDQ];
-  __shared__ __align__(16) float Ws[2][BM][4];  // d*sc0, dmin*m0, d*sc1, dmin*m1
-  __shared__ __align__(16) float Xa[2][BN8][4];  // xs0, xs0*sum0, xs1, xs1*sum1
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
-  const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN8;
-  const int stages = kpad / BK;
-  const int nb32 = kpad / 32;
-
-  auto load_x = [&](int kt, uint4 (&xr)[2], float4 &xa) {
+// X fp32 [n][k] -> per-32 Q8 (KvDtype::Q8_0::pack: amax / 127, f16 scale,
+// codes from the f32 scale) in MFMA B-operand fragments for
+// v_mfma_i32_16x16x32_i8: fragment (token tile nt, 32-k block kb) is 64
+// lane slots of 8 codes (lane l: token 16 nt + l % 16, k 32 kb + 8 (l / 16)),
+// 512 B, ordered [nt][kb]; beside it, per (nt, kb), 16 records
+// (xs, xs * sum(q)) with xs the f16-rounded scale.  Tokens past n get
+// zero records.  One thread per 8 consecutive k of one token; the 4
+// threads of a 32-block are consecutive lanes.
+__global__ void k_x_to_q8_frag(const float *X, int n, int npad, int k, int kpad, int8_t *q,
+                               float2 *xr) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  const int g8 = kpad / 8;
+  const bool ok = i < (long)npad * g8;
+  const int t = ok ? (int)(i / g8) : 0, c0 = ok ? (int)(i % g8) * 8 : 0;
+  float v[8];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int c = tid + 256 * i, tok = c >> 2, part = c & 3;
-      const int tn = min(n0 + tok, n - 1);
-      xr[i] = *(const uint4 *)(Xq + (long)tn * kpad + kt * BK + 16 * part);
-      if (n0 + tok >= n) xr[i] = make_uint4(0, 0, 0, 0);
-    }
-    const int tn = min(n0 + (tid & (BN8 - 1)), n - 1);
-    const long bi = (long)tn * nb32 + 2 * kt;
-    const float s0 = Xs[bi], s1 = Xs[bi + 1];
-    xa = make_float4(s0, s0 * (float)Xsum[bi], s1, s1 * (float)Xsum[bi + 1]);
-    if (n0 + (tid & (BN8 - 1)) >= n) xa = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int e = 0; e < 8; e++) v[e] = ok && t < n && c0 + e < k ? X[(long)t * k + c0 + e] : 0.f;
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+  amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+  const float s = amax > 0.f ? amax / 127.0f : 1.0f;
+  uint32_t w[2] = {0, 0};
+  int sum = 0;
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    float r = roundf(v[e] / s);
+    r = fminf(fmaxf(r, -127.f), 127.f);
+    const int qi = (int)r;
+    sum += qi;
+    w[e >> 2] |= ((uint32_t)qi & 0xFFu) << (8 * (e & 3));
+  }
+  sum += __shfl_xor(sum, 1, 64);
+  sum += __shfl_xor(sum, 2, 64);
+  if (!ok) return;
+  const int nt = t >> 4, kb = c0 >> 5, sub = (c0 & 31) >> 3;
+  const long f = (long)nt * (kpad / 32) + kb;
+  *(uint2 *)(q + f * 512 + ((t & 15) + 16 * sub) * 8) = make_uint2(w[0], w[1]);
+  if (sub == 0) {
+    const float xs = t < n ? __half2float(__float2half_rn(s)) : 0.f;
+    xr[f * 16 + (t & 15)] = make_float2(xs, xs * (float)sum);
+  }
+}
+
+// Block tile 160 rows x 256 tokens, 512 threads = 8 waves, each both
+// multiplying and scaling: wave w owns rows 80 (w & 1) .. + 79 and tokens
+// 64 (w >> 1) .. + 63 (5 x 4 tiles of 16 x 16), so a SIMD's two waves
+// overlap one's scaling VALU with the other's MFMAs.  K-steps ("stages")
+// of 64 = one Q4_K group = two 32-element sub-blocks.  Per stage:
+//   * every thread fetches one 16-byte chunk of the block's W rows (the
+//     group's header or one of its two quant chunks, ggml order) a stage
+//     ahead and, after the stage's MFMAs, writes it to LDS: quant bytes as
+//     int8 A fragments (low nibbles = sub-block 0, high = sub-block 1; no
+//     scaling), the header as (d sc, dmin m) per row and sub-block;
+//   * each wave loads its X fragments and (xs, xs sum q) records from
+//     global memory (L2) straight into registers, a stage ahead;
+//   * per sub-block and tile, one v_mfma_i32_16x16x32_i8 gives the exact
+//     integer dot D, and y += (d sc) xs D - (dmin m) xs sum(q) in fp32.
+// One barrier per stage.
+constexpr int I8M = 160, I8N = 256;
+__global__ __launch_bounds__(512) void k_gemm_i8_direct(const uint8_t *rec, int rows, int ntiles,
+                                                        const int8_t *xq, const float2 *xr, int n,
+                                                        int kpad, float *Y) {
+  __shared__ __align__(16) uint8_t Aq[2][2 * 10 * 512];      // [buf][ks][row tile] fragments
+  __shared__ __align__(16) float2 Ws[2][2][I8M];              // [buf][ks][row] (d sc, dmin m)
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ntile = blockIdx.x % ntiles, tile = blockIdx.x / ntiles;
+  const int m0 = tile * I8M, n0 = ntile * I8N;
+  const int stages = kpad / 64, kb_all = kpad / 32;
+  const long row_stride = (long)(stages / 4) * 144;
+  // W chunk of this thread: row wr, chunk wc (0 header, 1-2 quants)
+  const bool wact = tid < 3 * I8M;
+  const int wr = wact ? tid / 3 : 0, wc = wact ? tid % 3 : 0;
+  const bool wok = wact && m0 + wr < rows;
+  const uint8_t *wsrc = rec + (long)min(m0 + wr, rows - 1) * row_stride;
+  auto load_w = [&](int s) -> uint4 {
+    const long off = (long)(s >> 2) * 144 + (wc == 0 ? 0 : 16 + 32 * (s & 3) + 16 * (wc - 1));
+    return *(const uint4 *)(wsrc + off);
   };
-  auto store_x = [&](int buf, const uint4 (&xr)[2], const float4 &xa) {
+  auto store_w = [&](int s, int buf, uint4 c) {
+    if (!wact) return;
+    if (wc == 0) {
+      const int j = s & 3;
+      uint32_t sc0, mn0, sc1, mn1;
+      scale_min_k4(2 * j, c.y, c.z, c.w, sc0, mn0);
+      scale_min_k4(2 * j + 1, c.y, c.z, c.w, sc1, mn1);
+      const float d = h2f(c.x), dmin = h2f(c.x >> 16);
+      Ws[buf][0][wr] = wok ? make_float2(d * (float)sc0, dmin * (float)mn0) : make_float2(0.f, 0.f);
+      Ws[buf][1][wr] = wok ? make_float2(d * (float)sc1, dmin * (float)mn1) : make_float2(0.f, 0.f);
+    } else {
+      // bytes 16 (wc - 1) + b: element 16 (wc - 1) + b (low nibble, sub-block 0)
+      // and 32 + 16 (wc - 1) + b (high nibble, sub-block 1); k within the
+      // sub-block 16 (wc - 1) + b -> lane slot (row % 16) + 16 * (k / 8)
+      const uint32_t qw[4] = {c.x, c.y, c.z, c.w};
+      const int rt = wr >> 4, slot0 = (wr & 15) + 32 * (wc - 1);
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-      const int c = tid + 256 * i, tok = c >> 2, part = c & 3;
-      *(uint4 *)(&Bs[buf][tok * LDQ + 16 * part]) = xr[i];
-    }
-    if (tid < BN8) *(float4 *)(&Xa[buf][tid][0]) = xa;
-  };
-
-  f32x4_t acc[TM][TN8];
-#pragma unroll
-  for (int i = 0; i < TM; i++)
-#pragma unroll
-    for (int j = 0; j < TN8; j++) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  WRegs wr;
-  uint4 xr[2];
-  float4 xa;
-  if (tid < BM) wr = load_w(L, body, m0 + tid, 0, 0);
-  load_x(0, xr, xa);
-  if (tid < BM) store_w_i8(wr, 0, &As[0][tid * LDQ], &Ws[0][tid][0]);
-  store_x(0, xr, xa);
-  __syncthreads();
-
-  for (int kt = 0; kt < stages; kt++) {
-    const int buf = kt & 1;
-    const bool more = kt + 1 < stages;
-    if (more) {
-      if (tid < BM) wr = load_w(L, body, m0 + tid, (kt + 1) >> 2, (kt + 1) & 3);
-      load_x(kt + 1, xr, xa);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {  // one 32-element sub-block per ks
-      const int kk = 32 * ks + 8 * (lane >> 4);
-      long bfr[TN8];
-      float xs[TN8], xm[TN8];
-#pragma unroll
-      for (int j = 0; j < TN8; j++) {
-        const int tok = WN8 * wn + 16 * j + (lane & 15);
-        bfr[j] = *(const long *)(&Bs[buf][tok * LDQ + kk]);
-        xs[j] = Xa[buf][tok][2 * ks];
-        xm[j] = Xa[buf][tok][2 * ks + 1];
+      for (int h = 0; h < 2; h++) {
+        uint8_t *fr = &Aq[buf][(h * 10 + rt) * 512];
+        const uint32_t l0 = (qw[0] >> (4 * h)) & 0x0F0F0F0Fu, l1 = (qw[1] >> (4 * h)) & 0x0F0F0F0Fu;
+        const uint32_t l2 = (qw[2] >> (4 * h)) & 0x0F0F0F0Fu, l3 = (qw[3] >> (4 * h)) & 0x0F0F0F0Fu;
+        *(uint2 *)(fr + slot0 * 8) = make_uint2(l0, l1);
+        *(uint2 *)(fr + (slot0 + 16) * 8) = make_uint2(l2, l3);
       }
+    }
+  };
+  // X: fragments (token tile 16-token nt, 32-k block kb) at xq + (nt * kb_all + kb) * 512
+  const int wm = wave & 1, wn = wave >> 1;
+  const long nt0 = (n0 >> 4) + 4 * wn;
+  struct XReg {
+    long b[2][4];
+    float2 r[2][4];
+  };
+  auto load_x = [&](int s, XReg &x) {
 #pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const int rb = WM * wm + 16 * i;
-        const long afr = *(const long *)(&As[buf][(rb + (lane & 15)) * LDQ + kk]);
-        float wsc[4], wmn[4];
+    for (int ks = 0; ks < 2; ks++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const int row = rb + 4 * (lane >> 4) + r;
-          wsc[r] = Ws[buf][row][2 * ks];
-          wmn[r] = Ws[buf][row][2 * ks + 1];
+      for (int jn = 0; jn < 4; jn++) {
+        const long f = (nt0 + jn) * kb_all + 2 * s + ks;
+        x.b[ks][jn] = *(const long *)(xq + f * 512 + lane * 8);
+        x.r[ks][jn] = xr[f * 16 + (lane & 15)];
+      }
+  };
+  f32x4_t acc[5][4];
+#pragma unroll
+  for (int i = 0; i < 5; i++)
+#pragma unroll
+    for (int jn = 0; jn < 4; jn++) acc[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int buf, const XReg &x) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+      for (int i = 0; i < 5; i++) {
+        const int rt = 5 * wm + i;
+        const long a = *(const long *)&Aq[buf][(ks * 10 + rt) * 512 + lane * 8];
+        const float4 w01 = *(const float4 *)&Ws[buf][ks][16 * rt + 4 * (lane >> 4)];
+        const float4 w23 = *(const float4 *)&Ws[buf][ks][16 * rt + 4 * (lane >> 4) + 2];
+        const float wsc[4] = {w01.x, w01.z, w23.x, w23.z}, wmn[4] = {w01.y, w01.w, w23.y, w23.w};
+        i32x4_t dq[4];
+#pragma unroll
+        for (int jn = 0; jn < 4; jn++) {
+          const i32x4_t z = {0, 0, 0, 0};
+          dq[jn] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, x.b[ks][jn], z, 0, 0, 0);
         }
 #pragma unroll
-        for (int j = 0; j < TN8; j++) {
-          const i32x4_t z = {0, 0, 0, 0};
-          const i32x4_t dq = __builtin_amdgcn_mfma_i32_16x16x32_i8(afr, bfr[j], z, 0, 0, 0);
+        for (int jn = 0; jn < 4; jn++) {
+          const float xs = x.r[ks][jn].x, xm = x.r[ks][jn].y;
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            const float v = fmaf(wsc[r] * xs[j], (float)dq[r], acc[i][j][r]);
-            acc[i][j][r] = fmaf(-wmn[r], xm[j], v);
+            const float v = fmaf(wsc[r] * xs, (float)dq[jn][r], acc[i][jn][r]);
+            acc[i][jn][r] = fmaf(-wmn[r], xm, v);
           }
+          // keep the update here (not sunk past the next tile's MFMAs,
+          // which would keep every tile's integer result live at once)
+          asm volatile("" : "+v"(acc[i][jn]));
         }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (more) {
-      if (tid < BM) store_w_i8(wr, (kt + 1) & 3, &As[buf ^ 1][tid * LDQ], &Ws[buf ^ 1][tid][0]);
-      store_x(buf ^ 1, xr, xa);
-    }
+  };
+  // prologue: stage 0 to LDS; each stage then loads its X and the next
+  // stage's W while it computes
+  {
+    const uint4 c = load_w(0);
+    store_w(0, 0, c);
+  }
+  __syncthreads();
+  for (int kt = 0; kt < stages; kt++) {
+    XReg x;
+    load_x(kt, x);
+    uint4 c = make_uint4(0, 0, 0, 0);
+    if (kt + 1 < stages) c = load_w(kt + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(kt & 1, x);
+    if (kt + 1 < stages) store_w(kt + 1, (kt + 1) & 1, c);
     __syncthreads();
   }
-
+  // D layout: lane holds rows 4 (lane / 16) + r of token column lane % 16.
 #pragma unroll
-  for (int i = 0; i < TM; i++) {
-    const int m = m0 + WM * wm + 16 * i + 4 * (lane >> 4);
+  for (int i = 0; i < 5; i++) {
+    const int m = m0 + 80 * wm + 16 * i + 4 * (lane >> 4);
 #pragma unroll
-    for (int j = 0; j < TN8; j++) {
-      const int t = n0 + WN8 * wn + 16 * j + (lane & 15);
+    for (int jn = 0; jn < 4; jn++) {
+      const int t = n0 + 64 * wn + 16 * jn + (lane & 15);
       if (t >= n) continue;
-      float *yp = Y + (long)t * L.rows + m;
-      if (m + 3 < L.rows && (L.rows & 3) == 0) {
-        *(float4 *)yp = make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
+      float *yp = Y + (long)t * rows + m;
+      if (m + 3 < rows && (rows & 3) == 0) {
+        *(float4 *)yp = make_float4(acc[i][jn][0], acc[i][jn][1], acc[i][jn][2], acc[i][jn][3]);
       } else {
 #pragma unroll
         for (int r = 0; r < 4; r++)
-          if (m + r < L.rows) yp[r] = acc[i][j][r];
+          if (m + r < rows) yp[r] = acc[i][jn][r];
       }
     }
   }
@@ -1114,8 +1113,9 @@ size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode, int num_cus) {
     return ((xb + 255) & ~(size_t)255) + gemm_part_floats(&w, 1, n, num_cus, false) * 4 + 256;
   }
   if (w->L.dtype != T_Q4_K) return (size_t)-1;
-  // int8: q [n][kpad] + scale f32 [n][kpad/32] + qsum int [n][kpad/32]
-  return (size_t)n * kpad + (size_t)n * (kpad / 32) * 8 + 512;
+  // int8: fragments [npad/16][kpad/32][512 B] + records [npad/16][kpad/32][16] float2
+  const size_t npad = (size_t)(n + I8N - 1) / I8N * I8N;
+  return ((npad * kpad + 255) & ~(size_t)255) + npad * (kpad / 32) * 8 + 256;
 }
 
 hipError_t launch_x_to_frag(const float *X, int n, int k, uint16_t *xb, hipStream_t st) {
@@ -1196,15 +1196,17 @@ hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int 
     if (e != hipSuccess) return e;
     return launch_gemm_bf16(&w, &Y, 1, xb, n, part, false, num_cus, st);
   } else {
+    if (!w->gemm_raw) return hipErrorInvalidValue;
+    const int npad = (n + I8N - 1) / I8N * I8N;
     int8_t *xq = (int8_t *)workspace;
-    float *xs = (float *)((char *)workspace + (((size_t)n * kpad + 255) & ~(size_t)255));
-    int *xsum = (int *)(xs + (size_t)n * (kpad / 32));
-    const dim3 grid((L.rows + BM - 1) / BM, (n + BN8 - 1) / BN8);
-    const long threads = (long)n * kpad;
-    hipLaunchKernelGGL(k_x_to_q8, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, X, n,
-                       L.k, kpad, xq, xs, xsum);
-    hipLaunchKernelGGL(k_gemm_i8, grid, dim3(256), 0, st, L, (const uint8_t *)w->body,
-                       (const int8_t *)xq, (const float *)xs, (const int *)xsum, n, kpad, Y);
+    float2 *xr = (float2 *)((char *)workspace + (((size_t)npad * kpad + 255) & ~(size_t)255));
+    const long threads = (long)npad * (kpad / 8);
+    hipLaunchKernelGGL(k_x_to_q8_frag, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, X,
+                       n, npad, L.k, kpad, xq, xr);
+    const int ntiles = npad / I8N, mtiles = (L.rows + I8M - 1) / I8M;
+    hipLaunchKernelGGL(k_gemm_i8_direct, dim3((unsigned)(mtiles * ntiles)), dim3(512), 0, st,
+                       (const uint8_t *)w->gemm_raw, L.rows, ntiles, (const int8_t *)xq,
+                       (const float2 *)xr, n, kpad, Y);
   }
   return hipGetLastError();
 }
