@@ -273,7 +273,7 @@ def q8_kv_leg(gq, cfg, hw, torch, stream):
     """The same decode with a Q8_0 KV cache (KvDtype::Q8_0): the context as
     synthetic Q8_0 rows (int8 codes ~ U[-127, 127], f16 scales ~ |N(0,1)|/127)
     prefilled to DECODE_PREFILL positions; DECODE_STEPS greedy steps."""
-    m = gq.DecodeModel(dict(cfg, max_tokens=DECODE_STEPS, kv_dtype="q8_0"), hw)
+    m = gq.DecodeModel(dict(cfg, max_tokens=max(DECODE_STEPS, 8), kv_dtype="q8_0"), hw)
     kvd = cfg["n_kv_heads"] * cfg["head_dim"]
     nb = kvd // 32
     rng = np.random.default_rng(13)
@@ -304,11 +304,11 @@ def decode_leg(be, gq, syn, torch, cpu_steps):
     f16 KV prefilled to 4096 positions, 128 greedy steps, one HIP graph
     replay per step).  Returns the figures and the oracle's host-side
     decode rate on a bounded sample (cpu_steps steps, same model)."""
-    cfg = dict(syn.QWEN25_7B, ctx=DECODE_PREFILL + DECODE_STEPS + 16)
+    cfg = dict(syn.QWEN25_7B, ctx=DECODE_PREFILL + max(DECODE_STEPS, 8) + 16)
     w = syn.make_decoder(cfg, seed=11)
     kv = syn.make_kv(cfg, DECODE_PREFILL, seed=12)
     hw = syn.upload_decoder(be, cfg, w)
-    m = gq.DecodeModel(dict(cfg, max_tokens=DECODE_STEPS), hw)
+    m = gq.DecodeModel(dict(cfg, max_tokens=max(DECODE_STEPS, 8)), hw)
     for layer in range(cfg["n_layers"]):
         m.kv_upload(layer, kv[0][layer], kv[1][layer])
     stream = torch.cuda.current_stream()
@@ -362,9 +362,12 @@ def main():
     ap.add_argument("--only", choices=["matvec", "decode", "gemm", "moe", "q8_0"],
                     help="run only this leg and print its figures (for profiling)")
     ap.add_argument("--cpu-decode-steps", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=DECODE_STEPS,
+                    help="greedy steps timed in the decode legs (128: BASELINE configs[3])")
     ap.add_argument("--calib-copy", action="store_true",
                     help="also run a plain 256 MiB device copy (HBM counter calibration)")
     args = ap.parse_args()
+    globals()["DECODE_STEPS"] = args.decode_steps
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
               "multi-GPU sharding of the path is not built.", file=sys.stderr)
