@@ -725,7 +725,7 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   if (!rc && L.kv_q8) rc = dalloc(m, &L.kscale, (size_t)d->n_layers * d->ctx * (kvd / 32));
   if (!rc && L.kv_q8) rc = dalloc(m, &L.vscale, (size_t)d->n_layers * d->ctx * (kvd / 32));
   float *buf = nullptr;
-  const int nb_amax = (d->vocab + gq::ARGMAX_SPAN - 1) / gq::ARGMAX_SPAN;
+  const int nb_amax = std::max((d->vocab + gq::ARGMAX_SPAN - 1) / gq::ARGMAX_SPAN, gq::ARGMAX_SLOTS);
   const size_t nbuf = 3 * ((size_t)H + 16) + 2 * ((size_t)nh * hd + 16) + 2 * (kvd + 16) +
                       ((size_t)d->ffn + 16) + ((size_t)d->vocab + 16) +
                       ((size_t)nh * L.att_chunks * (2 + hd) + 16) + (nb_amax + 16) + (hd / 2 + 16);
@@ -746,6 +746,13 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   L.rope_den = take(hd / 2);
   L.amax_count = ibuf; L.amax_i = ibuf + 1;
   hipError_t e = hipSuccess;
+  {  // argmax partial slots start neutral (-inf, INT_MAX): the fused head argmax
+     // reads all ARGMAX_SLOTS, of which only the head's blocks write
+    std::vector<float> nv((size_t)nb_amax, -INFINITY);
+    std::vector<int> ni((size_t)nb_amax, 0x7fffffff);
+    e = hipMemcpy(L.amax_v, nv.data(), nv.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(L.amax_i, ni.data(), ni.size() * 4, hipMemcpyHostToDevice);
+  }
   for (int l = 0; l < d->n_layers && e == hipSuccess; l++) {
     e = hipMemcpy(norms + (size_t)(2 * l) * H, d->attn_norm[l], H * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess)

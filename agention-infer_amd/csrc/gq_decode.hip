@@ -558,6 +558,28 @@ __global__ __launch_bounds__(256) void k_argmax(const float *logits, int n, floa
   }
 }
 
+// The head matvec's blocks leave the first maximum of their rows in
+// pv / pi[0 .. ARGMAX_SLOTS) (slots of blocks that do not exist keep
+// -inf / INT_MAX from set-up); one block reduces them and advances the step
+// state as k_argmax's last block does.  No fences: the kernel boundary
+// orders the partials before this read.
+__global__ __launch_bounds__(256) void k_argmax_final(const float *pv, const int *pi,
+                                                      DecodeState *st, int *tokens,
+                                                      int max_tokens) {
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int b = threadIdx.x; b < ARGMAX_SLOTS; b += 256) amax_merge(bv, bi, pv[b], pi[b]);
+  block_amax(bv, bi, sv, si);
+  if (threadIdx.x == 0) {
+    const int idx = bi == 0x7fffffff ? 0 : bi;  // no logit above -inf: index 0
+    const int step = st->step;
+    if (tokens && step < max_tokens) tokens[step] = idx;
+    *st = DecodeState{idx, st->pos + 1, step + 1, 0};
+  }
+}
+
 // Start a decode sequence: token and position from the host, step 0.
 __global__ void k_set_state(DecodeState *st, int token, int pos) {
   if (threadIdx.x == 0) *st = DecodeState{token, pos, 0, 0};
@@ -662,6 +684,14 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
   hin.q8k = true;  // the head: matmul_into (cpu_path.rs:815)
   const gq_weight *hw[1] = {m.lm_head};
   float *lo[1] = {m.logits};
+  if (m.lm_head->L.quad) {  // argmax partials from the head's blocks, one final block
+    hin.amax_v = m.amax_v;
+    hin.amax_i = m.amax_i;
+    if ((e = matvec_launch(hw, 1, hin, lo, s)) != hipSuccess) return e;
+    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, m.amax_v, m.amax_i, m.state,
+                       m.tokens, m.max_tokens);
+    return hipGetLastError();
+  }
   if ((e = matvec_launch(hw, 1, hin, lo, s)) != hipSuccess) return e;
   const int nb = (m.vocab + ARGMAX_SPAN - 1) / ARGMAX_SPAN;
   hipLaunchKernelGGL(k_argmax, dim3(nb), dim3(256), 0, s, m.logits, m.vocab, m.amax_v, m.amax_i,

@@ -61,6 +61,11 @@ struct MvIn {
   // route, src/model/mod.rs:381-394) instead of the float dot (dot_row,
   // the route of CpuBackend::matmul_dequant and ffn_gate_up).
   bool q8k = false;
+  // Quad-layout launches of one matrix: each block also writes the first
+  // maximum of its rows of y (value, row) to amax_v / amax_i[block]
+  // (greedy argmax, sampler.rs:120-131); null: off.
+  float *amax_v = nullptr;
+  int *amax_i = nullptr;
 };
 
 struct MvArgs {
@@ -159,6 +164,7 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
 constexpr int ATT_CHUNK = 64;    // positions per attention block
 constexpr int ATT_MAX_CTX = 65536;
 constexpr int ARGMAX_SPAN = 4096;  // logits per argmax block
+constexpr int ARGMAX_SLOTS = 1024;  // per-block partials of the fused head argmax
 hipError_t launch_set_state(DecodeState *st, int token, int pos, hipStream_t s);
 
 // Host-side launch of y_i = W_i . in for weights sharing dtype and in_dim;

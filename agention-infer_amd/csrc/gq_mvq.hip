@@ -478,6 +478,8 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   __syncthreads();
 
   // ---- per-row sums over the items, in item order
+  float bv = -INFINITY;  // this thread's first maximum (fused argmax)
+  int bi = 0x7fffffff;
   for (int lr = tid; lr < rows_blk; lr += NTH) {
     const int lg = lr / QROWS, rr = lr % QROWS;
     const int fg = b + lg * B;
@@ -501,6 +503,34 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
     float out = v[0];
     if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
     sg.y[row] = out;
+    if (out > bv) {  // rows rise with lr: strict > keeps the first maximum; NaN never wins
+      bv = out;
+      bi = row;
+    }
+  }
+  if constexpr (NT == 1) {
+    if (a.in.amax_v) {  // the block's first maximum (ties: lower row)
+      __shared__ float av[NW];
+      __shared__ int ai[NW];
+      auto merge = [](float &v0, int &i0, float v1, int i1) {
+        if (v1 > v0 || (v1 == v0 && i1 < i0)) {
+          v0 = v1;
+          i0 = i1;
+        }
+      };
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) merge(bv, bi, __shfl_xor(bv, off, 64), __shfl_xor(bi, off, 64));
+      if (lane == 0) {
+        av[wave] = bv;
+        ai[wave] = bi;
+      }
+      __syncthreads();
+      if (tid == 0) {
+        for (int w = 1; w < NW; w++) merge(bv, bi, av[w], ai[w]);
+        a.in.amax_v[b] = bv;
+        a.in.amax_i[b] = bi;
+      }
+    }
   }
 }
 

@@ -104,8 +104,26 @@ def test_generate_edges(backend):
         gm.decode(1, cfg["ctx"])
 
 
-@pytest.mark.timeout(1200)
-def test_generate_qwen25_7b_shape(backend):
+@pytest.fixture(scope="module")
+def qwen7b(backend):
+    """The 7B Q4_K_M-shaped decoder and a 4096-row KV context, uploaded once
+    for the three streams below."""
+    cfg = dict(syn.QWEN25_7B, ctx=4096 + 160)
+    w = syn.make_decoder(cfg, 11)
+    kv = syn.make_kv(cfg, 4096, 12)
+    hw = syn.upload_decoder(backend, cfg, w)
+    return cfg, w, kv, hw
+
+
+# (embedding scale, steps, KV from gq_model_prefill); one test each, so that
+# no single test runs the CPU oracle for much more than a minute.
+QWEN7B_STREAMS = [(1.0, 24, False), (1e9, 128, False), (1e9, 128, True)]
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("scale,n_steps,prefill", QWEN7B_STREAMS,
+                         ids=["constant-24", "varying-128-uploaded", "varying-128-prefilled"])
+def test_generate_qwen25_7b_shape(qwen7b, scale, n_steps, prefill):
     """the 7B Q4_K_M shape, 4096 cached positions, 128
     greedy steps.  With the specified N(0, 1) embedding the greedy token is
     the same at every step: the Q4_K blocks' positive mean (d*sc*7.5 -
@@ -122,44 +140,40 @@ def test_generate_qwen25_7b_shape(backend):
     Both streams must equal the oracle's greedy tokens for all 128 steps,
     and each first step's logits agree to LOGIT_TOL."""
     import gq
-    cfg = dict(syn.QWEN25_7B, ctx=4096 + 160)
-    w = syn.make_decoder(cfg, 11)
-    kv = syn.make_kv(cfg, 4096, 12)
-    hw = syn.upload_decoder(backend, cfg, w)
-    for scale, n_steps, prefill in ((1.0, 24, False), (1e9, 128, False), (1e9, 128, True)):
-        print(f"7b stream: embedding x{scale:g}, {n_steps} steps, "
-              f"{'prefilled by gq_model_prefill' if prefill else 'uploaded KV'}", flush=True)
-        ws = w
-        if scale != 1.0:
-            ws = dict(w, embd=w["embd"] * np.float32(scale),
-                      ffn_norm=[np.float32(1e-3) * a for a in w["ffn_norm"]])
-        gm = gq.DecodeModel(dict(cfg, max_tokens=160),
-                            dict(hw, embd=ws["embd"], ffn_norm=ws["ffn_norm"]))
-        if prefill:
-            toks = np.random.default_rng(13).integers(0, cfg["vocab"], 4096).astype(np.int32)
-            first, _ = gm.prefill(toks, 0, want_logits=False)
-            cache = [[], []]
-            for l in range(cfg["n_layers"]):
-                k, v = gm.kv_download(l, 4096)
-                cache[0].append(k)
-                cache[1].append(v)
-            ckv = (np.stack(cache[0]), np.stack(cache[1]))
-        else:
-            first = 1234
-            for l in range(cfg["n_layers"]):
-                gm.kv_upload(l, kv[0][l], kv[1][l])
-            ckv = kv
-        om = oracle.DecoderModel(cfg, ws, ckv)
-        ref0 = om.step(int(first), 4096)
-        nxt, got0 = gm.decode(int(first), 4096)
-        assert np.abs(got0 - ref0).max() <= LOGIT_TOL * np.abs(ref0).max()
-        assert nxt == oracle.argmax(ref0)
-        ref = [nxt] + list(_oracle_greedy(om, nxt, 4097, n_steps - 1))
-        got = gm.generate(int(first), 4096, n_steps)
-        np.testing.assert_array_equal(got, np.array(ref, np.int32))
-        if scale != 1.0:
-            assert len(set(ref)) > 8, "token stream should vary"
-        del gm, om
+    cfg, w, kv, hw = qwen7b
+    print(f"7b stream: embedding x{scale:g}, {n_steps} steps, "
+          f"{'prefilled by gq_model_prefill' if prefill else 'uploaded KV'}", flush=True)
+    ws = w
+    if scale != 1.0:
+        ws = dict(w, embd=w["embd"] * np.float32(scale),
+                  ffn_norm=[np.float32(1e-3) * a for a in w["ffn_norm"]])
+    gm = gq.DecodeModel(dict(cfg, max_tokens=160),
+                        dict(hw, embd=ws["embd"], ffn_norm=ws["ffn_norm"]))
+    if prefill:
+        toks = np.random.default_rng(13).integers(0, cfg["vocab"], 4096).astype(np.int32)
+        first, _ = gm.prefill(toks, 0, want_logits=False)
+        cache = [[], []]
+        for l in range(cfg["n_layers"]):
+            k, v = gm.kv_download(l, 4096)
+            cache[0].append(k)
+            cache[1].append(v)
+        ckv = (np.stack(cache[0]), np.stack(cache[1]))
+    else:
+        first = 1234
+        for l in range(cfg["n_layers"]):
+            gm.kv_upload(l, kv[0][l], kv[1][l])
+        ckv = kv
+    om = oracle.DecoderModel(cfg, ws, ckv)
+    ref0 = om.step(int(first), 4096)
+    nxt, got0 = gm.decode(int(first), 4096)
+    assert np.abs(got0 - ref0).max() <= LOGIT_TOL * np.abs(ref0).max()
+    assert nxt == oracle.argmax(ref0)
+    ref = [nxt] + list(_oracle_greedy(om, nxt, 4097, n_steps - 1))
+    got = gm.generate(int(first), 4096, n_steps)
+    np.testing.assert_array_equal(got, np.array(ref, np.int32))
+    if scale != 1.0:
+        assert len(set(ref)) > 8, "token stream should vary"
+    del gm, om
 
 
 def _q8_kv(cfg, n_ctx, seed):
