@@ -609,6 +609,48 @@ static int gq_ensure_gemm_records(const gq_weight *w, hipStream_t stream) {
   return GQ_OK;
 }
 
+}  // extern "C"
+
+namespace {
+// gq_gemm's workspace (the packed X), kept per (device, stream) and grown on
+// demand: calls on one stream are ordered, so they can share it.  Held until
+// the process ends.
+struct GemmWs {
+  int dev;
+  hipStream_t st;
+  void *p;
+  size_t bytes;
+};
+std::vector<GemmWs> g_gemm_ws;  // guarded by g_mu
+
+int gemm_workspace(hipStream_t st, size_t bytes, void **out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  for (GemmWs &w : g_gemm_ws) {
+    if (w.dev != dev || w.st != st) continue;
+    if (w.bytes < bytes) {
+      (void)hipStreamSynchronize(st);  // the old buffer may still be in use on st
+      (void)hipFree(w.p);
+      w.p = nullptr;
+      w.bytes = 0;
+      if (hipMalloc(&w.p, bytes) != hipSuccess)
+        return fail(GQ_ENOMEM, "gemm workspace of %zu bytes: hipMalloc failed", bytes);
+      w.bytes = bytes;
+    }
+    *out = w.p;
+    return GQ_OK;
+  }
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess)
+    return fail(GQ_ENOMEM, "gemm workspace of %zu bytes: hipMalloc failed", bytes);
+  g_gemm_ws.push_back(GemmWs{dev, st, p, bytes});
+  *out = p;
+  return GQ_OK;
+}
+}  // namespace
+
+extern "C" {
 int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mode,
             void *stream) {
   int rc = ensure_init();
@@ -626,10 +668,9 @@ int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mod
     if (rc2) return rc2;
   }
   void *wsp = nullptr;
-  if (ws) HIP_TRY(hipMallocAsync(&wsp, ws, (hipStream_t)stream));
+  if (ws && (rc = gemm_workspace((hipStream_t)stream, ws, &wsp))) return rc;
   hipError_t e = gq::launch_gemm(w, X_dev, n, Y_dev, mode, wsp, ws, g_dev.num_cus,
                                  (hipStream_t)stream);
-  if (wsp) (void)hipFreeAsync(wsp, (hipStream_t)stream);
   if (e != hipSuccess) return fail(GQ_EHIP, "gemm launch failed: %s", hipGetErrorString(e));
   return GQ_OK;
 }
