@@ -902,7 +902,8 @@ __global__ void k_x_to_q8_frag(const float *X, int n, int npad, int k, int kpad,
 //   * each wave loads its X fragments and (xs, xs sum q) records from
 //     global memory (L2) straight into registers, a stage ahead;
 //   * per sub-block and tile, one v_mfma_i32_16x16x32_i8 gives the exact
-//     integer dot D, and y += (d sc) xs D - (dmin m) xs sum(q) in fp32.
+//     integer dot D, and y += (d sc) xs D in fp32 (VALU); the min term
+//     - (dmin m) xs sum(q) goes through an fp32 MFMA every two stages.
 // One barrier per stage.
 constexpr int I8M = 160, I8N = 256;
 __global__ __launch_bounds__(512) void k_gemm_i8_direct(const uint8_t *rec, int rows, int ntiles,
@@ -972,37 +973,49 @@ __global__ __launch_bounds__(512) void k_gemm_i8_direct(const uint8_t *rec, int 
   for (int i = 0; i < 5; i++)
 #pragma unroll
     for (int jn = 0; jn < 4; jn++) acc[i][jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // Tiles t = 5 ks + i in a software pipeline: the MFMAs of tile t are
+  // issued before the scaling of tile t - 1, so the scaling VALU never
+  // waits for the integer results it needs.
   auto compute = [&](int buf, const XReg &x) {
+    i32x4_t dq[2][4];
+    float ws[2][4];
+    auto mf = [&](int t) {
+      const int ks = t / 5, rt = 5 * wm + t % 5;
+      const long a = *(const long *)&Aq[buf][(ks * 10 + rt) * 512 + lane * 8];
+      const float4 w01 = *(const float4 *)&Ws[buf][ks][16 * rt + 4 * (lane >> 4)];
+      const float4 w23 = *(const float4 *)&Ws[buf][ks][16 * rt + 4 * (lane >> 4) + 2];
+      ws[t & 1][0] = w01.x;
+      ws[t & 1][1] = w01.z;
+      ws[t & 1][2] = w23.x;
+      ws[t & 1][3] = w23.z;
 #pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-      for (int i = 0; i < 5; i++) {
-        const int rt = 5 * wm + i;
-        const long a = *(const long *)&Aq[buf][(ks * 10 + rt) * 512 + lane * 8];
-        const float4 w01 = *(const float4 *)&Ws[buf][ks][16 * rt + 4 * (lane >> 4)];
-        const float4 w23 = *(const float4 *)&Ws[buf][ks][16 * rt + 4 * (lane >> 4) + 2];
-        const float wsc[4] = {w01.x, w01.z, w23.x, w23.z}, wmn[4] = {w01.y, w01.w, w23.y, w23.w};
-        i32x4_t dq[4];
-#pragma unroll
-        for (int jn = 0; jn < 4; jn++) {
-          const i32x4_t z = {0, 0, 0, 0};
-          dq[jn] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, x.b[ks][jn], z, 0, 0, 0);
-        }
-#pragma unroll
-        for (int jn = 0; jn < 4; jn++) {
-          const float xs = x.r[ks][jn].x, xm = x.r[ks][jn].y;
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float v = fmaf(wsc[r] * xs, (float)dq[jn][r], acc[i][jn][r]);
-            acc[i][jn][r] = fmaf(-wmn[r], xm, v);
-          }
-          // keep the update here (not sunk past the next tile's MFMAs,
-          // which would keep every tile's integer result live at once)
-          asm volatile("" : "+v"(acc[i][jn]));
-        }
-        __builtin_amdgcn_sched_barrier(0);
+      for (int jn = 0; jn < 4; jn++) {
+        const i32x4_t z = {0, 0, 0, 0};
+        dq[t & 1][jn] = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, x.b[ks][jn], z, 0, 0, 0);
       }
+    };
+    auto scale = [&](int t) {
+      const int ks = t / 5, i = t % 5;
+#pragma unroll
+      for (int jn = 0; jn < 4; jn++) {
+        const float xs = x.r[ks][jn].x;
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          acc[i][jn][r] = fmaf(ws[t & 1][r] * xs, (float)dq[t & 1][jn][r], acc[i][jn][r]);
+        // keep the update here (not sunk below later tiles' MFMAs, which
+        // would keep every tile's integer result live at once)
+        asm volatile("" : "+v"(acc[i][jn]));
+      }
+    };
+    mf(0);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 1; t < 10; t++) {
+      mf(t);
+      scale(t - 1);
+      __builtin_amdgcn_sched_barrier(0);
     }
+    scale(9);
   };
   // prologue: stage 0 to LDS; each stage then loads its X and the next
   // stage's W while it computes
@@ -1011,15 +1024,63 @@ __global__ __launch_bounds__(512) void k_gemm_i8_direct(const uint8_t *rec, int 
     store_w(0, 0, c);
   }
   __syncthreads();
-  for (int kt = 0; kt < stages; kt++) {
-    XReg x;
-    load_x(kt, x);
+  // The min term -sum_sb (dmin m)[row][sb] (xs sum q)[token][sb] is a small
+  // product over the sub-blocks: every two stages (4 sub-blocks, both W
+  // slots of LDS still valid) one v_mfma_f32_16x16x4_f32 per tile adds it,
+  // lane l giving row l % 16 of -(dmin m) and token l % 16 of xs sum q for
+  // sub-block l / 16 (stages is a multiple of 4: kpad is whole units).
+  // The previous stage's LDS slot is being refilled with the next stage's W
+  // by other waves during an odd stage, so its (dmin m) values are taken
+  // into registers at the even stage.
+  const int sbl = lane >> 4;
+  float xmp[2][4];  // xs sum q of the previous stage, per (ks, token tile)
+  float amp[5];     // -(dmin m) of the previous stage, per row tile (lanes sbl < 2)
+  auto mins = [&](int kt, const XReg &x) {
+    const int mks = sbl & 1;
+    float bq[4];
+#pragma unroll
+    for (int jn = 0; jn < 4; jn++) {
+      const float p0 = mks ? xmp[1][jn] : xmp[0][jn];
+      const float c0 = mks ? x.r[1][jn].y : x.r[0][jn].y;
+      bq[jn] = sbl < 2 ? p0 : c0;
+    }
+#pragma unroll
+    for (int i = 0; i < 5; i++) {
+      const float am = sbl < 2 ? amp[i] : -Ws[kt & 1][mks][16 * (5 * wm + i) + (lane & 15)].y;
+#pragma unroll
+      for (int jn = 0; jn < 4; jn++)
+        acc[i][jn] = __builtin_amdgcn_mfma_f32_16x16x4f32(am, bq[jn], acc[i][jn], 0, 0, 0);
+    }
+  };
+  // X of stage kt + 1 is loaded while stage kt computes (two register sets,
+  // the loop unrolled by two).
+  auto stage = [&](int kt, const XReg &x, XReg &xn) {
     uint4 c = make_uint4(0, 0, 0, 0);
-    if (kt + 1 < stages) c = load_w(kt + 1);
+    if (kt + 1 < stages) {
+      c = load_w(kt + 1);
+      load_x(kt + 1, xn);
+    }
     __builtin_amdgcn_sched_barrier(0);
     compute(kt & 1, x);
+    if (kt & 1) {
+      mins(kt, x);
+    } else {
+#pragma unroll
+      for (int jn = 0; jn < 4; jn++) {
+        xmp[0][jn] = x.r[0][jn].y;
+        xmp[1][jn] = x.r[1][jn].y;
+      }
+#pragma unroll
+      for (int i = 0; i < 5; i++) amp[i] = -Ws[kt & 1][sbl & 1][16 * (5 * wm + i) + (lane & 15)].y;
+    }
     if (kt + 1 < stages) store_w(kt + 1, (kt + 1) & 1, c);
     __syncthreads();
+  };
+  XReg x0, x1;
+  load_x(0, x0);
+  for (int kt = 0; kt < stages; kt += 2) {  // stages is even (a multiple of 4)
+    stage(kt, x0, x1);
+    stage(kt + 1, x1, x0);
   }
   // D layout: lane holds rows 4 (lane / 16) + r of token column lane % 16.
 #pragma unroll
