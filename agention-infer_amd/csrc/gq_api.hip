@@ -184,9 +184,9 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   w->L.units = (in_dim + 255) / 256;
   w->L.chunks = gq::unit_chunks(dtype);
   w->L.rt = std::max(out_dim, 1);  // one tile: the whole matrix
-  // Dense Q4_K / Q5_K / Q6_K / Q8_0 matrices take the quad layout of the
-  // MFMA matvec; IQ3_XXS and stacked expert tensors the wave-tiled one.
-  w->L.quad = rows_per_group == 0 && dtype != gq::T_IQ3_XXS;
+  // Dense matrices take the quad layout of the MFMA matvec; stacked expert
+  // tensors the wave-tiled one.
+  w->L.quad = rows_per_group == 0;
   // Stacked expert tensors: one tile per expert.
   if (rows_per_group > 0) w->L.rt = rows_per_group;
   w->ggml_bytes = need;

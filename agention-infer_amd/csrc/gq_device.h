@@ -95,6 +95,15 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
   }
 }
 
+// IQ3_XXS: a sign is applied by two's-complement negation of a magnitude
+// byte, (g ^ 0xff) + 1 per byte (bit b of the nibble: byte b negative),
+// which cannot carry because magnitudes are in 1..127 (enforced when a
+// codebook is installed).
+__device__ __forceinline__ uint32_t neg_bytes(uint32_t g, uint32_t nib) {
+  const uint32_t m = ((nib * 0x00204081u) & 0x01010101u) * 0xFFu;  // 0xff per negative byte
+  return (g ^ m) + (m & 0x01010101u);
+}
+
 // ksigns_iq2xs[i]: 7 sign bits plus an even-parity 8th bit.
 __device__ __forceinline__ uint32_t ksign7(uint32_t i) {
   return i | ((uint32_t)(__popc(i) & 1) << 7);

@@ -231,13 +231,8 @@ __device__ __forceinline__ float unit_q80(const uint4 *ch, int u, const Smem &S)
 
 // ------------------------------------------------------------- IQ3_XXS
 // ch[0..3] = 64 grid indices, ch[4..5] = 8 sign/scale words; d separate.
-// A sign is applied by two's-complement negation of the magnitude byte:
-// (g ^ 0xff) + 1 per byte, which cannot carry because magnitudes are in
-// 1..127 (enforced when a codebook is installed).
-__device__ __forceinline__ uint32_t neg_bytes(uint32_t g, uint32_t nib) {
-  const uint32_t m = ((nib * 0x00204081u) & 0x01010101u) * 0xFFu;  // 0xff per negative byte
-  return (g ^ m) + (m & 0x01010101u);
-}
+// A sign is applied by two's-complement negation of the magnitude byte
+// (neg_bytes, gq_device.h).
 
 __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u, const Smem &S) {
   const float d = h2f(dbits);

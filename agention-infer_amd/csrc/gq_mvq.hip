@@ -70,12 +70,14 @@ template <> struct QF<T_Q5_K> { static constexpr int C = 11, AUX = 8; };
 template <> struct QF<T_Q5_K8> { static constexpr int C = 11, AUX = 16; };
 template <> struct QF<T_Q6_K> { static constexpr int C = 13, AUX = 16; };
 template <> struct QF<T_Q8_0> { static constexpr int C = 17, AUX = 0; };
+template <> struct QF<T_IQ3_XXS> { static constexpr int C = 6, AUX = 0; };
 
 // LDS: limbs [3][units][QL_STRIDE] (Q5_K8: the Q8_K codes in limb 0),
 // zeros [QZERO], per-unit scale s [units] (Q5_K8: the Q8_K d), per-unit aux
 // [units][AUX] (Q4_K/Q5_K: fp32 sums of the 8 sub-blocks; Q6_K: int sums of
 // the 16 runs of X; Q5_K8: bsums as int), per-item row sums [items][16],
-// 16 floats of reduction scratch, the item counter.
+// 16 floats of reduction scratch, the item counter, and for IQ3_XXS the
+// signed codebook (4096 words: 256 entries x 16 sign nibbles).
 struct QSmem {
   uint8_t *limb;
   uint32_t zero_off;
@@ -84,10 +86,11 @@ struct QSmem {
   float *part;
   float *red;
   int *ctr;
+  uint32_t *grid;  // IQ3_XXS: the signed codebook, [entry][sign nibble]
 };
 
 __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int part_floats,
-                                               QSmem *s, char *base) {
+                                               QSmem *s, char *base, int grid_words = 0) {
   size_t o = 0;
   auto take = [&](size_t n) { size_t r = o; o += (n + 15) & ~(size_t)15; return r; };
   const int upad = (units + 3) & ~3;  // the last quad's missing units stay in bounds
@@ -98,6 +101,7 @@ __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int 
   const size_t op = take((size_t)part_floats * 4);
   const size_t orr = take(64);
   const size_t oc = take(16);
+  const size_t og = take((size_t)grid_words * 4);
   if (s) {
     s->limb = (uint8_t *)(base + ol);
     s->zero_off = (uint32_t)oz;
@@ -106,6 +110,7 @@ __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int 
     s->part = (float *)(base + op);
     s->red = (float *)(base + orr);
     s->ctr = (int *)(base + oc);
+    s->grid = (uint32_t *)(base + og);
   }
   return o;
 }
@@ -273,6 +278,35 @@ __device__ __forceinline__ float item_dot(const uint4 *ch, uint32_t dbits, const
       }
     }
     return h2f(dbits) * S.us[u] * (combine(acc2, acc1, acc0) - 32.f * corr);
+  } else if constexpr (FMT == T_IQ3_XXS) {
+    // ch[0..3] = 64 grid indices (8 per 32-element sub-block), ch[4..5] = 8
+    // words of 4 x 7-bit sign indices + 4-bit scale s; d separately.
+    // w = d (0.5 + s) 0.5 * grid * sign = d/4 * (2s + 1) * (signed grid):
+    // the signed grid values are the MFMA codes, (2s + 1) applies per
+    // sub-block in integers.
+    int acc2 = 0, acc1 = 0, acc0 = 0;
+#pragma unroll
+    for (int ib = 0; ib < 8; ib++) {
+      const uint32_t aux = dw(ch + 4, ib);
+      const uint32_t i0 = dw(ch, 2 * ib), i1 = dw(ch, 2 * ib + 1);
+      uint32_t q[8];
+#pragma unroll
+      for (int l = 0; l < 4; l++) {
+        const uint32_t sg = ksign7((aux >> (7 * l)) & 127u);
+        const uint32_t word = l < 2 ? i0 : i1;
+        const uint32_t e1 = (word >> (16 * (l & 1))) & 0xffu, e2 = (word >> (16 * (l & 1) + 8)) & 0xffu;
+        q[2 * l] = S.grid[(e1 << 4) | (sg & 15u)];
+        q[2 * l + 1] = S.grid[(e2 << 4) | (sg >> 4)];
+      }
+      i32x4 dd = mfma(lds16(smem, a + 32 * ib), i32x4{(int)q[0], (int)q[1], (int)q[2], (int)q[3]},
+                      i32x4{0, 0, 0, 0});
+      dd = mfma(lds16(smem, a + 32 * ib + 16), i32x4{(int)q[4], (int)q[5], (int)q[6], (int)q[7]}, dd);
+      const int s2 = (int)(2 * (aux >> 28) + 1);
+      acc2 += __mul24(s2, dd[0]);
+      acc1 += __mul24(s2, dd[1]);
+      acc0 += __mul24(s2, dd[2]);
+    }
+    return 0.25f * h2f(dbits) * S.us[u] * combine(acc2, acc1, acc0);
   } else {  // Q8_0: ch[0..15] qs of 8 blocks, ch[16] their f16 d
     float acc = 0.f;
 #pragma unroll
@@ -298,7 +332,7 @@ template <int FMT, bool K4, int SRC, int NT>
 __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   extern __shared__ __align__(16) char smem[];
   constexpr int NW = mvq_waves(FMT), NTH = 64 * NW, C = QF<FMT>::C;
-  constexpr bool HAS_D = FMT == T_Q6_K;
+  constexpr bool HAS_D = FMT == T_Q6_K || FMT == T_IQ3_XXS;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int U = a.units, T = (U + 3) >> 2, upad = 4 * T;
@@ -317,7 +351,7 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   const int nitems = ngb * NT * T;
   const int rows_blk = ngb * QROWS;
   QSmem S;
-  qsmem_layout(QF<FMT>::AUX, U, nitems * QROWS, &S, smem);
+  qsmem_layout(QF<FMT>::AUX, U, nitems * QROWS, &S, smem, FMT == T_IQ3_XXS ? 4096 : 0);
 
   // Item cursor (wave-uniform): local and flat group, matrix, quad, segment.
   struct Cur {
@@ -389,6 +423,13 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
     // the x loads of the first NP passes, then the first items' loads, then
     // the conversion (later passes one by one)
     constexpr int NP = sizeof(typename XS::Raw) <= 64 ? 3 : 2;
+    // IQ3_XXS: this thread's words of the codebook, loaded first (before x
+    // and the weights: loads complete in order), signed into LDS below.
+    constexpr int GW = FMT == T_IQ3_XXS ? 4096 / NTH : 1;
+    uint32_t gword[GW];
+    if constexpr (FMT == T_IQ3_XXS)
+#pragma unroll
+      for (int i = 0; i < GW; i++) gword[i] = a.grid[(tid + NTH * i) >> 4];
     typename XS::Raw raw[NP];
 #pragma unroll
     for (int k = 0; k < NP; k++)
@@ -414,6 +455,12 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
       xsrc.make(r1, e0, xv);
       stage16<FMT>(kpad, e0, xv, S, upad);
     }
+    if constexpr (FMT == T_IQ3_XXS)
+#pragma unroll
+      for (int i = 0; i < GW; i++) {
+        const int o = tid + NTH * i;
+        S.grid[o] = neg_bytes(gword[i], o & 15);
+      }
     if constexpr (!IsExact<XS>::value) xsrc.pre_barrier(S.red);
     __syncthreads();
     rscale = xsrc.scale(S.red);
@@ -560,7 +607,7 @@ hipError_t mvq_launch_f(const MvArgs &a, size_t lds, hipStream_t st) {
 }
 
 int aux_per_unit(int fmt) {
-  return fmt == T_Q4_K || fmt == T_Q5_K ? 8 : fmt == T_Q8_0 ? 0 : 16;
+  return fmt == T_Q4_K || fmt == T_Q5_K ? 8 : fmt == T_Q8_0 || fmt == T_IQ3_XXS ? 0 : 16;
 }
 
 }  // namespace
@@ -585,7 +632,8 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
   a.blocks = std::max(1, std::min(G, num_cus * bpc));
   const int fmt = a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt;
   const int ngb = (G + a.blocks - 1) / a.blocks, T = (a.units + 3) / 4;
-  return qsmem_layout(aux_per_unit(fmt), a.units, ngb * nt * T * QROWS, nullptr, nullptr);
+  return qsmem_layout(aux_per_unit(fmt), a.units, ngb * nt * T * QROWS, nullptr, nullptr,
+                      fmt == T_IQ3_XXS ? 4096 : 0);
 }
 
 hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {
@@ -595,6 +643,7 @@ hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {
   case T_Q5_K: return a.in.q8k && !a.pair ? mvq_launch_f<T_Q5_K8>(a, lds, st) : mvq_launch_f<T_Q5_K>(a, lds, st);
   case T_Q6_K: return mvq_launch_f<T_Q6_K>(a, lds, st);
   case T_Q8_0: return mvq_launch_f<T_Q8_0>(a, lds, st);
+  case T_IQ3_XXS: return mvq_launch_f<T_IQ3_XXS>(a, lds, st);
   default: return hipErrorInvalidValue;
   }
 }
