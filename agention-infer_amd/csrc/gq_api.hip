@@ -184,9 +184,10 @@ int upload_common(int dtype, const void *src, bool src_on_device, size_t nbytes,
   w->L.units = (in_dim + 255) / 256;
   w->L.chunks = gq::unit_chunks(dtype);
   w->L.rt = std::max(out_dim, 1);  // one tile: the whole matrix
-  // Dense matrices take the quad layout of the MFMA matvec; stacked expert
+  // Dense matrices, and stacked expert tensors whose experts are whole row
+  // groups of 16, take the quad layout of the MFMA kernels; other stacked
   // tensors the wave-tiled one.
-  w->L.quad = rows_per_group == 0;
+  w->L.quad = rows_per_group == 0 || rows_per_group % gq::QROWS == 0;
   // Stacked expert tensors: one tile per expert.
   if (rows_per_group > 0) w->L.rt = rows_per_group;
   w->ggml_bytes = need;
@@ -320,16 +321,56 @@ int gq_upload_experts(int dtype, const void *w_host, size_t nbytes, int in_dim,
 }  // extern "C"
 
 namespace {
+// The workspace of gq_gemm (the packed X) and gq_moe_ffn (the SwiGLU
+// outputs and routing), kept per (device, stream) and grown on
+// demand: calls on one stream are ordered, so they can share it.  Held until
+// the process ends.
+struct StreamWs {
+  int dev;
+  hipStream_t st;
+  void *p;
+  size_t bytes;
+};
+std::vector<StreamWs> g_stream_ws;  // guarded by g_mu
+
+int stream_workspace(hipStream_t st, size_t bytes, void **out) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  for (StreamWs &w : g_stream_ws) {
+    if (w.dev != dev || w.st != st) continue;
+    if (w.bytes < bytes) {
+      (void)hipStreamSynchronize(st);  // the old buffer may still be in use on st
+      (void)hipFree(w.p);
+      w.p = nullptr;
+      w.bytes = 0;
+      if (hipMalloc(&w.p, bytes) != hipSuccess)
+        return fail(GQ_ENOMEM, "workspace of %zu bytes: hipMalloc failed", bytes);
+      w.bytes = bytes;
+    }
+    *out = w.p;
+    return GQ_OK;
+  }
+  void *p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess)
+    return fail(GQ_ENOMEM, "workspace of %zu bytes: hipMalloc failed", bytes);
+  g_stream_ws.push_back(StreamWs{dev, st, p, bytes});
+  *out = p;
+  return GQ_OK;
+}
+}  // namespace
+
+namespace {
 // gq_moe_ffn and its no-allocation variant: with noalloc the workspace is
 // the device's scratch array (sizes above GQ_MOE_NOALLOC_MAX_BYTES are
-// refused), otherwise a stream-ordered allocation freed after the launch.
+// refused), otherwise the stream's cached workspace.
 int moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, int n_experts,
             const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
             int *ids_dev, float *w_dev, void *stream, bool noalloc) {
   int rc = ensure_init();
   if (rc) return rc;
   if (!gate || !up || !down) return fail(GQ_EINVAL, "null expert weight handle");
-  if (T < 0 || n_experts <= 0 || n_experts > 4096 || top_k <= 0 || top_k > n_experts)
+  if (T < 0 || n_experts <= 0 || n_experts > 4096 || top_k <= 0 || top_k > n_experts || top_k > 64)
     return fail(GQ_EINVAL, "bad MoE shape T=%d experts=%d top_k=%d", T, n_experts, top_k);
   if (T == 0) return GQ_OK;
   const int h = gate->L.k, f = down->L.k;
@@ -342,7 +383,10 @@ int moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, i
   if (gate->L.rt != f || up->L.rt != f || down->L.rt != h)
     return fail(GQ_EINVAL, "expert tensors must be uploaded with gq_upload_experts");
   if (!logits_dev || !x_dev || !out_dev) return fail(GQ_EINVAL, "null MoE buffer");
-  if (gq::moe_lds_bytes(gate->L.dtype, h, f, top_k, T, g_dev.num_cus) > 160 * 1024)
+  if (gate->L.quad != up->L.quad)
+    return fail(GQ_EINVAL, "gate and up expert tensors must share one layout");
+  if (gq::moe_lds_bytes(gate->L.dtype, h, f, top_k, T, g_dev.num_cus, gate->L.quad, down->L.quad) >
+      160 * 1024)
     return fail(GQ_EINVAL, "MoE shape h %d f %d top_k %d too large for the LDS-staged kernels", h, f,
                 top_k);
   const int pairs = T * top_k;
@@ -357,8 +401,8 @@ int moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, i
     if (g_dev.device < 0 || g_dev.device >= MAX_DEVICES || !g_scratch_dev[g_dev.device])
       return fail(GQ_ENODEV, "gq_moe_ffn_noalloc: no scratch on device %d", g_dev.device);
     wsp = (char *)g_scratch_dev[g_dev.device];
-  } else {
-    HIP_TRY(hipMallocAsync((void **)&wsp, ws, (hipStream_t)stream));
+  } else if ((rc = stream_workspace((hipStream_t)stream, ws, (void **)&wsp))) {
+    return rc;
   }
   gq::MoeArgs a{};
   a.fmt = gate->L.dtype;
@@ -378,8 +422,9 @@ int moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, i
   a.ids = ids_dev ? ids_dev : (int *)(a.hbuf + (size_t)pairs * f);
   a.w = w_dev ? w_dev : (float *)((int *)(a.hbuf + (size_t)pairs * f) + pairs);
   a.out = out_dev;
+  a.quad_gu = gate->L.quad;
+  a.quad_dn = down->L.quad;
   hipError_t e = gq::launch_moe(a, T, (hipStream_t)stream);
-  if (!noalloc) (void)hipFreeAsync(wsp, (hipStream_t)stream);
   if (e != hipSuccess) return fail(GQ_EHIP, "MoE launch failed: %s", hipGetErrorString(e));
   return GQ_OK;
 }
@@ -611,44 +656,6 @@ static int gq_ensure_gemm_records(const gq_weight *w, hipStream_t stream) {
 
 }  // extern "C"
 
-namespace {
-// gq_gemm's workspace (the packed X), kept per (device, stream) and grown on
-// demand: calls on one stream are ordered, so they can share it.  Held until
-// the process ends.
-struct GemmWs {
-  int dev;
-  hipStream_t st;
-  void *p;
-  size_t bytes;
-};
-std::vector<GemmWs> g_gemm_ws;  // guarded by g_mu
-
-int gemm_workspace(hipStream_t st, size_t bytes, void **out) {
-  std::lock_guard<std::mutex> lk(g_mu);
-  int dev = 0;
-  (void)hipGetDevice(&dev);
-  for (GemmWs &w : g_gemm_ws) {
-    if (w.dev != dev || w.st != st) continue;
-    if (w.bytes < bytes) {
-      (void)hipStreamSynchronize(st);  // the old buffer may still be in use on st
-      (void)hipFree(w.p);
-      w.p = nullptr;
-      w.bytes = 0;
-      if (hipMalloc(&w.p, bytes) != hipSuccess)
-        return fail(GQ_ENOMEM, "gemm workspace of %zu bytes: hipMalloc failed", bytes);
-      w.bytes = bytes;
-    }
-    *out = w.p;
-    return GQ_OK;
-  }
-  void *p = nullptr;
-  if (hipMalloc(&p, bytes) != hipSuccess)
-    return fail(GQ_ENOMEM, "gemm workspace of %zu bytes: hipMalloc failed", bytes);
-  g_gemm_ws.push_back(GemmWs{dev, st, p, bytes});
-  *out = p;
-  return GQ_OK;
-}
-}  // namespace
 
 extern "C" {
 int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mode,
@@ -668,7 +675,7 @@ int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mod
     if (rc2) return rc2;
   }
   void *wsp = nullptr;
-  if (ws && (rc = gemm_workspace((hipStream_t)stream, ws, &wsp))) return rc;
+  if (ws && (rc = stream_workspace((hipStream_t)stream, ws, &wsp))) return rc;
   hipError_t e = gq::launch_gemm(w, X_dev, n, Y_dev, mode, wsp, ws, g_dev.num_cus,
                                  (hipStream_t)stream);
   if (e != hipSuccess) return fail(GQ_EHIP, "gemm launch failed: %s", hipGetErrorString(e));

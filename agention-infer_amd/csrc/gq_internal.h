@@ -98,12 +98,14 @@ struct MoeArgs {
   float *w;                         // [T][top_k]
   float *hbuf;                      // [T*top_k][f] silu(gate . x) * (up . x)
   float *out;                       // [T][h]
+  int quad_gu, quad_dn;             // gate/up, down in the quad layout (MFMA kernels)
+  int lds_gu, lds_dn;               // dynamic LDS bytes of the two stages' blocks
 };
 
 constexpr int MOE_ROUTE_MAX = 1024;  // experts routed inside the gate/up kernel
 
 // LDS bytes of the MoE kernels' blocks for this shape (<= 160 KiB to run).
-size_t moe_lds_bytes(int fmt, int h, int f, int top_k, int T, int cus);
+size_t moe_lds_bytes(int fmt, int h, int f, int top_k, int T, int cus, bool quad_gu, bool quad_dn);
 hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st);
 
 // LDS bytes of a matvec block: x limbs, records, codebook and part_total
@@ -117,6 +119,12 @@ hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st);
 // (returns the LDS bytes of a block) and launch.
 size_t mvq_plan(MvArgs &a, int num_cus);
 hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st);
+// The MFMA MoE stages over quad-layout experts (stage 1: gate/up with the
+// SwiGLU, routing inside when route; stage 2: down with the weighted
+// combine): plan (sets bpp or bpt, part and lds fields; returns the LDS
+// bytes of a block, static included) and launch.
+size_t mvq_moe_plan(MoeArgs &a, int T, int stage, int num_cus);
+hipError_t launch_mvq_moe(const MoeArgs &a, int T, int stage, bool route, hipStream_t st);
 
 // Decode step state in device memory (advanced by the argmax kernel).
 struct DecodeState {

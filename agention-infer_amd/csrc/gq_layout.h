@@ -44,7 +44,9 @@ struct Layout {
   int rt;      // rows per tile: all rows (one tile) for matvec weights; a
                // power of two <= 64 dividing the rows per expert for stacked
                // expert tensors
-  int quad;    // 1: the quad layout (one tile, rt = rows)
+  int quad;    // 1: the quad layout (row groups of 16 over all rows; with
+               // stacked experts rt is a multiple of 16, so expert e's
+               // matrix is a quad matrix of its own starting at unit e rt U)
 };
 
 constexpr int QROWS = 16;  // rows per row group of the quad layout
@@ -63,8 +65,8 @@ __host__ __device__ constexpr int unit_chunks(int t) {
 
 // Byte offset of chunk c of unit j (0 <= j < units in tile) of tile t.
 __host__ __device__ inline long chunk_offset(const Layout &L, int t, int j, int c) {
-  if (L.quad) {  // one tile; j = row * U + unit
-    const int row = j / L.units, u = j - row * L.units;
+  if (L.quad) {  // j = row * U + unit within tile t
+    const int row = t * L.rt + j / L.units, u = j % L.units;
     int nr, nq;
     const long base = quad_item_unit(L, row / QROWS, u >> 2, nr, nq);
     return (base * L.chunks + (long)c * nr * nq + (long)nr * (u & 3) + row % QROWS) * 16;
@@ -82,7 +84,7 @@ __host__ __device__ inline long chunk_offset(const Layout &L, int t, int j, int 
 
 __host__ __device__ inline long unit_index(const Layout &L, int t, int j) {
   if (L.quad) {
-    const int row = j / L.units, u = j - row * L.units;
+    const int row = t * L.rt + j / L.units, u = j % L.units;
     int nr, nq;
     return quad_item_unit(L, row / QROWS, u >> 2, nr, nq) + (long)nr * (u & 3) + row % QROWS;
   }

@@ -33,6 +33,7 @@
 
 #include "gq_device.h"
 #include "gq_internal.h"
+#include "gq_moe.h"
 #include "gq_xsrc.h"
 
 namespace gq {
@@ -629,69 +630,8 @@ __global__ __launch_bounds__(mv_threads(FMT)) void k_moe_gate_up(MoeArgs a) {
   XPlain<K4> xs{a.x + (long)tok * a.h, a.h};
   // Routing runs while the x loads are in flight.
   auto route = [&] {
-    if constexpr (ROUTE) {
-      __shared__ __align__(16) float lv[MOE_ROUTE_MAX];
-      __shared__ int prank[4][MOE_ROUTE_MAX / 4];
-      __shared__ float rmax[NW], rsum[NW];
-      __shared__ int eid_s;
-      const int E = a.n_experts, slot = p - tok * a.top_k;
-      const float *lg = a.logits + (long)tok * E;
-      // Logits padded with -inf to a multiple of 16 (-inf past E beats
-      // nothing and, at a higher index, ties with nothing).
-      const int E16 = (E + 15) & ~15;
-      if (tid == 0) eid_s = 0;  // (NaN logits can leave a rank unused)
-      float mx = -INFINITY;
-      for (int i = tid; i < E16; i += NTH) {
-        lv[i] = i < E ? lg[i] : -INFINITY;
-        mx = fmaxf(mx, lv[i]);
-      }
-      __syncthreads();
-      // rank(i) = #{o : l_o > l_i or (l_o == l_i and o < i)}; with 4 * E16
-      // threads or more, thread (q, i) counts over the quarter q of o.
-      const bool split = 4 * E16 <= NTH;
-      const int nq = split ? 4 : 1, span = E16 / nq;
-      for (int t = tid; t < nq * E16; t += NTH) {
-        const int i = t % E16, q = t / E16;
-        const float me = lv[i];
-        int rank = 0;
-#pragma unroll 4
-        for (int o = q * span; o < (q + 1) * span; o += 4) {
-          const float4 ov = *(const float4 *)&lv[o];
-          rank += (ov.x > me) || (ov.x == me && o < i);
-          rank += (ov.y > me) || (ov.y == me && o + 1 < i);
-          rank += (ov.z > me) || (ov.z == me && o + 2 < i);
-          rank += (ov.w > me) || (ov.w == me && o + 3 < i);
-        }
-        if (split) prank[q][i] = rank;
-        else if (i < E && rank == slot) eid_s = i;
-      }
-      if (split) {
-        __syncthreads();
-        if (tid < E && prank[0][tid] + prank[1][tid] + prank[2][tid] + prank[3][tid] == slot)
-          eid_s = tid;
-      }
-      if (lb == 0) {  // softmax over all experts (k_moe_route)
-        mx = wave_max(mx);
-        if (lane == 0) rmax[wave] = mx;
-        __syncthreads();
-        mx = rmax[0];
-        for (int w = 1; w < NW; w++) mx = fmaxf(mx, rmax[w]);
-        float sum = 0.f;
-        for (int i = tid; i < E; i += NTH) sum += expf(lv[i] - mx);
-        sum = wave_sum(sum);
-        if (lane == 0) rsum[wave] = sum;
-      }
-      __syncthreads();
-      e = eid_s;
-      if (lb == 0 && tid == 0) {
-        float sum = 0.f;
-        for (int w = 0; w < NW; w++) sum += rsum[w];
-        a.ids[p] = e;
-        a.w[p] = expf(lv[e] - mx) / sum;
-      }
-    } else {
-      e = a.ids[p];
-    }
+    if constexpr (ROUTE) e = moe_route_pair<NTH>(a, p, lb == 0);
+    else e = a.ids[p];
   };
   stage_block<FMT, 1, NTH>(xs, U * 256, S, a.grid, [&] {
     route();
@@ -708,25 +648,6 @@ __global__ __launch_bounds__(mv_threads(FMT)) void k_moe_gate_up(MoeArgs a) {
     if (sub == G - 1 && r < rows_b) a.hbuf[(long)p * f + r0 + r] = g / (1.0f + expf(-g)) * u;
   }
 }
-
-// The top_k inputs h_(t, s) of a token, one after another, each padded to
-// whole units: element e is element e % (U_f * 256) of slot e / (U_f * 256).
-template <bool K4>
-struct XSlots {
-  const float *h;  // [pairs][f]
-  int f, span, top_k, p0;
-  struct Raw { float v[16]; };
-  __device__ __forceinline__ void issue(int e0, Raw &r) const {
-    const int s = min(e0 / span, top_k - 1), i0 = e0 - s * span;
-    load_x16<K4>(h + (long)(p0 + s) * f, f, i0 < span ? i0 : span, r.v);
-  }
-  __device__ __forceinline__ void make(const Raw &r, int, float (&xv)[16]) {
-#pragma unroll
-    for (int i = 0; i < 16; i++) xv[i] = r.v[i];
-  }
-  __device__ __forceinline__ void pre_barrier(float *) const {}
-  __device__ __forceinline__ float scale(const float *) const { return 1.f; }
-};
 
 // Stage 2 with the weighted combine (moe_ffn): out[t] = sum_s w[t][s] *
 // (down_(e_s) . h_(t, s)), slots in order.  Block lb of token t (bpt per
@@ -887,30 +808,41 @@ static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
 }
 
 // Blocks per pair (gate/up) and per token (down): about one block per CU
-// in all, more while a block's partial sums would not fit in LDS.
+// in all, more while a block's partial sums would not fit in LDS.  Stages
+// over quad-layout experts take the MFMA kernels' plan.
 static size_t moe_plan(MoeArgs &a, int T, int cus) {
   const int pairs = T * a.top_k;
-  a.bpp = std::max(1, std::min(a.f, cus / pairs));
-  a.bpt = std::max(1, std::min(a.h, cus / T));
   size_t l1, l2;
-  for (;;) {
-    const long u1 = (long)((a.f + a.bpp - 1) / a.bpp) * a.units_h;
-    a.part_h = (int)(2 * 64 * ((u1 + 63) / 64 + 1));
-    l1 = matvec_lds_bytes(a.fmt, a.units_h, a.part_h) + MOE_ROUTE_MAX * 8 + 256;  // + routing
-    if (l1 <= 160 * 1024 || a.bpp >= a.f) break;
-    a.bpp = std::min(a.f, 2 * a.bpp);
+  if (a.quad_gu) {
+    l1 = mvq_moe_plan(a, T, 1, cus);
+  } else {
+    a.bpp = std::max(1, std::min(a.f, cus / pairs));
+    for (;;) {
+      const long u1 = (long)((a.f + a.bpp - 1) / a.bpp) * a.units_h;
+      a.part_h = (int)(2 * 64 * ((u1 + 63) / 64 + 1));
+      a.lds_gu = (int)matvec_lds_bytes(a.fmt, a.units_h, a.part_h);
+      l1 = a.lds_gu + MOE_ROUTE_MAX * 16 + 256;  // + routing
+      if (l1 <= 160 * 1024 || a.bpp >= a.f) break;
+      a.bpp = std::min(a.f, 2 * a.bpp);
+    }
   }
-  for (;;) {
-    const long u2 = (long)((a.h + a.bpt - 1) / a.bpt) * a.units_f;
-    a.part_f = (int)(a.top_k * 64 * ((u2 + 63) / 64 + 1));
-    l2 = matvec_lds_bytes(a.fmt, a.top_k * a.units_f, a.part_f);
-    if (l2 <= 160 * 1024 || a.bpt >= a.h) break;
-    a.bpt = std::min(a.h, 2 * a.bpt);
+  if (a.quad_dn) {
+    l2 = mvq_moe_plan(a, T, 2, cus);
+  } else {
+    a.bpt = std::max(1, std::min(a.h, cus / T));
+    for (;;) {
+      const long u2 = (long)((a.h + a.bpt - 1) / a.bpt) * a.units_f;
+      a.part_f = (int)(a.top_k * 64 * ((u2 + 63) / 64 + 1));
+      a.lds_dn = (int)matvec_lds_bytes(a.fmt, a.top_k * a.units_f, a.part_f);
+      l2 = a.lds_dn;
+      if (l2 <= 160 * 1024 || a.bpt >= a.h) break;
+      a.bpt = std::min(a.h, 2 * a.bpt);
+    }
   }
   return std::max(l1, l2);
 }
 
-size_t moe_lds_bytes(int fmt, int h, int f, int top_k, int T, int cus) {
+size_t moe_lds_bytes(int fmt, int h, int f, int top_k, int T, int cus, bool quad_gu, bool quad_dn) {
   MoeArgs a{};
   a.fmt = fmt;
   a.h = h;
@@ -918,57 +850,78 @@ size_t moe_lds_bytes(int fmt, int h, int f, int top_k, int T, int cus) {
   a.top_k = top_k;
   a.units_h = (h + 255) / 256;
   a.units_f = (f + 255) / 256;
+  a.quad_gu = quad_gu;
+  a.quad_dn = quad_dn;
   return moe_plan(a, T, cus);
 }
 
+static void big_lds(const void *fn, int lds) {
+  if (lds > 64 * 1024) (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+}
+
 template <int F, bool R>
-static void moe_launch_f(const MoeArgs &a, int T, size_t lds1, size_t lds2, hipStream_t st) {
-  const dim3 g1(T * a.top_k * a.bpp), g2(T * a.bpt), nt(mv_threads(F));
-  auto big = [](const void *fn, size_t lds) {
-    if (lds > 64 * 1024)
-      (void)hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  };
+static void moe_gate_up_f(const MoeArgs &a, int T, hipStream_t st) {
+  const dim3 g1(T * a.top_k * a.bpp), nt(mv_threads(F));
   if (a.h % 4 == 0) {
-    big((const void *)k_moe_gate_up<F, true, R>, lds1);
-    hipLaunchKernelGGL((k_moe_gate_up<F, true, R>), g1, nt, lds1, st, a);
+    big_lds((const void *)k_moe_gate_up<F, true, R>, a.lds_gu);
+    hipLaunchKernelGGL((k_moe_gate_up<F, true, R>), g1, nt, a.lds_gu, st, a);
   } else {
-    big((const void *)k_moe_gate_up<F, false, R>, lds1);
-    hipLaunchKernelGGL((k_moe_gate_up<F, false, R>), g1, nt, lds1, st, a);
+    big_lds((const void *)k_moe_gate_up<F, false, R>, a.lds_gu);
+    hipLaunchKernelGGL((k_moe_gate_up<F, false, R>), g1, nt, a.lds_gu, st, a);
   }
+}
+
+template <int F>
+static void moe_down_f(const MoeArgs &a, int T, hipStream_t st) {
+  const dim3 g2(T * a.bpt), nt(mv_threads(F));
   if (a.f % 4 == 0) {
-    big((const void *)k_moe_down<F, true>, lds2);
-    hipLaunchKernelGGL((k_moe_down<F, true>), g2, nt, lds2, st, a);
+    big_lds((const void *)k_moe_down<F, true>, a.lds_dn);
+    hipLaunchKernelGGL((k_moe_down<F, true>), g2, nt, a.lds_dn, st, a);
   } else {
-    big((const void *)k_moe_down<F, false>, lds2);
-    hipLaunchKernelGGL((k_moe_down<F, false>), g2, nt, lds2, st, a);
+    big_lds((const void *)k_moe_down<F, false>, a.lds_dn);
+    hipLaunchKernelGGL((k_moe_down<F, false>), g2, nt, a.lds_dn, st, a);
   }
 }
 
 hipError_t launch_moe(const MoeArgs &args, int T, hipStream_t st) {
   MoeArgs a = args;
   if (moe_plan(a, T, a.cus) > 160 * 1024) return hipErrorInvalidValue;
-  const size_t lds1 = matvec_lds_bytes(a.fmt, a.units_h, a.part_h);  // dynamic part
-  const size_t lds2 = matvec_lds_bytes(a.fmt, a.top_k * a.units_f, a.part_f);
   // Few experts: the gate/up blocks route (one launch less); many: the
   // router kernel first.
   const bool fused = a.n_experts <= MOE_ROUTE_MAX;
   if (!fused)
     hipLaunchKernelGGL(k_moe_route, dim3(T), dim3(256), 0, st, a.logits, a.n_experts, a.top_k,
                        a.ids, a.w);
-#define GQ_MOE_F(F)                                                                     \
-  case F:                                                                               \
-    if (fused) moe_launch_f<F, true>(a, T, lds1, lds2, st);                             \
-    else moe_launch_f<F, false>(a, T, lds1, lds2, st);                                  \
+  hipError_t e = hipSuccess;
+  if (a.quad_gu) {
+    e = launch_mvq_moe(a, T, 1, fused, st);
+  } else {
+#define GQ_MOE_GU(F)                                        \
+  case F:                                                   \
+    if (fused) moe_gate_up_f<F, true>(a, T, st);            \
+    else moe_gate_up_f<F, false>(a, T, st);                 \
     break;
+    switch (a.fmt) {
+      GQ_MOE_GU(T_IQ3_XXS)
+      GQ_MOE_GU(T_Q4_K)
+      GQ_MOE_GU(T_Q5_K)
+      GQ_MOE_GU(T_Q6_K)
+      GQ_MOE_GU(T_Q8_0)
+    default: return hipErrorInvalidValue;
+    }
+#undef GQ_MOE_GU
+    e = hipGetLastError();
+  }
+  if (e != hipSuccess) return e;
+  if (a.quad_dn) return launch_mvq_moe(a, T, 2, false, st);
   switch (a.fmt) {
-    GQ_MOE_F(T_IQ3_XXS)
-    GQ_MOE_F(T_Q4_K)
-    GQ_MOE_F(T_Q5_K)
-    GQ_MOE_F(T_Q6_K)
-    GQ_MOE_F(T_Q8_0)
+  case T_IQ3_XXS: moe_down_f<T_IQ3_XXS>(a, T, st); break;
+  case T_Q4_K: moe_down_f<T_Q4_K>(a, T, st); break;
+  case T_Q5_K: moe_down_f<T_Q5_K>(a, T, st); break;
+  case T_Q6_K: moe_down_f<T_Q6_K>(a, T, st); break;
+  case T_Q8_0: moe_down_f<T_Q8_0>(a, T, st); break;
   default: return hipErrorInvalidValue;
   }
-#undef GQ_MOE_F
   return hipGetLastError();
 }
 

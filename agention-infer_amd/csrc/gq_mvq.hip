@@ -47,6 +47,7 @@
 
 #include "gq_device.h"
 #include "gq_internal.h"
+#include "gq_moe.h"
 #include "gq_xsrc.h"
 
 namespace gq {
@@ -328,30 +329,62 @@ struct QItem {
 };
 
 
-template <int FMT, bool K4, int SRC, int NT>
-__global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
+// What a launch of the body computes: a dense matvec (MvArgs), or one of
+// the two MoE stages (MoeArgs) over stacked experts in the quad layout
+// (rows per expert a multiple of 16, so expert e's matrix is a quad matrix
+// starting at unit e rows U).
+enum { MQ_DENSE = 0, MQ_GATE_UP = 1, MQ_DOWN = 2 };
+
+template <int FMT, bool K4, int SRC, int NT, int MODE, bool ROUTE>
+__device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   extern __shared__ __align__(16) char smem[];
   constexpr int NW = mvq_waves(FMT), NTH = 64 * NW, C = QF<FMT>::C;
   constexpr bool HAS_D = FMT == T_Q6_K || FMT == T_IQ3_XXS;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int U = a.units, T = (U + 3) >> 2, upad = 4 * T;
   // This block's row groups: flat groups b, b + B, b + 2B, ... (local
   // group lg is flat group b + lg B: at any time the blocks stream
   // neighbouring groups, spreading the traffic evenly over the memory
   // channels), and their items (group, matrix, quad), numbered
-  // it = (lg NT + m) T + t.  The waves take items in turn: wave w starts
+  // it = (lg NM + m) T + t.  The waves take items in turn: wave w starts
   // with items w and w + NW, and each further item comes from an LDS
   // counter, so the waves finish within about one item of each other.
   // Each item's 16 row sums go to their own LDS slot and a row adds its
   // items in item order, so results do not depend on which wave took what.
-  const int G = a.groups;  // flat row groups of the launch
-  const int B = a.blocks, b = blockIdx.x;
+  //   dense:   the launch's flat groups over all blocks; NM = NT matrices.
+  //   gate/up: pair p = (token, slot) takes blocks [p bpp, (p + 1) bpp) and
+  //            the f / 16 groups of its expert's gate and up (NM = 2).
+  //   down:    token p takes blocks [p bpt, (p + 1) bpt) and the h / 16
+  //            groups of its top_k experts' down matrices (NM = top_k,
+  //            matrix m = slot m, against slot m's input).
+  int G, B, b, p = 0, Uw;
+  if constexpr (MODE == MQ_DENSE) {
+    G = a.groups;
+    B = a.blocks;
+    b = blockIdx.x;
+    Uw = a.units;
+  } else if constexpr (MODE == MQ_GATE_UP) {
+    B = mo.bpp;
+    p = blockIdx.x / B;
+    b = blockIdx.x - p * B;
+    G = mo.f / QROWS;
+    Uw = mo.units_h;
+  } else {
+    B = mo.bpt;
+    p = blockIdx.x / B;
+    b = blockIdx.x - p * B;
+    G = mo.h / QROWS;
+    Uw = mo.units_f;
+  }
+  const int NM = MODE == MQ_DOWN ? mo.top_k : NT;  // matrices per group
+  const int U = Uw, T = (U + 3) >> 2;              // weight units per row, quads
+  // Staged x: U units (down: top_k slot inputs of 4T units each).
+  const int Ux = MODE == MQ_DOWN ? NM * 4 * T : U, upad = 4 * ((Ux + 3) >> 2);
   const int ngb = (G - b + B - 1) / B;
-  const int nitems = ngb * NT * T;
+  const int nitems = ngb * NM * T;
   const int rows_blk = ngb * QROWS;
   QSmem S;
-  qsmem_layout(QF<FMT>::AUX, U, nitems * QROWS, &S, smem, FMT == T_IQ3_XXS ? 4096 : 0);
+  qsmem_layout(QF<FMT>::AUX, Ux, nitems * QROWS, &S, smem, FMT == T_IQ3_XXS ? 4096 : 0);
 
   // Item cursor (wave-uniform): local and flat group, matrix, quad, segment.
   struct Cur {
@@ -359,18 +392,43 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   };
   auto cur_at = [&](int it) {
     Cur c;
-    const int per = NT * T, gi = it / per, rem = it - gi * per;
+    const int per = NM * T, gi = it / per, rem = it - gi * per;
     c.lg = gi;
     c.fg = b + gi * B;
     c.m = rem / T;
     c.t = rem - c.m * T;
     c.seg = 0;
-    if constexpr (NT == 1) {
+    if constexpr (MODE == MQ_DENSE && NT == 1) {
 #pragma unroll
       for (int i = 1; i < MV_MAX_SEG; i++)
         if (i < a.nseg && c.fg >= a.seg[i].blk_begin) c.seg = i;
     }
     return c;
+  };
+  // The matrix of item cursor c: body, d array, rows, and c's group in it.
+  int eid = 0;  // gate/up: the pair's expert (set before the first load)
+  // down: lane m holds slot m's expert (loaded with the x loads in flight)
+  const int eids = MODE == MQ_DOWN && lane < NM ? mo.ids[p * NM + lane] : 0;
+  struct Mat {
+    const uint8_t *body;
+    const uint16_t *d;
+    int rows, g;
+  };
+  auto mat_of = [&](const Cur &c) {
+    Mat M;
+    if constexpr (MODE == MQ_DENSE) {
+      const MvSeg &sg = a.seg[NT == 2 ? c.m : c.seg];
+      M = Mat{sg.body, sg.d, sg.rows, c.fg - a.seg[c.seg].blk_begin};
+    } else if constexpr (MODE == MQ_GATE_UP) {
+      const long e0 = (long)eid * mo.f * U;  // expert's first unit
+      M = c.m ? Mat{mo.up + e0 * (C * 16), mo.up_d + e0, mo.f, c.fg}
+              : Mat{mo.gate + e0 * (C * 16), mo.gate_d + e0, mo.f, c.fg};
+    } else {
+      const int e = __builtin_amdgcn_readlane(eids, c.m);
+      const long e0 = (long)e * mo.h * U;
+      M = Mat{mo.down + e0 * (C * 16), mo.down_d + e0, mo.h, c.fg};
+    }
+    return M;
   };
   auto grab = [&]() {
     int v = 0;
@@ -380,8 +438,8 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   const int q = lane >> 4, r = lane & 15;
   auto load = [&](QItem<FMT> &dst, int it) {
     const Cur lc = cur_at(it);
-    const MvSeg &sg = a.seg[NT == 2 ? lc.m : lc.seg];
-    const int g = lc.fg - a.seg[lc.seg].blk_begin;
+    const Mat sg = mat_of(lc);
+    const int g = sg.g;
     const int nr = min(QROWS, sg.rows - QROWS * g), nq = min(4, U - 4 * lc.t);
     const long base = (long)g * QROWS * U + (long)lc.t * 4 * nr;  // quad_item_unit
     const bool live = r < nr && q < nq;
@@ -405,7 +463,7 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   int c0 = wave, c1 = wave + NW, c2 = nitems;  // items held by R0, R1, R2
   if (tid < QZERO / 16) *(uint4 *)(smem + S.zero_off + 16 * tid) = make_uint4(0, 0, 0, 0);
   float rscale = 1.f;
-  const int kpad = U * 256;
+  const int kpad = Ux * 256;
   auto stage_all = [&](auto &xsrc) {
     const int passes = (kpad + 16 * NTH - 1) / (16 * NTH);
     using XS = std::remove_reference_t<decltype(xsrc)>;
@@ -429,11 +487,15 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
     uint32_t gword[GW];
     if constexpr (FMT == T_IQ3_XXS)
 #pragma unroll
-      for (int i = 0; i < GW; i++) gword[i] = a.grid[(tid + NTH * i) >> 4];
+      for (int i = 0; i < GW; i++) gword[i] = (MODE == MQ_DENSE ? a.grid : mo.grid)[(tid + NTH * i) >> 4];
     typename XS::Raw raw[NP];
 #pragma unroll
     for (int k = 0; k < NP; k++)
       if (k < passes) xsrc.issue(16 * NTH * k + 16 * tid, raw[k]);
+    if constexpr (MODE == MQ_GATE_UP) {  // (while the x loads are in flight)
+      if constexpr (ROUTE) eid = moe_route_pair<NTH>(mo, p, b == 0);
+      else eid = __builtin_amdgcn_readfirstlane(mo.ids[p]);
+    }
     float xv[NP][16];
 #pragma unroll
     for (int k = 0; k < NP; k++)
@@ -465,7 +527,13 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
     __syncthreads();
     rscale = xsrc.scale(S.red);
   };
-  if constexpr (SRC == MV_NORM) {
+  if constexpr (MODE == MQ_GATE_UP) {
+    XPlain<K4> xs{mo.x + (long)(p / mo.top_k) * mo.h, mo.h};
+    stage_all(xs);
+  } else if constexpr (MODE == MQ_DOWN) {
+    XSlots<K4> xs{mo.hbuf, mo.f, 4 * T * 256, NM, p * NM};
+    stage_all(xs);
+  } else if constexpr (SRC == MV_NORM) {
     const float *x = a.in.tok ? a.in.x + (long)(*a.in.tok) * a.k : a.in.x;
     XNorm<K4, FMT == T_Q5_K8> xs{x, a.in.r, a.in.nw, blockIdx.x == 0 ? a.in.xo : nullptr, a.k, a.in.eps};
     stage_all(xs);
@@ -486,11 +554,19 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   auto consume = [&](const QItem<FMT> &src, int it) {
     const Cur cc = cur_at(it);
     const int u = 4 * cc.t + q;  // this lane's unit
-    const uint32_t aoff = alive ? limb_off + (uint32_t)(4 * cc.t + aq) * QL_STRIDE : S.zero_off;
-    float v = item_dot<FMT>(src.ch, src.d, smem, aoff, min(u, upad - 1), S);
-    const MvSeg &sg = a.seg[NT == 2 ? cc.m : cc.seg];
-    const int g = cc.fg - a.seg[cc.seg].blk_begin;
-    if (!(u < U && QROWS * g + r < sg.rows)) v = 0.f;
+    // first staged unit of the item's quad (down: in slot m's input)
+    const int xq = (MODE == MQ_DOWN ? cc.m * 4 * T : 0) + 4 * cc.t;
+    const uint32_t aoff = alive ? limb_off + (uint32_t)(xq + aq) * QL_STRIDE : S.zero_off;
+    float v = item_dot<FMT>(src.ch, src.d, smem, aoff, min(xq + q, upad - 1), S);
+    int rows, g;
+    if constexpr (MODE == MQ_DENSE) {
+      rows = a.seg[NT == 2 ? cc.m : cc.seg].rows;
+      g = cc.fg - a.seg[cc.seg].blk_begin;
+    } else {
+      rows = MODE == MQ_GATE_UP ? mo.f : mo.h;
+      g = cc.fg;
+    }
+    if (!(u < U && QROWS * g + r < rows)) v = 0.f;
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
     if (q == 0) S.part[it * QROWS + r] = v;
@@ -525,6 +601,37 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
   __syncthreads();
 
   // ---- per-row sums over the items, in item order
+  if constexpr (MODE == MQ_GATE_UP) {  // h_p = silu(gate . x) * (up . x)
+    for (int lr = tid; lr < rows_blk; lr += NTH) {
+      const int lg = lr / QROWS, rr = lr % QROWS;
+      const int row = (b + lg * B) * QROWS + rr;
+      float v[2];
+#pragma unroll
+      for (int m = 0; m < 2; m++) {
+        float s = 0.f;
+        const float *pp = S.part + ((lg * 2 + m) * T) * QROWS + rr;
+        for (int t = 0; t < T; t++) s += pp[t * QROWS];
+        v[m] = s;
+      }
+      mo.hbuf[(long)p * mo.f + row] = v[0] / (1.0f + expf(-v[0])) * v[1];
+    }
+    return;
+  }
+  if constexpr (MODE == MQ_DOWN) {  // out_t = sum_s w_s (down_(e_s) . h_s), slots in order
+    for (int lr = tid; lr < rows_blk; lr += NTH) {
+      const int lg = lr / QROWS, rr = lr % QROWS;
+      const int row = (b + lg * B) * QROWS + rr;
+      float out = 0.f;
+      for (int m = 0; m < NM; m++) {
+        float s = 0.f;
+        const float *pp = S.part + ((lg * NM + m) * T) * QROWS + rr;
+        for (int t = 0; t < T; t++) s += pp[t * QROWS];
+        out += mo.w[p * NM + m] * s;
+      }
+      mo.out[(long)p * mo.h + row] = out;
+    }
+    return;
+  }
   float bv = -INFINITY;  // this thread's first maximum (fused argmax)
   int bi = 0x7fffffff;
   for (int lr = tid; lr < rows_blk; lr += NTH) {
@@ -582,6 +689,18 @@ __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
 }
 
 template <int FMT, bool K4, int SRC, int NT>
+__global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
+  mvq_body<FMT, K4, SRC, NT, MQ_DENSE, false>(a, MoeArgs{});
+}
+
+// The MoE stages (MODE MQ_GATE_UP with or without in-kernel routing, or
+// MQ_DOWN); K4: the staged inputs' length (h, f) is a multiple of 4.
+template <int FMT, bool K4, int MODE, bool ROUTE>
+__global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq_moe(MoeArgs mo) {
+  mvq_body<FMT, K4, MV_X, MODE == MQ_GATE_UP ? 2 : 1, MODE, ROUTE>(MvArgs{}, mo);
+}
+
+template <int FMT, bool K4, int SRC, int NT>
 hipError_t mvq_launch_t(const MvArgs &a, size_t lds, hipStream_t st) {
   if (lds > 64 * 1024)
     (void)hipFuncSetAttribute((const void *)k_mvq<FMT, K4, SRC, NT>,
@@ -634,6 +753,70 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
   const int ngb = (G + a.blocks - 1) / a.blocks, T = (a.units + 3) / 4;
   return qsmem_layout(aux_per_unit(fmt), a.units, ngb * nt * T * QROWS, nullptr, nullptr,
                       fmt == T_IQ3_XXS ? 4096 : 0);
+}
+
+// MoE stage plans: about one block per CU in all (blocks per pair / per
+// token), more while a block's LDS would not fit.
+size_t mvq_moe_plan(MoeArgs &a, int T, int stage, int num_cus) {
+  const int fmt = a.fmt, aux = aux_per_unit(fmt), gw = fmt == T_IQ3_XXS ? 4096 : 0;
+  if (stage == 1) {
+    const int G = a.f / QROWS, Tq = (a.units_h + 3) / 4, pairs = T * a.top_k;
+    const int rstatic = MOE_ROUTE_MAX * 16 + 256;  // moe_route_pair's arrays
+    a.bpp = std::max(1, std::min(G, num_cus / std::max(1, pairs)));
+    for (;;) {
+      const int ngb = (G + a.bpp - 1) / a.bpp;
+      a.part_h = ngb * 2 * Tq * QROWS;
+      a.lds_gu = (int)qsmem_layout(aux, a.units_h, a.part_h, nullptr, nullptr, gw);
+      if (a.lds_gu + rstatic <= 160 * 1024 || a.bpp >= G) return a.lds_gu + rstatic;
+      a.bpp = std::min(G, 2 * a.bpp);
+    }
+  }
+  const int G = a.h / QROWS, Tq = (a.units_f + 3) / 4, K = a.top_k;
+  a.bpt = std::max(1, std::min(G, num_cus / std::max(1, T)));
+  for (;;) {
+    const int ngb = (G + a.bpt - 1) / a.bpt;
+    a.part_f = ngb * K * Tq * QROWS;
+    a.lds_dn = (int)qsmem_layout(aux, K * 4 * Tq, a.part_f, nullptr, nullptr, gw);
+    if (a.lds_dn + 256 <= 160 * 1024 || a.bpt >= G) return a.lds_dn + 256;
+    a.bpt = std::min(G, 2 * a.bpt);
+  }
+}
+
+template <int FMT, bool K4, int MODE, bool ROUTE>
+static hipError_t mvq_moe_t(const MoeArgs &a, int grid, int lds, hipStream_t st) {
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute((const void *)k_mvq_moe<FMT, K4, MODE, ROUTE>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  hipLaunchKernelGGL((k_mvq_moe<FMT, K4, MODE, ROUTE>), dim3(grid), dim3(64 * mvq_waves(FMT)), lds,
+                     st, a);
+  return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t mvq_moe_f(const MoeArgs &a, int T, int stage, bool route, hipStream_t st) {
+  if (stage == 1) {
+    const int grid = T * a.top_k * a.bpp;
+    if (a.h % 4 == 0)
+      return route ? mvq_moe_t<FMT, true, MQ_GATE_UP, true>(a, grid, a.lds_gu, st)
+                   : mvq_moe_t<FMT, true, MQ_GATE_UP, false>(a, grid, a.lds_gu, st);
+    return route ? mvq_moe_t<FMT, false, MQ_GATE_UP, true>(a, grid, a.lds_gu, st)
+                 : mvq_moe_t<FMT, false, MQ_GATE_UP, false>(a, grid, a.lds_gu, st);
+  }
+  const int grid = T * a.bpt;
+  return a.f % 4 == 0 ? mvq_moe_t<FMT, true, MQ_DOWN, false>(a, grid, a.lds_dn, st)
+                      : mvq_moe_t<FMT, false, MQ_DOWN, false>(a, grid, a.lds_dn, st);
+}
+
+hipError_t launch_mvq_moe(const MoeArgs &a, int T, int stage, bool route, hipStream_t st) {
+  if ((stage == 1 ? a.f : a.h) % QROWS || a.top_k > 64) return hipErrorInvalidValue;
+  switch (a.fmt) {
+  case T_Q4_K: return mvq_moe_f<T_Q4_K>(a, T, stage, route, st);
+  case T_Q5_K: return mvq_moe_f<T_Q5_K>(a, T, stage, route, st);
+  case T_Q6_K: return mvq_moe_f<T_Q6_K>(a, T, stage, route, st);
+  case T_Q8_0: return mvq_moe_f<T_Q8_0>(a, T, stage, route, st);
+  case T_IQ3_XXS: return mvq_moe_f<T_IQ3_XXS>(a, T, stage, route, st);
+  default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {

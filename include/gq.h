@@ -152,7 +152,10 @@ int gq_upload_experts(int dtype, const void *w_host, size_t nbytes, int in_dim,
  * SwiGLU as ffn_gate_up (src/model/llama/cpu_path.rs:200-232).  gate/up:
  * [n_experts][f][h], down: [n_experts][h][f], uploaded with
  * gq_upload_experts.  logits_dev [T][n_experts], x_dev/out_dev [T][h];
- * ids_dev/w_dev ([T][top_k]) receive the routing if non-NULL. */
+ * ids_dev/w_dev ([T][top_k]) receive the routing if non-NULL; top_k <= 64.
+ * The workspace (T * top_k * (4 * f + 8) + 1024 bytes) is the stream's own,
+ * allocated on first use and grown on demand, shared with gq_gemm's calls
+ * on that stream and held until the process ends. */
 int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, int n_experts,
                const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
                int *ids_dev, float *w_dev, void *stream);

@@ -55,7 +55,11 @@ def run(backend, orc, E, H, F, T, k, seed, check_tokens=None, weights=None):
     return ids
 
 
-@pytest.mark.parametrize("E,H,F,T,k", [(16, 512, 256, 3, 4), (8, 256, 768, 5, 2), (4, 1024, 512, 1, 4)])
+# Expert row counts that are multiples of 16 (F for gate/up, H for down)
+# take the quad layout and the MFMA kernels, others the wave-tiled layout
+# and the v_dot4 kernels; the last three shapes mix the two.
+@pytest.mark.parametrize("E,H,F,T,k", [(16, 512, 256, 3, 4), (8, 256, 768, 5, 2), (4, 1024, 512, 1, 4),
+                                       (4, 200, 40, 2, 2), (4, 208, 40, 3, 2), (4, 200, 48, 2, 3)])
 def test_moe_small(backend, orc, E, H, F, T, k):
     say(f"moe small E={E} H={H} F={F} T={T} k={k}")
     run(backend, orc, E, H, F, T, k, seed=E + H + T)
@@ -88,3 +92,32 @@ def test_moe_errors(backend):
     hq = backend.upload_experts(12, syn.make_blocks(12, 4 * 256, 256, seed=2), 256, 256, 4)
     with pytest.raises(gq.GqError):
         backend.moe_ffn(hq, hu, hd, 4, lg, x, 2)       # mixed dtypes
+
+
+def test_moe_routing_ties(backend, orc):
+    """Tied logits go to the lower expert index, -0.0 ties +0.0, and -inf
+    logits rank like any other value (both routing kernels: in-kernel for
+    few experts, the router kernel past 1024)."""
+    import torch
+    for E, H, F in ((16, 256, 32), (1100, 256, 16)):
+        k = 4
+        gate, up, down = make(E, H, F, seed=5)
+        hg = backend.upload_experts(IQ3, gate, H, F, E)
+        hu = backend.upload_experts(IQ3, up, H, F, E)
+        hd = backend.upload_experts(IQ3, down, F, H, E)
+        rng = np.random.default_rng(6)
+        lg = np.zeros((4, E), np.float32)
+        lg[0, ::2] = -0.0                                 # all ties, mixed signs of zero
+        lg[1] = rng.integers(0, 3, E).astype(np.float32)  # many ties
+        lg[2] = -np.inf
+        lg[2, E // 2] = 1.0
+        lg[3] = rng.integers(-2, 2, E).astype(np.float32) * 0.5
+        x = syn.make_x(H, seed=7, batch=4)
+        say(f"routing ties E={E}")
+        _, ids, w = backend.moe_ffn(hg, hu, hd, E, torch.from_numpy(lg).cuda(),
+                                    torch.from_numpy(x).cuda(), k, want_routing=True)
+        torch.cuda.synchronize()
+        rids, rw = orc.moe_route(lg, k)
+        assert np.array_equal(ids.cpu().numpy(), rids)
+        # softmax sums over E terms in another order: a few ulps per term
+        assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=0)
