@@ -142,7 +142,7 @@ size_t matvec_block_lds(const gq_weight *w, bool pair) {
   if (w->L.quad) {
     a.nseg = pair ? 2 : 1;
     a.seg[1].rows = a.seg[0].rows;
-    return gq::mvq_plan(a, g_dev.num_cus);
+    return gq::mvq_plan(a, g_dev.num_cus) + gq::mvq_static_lds(a.fmt);
   }
   return gq::matvec_plan(a, g_dev.num_cus);
 }

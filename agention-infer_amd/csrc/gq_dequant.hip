@@ -15,7 +15,12 @@ namespace gq {
 // ------------------------------------------------------------------ repack
 // Byte o of the logical bytes of unit `u` of row r, read from the raw ggml
 // row (nb ggml blocks).  Q8_0 units past the row's last block read zero.
-__device__ inline uint8_t logical_byte(int dtype, const uint8_t *row, int nb, int u, int o) {
+__device__ inline uint8_t logical_byte(int dtype, bool quad, const uint8_t *row, int nb, int u, int o) {
+  if (dtype == T_IQ3_XXS && quad) {  // re-encoded sub-blocks (iq3q_pack)
+    uint32_t w[3];
+    iq3q_pack(row + u * 98 + 2, o / 12, w);
+    return (uint8_t)(w[(o % 12) >> 2] >> (8 * (o & 3)));
+  }
   switch (dtype) {
   case T_Q4_K: return row[u * 144 + o];
   case T_Q5_K: return row[u * 176 + o];
@@ -39,7 +44,7 @@ __global__ void k_repack(Layout L, const uint8_t *raw, long raw_row_bytes, int n
   const int t = r / L.rt, j = (r % L.rt) * L.units + u;
   for (int c = 0; c < L.chunks; c++) {
     uint8_t *dst = body + chunk_offset(L, t, j, c);
-    for (int k = 0; k < 16; k++) dst[k] = logical_byte(L.dtype, row, nb, u, 16 * c + k);
+    for (int k = 0; k < 16; k++) dst[k] = logical_byte(L.dtype, L.quad, row, nb, u, 16 * c + k);
   }
   if (dd) {
     const uint8_t *b = L.dtype == T_Q6_K ? row + u * 210 + 208 : row + u * 98;
@@ -62,7 +67,8 @@ hipError_t launch_repack(const Layout &L, const uint8_t *raw, uint8_t *body, uin
 // ----------------------------------------------------------------- dequant
 // Element e (0..255) of a unit whose logical bytes are read through `lb`.
 template <typename LB>
-__device__ float dq_element(int dtype, const LB &lb, uint32_t dbits, int e, const uint32_t *grid) {
+__device__ float dq_element(int dtype, bool quad, const LB &lb, uint32_t dbits, int e,
+                           const uint32_t *grid) {
   if (dtype == T_Q8_0) {
     const int b = e >> 5;
     const float scale = h2f(lb(256 + 2 * b) | (lb(257 + 2 * b) << 8));
@@ -94,9 +100,26 @@ __device__ float dq_element(int dtype, const LB &lb, uint32_t dbits, int e, cons
     const int sc = (int)(int8_t)lb(192 + 8 * h + l / 16 + 2 * t);
     return d * (float)sc * (float)q;
   }
-  // IQ3_XXS: logical bytes are ggml bytes 2..97
   const float d = h2f(dbits);
   const int ib = e / 32, l = (e % 32) / 8, j = e % 8;
+  if (quad) {  // re-encoded sub-blocks (iq3q_pack)
+    auto word = [&](int i) {
+      const int o = 12 * ib + 4 * i;
+      return lb(o) | (lb(o + 1) << 8) | (lb(o + 2) << 16) | ((uint32_t)lb(o + 3) << 24);
+    };
+    const uint32_t w0 = word(0), w1 = word(1), w2 = word(2);
+    const uint64_t lo = (uint64_t)w1 << 32 | w0;
+    const uint32_t g = l == 0 ? w0 & 0x7FFFFFu : l == 1 ? (uint32_t)(lo >> 23) & 0x7FFFFFu
+                     : l == 2 ? (uint32_t)((((uint64_t)w2 << 32 | w1) >> 14)) & 0x7FFFFFu
+                              : (w2 >> 5) & 0x7FFFFFu;
+    uint32_t e1, e2, sg;
+    iq3q_unpack(g, e1, e2, sg);
+    const float db = d * (0.5f + (float)(w2 >> 28)) * 0.5f;
+    const uint32_t gv = grid[j < 4 ? e1 : e2];
+    const float mag = (float)((gv >> (8 * (j & 3))) & 0xff);
+    return db * mag * (((sg >> j) & 1u) ? -1.0f : 1.0f);
+  }
+  // IQ3_XXS, wave-tiled: logical bytes are ggml bytes 2..97
   const uint32_t aux = lb(64 + 4 * ib) | (lb(65 + 4 * ib) << 8) | (lb(66 + 4 * ib) << 16) |
                        ((uint32_t)lb(67 + 4 * ib) << 24);
   const float db = d * (0.5f + (float)(aux >> 28)) * 0.5f;
@@ -115,7 +138,7 @@ __global__ void k_dequant(Layout L, const uint8_t *body, const uint16_t *dd,
   const int t = r / L.rt, j = (r % L.rt) * L.units + c / 256;
   auto lb = [&](int o) -> uint32_t { return body[chunk_offset(L, t, j, o >> 4) + (o & 15)]; };
   const uint32_t dbits = dd ? dd[unit_index(L, t, j)] : 0u;
-  out[i] = dq_element(L.dtype, lb, dbits, c % 256, grid);
+  out[i] = dq_element(L.dtype, L.quad, lb, dbits, c % 256, grid);
 }
 
 hipError_t launch_dequant(const gq_weight *w, const uint32_t *grid, int row0, int nrows,

@@ -109,6 +109,44 @@ __device__ __forceinline__ uint32_t ksign7(uint32_t i) {
   return i | ((uint32_t)(__popc(i) & 1) << 7);
 }
 
+// IQ3_XXS in the quad layout is re-encoded at upload (same 96 bytes per
+// unit): sub-block ib is 12 bytes, a 96-bit little-endian value holding
+// four 23-bit groups (group l at bit 23 l) and the 4-bit scale at bit 92.
+// Group l of ggml's sub-block (codebook entries e1 = qs[8 ib + 2 l],
+// e2 = qs[8 ib + 2 l + 1], 7 sign bits s7 = (aux >> 7 l) & 127) is
+//   e1 | lo3 << 8 | x << 11 | hi3 << 12 | e2 << 15,
+// lo3 = s7 & 7, hi3 = s7 >> 4, x = parity(s7 & 15).  Bits 0..11 and 11..22
+// are then whole indices of two signed-codebook tables:
+//   T1[e1 | lo3 << 8 | x << 11] = e1's entry with signs lo3 | (x ^ parity(lo3)) << 3
+//   T2[x | hi3 << 1 | e2 << 4]  = e2's entry with signs hi3 | (x ^ parity(hi3)) << 3
+// (the 8th sign bit of ksign7 is parity(s7) = x ^ parity(hi3)), so a
+// lookup is one shift and one mask.
+__host__ __device__ inline uint32_t iq3q_group(uint32_t e1, uint32_t e2, uint32_t s7) {
+  const uint32_t lo4 = s7 & 15u;
+  const uint32_t x = (lo4 ^ (lo4 >> 1) ^ (lo4 >> 2) ^ (lo4 >> 3)) & 1u;
+  return e1 | (s7 & 7u) << 8 | x << 11 | (s7 >> 4) << 12 | e2 << 15;
+}
+// The 12 bytes of sub-block ib of a ggml IQ3_XXS block (qs = block + 2).
+__host__ __device__ inline void iq3q_pack(const uint8_t *qs, int ib, uint32_t w[3]) {
+  const uint8_t *a = qs + 64 + 4 * ib;
+  const uint32_t aux = a[0] | a[1] << 8 | a[2] << 16 | (uint32_t)a[3] << 24;
+  uint32_t g[4];
+  for (int l = 0; l < 4; l++)
+    g[l] = iq3q_group(qs[8 * ib + 2 * l], qs[8 * ib + 2 * l + 1], (aux >> (7 * l)) & 127u);
+  w[0] = g[0] | g[1] << 23;
+  w[1] = g[1] >> 9 | g[2] << 14;
+  w[2] = g[2] >> 18 | g[3] << 5 | (aux >> 28) << 28;
+}
+// Back from a group: e1, e2 and ggml's 8 sign bits (ksign7 of s7).
+__host__ __device__ inline void iq3q_unpack(uint32_t g, uint32_t &e1, uint32_t &e2, uint32_t &sg) {
+  e1 = g & 255u;
+  e2 = (g >> 15) & 255u;
+  const uint32_t lo3 = (g >> 8) & 7u, x = (g >> 11) & 1u, hi3 = (g >> 12) & 7u;
+  const uint32_t b3 = x ^ ((lo3 ^ (lo3 >> 1) ^ (lo3 >> 2)) & 1u);
+  const uint32_t ph = (hi3 ^ (hi3 >> 1) ^ (hi3 >> 2)) & 1u;
+  sg = lo3 | b3 << 3 | hi3 << 4 | (x ^ ph) << 7;
+}
+
 // quantize_row_q8_k (src/quant/q8_k.rs:49-91) of one 256-element block held
 // by 16 aligned lanes, 16 consecutive elements each (idx0 = index of this
 // lane's first element in the block).  The block's pivot is the first

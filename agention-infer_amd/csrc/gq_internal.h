@@ -119,6 +119,8 @@ hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st);
 // (returns the LDS bytes of a block) and launch.
 size_t mvq_plan(MvArgs &a, int num_cus);
 hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st);
+// Static LDS bytes (a bound) a quad-layout kernel's block adds to the plan's.
+size_t mvq_static_lds(int fmt);
 // The MFMA MoE stages over quad-layout experts (stage 1: gate/up with the
 // SwiGLU, routing inside when route; stage 2: down with the weighted
 // combine): plan (sets bpp or bpt, part and lds fields; returns the LDS

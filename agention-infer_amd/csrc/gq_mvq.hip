@@ -58,6 +58,15 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int QL_STRIDE = 272;  // LDS bytes per unit of one limb (16 B pad: bank spread)
 constexpr int QZERO = 256;      // bytes of zeros the A operand's idle lanes read
+constexpr int IQ3_TABLE_WORDS = 8192;  // IQ3_XXS: T1 and T2, 4096 words each
+constexpr uint32_t IQ3_T2 = 16384;     // byte offset of T2 from T1
+
+// The IQ3_XXS tables live in static LDS: its address is a constant after
+// LDS lowering, so a lookup's base folds into the instruction's offset.
+__device__ __forceinline__ uint32_t *iq3_tables() {
+  __shared__ __align__(16) uint32_t t[IQ3_TABLE_WORDS];
+  return t;
+}
 
 // Waves per block, and items per lane in registers at once (the current
 // one and DEPTH - 1 in flight): 8 waves (two per SIMD, 256 registers per
@@ -77,8 +86,8 @@ template <> struct QF<T_IQ3_XXS> { static constexpr int C = 6, AUX = 0; };
 // zeros [QZERO], per-unit scale s [units] (Q5_K8: the Q8_K d), per-unit aux
 // [units][AUX] (Q4_K/Q5_K: fp32 sums of the 8 sub-blocks; Q6_K: int sums of
 // the 16 runs of X; Q5_K8: bsums as int), per-item row sums [items][16],
-// 16 floats of reduction scratch, the item counter, and for IQ3_XXS the
-// signed codebook (4096 words: 256 entries x 16 sign nibbles).
+// 16 floats of reduction scratch and the item counter.  (IQ3_XXS's
+// codebook tables are static LDS, iq3_tables.)
 struct QSmem {
   uint8_t *limb;
   uint32_t zero_off;
@@ -87,11 +96,10 @@ struct QSmem {
   float *part;
   float *red;
   int *ctr;
-  uint32_t *grid;  // IQ3_XXS: the signed codebook, [entry][sign nibble]
 };
 
 __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int part_floats,
-                                               QSmem *s, char *base, int grid_words = 0) {
+                                               QSmem *s, char *base) {
   size_t o = 0;
   auto take = [&](size_t n) { size_t r = o; o += (n + 15) & ~(size_t)15; return r; };
   const int upad = (units + 3) & ~3;  // the last quad's missing units stay in bounds
@@ -102,7 +110,6 @@ __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int 
   const size_t op = take((size_t)part_floats * 4);
   const size_t orr = take(64);
   const size_t oc = take(16);
-  const size_t og = take((size_t)grid_words * 4);
   if (s) {
     s->limb = (uint8_t *)(base + ol);
     s->zero_off = (uint32_t)oz;
@@ -111,7 +118,6 @@ __host__ __device__ inline size_t qsmem_layout(int aux_per_unit, int units, int 
     s->part = (float *)(base + op);
     s->red = (float *)(base + orr);
     s->ctr = (int *)(base + oc);
-    s->grid = (uint32_t *)(base + og);
   }
   return o;
 }
@@ -280,29 +286,30 @@ __device__ __forceinline__ float item_dot(const uint4 *ch, uint32_t dbits, const
     }
     return h2f(dbits) * S.us[u] * (combine(acc2, acc1, acc0) - 32.f * corr);
   } else if constexpr (FMT == T_IQ3_XXS) {
-    // ch[0..3] = 64 grid indices (8 per 32-element sub-block), ch[4..5] = 8
-    // words of 4 x 7-bit sign indices + 4-bit scale s; d separately.
-    // w = d (0.5 + s) 0.5 * grid * sign = d/4 * (2s + 1) * (signed grid):
-    // the signed grid values are the MFMA codes, (2s + 1) applies per
-    // sub-block in integers.
+    // ch: 8 sub-blocks of 12 bytes in the re-encoded format (iq3q_pack):
+    // each 12-bit field of a group is an index into T1 (LDS byte 0) or T2
+    // (LDS byte IQ3_T2) whose words are the signed codebook bytes, i.e. the
+    // MFMA codes.  w = d (0.5 + s) 0.5 * grid * sign = d/4 * (2s + 1) *
+    // (signed grid): (2s + 1) applies per sub-block in integers.
+    const char *tb = (const char *)iq3_tables();
+    auto tw = [&](uint32_t off) { return *(const uint32_t *)(tb + off); };
     int acc2 = 0, acc1 = 0, acc0 = 0;
 #pragma unroll
     for (int ib = 0; ib < 8; ib++) {
-      const uint32_t aux = dw(ch + 4, ib);
-      const uint32_t i0 = dw(ch, 2 * ib), i1 = dw(ch, 2 * ib + 1);
-      uint32_t q[8];
-#pragma unroll
-      for (int l = 0; l < 4; l++) {
-        const uint32_t sg = ksign7((aux >> (7 * l)) & 127u);
-        const uint32_t word = l < 2 ? i0 : i1;
-        const uint32_t e1 = (word >> (16 * (l & 1))) & 0xffu, e2 = (word >> (16 * (l & 1) + 8)) & 0xffu;
-        q[2 * l] = S.grid[(e1 << 4) | (sg & 15u)];
-        q[2 * l + 1] = S.grid[(e2 << 4) | (sg >> 4)];
-      }
-      i32x4 dd = mfma(lds16(smem, a + 32 * ib), i32x4{(int)q[0], (int)q[1], (int)q[2], (int)q[3]},
+      const uint32_t w0 = dw(ch, 3 * ib), w1 = dw(ch, 3 * ib + 1), w2 = dw(ch, 3 * ib + 2);
+      // byte offsets 4 * field: the field's bits shifted to bit 2, masked
+      const uint32_t q0 = tw((w0 << 2) & 0x3FFCu);
+      const uint32_t q1 = tw(IQ3_T2 + ((w0 >> 9) & 0x3FFCu));
+      const uint32_t q2 = tw(__builtin_amdgcn_alignbit(w1, w0, 21) & 0x3FFCu);
+      const uint32_t q3 = tw(IQ3_T2 + (w1 & 0x3FFCu));
+      const uint32_t q4 = tw((w1 >> 12) & 0x3FFCu);
+      const uint32_t q5 = tw(IQ3_T2 + (__builtin_amdgcn_alignbit(w2, w1, 23) & 0x3FFCu));
+      const uint32_t q6 = tw((w2 >> 3) & 0x3FFCu);
+      const uint32_t q7 = tw(IQ3_T2 + ((w2 >> 14) & 0x3FFCu));
+      i32x4 dd = mfma(lds16(smem, a + 32 * ib), i32x4{(int)q0, (int)q1, (int)q2, (int)q3},
                       i32x4{0, 0, 0, 0});
-      dd = mfma(lds16(smem, a + 32 * ib + 16), i32x4{(int)q[4], (int)q[5], (int)q[6], (int)q[7]}, dd);
-      const int s2 = (int)(2 * (aux >> 28) + 1);
+      dd = mfma(lds16(smem, a + 32 * ib + 16), i32x4{(int)q4, (int)q5, (int)q6, (int)q7}, dd);
+      const int s2 = (int)(2 * (w2 >> 28) + 1);
       acc2 += __mul24(s2, dd[0]);
       acc1 += __mul24(s2, dd[1]);
       acc0 += __mul24(s2, dd[2]);
@@ -384,7 +391,7 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   const int nitems = ngb * NM * T;
   const int rows_blk = ngb * QROWS;
   QSmem S;
-  qsmem_layout(QF<FMT>::AUX, Ux, nitems * QROWS, &S, smem, FMT == T_IQ3_XXS ? 4096 : 0);
+  qsmem_layout(QF<FMT>::AUX, Ux, nitems * QROWS, &S, smem);
 
   // Item cursor (wave-uniform): local and flat group, matrix, quad, segment.
   struct Cur {
@@ -481,13 +488,18 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
     // the x loads of the first NP passes, then the first items' loads, then
     // the conversion (later passes one by one)
     constexpr int NP = sizeof(typename XS::Raw) <= 64 ? 3 : 2;
-    // IQ3_XXS: this thread's words of the codebook, loaded first (before x
-    // and the weights: loads complete in order), signed into LDS below.
+    // IQ3_XXS: this thread's codebook entries, loaded first (before x and
+    // the weights: loads complete in order), signed into T1 and T2 below:
+    // entries o = tid + NTH i of each table (T1's all take entry tid % 256).
     constexpr int GW = FMT == T_IQ3_XXS ? 4096 / NTH : 1;
-    uint32_t gword[GW];
-    if constexpr (FMT == T_IQ3_XXS)
+    static_assert(NTH % 256 == 0 && 4096 % NTH == 0, "table staging assumes 256 | NTH | 4096");
+    uint32_t gword[GW], gword1 = 0;
+    if constexpr (FMT == T_IQ3_XXS) {
+      const uint32_t *gr = MODE == MQ_DENSE ? a.grid : mo.grid;
+      gword1 = gr[tid & 255];
 #pragma unroll
-      for (int i = 0; i < GW; i++) gword[i] = (MODE == MQ_DENSE ? a.grid : mo.grid)[(tid + NTH * i) >> 4];
+      for (int i = 0; i < GW; i++) gword[i] = gr[(tid + NTH * i) >> 4];
+    }
     typename XS::Raw raw[NP];
 #pragma unroll
     for (int k = 0; k < NP; k++)
@@ -517,12 +529,17 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
       xsrc.make(r1, e0, xv);
       stage16<FMT>(kpad, e0, xv, S, upad);
     }
-    if constexpr (FMT == T_IQ3_XXS)
+    if constexpr (FMT == T_IQ3_XXS) {
+      auto par3 = [](uint32_t v) { return (v ^ (v >> 1) ^ (v >> 2)) & 1u; };
 #pragma unroll
       for (int i = 0; i < GW; i++) {
-        const int o = tid + NTH * i;
-        S.grid[o] = neg_bytes(gword[i], o & 15);
+        const uint32_t o = tid + NTH * i;
+        const uint32_t lo3 = (o >> 8) & 7u, x1 = o >> 11;  // T1[e1 | lo3 << 8 | x << 11]
+        iq3_tables()[o] = neg_bytes(gword1, lo3 | (x1 ^ par3(lo3)) << 3);
+        const uint32_t hi3 = (o >> 1) & 7u, x2 = o & 1u;   // T2[x | hi3 << 1 | e2 << 4]
+        iq3_tables()[4096 + o] = neg_bytes(gword[i], hi3 | (x2 ^ par3(hi3)) << 3);
       }
+    }
     if constexpr (!IsExact<XS>::value) xsrc.pre_barrier(S.red);
     __syncthreads();
     rscale = xsrc.scale(S.red);
@@ -725,6 +742,13 @@ hipError_t mvq_launch_f(const MvArgs &a, size_t lds, hipStream_t st) {
   }
 }
 
+}  // namespace
+
+// Static LDS of the quad-layout kernels' blocks, a bound: IQ3_XXS's tables
+// and the fused argmax's per-wave maxima.
+size_t mvq_static_lds(int fmt) { return (fmt == T_IQ3_XXS ? IQ3_TABLE_WORDS * 4 : 0) + 256; }
+
+namespace {
 int aux_per_unit(int fmt) {
   return fmt == T_Q4_K || fmt == T_Q5_K ? 8 : fmt == T_Q8_0 || fmt == T_IQ3_XXS ? 0 : 16;
 }
@@ -751,14 +775,14 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
   a.blocks = std::max(1, std::min(G, num_cus * bpc));
   const int fmt = a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt;
   const int ngb = (G + a.blocks - 1) / a.blocks, T = (a.units + 3) / 4;
-  return qsmem_layout(aux_per_unit(fmt), a.units, ngb * nt * T * QROWS, nullptr, nullptr,
-                      fmt == T_IQ3_XXS ? 4096 : 0);
+  return qsmem_layout(aux_per_unit(fmt), a.units, ngb * nt * T * QROWS, nullptr, nullptr);
 }
 
 // MoE stage plans: about one block per CU in all (blocks per pair / per
 // token), more while a block's LDS would not fit.
 size_t mvq_moe_plan(MoeArgs &a, int T, int stage, int num_cus) {
-  const int fmt = a.fmt, aux = aux_per_unit(fmt), gw = fmt == T_IQ3_XXS ? 4096 : 0;
+  const int fmt = a.fmt, aux = aux_per_unit(fmt);
+  const int st = (int)mvq_static_lds(fmt);
   if (stage == 1) {
     const int G = a.f / QROWS, Tq = (a.units_h + 3) / 4, pairs = T * a.top_k;
     const int rstatic = MOE_ROUTE_MAX * 16 + 256;  // moe_route_pair's arrays
@@ -766,8 +790,8 @@ size_t mvq_moe_plan(MoeArgs &a, int T, int stage, int num_cus) {
     for (;;) {
       const int ngb = (G + a.bpp - 1) / a.bpp;
       a.part_h = ngb * 2 * Tq * QROWS;
-      a.lds_gu = (int)qsmem_layout(aux, a.units_h, a.part_h, nullptr, nullptr, gw);
-      if (a.lds_gu + rstatic <= 160 * 1024 || a.bpp >= G) return a.lds_gu + rstatic;
+      a.lds_gu = (int)qsmem_layout(aux, a.units_h, a.part_h, nullptr, nullptr);
+      if (a.lds_gu + rstatic + st <= 160 * 1024 || a.bpp >= G) return a.lds_gu + rstatic + st;
       a.bpp = std::min(G, 2 * a.bpp);
     }
   }
@@ -776,8 +800,8 @@ size_t mvq_moe_plan(MoeArgs &a, int T, int stage, int num_cus) {
   for (;;) {
     const int ngb = (G + a.bpt - 1) / a.bpt;
     a.part_f = ngb * K * Tq * QROWS;
-    a.lds_dn = (int)qsmem_layout(aux, K * 4 * Tq, a.part_f, nullptr, nullptr, gw);
-    if (a.lds_dn + 256 <= 160 * 1024 || a.bpt >= G) return a.lds_dn + 256;
+    a.lds_dn = (int)qsmem_layout(aux, K * 4 * Tq, a.part_f, nullptr, nullptr);
+    if (a.lds_dn + st <= 160 * 1024 || a.bpt >= G) return a.lds_dn + st;
     a.bpt = std::min(G, 2 * a.bpt);
   }
 }
@@ -820,7 +844,7 @@ hipError_t launch_mvq_moe(const MoeArgs &a, int T, int stage, bool route, hipStr
 }
 
 hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {
-  if (lds > 160 * 1024) return hipErrorInvalidValue;
+  if (lds + mvq_static_lds(a.fmt) > 160 * 1024) return hipErrorInvalidValue;
   switch (a.fmt) {
   case T_Q4_K: return mvq_launch_f<T_Q4_K>(a, lds, st);
   case T_Q5_K: return a.in.q8k && !a.pair ? mvq_launch_f<T_Q5_K8>(a, lds, st) : mvq_launch_f<T_Q5_K>(a, lds, st);

@@ -64,6 +64,18 @@ def test_dequant_bit_exact(backend, orc, dtype, rows, k):
     torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("dtype,E,f,k", [(IQ3, 5, 32, 512), (Q4_K, 3, 48, 256), (IQ3, 3, 24, 256)])
+def test_dequant_experts_bit_exact(backend, orc, dtype, E, f, k):
+    # stacked experts: rows per expert a multiple of 16 (quad layout, experts
+    # back to back) or not (wave-tiled, one tile per expert)
+    say(f"dequant experts dtype={dtype} E={E} f={f} k={k}")
+    w = syn.make_blocks(dtype, E * f, k, seed=E * f + k)
+    h = backend.upload_experts(dtype, w, k, f, E)
+    got = h.dequant_rows(0, E * f).cpu().numpy()
+    ref = orc.dequant_rows(dtype, w, k)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_dequant_f16_scale_every_pattern(backend, orc):
     # Q8_0 blocks whose scale runs through all 65536 f16 bit patterns (incl.
     # subnormals, inf, nan) with q = 1: pins the device f16 decode exactly.
