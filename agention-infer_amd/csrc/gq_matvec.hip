@@ -380,7 +380,7 @@ __device__ __forceinline__ void stage_block(XS &xsrc, int kpad, const Smem &S,
     for (int p = 0; p < passes; p++) {
       typename XS::Raw r0;
       xsrc.issue(pass_e0(p), r0);
-      xsrc.accum_ss(r0);
+      xsrc.accum_ss(r0, pass_e0(p));
     }
     xsrc.pre_barrier(S.red);
     __syncthreads();

@@ -101,13 +101,18 @@ struct XSlots {
   const float *h;  // [pairs][f]
   int f, span, top_k, p0;
   struct Raw { float v[16]; };
-  __device__ __forceinline__ void issue(int e0, Raw &r) const {
+  __device__ __forceinline__ int first(int e0) const {  // element index in its slot
     const int s = min(e0 / span, top_k - 1), i0 = e0 - s * span;
-    load_x16<K4>(h + (long)(p0 + s) * f, f, i0 < span ? i0 : span, r.v);
+    return i0 < span ? i0 : span;
   }
-  __device__ __forceinline__ void make(const Raw &r, int, float (&xv)[16]) {
+  __device__ __forceinline__ void issue(int e0, Raw &r) const {
+    const int s = min(e0 / span, top_k - 1);
+    load_raw16<K4>(h + (long)(p0 + s) * f, f, first(e0), r.v);
+  }
+  __device__ __forceinline__ void make(const Raw &r, int e0, float (&xv)[16]) {
 #pragma unroll
     for (int i = 0; i < 16; i++) xv[i] = r.v[i];
+    mask16(f, first(e0), xv);
   }
   __device__ __forceinline__ void pre_barrier(float *) const {}
   __device__ __forceinline__ float scale(const float *) const { return 1.f; }

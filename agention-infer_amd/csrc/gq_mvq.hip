@@ -342,7 +342,7 @@ struct QItem {
 // starting at unit e rows U).
 enum { MQ_DENSE = 0, MQ_GATE_UP = 1, MQ_DOWN = 2 };
 
-template <int FMT, bool K4, int SRC, int NT, int MODE, bool ROUTE>
+template <int FMT, bool K4, int SRC, int NT, int MODE, bool ROUTE, bool ONE>
 __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   extern __shared__ __align__(16) char smem[];
   constexpr int NW = mvq_waves(FMT), NTH = 64 * NW, C = QF<FMT>::C;
@@ -443,16 +443,19 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
     return __builtin_amdgcn_readfirstlane(v);
   };
   const int q = lane >> 4, r = lane & 15;
-  auto load = [&](QItem<FMT> &dst, int it) {
+  // idle: a wave without an item issues the same loads, every one of them
+  // reading the item's first 16 bytes (one line), so that the staging's
+  // waits do not depend on whether the wave has an item.
+  auto load = [&](QItem<FMT> &dst, int it, bool idle = false) {
     const Cur lc = cur_at(it);
     const Mat sg = mat_of(lc);
     const int g = sg.g;
     const int nr = min(QROWS, sg.rows - QROWS * g), nq = min(4, U - 4 * lc.t);
     const long base = (long)g * QROWS * U + (long)lc.t * 4 * nr;  // quad_item_unit
-    const bool live = r < nr && q < nq;
+    const bool live = r < nr && q < nq && !idle;
     const int l = live ? nr * q + r : 0;  // idle lanes re-read lane 0 (same lines)
     const uint8_t *bp = sg.body + base * (C * 16);
-    const int cs = 16 * nr * nq;
+    const int cs = idle ? 0 : 16 * nr * nq;
 #pragma unroll
     for (int c = 0; c < C; c++) dst.ch[c] = ldw4(bp + (uint32_t)(c * cs + 16 * l));
     if constexpr (HAS_D) dst.d = ldh(sg.d + base + l);
@@ -478,7 +481,7 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
       for (int p = 0; p < passes; p++) {
         typename XS::Raw r0;
         xsrc.issue(16 * NTH * p + 16 * tid, r0);
-        xsrc.accum_ss(r0);
+        xsrc.accum_ss(r0, 16 * NTH * p + 16 * tid);
       }
       xsrc.pre_barrier(S.red);
       __syncthreads();
@@ -500,35 +503,47 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
 #pragma unroll
       for (int i = 0; i < GW; i++) gword[i] = gr[(tid + NTH * i) >> 4];
     }
-    typename XS::Raw raw[NP];
+    // All NPc passes' loads go out (NPc = 1 for one pass, else NP; clamped
+    // addresses past the input, masked in make), then the first item's,
+    // right behind them: a wave's loads complete in order, so x still
+    // arrives first, and the item's HBM latency overlaps x's.  Later passes
+    // go one by one.
+    auto pipeline = [&](auto npc) {
+      constexpr int NPc = decltype(npc)::value;
+      typename XS::Raw raw[NPc];
 #pragma unroll
-    for (int k = 0; k < NP; k++)
-      if (k < passes) xsrc.issue(16 * NTH * k + 16 * tid, raw[k]);
-    if constexpr (MODE == MQ_GATE_UP) {  // (while the x loads are in flight)
-      if constexpr (ROUTE) eid = moe_route_pair<NTH>(mo, p, b == 0);
-      else eid = __builtin_amdgcn_readfirstlane(mo.ids[p]);
-    }
-    float xv[NP][16];
+      for (int k = 0; k < NPc; k++) xsrc.issue(16 * NTH * k + 16 * tid, raw[k]);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (MODE == MQ_GATE_UP) {  // (while the x loads are in flight)
+        if constexpr (ROUTE) eid = moe_route_pair<NTH>(mo, p, b == 0);
+        else eid = __builtin_amdgcn_readfirstlane(mo.ids[p]);
+      }
+      // (unconditional, so that the waits for x count exactly the loads
+      // behind them)
+      load(R0, min(c0, nitems - 1), c0 >= nitems);
+      __builtin_amdgcn_sched_barrier(0);
+      float xv[NPc][16];
 #pragma unroll
-    for (int k = 0; k < NP; k++)
-      if (k < passes) xsrc.make(raw[k], 16 * NTH * k + 16 * tid, xv[k]);
-    __builtin_amdgcn_sched_barrier(0);
-    if (c0 < nitems) load(R0, c0);
-    __builtin_amdgcn_sched_barrier(0);
+      for (int k = 0; k < NPc; k++) xsrc.make(raw[k], 16 * NTH * k + 16 * tid, xv[k]);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int k = 0; k < NP; k++)
-      if (k < passes) stage16<FMT>(kpad, 16 * NTH * k + 16 * tid, xv[k], S, upad);
-    __builtin_amdgcn_sched_barrier(0);
-    if (DEPTH == 3 && c1 < nitems) load(R1, c1);
-    __builtin_amdgcn_sched_barrier(0);
-    for (int p = NP; p < passes; p++) {
-      typename XS::Raw r1;
-      const int e0 = 16 * NTH * p + 16 * tid;
-      xsrc.issue(e0, r1);
-      float xv[16];
-      xsrc.make(r1, e0, xv);
-      stage16<FMT>(kpad, e0, xv, S, upad);
-    }
+      for (int k = 0; k < NPc; k++)
+        if (k < passes) stage16<FMT>(kpad, 16 * NTH * k + 16 * tid, xv[k], S, upad);
+      __builtin_amdgcn_sched_barrier(0);
+      if (DEPTH == 3 && c1 < nitems) load(R1, c1);
+      __builtin_amdgcn_sched_barrier(0);
+      for (int p = NPc; p < passes; p++) {
+        typename XS::Raw r1;
+        const int e0 = 16 * NTH * p + 16 * tid;
+        xsrc.issue(e0, r1);
+        float xv1[16];
+        xsrc.make(r1, e0, xv1);
+        stage16<FMT>(kpad, e0, xv1, S, upad);
+      }
+    };
+    // ONE: the launch stages x in one pass (k <= 16 NTH)
+    if constexpr (ONE) pipeline(std::integral_constant<int, 1>{});
+    else pipeline(std::integral_constant<int, NP>{});
     if constexpr (FMT == T_IQ3_XXS) {
       auto par3 = [](uint32_t v) { return (v ^ (v >> 1) ^ (v >> 2)) & 1u; };
 #pragma unroll
@@ -705,25 +720,32 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   }
 }
 
-template <int FMT, bool K4, int SRC, int NT>
+template <int FMT, bool K4, int SRC, int NT, bool ONE>
 __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq(MvArgs a) {
-  mvq_body<FMT, K4, SRC, NT, MQ_DENSE, false>(a, MoeArgs{});
+  mvq_body<FMT, K4, SRC, NT, MQ_DENSE, false, ONE>(a, MoeArgs{});
 }
 
 // The MoE stages (MODE MQ_GATE_UP with or without in-kernel routing, or
 // MQ_DOWN); K4: the staged inputs' length (h, f) is a multiple of 4.
-template <int FMT, bool K4, int MODE, bool ROUTE>
+template <int FMT, bool K4, int MODE, bool ROUTE, bool ONE>
 __global__ __launch_bounds__(64 * mvq_waves(FMT)) void k_mvq_moe(MoeArgs mo) {
-  mvq_body<FMT, K4, MV_X, MODE == MQ_GATE_UP ? 2 : 1, MODE, ROUTE>(MvArgs{}, mo);
+  mvq_body<FMT, K4, MV_X, MODE == MQ_GATE_UP ? 2 : 1, MODE, ROUTE, ONE>(MvArgs{}, mo);
 }
 
+template <int FMT, bool K4, int SRC, int NT, bool ONE>
+hipError_t mvq_launch_o(const MvArgs &a, size_t lds, hipStream_t st) {
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute((const void *)k_mvq<FMT, K4, SRC, NT, ONE>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipLaunchKernelGGL((k_mvq<FMT, K4, SRC, NT, ONE>), dim3(a.blocks), dim3(64 * mvq_waves(FMT)), lds, st, a);
+  return hipGetLastError();
+}
+
+// one staging pass when the input fits one (units <= NTH / 16)
 template <int FMT, bool K4, int SRC, int NT>
 hipError_t mvq_launch_t(const MvArgs &a, size_t lds, hipStream_t st) {
-  if (lds > 64 * 1024)
-    (void)hipFuncSetAttribute((const void *)k_mvq<FMT, K4, SRC, NT>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL((k_mvq<FMT, K4, SRC, NT>), dim3(a.blocks), dim3(64 * mvq_waves(FMT)), lds, st, a);
-  return hipGetLastError();
+  return a.units * 16 <= 64 * mvq_waves(FMT) ? mvq_launch_o<FMT, K4, SRC, NT, true>(a, lds, st)
+                                             : mvq_launch_o<FMT, K4, SRC, NT, false>(a, lds, st);
 }
 
 template <int FMT>
@@ -806,14 +828,22 @@ size_t mvq_moe_plan(MoeArgs &a, int T, int stage, int num_cus) {
   }
 }
 
+template <int FMT, bool K4, int MODE, bool ROUTE, bool ONE>
+static hipError_t mvq_moe_o(const MoeArgs &a, int grid, int lds, hipStream_t st) {
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute((const void *)k_mvq_moe<FMT, K4, MODE, ROUTE, ONE>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+  hipLaunchKernelGGL((k_mvq_moe<FMT, K4, MODE, ROUTE, ONE>), dim3(grid), dim3(64 * mvq_waves(FMT)),
+                     lds, st, a);
+  return hipGetLastError();
+}
+
 template <int FMT, bool K4, int MODE, bool ROUTE>
 static hipError_t mvq_moe_t(const MoeArgs &a, int grid, int lds, hipStream_t st) {
-  if (lds > 64 * 1024)
-    (void)hipFuncSetAttribute((const void *)k_mvq_moe<FMT, K4, MODE, ROUTE>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-  hipLaunchKernelGGL((k_mvq_moe<FMT, K4, MODE, ROUTE>), dim3(grid), dim3(64 * mvq_waves(FMT)), lds,
-                     st, a);
-  return hipGetLastError();
+  // staged units: gate/up units_h; down top_k slots of 4T units each
+  const int ux = MODE == MQ_GATE_UP ? a.units_h : a.top_k * 4 * ((a.units_f + 3) / 4);
+  return ux * 16 <= 64 * mvq_waves(FMT) ? mvq_moe_o<FMT, K4, MODE, ROUTE, true>(a, grid, lds, st)
+                                        : mvq_moe_o<FMT, K4, MODE, ROUTE, false>(a, grid, lds, st);
 }
 
 template <int FMT>

@@ -8,26 +8,40 @@
 
 namespace gq {
 
+// 16 consecutive input values from element e0 on, in two steps so that a
+// wave can issue its loads and use them later: load_raw16 loads from
+// clamped addresses (every address in [0, k)), mask16 zeroes the values
+// past k.
+// (Global-address-space loads: a flat load also counts against the LDS
+// counter, and the compiler then waits for every outstanding load first.)
+typedef float xf32x4 __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) float gfloat;
+typedef const __attribute__((address_space(1))) xf32x4 gfloat4;
 template <bool K4>
-__device__ __forceinline__ void load_x16(const float *x, int k, int e0, float (&xv)[16]) {
-  if (K4) {  // k % 4 == 0: clamped vector loads, zeroed past k
+__device__ __forceinline__ void load_raw16(const float *xp, int k, int e0, float (&v)[16]) {
+  gfloat *x = (gfloat *)xp;
+  if (K4) {  // k % 4 == 0: clamped vector loads
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const int e = e0 + 4 * q;
-      const float4 v = *(const float4 *)(x + min(e, k - 4));
-      const bool in = e < k;
-      xv[4 * q + 0] = in ? v.x : 0.f;
-      xv[4 * q + 1] = in ? v.y : 0.f;
-      xv[4 * q + 2] = in ? v.z : 0.f;
-      xv[4 * q + 3] = in ? v.w : 0.f;
+      const xf32x4 w = *(gfloat4 *)(x + min(e0 + 4 * q, k - 4));
+      v[4 * q + 0] = w.x;
+      v[4 * q + 1] = w.y;
+      v[4 * q + 2] = w.z;
+      v[4 * q + 3] = w.w;
     }
   } else {
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const float v = x[min(e0 + i, k - 1)];
-      xv[i] = e0 + i < k ? v : 0.f;
-    }
+    for (int i = 0; i < 16; i++) v[i] = x[min(e0 + i, k - 1)];
   }
+}
+__device__ __forceinline__ void mask16(int k, int e0, float (&v)[16]) {
+#pragma unroll
+  for (int i = 0; i < 16; i++) v[i] = e0 + i < k ? v[i] : 0.f;
+}
+template <bool K4>
+__device__ __forceinline__ void load_x16(const float *x, int k, int e0, float (&xv)[16]) {
+  load_raw16<K4>(x, k, e0, xv);
+  mask16(k, e0, xv);
 }
 
 // x sources.  issue() starts the loads of 16 consecutive input values
@@ -39,10 +53,11 @@ struct XPlain {
   const float *x;
   int k;
   struct Raw { float v[16]; };
-  __device__ __forceinline__ void issue(int e0, Raw &r) const { load_x16<K4>(x, k, e0, r.v); }
-  __device__ __forceinline__ void make(const Raw &r, int, float (&xv)[16]) {
+  __device__ __forceinline__ void issue(int e0, Raw &r) const { load_raw16<K4>(x, k, e0, r.v); }
+  __device__ __forceinline__ void make(const Raw &r, int e0, float (&xv)[16]) {
 #pragma unroll
     for (int i = 0; i < 16; i++) xv[i] = r.v[i];
+    mask16(k, e0, xv);
   }
   __device__ __forceinline__ void pre_barrier(float *) const {}
   __device__ __forceinline__ float scale(const float *) const { return 1.f; }
@@ -56,12 +71,15 @@ struct XSwiGLU {
   int k;
   struct Raw { float g[16], u[16]; };
   __device__ __forceinline__ void issue(int e0, Raw &r) const {
-    load_x16<K4>(g, k, e0, r.g);
-    load_x16<K4>(u, k, e0, r.u);
+    load_raw16<K4>(g, k, e0, r.g);
+    load_raw16<K4>(u, k, e0, r.u);
   }
-  __device__ __forceinline__ void make(const Raw &r, int, float (&xv)[16]) {
+  __device__ __forceinline__ void make(const Raw &r, int e0, float (&xv)[16]) {
 #pragma unroll
-    for (int i = 0; i < 16; i++) xv[i] = r.g[i] / (1.0f + expf(-r.g[i])) * r.u[i];
+    for (int i = 0; i < 16; i++) {
+      const float gi = e0 + i < k ? r.g[i] : 0.f, ui = e0 + i < k ? r.u[i] : 0.f;
+      xv[i] = gi / (1.0f + expf(-gi)) * ui;
+    }
   }
   __device__ __forceinline__ void pre_barrier(float *) const {}
   __device__ __forceinline__ float scale(const float *) const { return 1.f; }
@@ -86,10 +104,10 @@ struct XNorm {
   struct Raw { float x[16], r[16], w[16]; };
   static constexpr bool kExact = EXACT;
   // sum of squares of the residual-added input (first pass of EXACT)
-  __device__ __forceinline__ void accum_ss(const Raw &q) {
+  __device__ __forceinline__ void accum_ss(const Raw &q, int e0) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      const float v = r ? q.x[i] + q.r[i] : q.x[i];
+      const float v = e0 + i < k ? (r ? q.x[i] + q.r[i] : q.x[i]) : 0.f;
       ss += v * v;
     }
   }
@@ -100,20 +118,23 @@ struct XNorm {
     rms = sqrtf(t / (float)k + eps);
   }
   __device__ __forceinline__ void issue(int e0, Raw &q) const {
-    load_x16<K4>(x, k, e0, q.x);
-    if (r) load_x16<K4>(r, k, e0, q.r);
-    load_x16<K4>(nw, k, e0, q.w);
+    // (r's loads are unconditional, from x without a residual, so that the
+    // waits for these loads count exactly the loads behind them)
+    load_raw16<K4>(x, k, e0, q.x);
+    load_raw16<K4>(r ? r : x, k, e0, q.r);
+    load_raw16<K4>(nw, k, e0, q.w);
   }
   __device__ __forceinline__ void make(const Raw &q, int e0, float (&xv)[16]) {
     float v[16];
 #pragma unroll
     for (int i = 0; i < 16; i++) {
-      v[i] = r ? q.x[i] + q.r[i] : q.x[i];
+      v[i] = e0 + i < k ? (r ? q.x[i] + q.r[i] : q.x[i]) : 0.f;
+      const bool in = e0 + i < k;
       if constexpr (EXACT) {
-        xv[i] = q.w[i] * v[i] / rms;
+        xv[i] = in ? q.w[i] * v[i] / rms : 0.f;
       } else {
         ss += v[i] * v[i];
-        xv[i] = q.w[i] * v[i];
+        xv[i] = in ? q.w[i] * v[i] : 0.f;
       }
     }
     if (xo) {
