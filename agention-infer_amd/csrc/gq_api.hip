@@ -139,12 +139,10 @@ size_t matvec_block_lds(const gq_weight *w, bool pair) {
   a.pair = pair;
   a.nseg = 1;
   a.seg[0].rows = std::max(w->L.rows, 1);
-  if (w->L.quad) {
-    a.nseg = pair ? 2 : 1;
-    a.seg[1].rows = a.seg[0].rows;
-    return gq::mvq_plan(a, g_dev.num_cus) + gq::mvq_static_lds(a.fmt);
-  }
-  return gq::matvec_plan(a, g_dev.num_cus);
+  if (!w->L.quad) return SIZE_MAX;  // stacked experts (wave-tiled) take gq_moe_ffn
+  a.nseg = pair ? 2 : 1;
+  a.seg[1].rows = a.seg[0].rows;
+  return gq::mvq_plan(a, g_dev.num_cus) + gq::mvq_static_lds(a.fmt);
 }
 
 int check_matvec(const gq_weight *w) {
@@ -247,9 +245,8 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
     a.nseg = 2;
     a.seg[0] = MvSeg{w0->body, w0->d, ys[0], w0->L.rows, 0, 0};
     a.seg[1] = MvSeg{ws[1]->body, ws[1]->d, nullptr, ws[1]->L.rows, 0, 0};
-    if (w0->L.quad) return launch_mvq(a, mvq_plan(a, g_dev.num_cus), st);
-    matvec_plan(a, g_dev.num_cus);
-    return launch_matvec(a, w0->L.dtype, st);
+    if (!w0->L.quad) return hipErrorInvalidValue;  // matvec weights are quad-layout
+    return launch_mvq(a, mvq_plan(a, g_dev.num_cus), st);
   }
   for (int base = 0; base < count; base += MV_MAX_SEG) {
     MvArgs a{};
@@ -267,13 +264,8 @@ hipError_t matvec_launch(const gq_weight *const *ws, int count, const MvIn &in, 
     }
     if (ns == 0) continue;
     a.nseg = ns;
-    hipError_t e;
-    if (w0->L.quad) {
-      e = launch_mvq(a, mvq_plan(a, g_dev.num_cus), st);
-    } else {
-      matvec_plan(a, g_dev.num_cus);
-      e = launch_matvec(a, w0->L.dtype, st);
-    }
+    if (!w0->L.quad) return hipErrorInvalidValue;  // matvec weights are quad-layout
+    const hipError_t e = launch_mvq(a, mvq_plan(a, g_dev.num_cus), st);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
@@ -773,12 +765,12 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   if (!rc && L.kv_q8) rc = dalloc(m, &L.kscale, (size_t)d->n_layers * d->ctx * (kvd / 32));
   if (!rc && L.kv_q8) rc = dalloc(m, &L.vscale, (size_t)d->n_layers * d->ctx * (kvd / 32));
   float *buf = nullptr;
-  const int nb_amax = std::max((d->vocab + gq::ARGMAX_SPAN - 1) / gq::ARGMAX_SPAN, gq::ARGMAX_SLOTS);
+  const int nb_amax = gq::ARGMAX_SLOTS;
   const size_t nbuf = 3 * ((size_t)H + 16) + 2 * ((size_t)nh * hd + 16) + 2 * (kvd + 16) +
                       ((size_t)d->ffn + 16) + ((size_t)d->vocab + 16) +
                       ((size_t)nh * L.att_chunks * (2 + hd) + 16) + (nb_amax + 16) + (hd / 2 + 16);
   int *ibuf = nullptr;
-  const size_t nibuf = 1 + (size_t)nb_amax;
+  const size_t nibuf = (size_t)nb_amax;
   if (!rc) rc = dalloc(m, &buf, nbuf);
   if (!rc) rc = dalloc(m, &ibuf, nibuf);
   if (!rc) rc = dalloc(m, &L.state, 1);
@@ -792,7 +784,7 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   L.logits = take(d->vocab); L.att_part = take((size_t)nh * L.att_chunks * (2 + hd));
   L.amax_v = take(nb_amax);
   L.rope_den = take(hd / 2);
-  L.amax_count = ibuf; L.amax_i = ibuf + 1;
+  L.amax_i = ibuf;
   hipError_t e = hipSuccess;
   {  // argmax partial slots start neutral (-inf, INT_MAX): the fused head argmax
      // reads all ARGMAX_SLOTS, of which only the head's blocks write

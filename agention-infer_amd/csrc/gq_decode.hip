@@ -19,9 +19,9 @@
 //
 // Step state (token, position, step counter) lives in device memory so that
 // a captured HIP graph of one step can be replayed for every greedy step:
-// the argmax writes the next token and advances the position.  The argmax
-// block counter returns to zero at the end of every launch, so a replay
-// starts from the same state.
+// the argmax writes the next token and advances the position.  The head's
+// per-block maxima are rewritten by every step, so a replay starts from the
+// same state.
 #include "gq_device.h"
 #include "gq_internal.h"
 
@@ -481,10 +481,8 @@ __global__ __launch_bounds__(ATT_MERGE_THREADS) void k_attn_merge(const DecodeSt
 }
 
 // -------------------------------------------------------------- argmax
-// Greedy argmax (first maximum wins, sampler.rs:120-131).  Block b takes
-// logits [b*SPAN, (b+1)*SPAN); the last block to finish reduces the block
-// results, records the token, makes it the next input and advances the
-// position.
+// Greedy argmax (first maximum wins, sampler.rs:120-131): the head
+// matvec's blocks leave per-block maxima, k_argmax_final merges them.
 __device__ __forceinline__ void amax_merge(float &bv, int &bi, float ov, int oi) {
   if (ov > bv || (ov == bv && oi < bi)) {
     bv = ov;
@@ -510,58 +508,11 @@ __device__ __forceinline__ void block_amax(float &bv, int &bi, float *sv, int *s
   for (int j = 1; j < 4; j++) amax_merge(bv, bi, sv[j], si[j]);
 }
 
-__global__ __launch_bounds__(256) void k_argmax(const float *logits, int n, float *pv, int *pi,
-                                                int *count, DecodeState *st, int *tokens,
-                                                int max_tokens) {
-  __shared__ float sv[4];
-  __shared__ int si[4];
-  __shared__ int last_s;
-  const int tid = threadIdx.x;
-  const int base = blockIdx.x * ARGMAX_SPAN;
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-#pragma unroll
-  for (int i = 0; i < ARGMAX_SPAN / 256; i++) {
-    const int e = base + tid + 256 * i;  // increasing per thread: strict > keeps the first
-    if (e < n) {
-      const float x = logits[e];
-      if (x > bv) {
-        bv = x;
-        bi = e;
-      }
-    }
-  }
-  block_amax(bv, bi, sv, si);
-  if (tid == 0) {
-    pv[blockIdx.x] = bv;
-    pi[blockIdx.x] = bi;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    __threadfence();
-    const bool last = atomicAdd(count, 1) == (int)gridDim.x - 1;
-    if (last) __threadfence();
-    last_s = last;
-  }
-  __syncthreads();
-  if (!last_s) return;
-  bv = -INFINITY;
-  bi = 0x7fffffff;
-  for (int b = tid; b < (int)gridDim.x; b += 256) amax_merge(bv, bi, pv[b], pi[b]);
-  block_amax(bv, bi, sv, si);
-  if (tid == 0) {
-    const int idx = bi == 0x7fffffff ? 0 : bi;  // no logit above -inf: index 0
-    const int step = st->step;
-    if (tokens && step < max_tokens) tokens[step] = idx;
-    *st = DecodeState{idx, st->pos + 1, step + 1, 0};
-    *count = 0;
-  }
-}
-
 // The head matvec's blocks leave the first maximum of their rows in
 // pv / pi[0 .. ARGMAX_SLOTS) (slots of blocks that do not exist keep
 // -inf / INT_MAX from set-up); one block reduces them and advances the step
-// state as k_argmax's last block does.  No fences: the kernel boundary
+// state (the token is recorded and becomes the next input; the position
+// advances).  No fences: the kernel boundary
 // orders the partials before this read.
 __global__ __launch_bounds__(256) void k_argmax_final(const float *pv, const int *pi,
                                                       DecodeState *st, int *tokens,
@@ -684,18 +635,13 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
   hin.q8k = true;  // the head: matmul_into (cpu_path.rs:815)
   const gq_weight *hw[1] = {m.lm_head};
   float *lo[1] = {m.logits};
-  if (m.lm_head->L.quad) {  // argmax partials from the head's blocks, one final block
-    hin.amax_v = m.amax_v;
-    hin.amax_i = m.amax_i;
-    if ((e = matvec_launch(hw, 1, hin, lo, s)) != hipSuccess) return e;
-    hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, m.amax_v, m.amax_i, m.state,
-                       m.tokens, m.max_tokens);
-    return hipGetLastError();
-  }
+  if (!m.lm_head->L.quad) return hipErrorInvalidValue;  // dense weights are quad-layout
+  // argmax partials from the head's blocks, one final block
+  hin.amax_v = m.amax_v;
+  hin.amax_i = m.amax_i;
   if ((e = matvec_launch(hw, 1, hin, lo, s)) != hipSuccess) return e;
-  const int nb = (m.vocab + ARGMAX_SPAN - 1) / ARGMAX_SPAN;
-  hipLaunchKernelGGL(k_argmax, dim3(nb), dim3(256), 0, s, m.logits, m.vocab, m.amax_v, m.amax_i,
-                     m.amax_count, m.state, m.tokens, m.max_tokens);
+  hipLaunchKernelGGL(k_argmax_final, dim3(1), dim3(256), 0, s, m.amax_v, m.amax_i, m.state,
+                     m.tokens, m.max_tokens);
   return hipGetLastError();
 }
 

@@ -39,7 +39,6 @@ struct MvSeg {
 __host__ __device__ constexpr int mv_threads(int fmt) {
   return fmt == 18 ? 1024 : fmt == 12 || fmt == 13 || fmt == 113 ? 768 : 512;
 }
-constexpr int MV_BLOCKS_PER_CU = 1;
 
 // Where the matvec input vector comes from.
 enum MvSource {
@@ -111,10 +110,6 @@ hipError_t launch_moe(const MoeArgs &a, int T, hipStream_t st);
 // LDS bytes of a matvec block: x limbs, records, codebook and part_total
 // floats of partial sums.
 size_t matvec_lds_bytes(int dtype, int units, int part_total);
-// Split the segments' rows over blocks (about MV_BLOCKS_PER_CU per CU) and
-// size the partial-sum region; returns the LDS bytes a block needs.
-size_t matvec_plan(MvArgs &a, int num_cus);
-hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st);
 // The MFMA matvec over quad-layout weights (Q4_K, Q5_K, Q6_K, Q8_0): plan
 // (returns the LDS bytes of a block) and launch.
 size_t mvq_plan(MvArgs &a, int num_cus);
@@ -151,7 +146,6 @@ struct DecodeLaunch {
   float *rope_den;            // [head_dim / 2] theta^(2i/head_dim), computed on the host
   float *amax_v;              // per-block argmax partials
   int *amax_i;
-  int *amax_count;            // argmax block counter (zero between launches)
   DecodeState *state;
   int *tokens;                // [max_tokens] generated tokens
 };
@@ -173,7 +167,6 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
                           int pos0, int num_cus, hipStream_t s);
 constexpr int ATT_CHUNK = 64;    // positions per attention block
 constexpr int ATT_MAX_CTX = 65536;
-constexpr int ARGMAX_SPAN = 4096;  // logits per argmax block
 constexpr int ARGMAX_SLOTS = 1024;  // per-block partials of the fused head argmax
 hipError_t launch_set_state(DecodeState *st, int token, int pos, hipStream_t s);
 

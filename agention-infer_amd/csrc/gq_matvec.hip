@@ -1,19 +1,22 @@
-// gq_matvec.hip -- batch-1 decode matvec y = W . x for Q8_0, Q4_K, Q5_K,
-// Q6_K and IQ3_XXS weights (gfx950, wave64).
+// gq_matvec.hip -- the v_dot4 MoE expert FFN over stacked expert tensors in
+// the wave-tiled layout (rows per expert not a multiple of 16; the others
+// take the quad layout and the MFMA stages of gq_mvq.hip), the router
+// kernel for more than MOE_ROUTE_MAX experts, and the MoE dispatch
+// (gfx950, wave64).
 //
 // Replaces the reference's per-row dot kernels (src/quant/q8_0.rs:58-90,
-// q4_k.rs:95-212, q5_k.rs:189-317, q6_k.rs:82-131) driven row-parallel by
-// WeightMap::matmul_into (src/model/mod.rs:362-403).  It does not follow
-// the reference GPU kernels (src/ops/kernels_wgpu.rs:1067-1706).
+// q4_k.rs:95-212, q5_k.rs:189-317, q6_k.rs:82-131) for the expert
+// matrices; the MoE layer itself has no counterpart in the reference
+// (docs/08-moe-routing.md describes it).
 //
 // Design (HBM-bound; every weight byte is read exactly once):
 //  * Weights sit in the wave-tiled layout (gq_layout.h), one tile per
-//    matrix (per expert for stacked experts): one lane owns one 256-element
-//    unit, and a wave-wide 128-bit load reads 1 KiB of contiguous HBM with
-//    a nontemporal hint.  Each lane keeps its next unit in flight while it
-//    computes the current one.
-//  * One block per CU: block b owns an equal range of rows (+-1), stages x
-//    once and streams the range's units with all its waves.
+//    expert: one lane owns one 256-element unit, and a wave-wide 128-bit
+//    load reads 1 KiB of contiguous HBM with a nontemporal hint.  Each lane
+//    keeps its next unit in flight while it computes the current one.
+//  * Blocks own equal row ranges of a (token, slot) pair's expert (gate/up)
+//    or of a token's output rows over its experts (down); x is staged once
+//    per block.
 //  * x is staged per block in LDS as fixed-point int8 "limbs": for each run
 //    of 32 elements, s = max|x| / (127 * 2^16), X = rint(x / s) (|X| <=
 //    127 * 2^16) and X = x2 * 2^16 + x1 * 2^8 + x0 with signed bytes.
@@ -144,41 +147,6 @@ __device__ __forceinline__ float unit_q4k(const uint4 *ch, int u, const Smem &S,
   return acc;
 }
 
-// Q5_K against the Q8_K-quantized input (dot_q5_k_q8k, src/quant/q5_k.rs:
-// 126-184): the codes sit in limb l0 and each 16-run record holds {d of the
-// Q8_K block, the run's bsums entry as int bits}.  The weight codes (5-bit,
-// 0..31) meet the int8 codes in v_dot4; acc_pos and acc_min are exact
-// integers, and the unit's value is the reference's per-block term
-// dx * (d * acc_pos - dmin * acc_min), rounded the same way.
-__device__ __forceinline__ float unit_q5k8(const uint4 *ch, int u, const Smem &S) {
-  const uint4 hd = ch[0];
-  const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
-  int acc_pos = 0, acc_min = 0;
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    uint32_t sc0, m0, sc1, m1;
-    scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
-    scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
-    int plo = 0, phi = 0;
-    const int off = u * LIMB_STRIDE + 64 * j;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t q = dw(ch + 3, 8 * j + i);
-      const uint32_t h = dw(ch + 1, i);  // qh bytes 4i..4i+3
-      const uint32_t lo = (q & 0x0F0F0F0Fu) | (((h >> (2 * j)) & 0x01010101u) << 4);
-      const uint32_t hi = ((q >> 4) & 0x0F0F0F0Fu) | (((h >> (2 * j + 1)) & 0x01010101u) << 4);
-      plo = __builtin_amdgcn_sdot4(lo, *(const uint32_t *)(S.l0 + off + 4 * i), plo, false);
-      phi = __builtin_amdgcn_sdot4(hi, *(const uint32_t *)(S.l0 + off + 32 + 4 * i), phi, false);
-    }
-    const int b0 = __float_as_int(aux_at(S, u, 4 * j).y) + __float_as_int(aux_at(S, u, 4 * j + 1).y);
-    const int b1 = __float_as_int(aux_at(S, u, 4 * j + 2).y) + __float_as_int(aux_at(S, u, 4 * j + 3).y);
-    acc_pos += (int)sc0 * plo + (int)sc1 * phi;
-    acc_min += (int)m0 * b0 + (int)m1 * b1;
-  }
-  const float dx = aux_at(S, u, 0).x;
-  return dx * (d * (float)acc_pos - dmin * (float)acc_min);
-}
-
 // ---------------------------------------------------------------- Q6_K
 // ch[0..7] = ql[128], ch[8..11] = qh[64], ch[12] = scales[16]; d separate.
 // 16-run s (elements 16s..16s+15 of the unit) uses scale index s.
@@ -265,17 +233,6 @@ __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u
 template <bool Q6>
 __device__ __forceinline__ void put_aux(const Smem &S, int e0, float sx, float sum32, int xs);
 
-// Q8_K route: the 16 threads of each 256-element block quantize it like
-// quantize_row_q8_k; the codes go to limb l0, {d, bsum} to the records.
-__device__ __forceinline__ void stage_x_q8k(int kpad, int e0, const float (&xv)[16], const Smem &S) {
-  const Q8K16 r = q8k_quant16(xv, e0 & 255);
-  if (e0 >= kpad) return;
-  const int lo = (e0 >> 8) * LIMB_STRIDE + (e0 & 255);
-  *(uint4 *)(S.l0 + lo) = make_uint4(r.q[0], r.q[1], r.q[2], r.q[3]);
-  const int u = e0 >> 8, rr = (e0 & 255) >> 4;
-  *(float2 *)((char *)S.aux + u * AUX_STRIDE + 8 * rr) = make_float2(r.d, __int_as_float(r.bsum));
-}
-
 template <bool Q6>
 __device__ __forceinline__ void stage_x(int kpad, int e0, const float (&xv)[16], const Smem &S) {
   float amax = 0.f, sum = 0.f;
@@ -332,7 +289,6 @@ template <int FMT> struct Fmt;
 // C: 16-byte chunks per unit.
 template <> struct Fmt<T_Q4_K> { static constexpr int C = 9; static constexpr bool HAS_D = false; };
 template <> struct Fmt<T_Q5_K> { static constexpr int C = 11; static constexpr bool HAS_D = false; };
-template <> struct Fmt<T_Q5_K8> { static constexpr int C = 11; static constexpr bool HAS_D = false; };
 template <> struct Fmt<T_Q6_K> { static constexpr int C = 13; static constexpr bool HAS_D = true; };
 template <> struct Fmt<T_Q8_0> { static constexpr int C = 17; static constexpr bool HAS_D = false; };
 template <> struct Fmt<T_IQ3_XXS> { static constexpr int C = 6; static constexpr bool HAS_D = true; };
@@ -355,7 +311,6 @@ template <int FMT>
 __device__ __forceinline__ float unit_dot(const Unit<FMT> &U, int u, const Smem &S) {
   if constexpr (FMT == T_Q4_K) return unit_q4k(U.ch, u, S, 0);
   else if constexpr (FMT == T_Q5_K) return unit_q4k(U.ch, u, S, 1);
-  else if constexpr (FMT == T_Q5_K8) return unit_q5k8(U.ch, u, S);
   else if constexpr (FMT == T_Q6_K) return unit_q6k(U.ch, U.d, u, S);
   else if constexpr (FMT == T_Q8_0) return unit_q80(U.ch, u, S);
   else return unit_iq3(U.ch, U.d, u, S);
@@ -374,23 +329,7 @@ __device__ __forceinline__ void stage_block(XS &xsrc, int kpad, const Smem &S,
   const int tid = threadIdx.x;
   const int passes = (kpad + 16 * NTH - 1) / (16 * NTH);
   auto pass_e0 = [&](int p) { return 16 * NTH * p + 16 * tid; };
-  if constexpr (IsExact<XS>::value) {
-    // rms of the whole input first (one extra barrier; the loads below hit
-    // the cache)
-    for (int p = 0; p < passes; p++) {
-      typename XS::Raw r0;
-      xsrc.issue(pass_e0(p), r0);
-      xsrc.accum_ss(r0, pass_e0(p));
-    }
-    xsrc.pre_barrier(S.red);
-    __syncthreads();
-    xsrc.set_rms(S.red);
-    __syncthreads();
-  }
-  auto stage = [&](int e0, const float (&xv)[16]) {
-    if constexpr (FMT == T_Q5_K8) stage_x_q8k(kpad, e0, xv, S);
-    else stage_x<FMT == T_Q6_K>(kpad, e0, xv, S);
-  };
+  auto stage = [&](int e0, const float (&xv)[16]) { stage_x<FMT == T_Q6_K>(kpad, e0, xv, S); };
   typename XS::Raw raw[NP];
 #pragma unroll
   for (int p = 0; p < NP; p++)
@@ -524,76 +463,6 @@ __device__ __forceinline__ float row_sum(const float *p, int U, int sub, int G, 
   if (G >= 8)
     acc += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(acc), 0x114, 0xF, 0xF, true));
   return acc;
-}
-
-// Decode matvec over one or more matrices (segments) sharing the input.
-// Weights are one tile per matrix, i.e. the units of the whole matrix in
-// row-major order, 64 per iteration.  Block b of a segment owns rows
-// [r0, r1) = [rows * lb / nblk, rows * (lb + 1) / nblk), i.e. units
-// [r0 * U, r1 * U): the blocks get equal work (+-1 row) and the grid is one
-// block per CU, so every block stages x exactly once and all of them run
-// at the same time.  The block's iterations (first and last ones partial:
-// lanes outside its units load nothing) are dealt round-robin to its
-// waves, each keeping two units per lane in flight; per-unit partial sums
-// go to LDS and are reduced per row in a fixed order.  With NT = 2
-// (gate/up pair) the block streams the same units of seg[1] as well and
-// writes silu(g) * u.
-template <int FMT, bool K4, int SRC, int NP, int NT>
-__global__ __launch_bounds__(mv_threads(FMT)) void k_matvec(MvArgs a) {
-  extern __shared__ __align__(16) char smem_raw[];
-  constexpr int NTH = mv_threads(FMT), NW = NTH / 64;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
-  const int b = blockIdx.x;
-  MvSeg sg = a.seg[0];
-  if constexpr (NT == 1) {
-#pragma unroll
-    for (int i = 1; i < MV_MAX_SEG; i++)
-      if (i < a.nseg && b >= a.seg[i].blk_begin) sg = a.seg[i];
-  }
-  const int U = a.units;
-  const int lb = b - sg.blk_begin;
-  const int r0 = (int)((long)sg.rows * lb / sg.nblk);
-  const int r1 = (int)((long)sg.rows * (lb + 1) / sg.nblk);
-  Smem S;
-  smem_layout(FMT, U, a.part_floats, &S, smem_raw);
-  const MvSeg s1 = a.seg[1];
-  auto mat = [&](int m) {
-    return NT == 2 && m ? MatRef{s1.body, s1.d, 0} : MatRef{sg.body, sg.d, 0};
-  };
-  const BlockStream<FMT, NW, NT, decltype(mat)> bs(mat, U, r0 * U, r1 * U, sg.rows * U, NT, lane,
-                                                   wave);
-  Unit<FMT> A, B;
-  auto first = [&] { bs.first(A); };
-  float rscale = 1.f;
-  if constexpr (SRC == MV_NORM) {
-    const float *x = a.in.tok ? a.in.x + (long)(*a.in.tok) * a.k : a.in.x;
-    XNorm<K4, FMT == T_Q5_K8> xs{x, a.in.r, a.in.nw, b == 0 ? a.in.xo : nullptr, a.k, a.in.eps};
-    stage_block<FMT, NP, NTH>(xs, U * 256, S, a.grid, first);
-    rscale = xs.scale(S.red);
-  } else if constexpr (SRC == MV_SWIGLU) {
-    XSwiGLU<K4> xs{a.in.xg, a.in.xu, a.k};
-    stage_block<FMT, NP, NTH>(xs, U * 256, S, a.grid, first);
-  } else {
-    XPlain<K4> xs{a.in.x, a.k};
-    stage_block<FMT, NP, NTH>(xs, U * 256, S, a.grid, first);
-  }
-  bs.run(A, B, S);
-  __syncthreads();
-
-  const int rows_b = r1 - r0;
-  const int G = row_lanes(U, rows_b, NTH), per = NTH / G;
-  for (int rb = 0; rb < rows_b; rb += per) {
-    const int r = rb + tid / G, sub = tid % G;
-    float v[NT];
-#pragma unroll
-    for (int m = 0; m < NT; m++) v[m] = row_sum(bs.row_part(S, m, r), U, sub, G, r < rows_b) * rscale;
-    if (sub == G - 1 && r < rows_b) {
-      float out = v[0];
-      if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
-      sg.y[r0 + r] = out;
-    }
-  }
 }
 
 // ------------------------------------------------------------------- MoE
@@ -736,77 +605,6 @@ size_t matvec_lds_bytes(int dtype, int units, int part_total) {
   return smem_layout(dtype, units, part_total, nullptr, nullptr);
 }
 
-size_t matvec_plan(MvArgs &a, int num_cus) {
-  static const int bpc = [] {
-    const char *e = getenv("GQ_MV_BLOCKS_PER_CU");  // tuning override
-    return e && atoi(e) > 0 ? atoi(e) : MV_BLOCKS_PER_CU;
-  }();
-  const int nt = a.pair ? 2 : 1, nseg = a.pair ? 1 : a.nseg;
-  long total = 0;
-  for (int i = 0; i < nseg; i++) total += a.seg[i].rows;
-  long target = std::max(1, num_cus * bpc);
-  for (;;) {
-    int blk = 0;
-    long max_units = 0;
-    for (int i = 0; i < nseg; i++) {
-      const int rows = a.seg[i].rows;
-      const int nb = (int)std::max(1L, std::min((long)rows, std::lround((double)target * rows / total)));
-      a.seg[i].blk_begin = blk;
-      a.seg[i].nblk = nb;
-      blk += nb;
-      max_units = std::max(max_units, (long)((rows + nb - 1) / nb) * a.units);
-    }
-    // A block's units may start mid-iteration: one more iteration.
-    const int part = (int)(nt * 64 * ((max_units + 63) / 64 + 1));
-    const size_t lds = matvec_lds_bytes(a.fmt, a.units, part);
-    if (lds <= 160 * 1024 || target >= total) {
-      a.blocks = blk;
-      a.part_floats = part;
-      return lds;
-    }
-    target *= 2;
-  }
-}
-
-template <int FMT, bool K4, int SRC, int NP, int NT>
-static hipError_t launch_t(const MvArgs &a, hipStream_t st) {
-  const size_t lds = matvec_lds_bytes(FMT, a.units, a.part_floats);
-  if (lds > 64 * 1024)
-    (void)hipFuncSetAttribute((const void *)k_matvec<FMT, K4, SRC, NP, NT>,
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL((k_matvec<FMT, K4, SRC, NP, NT>), dim3(a.blocks), dim3(mv_threads(FMT)), lds, st, a);
-  return hipGetLastError();
-}
-
-// Instances: plain x with 1, 4 or (512-thread blocks) 8 staging passes in
-// flight together;
-// the normalised source (k % 4 == 0, one pass in flight) alone or for a
-// gate/up pair; the SwiGLU source with one pass in flight.
-template <int FMT>
-static hipError_t launch_f(const MvArgs &a, hipStream_t st) {
-  const int passes = (a.units * 256 + 16 * mv_threads(FMT) - 1) / (16 * mv_threads(FMT));
-  const bool k4 = a.k % 4 == 0;
-  switch (a.in.src) {
-  case MV_NORM:
-    if (!k4) return hipErrorInvalidValue;
-    return a.pair ? launch_t<FMT, true, MV_NORM, 1, 2>(a, st) : launch_t<FMT, true, MV_NORM, 1, 1>(a, st);
-  case MV_SWIGLU:
-    if (a.pair) return hipErrorInvalidValue;
-    return k4 ? launch_t<FMT, true, MV_SWIGLU, 1, 1>(a, st) : launch_t<FMT, false, MV_SWIGLU, 1, 1>(a, st);
-  default:
-    if (a.pair) return hipErrorInvalidValue;
-    if (passes == 1)
-      return k4 ? launch_t<FMT, true, MV_X, 1, 1>(a, st) : launch_t<FMT, false, MV_X, 1, 1>(a, st);
-    // (Any NP is correct: passes past NP are staged one by one.  768-thread
-    // blocks stage at most 4 passes within the LDS limit.)
-    if (passes <= 4 || mv_threads(FMT) > 512)
-      return k4 ? launch_t<FMT, true, MV_X, 4, 1>(a, st) : launch_t<FMT, false, MV_X, 4, 1>(a, st);
-    if constexpr (mv_threads(FMT) <= 512)
-      return k4 ? launch_t<FMT, true, MV_X, 8, 1>(a, st) : launch_t<FMT, false, MV_X, 8, 1>(a, st);
-    return hipErrorInvalidValue;
-  }
-}
-
 // Blocks per pair (gate/up) and per token (down): about one block per CU
 // in all, more while a block's partial sums would not fit in LDS.  Stages
 // over quad-layout experts take the MFMA kernels' plan.
@@ -923,17 +721,6 @@ hipError_t launch_moe(const MoeArgs &args, int T, hipStream_t st) {
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
-}
-
-hipError_t launch_matvec(const MvArgs &a, int fmt, hipStream_t st) {
-  switch (fmt) {
-  case T_Q4_K: return launch_f<T_Q4_K>(a, st);
-  case T_Q5_K: return a.in.q8k ? launch_f<T_Q5_K8>(a, st) : launch_f<T_Q5_K>(a, st);
-  case T_Q6_K: return launch_f<T_Q6_K>(a, st);
-  case T_Q8_0: return launch_f<T_Q8_0>(a, st);
-  case T_IQ3_XXS: return launch_f<T_IQ3_XXS>(a, st);
-  default: return hipErrorInvalidValue;
-  }
 }
 
 }  // namespace gq
