@@ -390,6 +390,7 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   const int ngb = (G - b + B - 1) / B;
   const int nitems = ngb * NM * T;
   const int rows_blk = ngb * QROWS;
+  if (nitems == 0) return;  // (plans give every block a group; uniform per block)
   QSmem S;
   qsmem_layout(QF<FMT>::AUX, Ux, nitems * QROWS, &S, smem);
 
