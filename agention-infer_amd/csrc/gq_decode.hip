@@ -5,17 +5,17 @@
 // cpu_path.rs:695-818).
 //
 // One step is 6 launches per layer plus 2:
-//   qkv matvec   input RMSNorm(x + proj) (residual add fused; block 0 stores
-//                the new residual stream; layer 0 reads the embedding row)
+//   qkv matvec   input RMSNorm(x_b) (layer 0: of the embedding row, which
+//                block 0 stores as x_b)
 //   attention    RoPE of q and of the new k, f16 KV row store, scores,
 //                softmax and the weighted V sum for all query heads of one
 //                KV head over a chunk of positions
 //   merge        the chunk partials of each query head combined
-//   o matvec
-//   gate/up      one matvec over both matrices with input RMSNorm(x + o)
+//   o matvec     epilogue x_a = x_b + o (the residual add)
+//   gate/up      one matvec over both matrices with input RMSNorm(x_a)
 //                and output silu(gate) * up
-//   down matvec
-// then the output head (input RMSNorm(x + proj)) and the greedy argmax.
+//   down matvec  epilogue x_b = x_a + down
+// then the output head (input RMSNorm(x_b)) and the greedy argmax.
 //
 // Step state (token, position, step counter) lives in device memory so that
 // a captured HIP graph of one step can be replayed for every greedy step:
@@ -547,14 +547,15 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
   const int kvd = nkv * hd, group = nh / nkv;
   hipError_t e;
   for (int L = 0; L < m.n_layers; L++) {
-    // x_b = x_a + proj (layer 0: the embedding row); q, k, v of RMSNorm(x_b)
+    // q, k, v of RMSNorm(x_b)
     MvIn in;
     in.src = MV_NORM;
-    in.x = L ? m.xa : m.embd;
+    // (layer 0 stores the embedding row as the residual stream x_b; later
+    // layers read x_b = x_a + proj, stored by the previous down launch)
+    in.x = L ? m.xb : m.embd;
     in.tok = L ? nullptr : &m.state->token;
-    in.r = L ? m.proj : nullptr;
     in.nw = m.attn_norm[L];
-    in.xo = m.xb;
+    in.xo = L ? nullptr : m.xb;
     in.eps = m.eps;
     in.q8k = true;  // matmul_qkv_into -> matmul_into (cpu_path.rs:319-321)
     // One launch per distinct dtype among q/k/v (GGUF Q4_K_M files carry
@@ -605,16 +606,15 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     MvIn ain;
     ain.x = m.att;
     ain.q8k = true;  // matmul_into (cpu_path.rs:757)
+    ain.res = m.xb;  // x_a = x_b + o (cpu_path.rs:780-782)
     const gq_weight *wo[1] = {m.wo[L]};
-    float *proj[1] = {m.proj};
-    if ((e = matvec_launch(wo, 1, ain, proj, s)) != hipSuccess) return e;
-    // x_a = x_b + o; h = silu(gate . n) * (up . n), n = RMSNorm(x_a)
+    float *xa[1] = {m.xa};
+    if ((e = matvec_launch(wo, 1, ain, xa, s)) != hipSuccess) return e;
+    // h = silu(gate . n) * (up . n), n = RMSNorm(x_a)
     MvIn fin;
     fin.src = MV_NORM;
-    fin.x = m.xb;
-    fin.r = m.proj;
+    fin.x = m.xa;
     fin.nw = m.ffn_norm[L];
-    fin.xo = m.xa;
     fin.eps = m.eps;
     const gq_weight *gu[2] = {m.wgate[L], m.wup[L]};
     float *hout[2] = {m.h, nullptr};
@@ -622,14 +622,15 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     MvIn din;
     din.x = m.h;
     din.q8k = true;  // matmul_ffn_into's down: matmul_into (cpu_path.rs:383)
+    din.res = m.xa;  // x_b = x_a + down (cpu_path.rs:806-808)
     const gq_weight *wd[1] = {m.wdown[L]};
-    if ((e = matvec_launch(wd, 1, din, proj, s)) != hipSuccess) return e;
+    float *xb[1] = {m.xb};
+    if ((e = matvec_launch(wd, 1, din, xb, s)) != hipSuccess) return e;
   }
   // logits of RMSNorm(x_a + proj)
   MvIn hin;
   hin.src = MV_NORM;
-  hin.x = m.xa;
-  hin.r = m.proj;
+  hin.x = m.xb;
   hin.nw = m.output_norm;
   hin.eps = m.eps;
   hin.q8k = true;  // the head: matmul_into (cpu_path.rs:815)

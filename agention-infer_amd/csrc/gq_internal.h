@@ -55,6 +55,8 @@ struct MvIn {
   const float *nw = nullptr;  // MV_NORM: norm weight
   float *xo = nullptr;        // MV_NORM: x + r written here (may be null)
   const int *tok = nullptr;   // MV_NORM: if set, x is row *tok of the table x
+  const float *res = nullptr; // one-matrix launches: y = res + W . x (the residual add,
+                              // x += proj of cpu_path.rs:780-782 / 806-808, in the producer)
   float eps = 0.f;
   // Q5_K weights: dot against the input quantized to Q8_K (matmul_into's
   // route, src/model/mod.rs:381-394) instead of the float dot (dot_row,

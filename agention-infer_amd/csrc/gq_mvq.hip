@@ -689,6 +689,7 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
     }
     float out = v[0];
     if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
+    if (NT == 1 && a.in.res) out = a.in.res[row] + out;  // (one-matrix launches)
     sg.y[row] = out;
     if (out > bv) {  // rows rise with lr: strict > keeps the first maximum; NaN never wins
       bv = out;
