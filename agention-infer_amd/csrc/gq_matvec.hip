@@ -147,6 +147,41 @@ __device__ __forceinline__ float unit_q4k(const uint4 *ch, int u, const Smem &S,
   return acc;
 }
 
+// Q5_K against the Q8_K-quantized input (dot_q5_k_q8k, src/quant/q5_k.rs:
+// 126-184): the codes sit in limb l0 and each 16-run record holds {d of the
+// Q8_K block, the run's bsums entry as int bits}.  The weight codes (5-bit,
+// 0..31) meet the int8 codes in v_dot4; acc_pos and acc_min are exact
+// integers, and the unit's value is the reference's per-block term
+// dx * (d * acc_pos - dmin * acc_min), rounded the same way.
+__device__ __forceinline__ float unit_q5k8(const uint4 *ch, int u, const Smem &S) {
+  const uint4 hd = ch[0];
+  const float d = h2f(hd.x), dmin = h2f(hd.x >> 16);
+  int acc_pos = 0, acc_min = 0;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    uint32_t sc0, m0, sc1, m1;
+    scale_min_k4(2 * j, hd.y, hd.z, hd.w, sc0, m0);
+    scale_min_k4(2 * j + 1, hd.y, hd.z, hd.w, sc1, m1);
+    int plo = 0, phi = 0;
+    const int off = u * LIMB_STRIDE + 64 * j;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const uint32_t q = dw(ch + 3, 8 * j + i);
+      const uint32_t h = dw(ch + 1, i);  // qh bytes 4i..4i+3
+      const uint32_t lo = (q & 0x0F0F0F0Fu) | (((h >> (2 * j)) & 0x01010101u) << 4);
+      const uint32_t hi = ((q >> 4) & 0x0F0F0F0Fu) | (((h >> (2 * j + 1)) & 0x01010101u) << 4);
+      plo = __builtin_amdgcn_sdot4(lo, *(const uint32_t *)(S.l0 + off + 4 * i), plo, false);
+      phi = __builtin_amdgcn_sdot4(hi, *(const uint32_t *)(S.l0 + off + 32 + 4 * i), phi, false);
+    }
+    const int b0 = __float_as_int(aux_at(S, u, 4 * j).y) + __float_as_int(aux_at(S, u, 4 * j + 1).y);
+    const int b1 = __float_as_int(aux_at(S, u, 4 * j + 2).y) + __float_as_int(aux_at(S, u, 4 * j + 3).y);
+    acc_pos += (int)sc0 * plo + (int)sc1 * phi;
+    acc_min += (int)m0 * b0 + (int)m1 * b1;
+  }
+  const float dx = aux_at(S, u, 0).x;
+  return dx * (d * (float)acc_pos - dmin * (float)acc_min);
+}
+
 // ---------------------------------------------------------------- Q6_K
 // ch[0..7] = ql[128], ch[8..11] = qh[64], ch[12] = scales[16]; d separate.
 // 16-run s (elements 16s..16s+15 of the unit) uses scale index s.
@@ -233,6 +268,17 @@ __device__ __forceinline__ float unit_iq3(const uint4 *ch, uint32_t dbits, int u
 template <bool Q6>
 __device__ __forceinline__ void put_aux(const Smem &S, int e0, float sx, float sum32, int xs);
 
+// Q8_K route: the 16 threads of each 256-element block quantize it like
+// quantize_row_q8_k; the codes go to limb l0, {d, bsum} to the records.
+__device__ __forceinline__ void stage_x_q8k(int kpad, int e0, const float (&xv)[16], const Smem &S) {
+  const Q8K16 r = q8k_quant16(xv, e0 & 255);
+  if (e0 >= kpad) return;
+  const int lo = (e0 >> 8) * LIMB_STRIDE + (e0 & 255);
+  *(uint4 *)(S.l0 + lo) = make_uint4(r.q[0], r.q[1], r.q[2], r.q[3]);
+  const int u = e0 >> 8, rr = (e0 & 255) >> 4;
+  *(float2 *)((char *)S.aux + u * AUX_STRIDE + 8 * rr) = make_float2(r.d, __int_as_float(r.bsum));
+}
+
 template <bool Q6>
 __device__ __forceinline__ void stage_x(int kpad, int e0, const float (&xv)[16], const Smem &S) {
   float amax = 0.f, sum = 0.f;
@@ -289,6 +335,7 @@ template <int FMT> struct Fmt;
 // C: 16-byte chunks per unit.
 template <> struct Fmt<T_Q4_K> { static constexpr int C = 9; static constexpr bool HAS_D = false; };
 template <> struct Fmt<T_Q5_K> { static constexpr int C = 11; static constexpr bool HAS_D = false; };
+template <> struct Fmt<T_Q5_K8> { static constexpr int C = 11; static constexpr bool HAS_D = false; };
 template <> struct Fmt<T_Q6_K> { static constexpr int C = 13; static constexpr bool HAS_D = true; };
 template <> struct Fmt<T_Q8_0> { static constexpr int C = 17; static constexpr bool HAS_D = false; };
 template <> struct Fmt<T_IQ3_XXS> { static constexpr int C = 6; static constexpr bool HAS_D = true; };
@@ -311,6 +358,7 @@ template <int FMT>
 __device__ __forceinline__ float unit_dot(const Unit<FMT> &U, int u, const Smem &S) {
   if constexpr (FMT == T_Q4_K) return unit_q4k(U.ch, u, S, 0);
   else if constexpr (FMT == T_Q5_K) return unit_q4k(U.ch, u, S, 1);
+  else if constexpr (FMT == T_Q5_K8) return unit_q5k8(U.ch, u, S);
   else if constexpr (FMT == T_Q6_K) return unit_q6k(U.ch, U.d, u, S);
   else if constexpr (FMT == T_Q8_0) return unit_q80(U.ch, u, S);
   else return unit_iq3(U.ch, U.d, u, S);
@@ -329,7 +377,10 @@ __device__ __forceinline__ void stage_block(XS &xsrc, int kpad, const Smem &S,
   const int tid = threadIdx.x;
   const int passes = (kpad + 16 * NTH - 1) / (16 * NTH);
   auto pass_e0 = [&](int p) { return 16 * NTH * p + 16 * tid; };
-  auto stage = [&](int e0, const float (&xv)[16]) { stage_x<FMT == T_Q6_K>(kpad, e0, xv, S); };
+  auto stage = [&](int e0, const float (&xv)[16]) {
+    if constexpr (FMT == T_Q5_K8) stage_x_q8k(kpad, e0, xv, S);
+    else stage_x<FMT == T_Q6_K>(kpad, e0, xv, S);
+  };
   typename XS::Raw raw[NP];
 #pragma unroll
   for (int p = 0; p < NP; p++)
@@ -694,17 +745,17 @@ hipError_t launch_moe(const MoeArgs &args, int T, hipStream_t st) {
   if (a.quad_gu) {
     e = launch_mvq_moe(a, T, 1, fused, st);
   } else {
-#define GQ_MOE_GU(F)                                        \
-  case F:                                                   \
+#define GQ_MOE_GU(C, F)                                     \
+  case C:                                                   \
     if (fused) moe_gate_up_f<F, true>(a, T, st);            \
     else moe_gate_up_f<F, false>(a, T, st);                 \
     break;
     switch (a.fmt) {
-      GQ_MOE_GU(T_IQ3_XXS)
-      GQ_MOE_GU(T_Q4_K)
-      GQ_MOE_GU(T_Q5_K)
-      GQ_MOE_GU(T_Q6_K)
-      GQ_MOE_GU(T_Q8_0)
+      GQ_MOE_GU(T_IQ3_XXS, T_IQ3_XXS)
+      GQ_MOE_GU(T_Q4_K, T_Q4_K)
+      GQ_MOE_GU(T_Q5_K, T_Q5_K8)  // matmul_into's Q8_K route
+      GQ_MOE_GU(T_Q6_K, T_Q6_K)
+      GQ_MOE_GU(T_Q8_0, T_Q8_0)
     default: return hipErrorInvalidValue;
     }
 #undef GQ_MOE_GU
@@ -715,7 +766,7 @@ hipError_t launch_moe(const MoeArgs &args, int T, hipStream_t st) {
   switch (a.fmt) {
   case T_IQ3_XXS: moe_down_f<T_IQ3_XXS>(a, T, st); break;
   case T_Q4_K: moe_down_f<T_Q4_K>(a, T, st); break;
-  case T_Q5_K: moe_down_f<T_Q5_K>(a, T, st); break;
+  case T_Q5_K: moe_down_f<T_Q5_K8>(a, T, st); break;
   case T_Q6_K: moe_down_f<T_Q6_K>(a, T, st); break;
   case T_Q8_0: moe_down_f<T_Q8_0>(a, T, st); break;
   default: return hipErrorInvalidValue;

@@ -805,7 +805,7 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
 // MoE stage plans: about one block per CU in all (blocks per pair / per
 // token), more while a block's LDS would not fit.
 size_t mvq_moe_plan(MoeArgs &a, int T, int stage, int num_cus) {
-  const int fmt = a.fmt, aux = aux_per_unit(fmt);
+  const int fmt = a.fmt == T_Q5_K ? T_Q5_K8 : a.fmt, aux = aux_per_unit(fmt);  // (Q5_K: Q8_K route)
   const int st = (int)mvq_static_lds(fmt);
   if (stage == 1) {
     const int G = a.f / QROWS, Tq = (a.units_h + 3) / 4, pairs = T * a.top_k;
@@ -867,7 +867,7 @@ hipError_t launch_mvq_moe(const MoeArgs &a, int T, int stage, bool route, hipStr
   if ((stage == 1 ? a.f : a.h) % QROWS || a.top_k > 64) return hipErrorInvalidValue;
   switch (a.fmt) {
   case T_Q4_K: return mvq_moe_f<T_Q4_K>(a, T, stage, route, st);
-  case T_Q5_K: return mvq_moe_f<T_Q5_K>(a, T, stage, route, st);
+  case T_Q5_K: return mvq_moe_f<T_Q5_K8>(a, T, stage, route, st);  // matmul_into's Q8_K route
   case T_Q6_K: return mvq_moe_f<T_Q6_K>(a, T, stage, route, st);
   case T_Q8_0: return mvq_moe_f<T_Q8_0>(a, T, stage, route, st);
   case T_IQ3_XXS: return mvq_moe_f<T_IQ3_XXS>(a, T, stage, route, st);

@@ -149,7 +149,8 @@ int gq_upload_experts(int dtype, const void *w_host, size_t nbytes, int in_dim,
  *   ids[t], w[t] = top_k of softmax(logits[t]) (ties: lower expert index;
  *                  weights are the full-softmax probabilities),
  *   out[t] = sum_s w[t][s] * down_e(silu(gate_e x_t) * up_e x_t),
- * SwiGLU as ffn_gate_up (src/model/llama/cpu_path.rs:200-232).  gate/up:
+ * SwiGLU as ffn_gate_up (src/model/llama/cpu_path.rs:200-232); each expert
+ * matvec is matmul_into's (src/model/mod.rs:362-403: Q5_K via Q8_K).  gate/up:
  * [n_experts][f][h], down: [n_experts][h][f], uploaded with
  * gq_upload_experts.  logits_dev [T][n_experts], x_dev/out_dev [T][h];
  * ids_dev/w_dev ([T][top_k]) receive the routing if non-NULL; top_k <= 64.

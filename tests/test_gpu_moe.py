@@ -121,3 +121,32 @@ def test_moe_routing_ties(backend, orc):
         assert np.array_equal(ids.cpu().numpy(), rids)
         # softmax sums over E terms in another order: a few ulps per term
         assert np.allclose(w.cpu().numpy(), rw, rtol=1e-5, atol=0)
+
+
+@pytest.mark.parametrize("dtype", [8, 12, 13, 14])
+@pytest.mark.parametrize("E,H,F,T,k", [(6, 512, 48, 3, 2), (5, 256, 40, 2, 2)])
+def test_moe_other_formats(backend, orc, dtype, E, H, F, T, k):
+    """Q8_0 / Q4_K / Q5_K / Q6_K experts: the quad-layout MFMA stages (F and H
+    multiples of 16) and the wave-tiled v_dot4 gate/up (F = 40)."""
+    import torch
+    say(f"moe dtype={dtype} E={E} H={H} F={F} T={T} k={k}")
+    gate = syn.make_blocks(dtype, E * F, H, seed=dtype + F)
+    up = syn.make_blocks(dtype, E * F, H, seed=dtype + F + 1)
+    down = syn.make_blocks(dtype, E * H, F, seed=dtype + F + 2)
+    hg = backend.upload_experts(dtype, gate, H, F, E)
+    hu = backend.upload_experts(dtype, up, H, F, E)
+    hd = backend.upload_experts(dtype, down, F, H, E)
+    rng = np.random.default_rng(dtype + 7)
+    logits = rng.standard_normal((T, E), dtype=np.float32)
+    x = syn.make_x(H, seed=dtype + 8, batch=T)
+    out, ids, w = backend.moe_ffn(hg, hu, hd, E, torch.from_numpy(logits).cuda(),
+                                  torch.from_numpy(x).cuda(), k, want_routing=True)
+    torch.cuda.synchronize()
+    out, ids, w = out.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy()
+    rids, rw = orc.moe_route(logits, k)
+    assert np.array_equal(ids, rids)
+    ref = orc.moe_ffn(dtype, gate, up, down, E, H, F, x, rids, rw)
+    err = float(np.max(np.abs(out.astype(np.float64) - ref)))
+    bound = TOL * float(np.max(np.abs(ref)))
+    say(f"  max|err| {err:.3g} bound {bound:.3g}")
+    assert err <= bound
