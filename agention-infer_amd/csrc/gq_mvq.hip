@@ -69,10 +69,13 @@ __device__ __forceinline__ uint32_t *iq3_tables() {
 }
 
 // Waves per block, and items per lane in registers at once (the current
-// one and DEPTH - 1 in flight): 8 waves (two per SIMD, 256 registers per
-// lane) keep 3 items of Q4_K / Q5_K / Q6_K (2 of Q8_0) per lane.
+// one and DEPTH - 1 in flight): 8 waves (two per SIMD), each lane keeping
+// one item in flight while it computes another.  (Three items per lane held
+// 60 more registers and streamed slower: the Q6_K head 72.5 against 70.0
+// us, the Q4_K gate/up pair 16.2 against 15.4; 12 waves of the two-item
+// Q4_K kernel were slower still.)
 __host__ __device__ constexpr int mvq_waves(int) { return 8; }
-__host__ __device__ constexpr int mvq_depth(int fmt) { return fmt == T_Q8_0 ? 2 : 3; }
+__host__ __device__ constexpr int mvq_depth(int) { return 2; }
 
 template <int FMT> struct QF;
 template <> struct QF<T_Q4_K> { static constexpr int C = 9, AUX = 8; };
@@ -496,7 +499,8 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
     // the weights: loads complete in order), signed into T1 and T2 below:
     // entries o = tid + NTH i of each table (T1's all take entry tid % 256).
     constexpr int GW = FMT == T_IQ3_XXS ? 4096 / NTH : 1;
-    static_assert(NTH % 256 == 0 && 4096 % NTH == 0, "table staging assumes 256 | NTH | 4096");
+    static_assert(FMT != T_IQ3_XXS || (NTH % 256 == 0 && 4096 % NTH == 0),
+                  "table staging assumes 256 | NTH | 4096");
     uint32_t gword[GW], gword1 = 0;
     if constexpr (FMT == T_IQ3_XXS) {
       const uint32_t *gr = MODE == MQ_DENSE ? a.grid : mo.grid;
