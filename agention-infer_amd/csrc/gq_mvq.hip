@@ -69,12 +69,13 @@ __device__ __forceinline__ uint32_t *iq3_tables() {
 }
 
 // Waves per block, and items per lane in registers at once (the current
-// one and DEPTH - 1 in flight): 8 waves (two per SIMD), each lane keeping
+// one and DEPTH - 1 in flight): 8 waves (two per SIMD; IQ3_XXS, whose item
+// math is LDS- and VALU-bound and needs fewer registers, 16), each lane keeping
 // one item in flight while it computes another.  (Three items per lane held
 // 60 more registers and streamed slower: the Q6_K head 72.5 against 70.0
 // us, the Q4_K gate/up pair 16.2 against 15.4; 12 waves of the two-item
 // Q4_K kernel were slower still.)
-__host__ __device__ constexpr int mvq_waves(int) { return 8; }
+__host__ __device__ constexpr int mvq_waves(int fmt) { return fmt == T_IQ3_XXS ? 16 : 8; }
 __host__ __device__ constexpr int mvq_depth(int) { return 2; }
 
 template <int FMT> struct QF;
