@@ -1,5 +1,6 @@
 // gq_mvq.hip -- batch-1 decode matvec y = W . x on int8 MFMA for dense
-// Q4_K, Q5_K, Q6_K and Q8_0 weights (gfx950, wave64).
+// Q4_K, Q5_K, Q6_K, Q8_0 and IQ3_XXS weights, and the two stages of the MoE
+// expert FFN over stacked experts in the same layout (gfx950, wave64).
 //
 // Replaces the reference's per-row dot kernels (src/quant/q8_0.rs:58-90,
 // q4_k.rs:95-212, q5_k.rs:126-184 and 189-317, q6_k.rs:82-131) driven
@@ -32,14 +33,18 @@
 //   Q5_K x Q8_K (matmul_into's route): A holds the Q8_K codes (one limb)
 //              and the block term dx * (d * acc_pos - dmin * acc_min) is
 //              the reference's, exactly.
+//   IQ3_XXS    B = signed codebook bytes from two LDS tables (the format is
+//              re-encoded at upload so that each lookup index is a bit
+//              field), acc_i = sum_sb (2 s_sb + 1) * D_sb,i,
+//              y += d / 4 * s * (acc_2 2^16 + acc_1 2^8 + acc_0)
 // The four lanes of a row add their units (lane swaps), waves write per-row
 // partial sums to LDS, and the block adds them per row in a fixed order
 // (deterministic results).
 //
-// Work split: block b owns the row groups [G b / B, G (b + 1) / B) of the
-// launch (all segments' groups in a row); its items (group, matrix, quad)
-// are split into NW equal contiguous ranges, one per wave.  Each lane keeps
-// its next item in flight while it computes the current one.
+// Work split: block b owns the row groups b, b + B, b + 2B, ... of the
+// launch (all segments' groups in a row); the waves take its items (group,
+// matrix, quad) in turn from an LDS counter.  Each lane keeps its next item
+// in flight while it computes the current one.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
