@@ -397,23 +397,45 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   // Staged x: U units (down: top_k slot inputs of 4T units each).
   const int Ux = MODE == MQ_DOWN ? NM * 4 * T : U, upad = 4 * ((Ux + 3) >> 2);
   const int ngb = (G - b + B - 1) / B;
-  const int nitems = ngb * NM * T;
+  // Row sums go to one LDS slot per (group, matrix, quad): (lg NM + m) T + t.
+  // down with 4F + 2 units per row and an even top_k (SP): the 2-unit tail
+  // quads of slots 2j and 2j + 1 form one item (lanes q < 2: slot 2j,
+  // q >= 2: slot 2j + 1), so no lane idles; per group and slot pair the
+  // items are slot 2j's F full quads, slot 2j + 1's, then the tail pair.
+  const int F = U >> 2;
+  const bool SP = MODE == MQ_DOWN && (U & 3) == 2 && (NM & 1) == 0;
+  const int per_sp = (NM / 2) * (2 * F + 1);
+  const int nslots = ngb * NM * T;
+  const int nitems = SP ? ngb * per_sp : nslots;
   const int rows_blk = ngb * QROWS;
   if (nitems == 0) return;  // (plans give every block a group; uniform per block)
   QSmem S;
-  qsmem_layout(QF<FMT>::AUX, Ux, nitems * QROWS, &S, smem);
+  qsmem_layout(QF<FMT>::AUX, Ux, nslots * QROWS, &S, smem);
 
-  // Item cursor (wave-uniform): local and flat group, matrix, quad, segment.
+  // Item cursor (wave-uniform): local and flat group, matrix, quad, segment,
+  // row-sum slot, and whether it is a down tail pair (slots m and m + 1).
   struct Cur {
-    int lg, fg, m, t, seg;
+    int lg, fg, m, t, seg, slot;
+    bool pair;
   };
   auto cur_at = [&](int it) {
     Cur c;
-    const int per = NM * T, gi = it / per, rem = it - gi * per;
-    c.lg = gi;
-    c.fg = b + gi * B;
-    c.m = rem / T;
-    c.t = rem - c.m * T;
+    c.pair = false;
+    if (SP) {
+      const int gi = it / per_sp, rem = it - gi * per_sp;
+      const int jp = rem / (2 * F + 1), k = rem - jp * (2 * F + 1);
+      c.lg = gi;
+      c.m = 2 * jp + (k >= F && k < 2 * F);
+      c.t = k < F ? k : k < 2 * F ? k - F : F;
+      c.pair = k == 2 * F;
+    } else {
+      const int per = NM * T, gi = it / per, rem = it - gi * per;
+      c.lg = gi;
+      c.m = rem / T;
+      c.t = rem - c.m * T;
+    }
+    c.fg = b + c.lg * B;
+    c.slot = (c.lg * NM + c.m) * T + c.t;
     c.seg = 0;
     if constexpr (MODE == MQ_DENSE && NT == 1) {
 #pragma unroll
@@ -458,12 +480,21 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   // waits do not depend on whether the wave has an item.
   auto load = [&](QItem<FMT> &dst, int it, bool idle = false) {
     const Cur lc = cur_at(it);
-    const Mat sg = mat_of(lc);
+    Mat sg = mat_of(lc);
+    if constexpr (MODE == MQ_DOWN) {
+      if (lc.pair) {  // lanes q >= 2: slot m + 1's expert
+        Cur c2 = lc;
+        c2.m = lc.m + 1;
+        const Mat s2 = mat_of(c2);
+        if (q >= 2) sg = s2;
+      }
+    }
     const int g = sg.g;
-    const int nr = min(QROWS, sg.rows - QROWS * g), nq = min(4, U - 4 * lc.t);
+    const int nr = min(QROWS, sg.rows - QROWS * g), nq = lc.pair ? 2 : min(4, U - 4 * lc.t);
+    const int ql = lc.pair ? (q & 1) : q;
     const long base = (long)g * QROWS * U + (long)lc.t * 4 * nr;  // quad_item_unit
-    const bool live = r < nr && q < nq && !idle;
-    const int l = live ? nr * q + r : 0;  // idle lanes re-read lane 0 (same lines)
+    const bool live = r < nr && ql < nq && !idle;
+    const int l = live ? nr * ql + r : 0;  // idle lanes re-read lane 0 (same lines)
     const uint8_t *bp = sg.body + base * (C * 16);
     const int cs = idle ? 0 : 16 * nr * nq;
 #pragma unroll
@@ -596,11 +627,17 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   const uint32_t limb_off = (uint32_t)((ai & 3) * upad * QL_STRIDE);
   auto consume = [&](const QItem<FMT> &src, int it) {
     const Cur cc = cur_at(it);
-    const int u = 4 * cc.t + q;  // this lane's unit
-    // first staged unit of the item's quad (down: in slot m's input)
-    const int xq = (MODE == MQ_DOWN ? cc.m * 4 * T : 0) + 4 * cc.t;
-    const uint32_t aoff = alive ? limb_off + (uint32_t)(xq + aq) * QL_STRIDE : S.zero_off;
-    float v = item_dot<FMT>(src.ch, src.d, smem, aoff, min(xq + q, upad - 1), S);
+    // lane group j (0..3) works on unit 4t + j of slot m, or for a tail pair
+    // on unit 4F + (j & 1) of slot m + j / 2
+    const int ql = cc.pair ? (q & 1) : q;
+    const int u = 4 * cc.t + ql;  // this lane's unit in its row
+    // staged unit of lane group j's input (down: in its slot's input)
+    auto xunit = [&](int j) {
+      const int m = cc.pair ? cc.m + (j >> 1) : cc.m;
+      return (MODE == MQ_DOWN ? m * 4 * T : 0) + 4 * cc.t + (cc.pair ? (j & 1) : j);
+    };
+    const uint32_t aoff = alive ? limb_off + (uint32_t)xunit(aq) * QL_STRIDE : S.zero_off;
+    float v = item_dot<FMT>(src.ch, src.d, smem, aoff, min(xunit(q), upad - 1), S);
     int rows, g;
     if constexpr (MODE == MQ_DENSE) {
       rows = a.seg[NT == 2 ? cc.m : cc.seg].rows;
@@ -611,8 +648,9 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
     }
     if (!(u < U && QROWS * g + r < rows)) v = 0.f;
     v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    if (q == 0) S.part[it * QROWS + r] = v;
+    if (!cc.pair) v += __shfl_xor(v, 32, 64);
+    if (q == 0) S.part[cc.slot * QROWS + r] = v;
+    if (cc.pair && q == 2) S.part[(cc.slot + T) * QROWS + r] = v;  // slot m + 1, same quad
   };
   if constexpr (DEPTH == 3) {
     for (;;) {
