@@ -551,7 +551,7 @@ __global__ __launch_bounds__(mv_threads(FMT)) void k_moe_gate_up(MoeArgs a) {
   // Routing runs while the x loads are in flight.
   auto route = [&] {
     if constexpr (ROUTE) e = moe_route_pair<NTH>(a, p, lb == 0);
-    else e = a.ids[p];
+    else e = min(max(a.ids[p], 0), a.n_experts - 1);
   };
   stage_block<FMT, 1, NTH>(xs, U * 256, S, a.grid, [&] {
     route();
@@ -585,7 +585,7 @@ __global__ __launch_bounds__(mv_threads(FMT)) void k_moe_down(MoeArgs a) {
   Smem S;
   smem_layout(FMT, K * U, a.part_f, &S, smem_raw);
   auto mat = [&](int m) {
-    const long tb = (long)a.ids[p0 + m] * h * U;
+    const long tb = (long)min(max(a.ids[p0 + m], 0), a.n_experts - 1) * h * U;
     return MatRef{a.down + tb * C * 16, a.down_d + tb, m * U};
   };
   const BlockStream<FMT, NW, 0, decltype(mat)> bs(mat, U, r0 * U, r1 * U, h * U, K, lane, wave);

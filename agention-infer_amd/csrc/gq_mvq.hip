@@ -447,7 +447,9 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   // The matrix of item cursor c: body, d array, rows, and c's group in it.
   int eid = 0;  // gate/up: the pair's expert (set before the first load)
   // down: lane m holds slot m's expert (loaded with the x loads in flight)
-  const int eids = MODE == MQ_DOWN && lane < NM ? mo.ids[p * NM + lane] : 0;
+  // (clamped: an expert index out of range, whatever a router wrote, stays a
+  // read inside the stacked tensor)
+  const int eids = MODE == MQ_DOWN && lane < NM ? min(max(mo.ids[p * NM + lane], 0), mo.n_experts - 1) : 0;
   struct Mat {
     const uint8_t *body;
     const uint16_t *d;
@@ -558,7 +560,7 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (MODE == MQ_GATE_UP) {  // (while the x loads are in flight)
         if constexpr (ROUTE) eid = moe_route_pair<NTH>(mo, p, b == 0);
-        else eid = __builtin_amdgcn_readfirstlane(mo.ids[p]);
+        else eid = __builtin_amdgcn_readfirstlane(min(max(mo.ids[p], 0), mo.n_experts - 1));
       }
       // (unconditional, so that the waits for x count exactly the loads
       // behind them)
