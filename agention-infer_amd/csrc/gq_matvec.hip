@@ -639,10 +639,14 @@ __global__ __launch_bounds__(256) void k_moe_route(const float *logits, int n_ex
   sum = red[0];
   for (int e = tid; e < n_experts; e += 256) {
     const float me = lv[e];
+    // (the count stops once it reaches top_k: such an expert has no slot)
     int rank = 0;
-    for (int o = 0; o < n_experts; o++) {
-      const float ov = lv[o];
-      rank += (ov > me) || (ov == me && o < e);
+    for (int o0 = 0; o0 < n_experts && rank < top_k; o0 += 16) {
+      const int o1 = min(o0 + 16, n_experts);
+      for (int o = o0; o < o1; o++) {
+        const float ov = lv[o];
+        rank += (ov > me) || (ov == me && o < e);
+      }
     }
     if (rank < top_k) {
       ids[t * top_k + rank] = e;
