@@ -313,10 +313,19 @@ int gq_upload_experts(int dtype, const void *w_host, size_t nbytes, int in_dim,
 }  // extern "C"
 
 namespace {
+// True while st is recording a HIP graph: nothing may allocate, free or
+// synchronize on it then.
+bool stream_capturing(hipStream_t st) {
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone;
+}
+
 // The workspace of gq_gemm (the packed X) and gq_moe_ffn (the SwiGLU
-// outputs and routing), kept per (device, stream) and grown on
-// demand: calls on one stream are ordered, so they can share it.  Held until
-// the process ends.
+// outputs and routing), kept per (device, stream) and grown on demand:
+// calls on one stream are ordered, so they can share it.  A buffer that a
+// larger call supersedes is never freed (a graph captured earlier may still
+// address it), so every workspace is held until the process ends.  Under
+// stream capture the workspace cannot grow: the call is refused.
 struct StreamWs {
   int dev;
   hipStream_t st;
@@ -324,29 +333,34 @@ struct StreamWs {
   size_t bytes;
 };
 std::vector<StreamWs> g_stream_ws;  // guarded by g_mu
+std::vector<void *> g_retired_ws;   // superseded workspaces, guarded by g_mu
 
 int stream_workspace(hipStream_t st, size_t bytes, void **out) {
   std::lock_guard<std::mutex> lk(g_mu);
   int dev = 0;
   (void)hipGetDevice(&dev);
-  for (StreamWs &w : g_stream_ws) {
-    if (w.dev != dev || w.st != st) continue;
-    if (w.bytes < bytes) {
-      (void)hipStreamSynchronize(st);  // the old buffer may still be in use on st
-      (void)hipFree(w.p);
-      w.p = nullptr;
-      w.bytes = 0;
-      if (hipMalloc(&w.p, bytes) != hipSuccess)
-        return fail(GQ_ENOMEM, "workspace of %zu bytes: hipMalloc failed", bytes);
-      w.bytes = bytes;
-    }
-    *out = w.p;
+  StreamWs *ws = nullptr;
+  for (StreamWs &w : g_stream_ws)
+    if (w.dev == dev && w.st == st) ws = &w;
+  if (ws && ws->bytes >= bytes) {
+    *out = ws->p;
     return GQ_OK;
   }
+  if (stream_capturing(st))
+    return fail(GQ_EINVAL,
+                "stream workspace of %zu bytes needed under graph capture (the stream holds %zu): "
+                "make one call of at least this size on the stream before capturing",
+                bytes, ws ? ws->bytes : (size_t)0);
   void *p = nullptr;
   if (hipMalloc(&p, bytes) != hipSuccess)
     return fail(GQ_ENOMEM, "workspace of %zu bytes: hipMalloc failed", bytes);
-  g_stream_ws.push_back(StreamWs{dev, st, p, bytes});
+  if (ws) {
+    g_retired_ws.push_back(ws->p);
+    ws->p = p;
+    ws->bytes = bytes;
+  } else {
+    g_stream_ws.push_back(StreamWs{dev, st, p, bytes});
+  }
   *out = p;
   return GQ_OK;
 }
@@ -632,6 +646,10 @@ static int gq_ensure_gemm_records(const gq_weight *w, hipStream_t stream) {
   if (w->gemm_raw) return GQ_OK;
   std::lock_guard<std::mutex> lk(g_mu);
   if (w->gemm_raw) return GQ_OK;
+  if (stream_capturing(stream))
+    return fail(GQ_EINVAL,
+                "gq_gemm: the first call on a weight builds its GEMM records and must not be "
+                "made under graph capture");
   uint8_t *rec = nullptr;
   const size_t bytes = gq::gemm_records_bytes(w->L);
   if (hipMalloc(&rec, bytes) != hipSuccess)
@@ -961,7 +979,8 @@ int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float 
       return fail(GQ_EINVAL, "token %d out of range", tokens_host[i]);
   hipStream_t s = (hipStream_t)stream;
   auto &L = m->L;
-  if (L.kv_q8) return fail(GQ_EINVAL, "prefill supports the F16 KV cache only");
+  if (L.kv_q8 && (L.n_kv_heads * L.head_dim) % 32)
+    return fail(GQ_EINVAL, "a Q8_0 KV cache needs kv_dim a multiple of 32");
   if (L.hidden % 8 || L.hidden > 8 * 256 * 4 || L.ffn % 8 || (L.n_heads * L.head_dim) % 8)
     return fail(GQ_EINVAL, "prefill needs hidden <= 8192 and hidden, ffn multiples of 8");
   for (int l = 0; l < L.n_layers; l++) {
@@ -987,6 +1006,8 @@ int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float 
     if (!rc) rc = dalloc(m, &m->pf.part, std::max<size_t>(1, gq::prefill_part_floats(L, gq::PREFILL_MAX, g_dev.num_cus)));
     if (!rc) rc = dalloc(m, &m->pf.xb, (size_t)gq::GEMM_NPAD * kmax);
     if (!rc) rc = dalloc(m, &m->pf.tokens, np);
+    if (!rc && L.kv_q8) rc = dalloc(m, &m->pf.kf, (size_t)L.ctx * kvd);
+    if (!rc && L.kv_q8) rc = dalloc(m, &m->pf.vf, (size_t)L.ctx * kvd);
     if (rc) { m->pf.x = nullptr; return rc; }
   }
   for (int off = 0; off < n; off += gq::PREFILL_MAX) {

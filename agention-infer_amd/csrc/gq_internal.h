@@ -163,6 +163,7 @@ struct PrefillBufs {
   float *part;     // GEMM K-split partials (prefill_part_floats)
   uint16_t *xb;    // GEMM X fragments [512][max(hidden, ffn, q_dim) rounded to 256] bf16
   int *tokens;     // [PREFILL_MAX]
+  uint16_t *kf, *vf;  // Q8_0 KV cache: one layer's rows unpacked to f16 [ctx][kv_dim]
 };
 size_t prefill_part_floats(const DecodeLaunch &m, int nmax, int num_cus);
 hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int *tokens_dev, int n,

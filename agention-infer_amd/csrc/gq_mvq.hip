@@ -847,6 +847,8 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
     return e && atoi(e) > 0 ? atoi(e) : 1;
   }();
   a.blocks = std::max(1, std::min(G, num_cus * bpc));
+  // The fused argmax writes one partial per block into ARGMAX_SLOTS slots.
+  if (a.in.amax_v) a.blocks = std::min(a.blocks, ARGMAX_SLOTS);
   const int fmt = a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt;
   const int ngb = (G + a.blocks - 1) / a.blocks, T = (a.units + 3) / 4;
   return qsmem_layout(aux_per_unit(fmt), a.units, ngb * nt * T * QROWS, nullptr, nullptr);
@@ -927,6 +929,7 @@ hipError_t launch_mvq_moe(const MoeArgs &a, int T, int stage, bool route, hipStr
 
 hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {
   if (lds + mvq_static_lds(a.fmt) > 160 * 1024) return hipErrorInvalidValue;
+  if (a.in.amax_v && a.blocks > ARGMAX_SLOTS) return hipErrorInvalidValue;
   switch (a.fmt) {
   case T_Q4_K: return mvq_launch_f<T_Q4_K>(a, lds, st);
   case T_Q5_K: return a.in.q8k && !a.pair ? mvq_launch_f<T_Q5_K8>(a, lds, st) : mvq_launch_f<T_Q5_K>(a, lds, st);

@@ -185,6 +185,69 @@ __global__ __launch_bounds__(256) void k_rope_kv(float *q, float *k, const float
   }
 }
 
+// The same for the Q8_0 KV cache (KvDtype::Q8_0, src/model/mod.rs:574-583):
+// the rotated k and v rows packed per 32 values exactly as the decode step
+// packs them (scale = max|x| / 127 stored as f16, 1 for an all-zero block;
+// codes = round(x / scale) clamped to [-127, 127]) into the int8 codes
+// kc / vc [ctx][kvd] and the f16 scales ksc / vsc [ctx][kvd / 32].  32
+// consecutive threads hold one block (kvd is a multiple of 32).
+__global__ __launch_bounds__(256) void k_rope_kv_q8(float *q, float *k, const float *v, int8_t *kc,
+                                                    int8_t *vc, uint16_t *ksc, uint16_t *vsc, int pos0,
+                                                    int nh, int nkv, int hd, const float *rope_den) {
+  __shared__ float sn[64], cs[64];
+  const int t = blockIdx.x, pos = pos0 + t, half = hd / 2, kvd = nkv * hd;
+  for (int i = threadIdx.x; i < half; i += 256) {
+    float s, c;
+    sincosf((float)pos / rope_den[i], &s, &c);
+    sn[i] = s;
+    cs[i] = c;
+  }
+  __syncthreads();
+  for (int o = threadIdx.x; o < (nh + nkv) * half; o += 256) {
+    const int hh = o / half, i = o % half;
+    float *p = hh < nh ? q + (long)t * nh * hd + (long)hh * hd : k + (long)t * kvd + (long)(hh - nh) * hd;
+    const float x0 = p[i], x1 = p[i + half];
+    p[i] = x0 * cs[i] - x1 * sn[i];
+    p[i + half] = x0 * sn[i] + x1 * cs[i];
+  }
+  __syncthreads();
+  const int nbr = kvd / 32;
+  for (int o0 = 0; o0 < kvd; o0 += 256) {  // (uniform trip count: the shuffles see whole blocks)
+    const int o = o0 + (int)threadIdx.x;
+    const bool live = o < kvd;
+    const float kv = live ? k[(long)t * kvd + o] : 0.f, vv = live ? v[(long)t * kvd + o] : 0.f;
+    float km = fabsf(kv), vm = fabsf(vv);
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) {
+      km = fmaxf(km, __shfl_xor(km, off, 32));
+      vm = fmaxf(vm, __shfl_xor(vm, off, 32));
+    }
+    const float kscale = km > 0.f ? km / 127.0f : 1.0f, vscale = vm > 0.f ? vm / 127.0f : 1.0f;
+    if (live) {
+      kc[(long)pos * kvd + o] = (int8_t)fminf(fmaxf(roundf(kv / kscale), -127.f), 127.f);
+      vc[(long)pos * kvd + o] = (int8_t)fminf(fmaxf(roundf(vv / vscale), -127.f), 127.f);
+      if ((o & 31) == 0) {
+        ksc[(long)pos * nbr + o / 32] = __half_as_ushort(__float2half_rn(kscale));
+        vsc[(long)pos * nbr + o / 32] = __half_as_ushort(__float2half_rn(vscale));
+      }
+    }
+  }
+}
+
+// KvDtype::Q8_0::unpack (src/model/mod.rs:595-602) of rows [0, npos) of one
+// layer, code * f16 scale in fp32, rounded to f16 for the prefill
+// attention's f16 operands: kf / vf [npos][kvd].
+__global__ __launch_bounds__(256) void k_kv_q8_to_f16(const int8_t *kc, const int8_t *vc,
+                                                      const uint16_t *ksc, const uint16_t *vsc,
+                                                      long total, int kvd, uint16_t *kf, uint16_t *vf) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= total) return;
+  const long row = i / kvd, b = (i % kvd) / 32;
+  const long sb = row * (kvd / 32) + b;
+  kf[i] = __half_as_ushort(__float2half_rn((float)kc[i] * __half2float(__ushort_as_half(ksc[sb]))));
+  vf[i] = __half_as_ushort(__float2half_rn((float)vc[i] * __half2float(__ushort_as_half(vsc[sb]))));
+}
+
 // Max / sum of x over the 4 lane groups (lanes 16 apart) of a wave, the
 // same value in every lane (gfx950 lane swaps; each combination is
 // symmetric, so every lane computes the identical bits).
@@ -552,9 +615,26 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
         }
       if ((e = launch_gemm_bf16(grp, gout, c, b.xb, n, b.part, false, num_cus, s)) != hipSuccess) return e;
     }
-    uint16_t *kc = m.kcache + (long)L * m.ctx * kvd, *vc = m.vcache + (long)L * m.ctx * kvd;
-    hipLaunchKernelGGL(k_rope_kv, dim3(n), dim3(256), 0, s, b.q, b.k, b.v, kc, vc, pos0, nh, nkv, hd,
-                       m.rope_den);
+    uint16_t *kc, *vc;  // the f16 K/V rows the attention reads
+    if (m.kv_q8) {
+      // pack the new rows into the Q8_0 cache, then attend over the
+      // unpacked rows of every position, the new ones included (run_batch
+      // writes the cache and reads it back, cpu_path.rs:904-906)
+      int8_t *kq = (int8_t *)m.kcache + (long)L * m.ctx * kvd, *vq = (int8_t *)m.vcache + (long)L * m.ctx * kvd;
+      uint16_t *ks = m.kscale + (long)L * m.ctx * (kvd / 32), *vs = m.vscale + (long)L * m.ctx * (kvd / 32);
+      hipLaunchKernelGGL(k_rope_kv_q8, dim3(n), dim3(256), 0, s, b.q, b.k, b.v, kq, vq, ks, vs, pos0,
+                         nh, nkv, hd, m.rope_den);
+      const long total = (long)(pos0 + n) * kvd;
+      hipLaunchKernelGGL(k_kv_q8_to_f16, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, kq, vq,
+                         ks, vs, total, kvd, b.kf, b.vf);
+      kc = b.kf;
+      vc = b.vf;
+    } else {
+      kc = m.kcache + (long)L * m.ctx * kvd;
+      vc = m.vcache + (long)L * m.ctx * kvd;
+      hipLaunchKernelGGL(k_rope_kv, dim3(n), dim3(256), 0, s, b.q, b.k, b.v, kc, vc, pos0, nh, nkv, hd,
+                         m.rope_den);
+    }
     const int items = (n + PF_Q - 1) / PF_Q * nkv;  // (query tile, KV head)
     const dim3 ag(8 * group * ((items + 7) / 8));
     if (hd == 128)

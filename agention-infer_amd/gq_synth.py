@@ -45,8 +45,14 @@ def pack_scale_min_k4(sc, m):
     return out
 
 
-def make_blocks(dtype, rows, in_dim, seed=0, zero=False):
-    """Return a uint8 array [rows, type_size(in_dim)] in ggml block order."""
+def make_blocks(dtype, rows, in_dim, seed=0, zero=False, centered=False):
+    """Return a uint8 array [rows, type_size(in_dim)] in ggml block order.
+
+    centered=True (Q4_K only) draws the same d, scales and quants but sets
+    dmin = f16(7.5 d) and every min equal to its scale, so each element is
+    d*sc*(q - 7.5) up to the f16 rounding of dmin: zero-mean rows, as in a
+    trained model, instead of the per-block positive bias of independent
+    mins."""
     nb = (in_dim + BLOCK_ELEMS[dtype] - 1) // BLOCK_ELEMS[dtype]
     bb = BLOCK_BYTES[dtype]
     if zero:
@@ -61,6 +67,12 @@ def make_blocks(dtype, rows, in_dim, seed=0, zero=False):
         blk[..., 2:4] = _f16_scale(rng, (rows, nb))[..., None].view(np.uint8)
         sc = rng.integers(0, 64, (rows, nb, 8), dtype=np.uint8)
         m = rng.integers(0, 64, (rows, nb, 8), dtype=np.uint8)
+        if centered:
+            if dtype != Q4_K:
+                raise ValueError("centered blocks are defined for Q4_K only")
+            d = blk[..., 0:2].copy().view(np.float16).astype(np.float32)
+            blk[..., 2:4] = (d * np.float32(7.5)).astype(np.float16).view(np.uint8)
+            m = sc
         blk[..., 4:16] = pack_scale_min_k4(sc, m)
         blk[..., 16:] = rng.integers(0, 256, (rows, nb, bb - 16), dtype=np.uint8)
     elif dtype == Q6_K:
@@ -87,7 +99,7 @@ QWEN25_7B = dict(n_layers=28, hidden=3584, n_heads=28, n_kv_heads=4, head_dim=12
                  down_type=Q6_K, head_type=Q6_K)
 
 
-def make_decoder(cfg, seed=0, embd_scale=1.0):
+def make_decoder(cfg, seed=0, embd_scale=1.0, centered=False):
     """Random-init weights of a dense decoder in ggml block order (the
     Q4_K_M layout of the benchmark: Q4_K attention/gate/up, Q6_K down/head),
     RMSNorm weights ~ N(1, 0.1), f32 embedding ~ N(0, 1) * embd_scale.
@@ -95,20 +107,26 @@ def make_decoder(cfg, seed=0, embd_scale=1.0):
     With the benchmark's block distributions every row carries a large
     per-block bias, so the layer outputs dwarf an N(0, 1) embedding and the
     greedy token stops depending on the input token; tests raise
-    embd_scale to keep the token path live."""
+    embd_scale to keep the token path live.  centered=True draws the Q4_K
+    tensors zero-mean (make_blocks), so that every layer's attention and
+    FFN output stays a visible part of the residual stream."""
     rng = np.random.default_rng(seed)
     L, H, F = cfg["n_layers"], cfg["hidden"], cfg["ffn"]
     qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
     w = {k: [] for k in ("wq", "wk", "wv", "wo", "wgate", "wup", "wdown", "attn_norm", "ffn_norm")}
     s = seed * 1000
+
+    def cq(kind):
+        return centered and cfg[kind] == Q4_K
+
     for l in range(L):
         s += 10
-        w["wq"].append(make_blocks(cfg["attn_type"], qd, H, seed=s + 1))
-        w["wk"].append(make_blocks(cfg["attn_type"], kvd, H, seed=s + 2))
-        w["wv"].append(make_blocks(cfg["attn_type"], kvd, H, seed=s + 3))
-        w["wo"].append(make_blocks(cfg["attn_type"], H, qd, seed=s + 4))
-        w["wgate"].append(make_blocks(cfg["gate_up_type"], F, H, seed=s + 5))
-        w["wup"].append(make_blocks(cfg["gate_up_type"], F, H, seed=s + 6))
+        w["wq"].append(make_blocks(cfg["attn_type"], qd, H, seed=s + 1, centered=cq("attn_type")))
+        w["wk"].append(make_blocks(cfg["attn_type"], kvd, H, seed=s + 2, centered=cq("attn_type")))
+        w["wv"].append(make_blocks(cfg["attn_type"], kvd, H, seed=s + 3, centered=cq("attn_type")))
+        w["wo"].append(make_blocks(cfg["attn_type"], H, qd, seed=s + 4, centered=cq("attn_type")))
+        w["wgate"].append(make_blocks(cfg["gate_up_type"], F, H, seed=s + 5, centered=cq("gate_up_type")))
+        w["wup"].append(make_blocks(cfg["gate_up_type"], F, H, seed=s + 6, centered=cq("gate_up_type")))
         w["wdown"].append(make_blocks(cfg["down_type"], H, F, seed=s + 7))
         w["attn_norm"].append((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))
         w["ffn_norm"].append((1.0 + 0.1 * rng.standard_normal(H)).astype(np.float32))

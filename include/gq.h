@@ -85,7 +85,9 @@ int gq_matvec(const gq_weight *w, const float *x_dev, float *y_dev, void *stream
 
 /* matmul_dequant_qkv / _multi / _ffn (src/ops/wgpu_backend/mod.rs:702-854):
  * several weights sharing one input, one launch.  All weights must have
- * the same in_dim; y_dev[i] receives out_dim(w[i]) floats. */
+ * the same in_dim; y_dev[i] receives out_dim(w[i]) floats.  The arithmetic
+ * is gq_matvec's per weight: Q5_K weights take matmul_into's Q8_K route
+ * (mod.rs:381-394), unlike the wgpu kernels' float dequant-dot. */
 int gq_matvec_multi(const gq_weight *const *w, int count, const float *x_dev,
                     float *const *y_dev, void *stream);
 
@@ -112,8 +114,13 @@ int gq_dequant_rows_host(const gq_weight *w, int row0, int nrows, float *out_hos
  * prefill path of WeightMap::matmul_batch_into (src/model/mod.rs:414-464):
  * X_dev [n][in_dim] fp32 token-major -> Y_dev [n][out_dim] fp32.
  * mode GQ_GEMM_BF16 (Q4_K or Q6_K weights) or GQ_GEMM_INT8 (Q4_K weights).
- * The first bf16 call on a weight builds its GEMM copy (per-stage records)
- * and synchronizes the stream once. */
+ * The first call on a weight builds its GEMM copy (per-stage records) and
+ * synchronizes the stream once.  The packed-X workspace is the stream's own
+ * (as gq_moe_ffn's).  Under HIP graph capture a call is accepted only if
+ * that first call was made before and the stream's workspace already holds
+ * the call's bytes; otherwise it fails with GQ_EINVAL and records nothing.
+ * Workspaces are never freed while the process runs, so a captured graph
+ * stays valid when later, larger calls grow the stream's workspace. */
 int gq_gemm(const gq_weight *w, const float *X_dev, int n, float *Y_dev, int mode, void *stream);
 
 /* Per-32 Q8 activation pack used by GQ_GEMM_INT8, identical to
@@ -150,13 +157,17 @@ int gq_upload_experts(int dtype, const void *w_host, size_t nbytes, int in_dim,
  *                  weights are the full-softmax probabilities),
  *   out[t] = sum_s w[t][s] * down_e(silu(gate_e x_t) * up_e x_t),
  * SwiGLU as ffn_gate_up (src/model/llama/cpu_path.rs:200-232); each expert
- * matvec is matmul_into's (src/model/mod.rs:362-403: Q5_K via Q8_K).  gate/up:
+ * matvec is matmul_into's (src/model/mod.rs:362-403): for Q5_K experts the
+ * gate, up and down matvecs all take the Q8_K route (quantize_row_q8_k of
+ * the input, dot_q5_k_q8k), not ffn_gate_up's float dot_row.  The
+ * reference has no MoE, so that choice is not pinned to a reference output.  gate/up:
  * [n_experts][f][h], down: [n_experts][h][f], uploaded with
  * gq_upload_experts.  logits_dev [T][n_experts], x_dev/out_dev [T][h];
  * ids_dev/w_dev ([T][top_k]) receive the routing if non-NULL; top_k <= 64.
  * The workspace (T * top_k * (4 * f + 8) + 1024 bytes) is the stream's own,
  * allocated on first use and grown on demand, shared with gq_gemm's calls
- * on that stream and held until the process ends. */
+ * on that stream and held until the process ends; under graph capture it
+ * cannot grow (GQ_EINVAL; see gq_gemm, or use gq_moe_ffn_noalloc). */
 int gq_moe_ffn(const gq_weight *gate, const gq_weight *up, const gq_weight *down, int n_experts,
                const float *logits_dev, int T, int top_k, const float *x_dev, float *out_dev,
                int *ids_dev, float *w_dev, void *stream);

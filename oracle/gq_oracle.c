@@ -957,7 +957,9 @@ int gqo_decode_step(const gqo_model *m, int token, int pos, float *logits, int n
         rc |= gqo_matmul_into(td, m->wdown[L], gqo_type_size(td, F) * H, act, F, proj, H, nthreads);
         for (int i = 0; i < H; i++) x[i] += proj[i];
     }
-    if (!rc) {
+    /* logits == NULL: a prompt position whose logits nobody reads (the
+     * batch path's non-final rows); the head is skipped. */
+    if (!rc && logits) {
         rms_norm(x, m->output_norm, H, m->eps, xn);
         rc = gqo_matmul_into(m->head_type, m->lm_head, gqo_type_size(m->head_type, H) * m->vocab,
                              xn, H, logits, m->vocab, nthreads);

@@ -270,7 +270,12 @@ class DecoderModel:
         m.vcache = ptr_array([self.vc[l] for l in range(L)])
         self.m = m
 
-    def step(self, token, pos, nthreads=0):
+    def step(self, token, pos, nthreads=0, want_logits=True):
+        """One decode step; want_logits=False skips the output head (the
+        KV rows are still written) and returns None."""
+        if not want_logits:
+            _chk(lib().gqo_decode_step(ctypes.byref(self.m), token, pos, None, nthreads))
+            return None
         logits = np.zeros(self.cfg["vocab"], np.float32)
         _chk(lib().gqo_decode_step(ctypes.byref(self.m), token, pos, _p(logits), nthreads))
         return logits

@@ -144,3 +144,50 @@ def test_gemm_errors_and_edges(backend):
         y = z.launch_only_batch(torch.randn((3, 512), device="cuda"), mode=mode)
         torch.cuda.synchronize()
         assert torch.all(y == 0)
+
+
+def test_gemm_capture_survives_workspace_growth(backend):
+    """A HIP graph captured around gq_gemm keeps its workspace: a later,
+    larger call on the same stream grows the stream's workspace without
+    freeing the captured one, and every replay (with eager work between)
+    reproduces the eager result.  Under capture, growing the workspace and
+    the first call on a weight (which builds its GEMM records) fail with
+    GqError instead of allocating."""
+    import torch
+    import gq
+    rows, k = 1024, 3584
+    w = syn.make_blocks(Q4_K, rows, k, seed=61)
+    h = backend.upload_weight(Q4_K, w, k, rows)
+    h_new = backend.upload_weight(Q4_K, syn.make_blocks(Q4_K, 256, k, seed=64), k, 256)
+    s = torch.cuda.Stream()
+    Xs = torch.from_numpy(syn.make_x(k, seed=62, batch=64)).cuda()
+    Xl = torch.from_numpy(syn.make_x(k, seed=63, batch=512)).cuda()
+    Ys = torch.zeros((64, rows), device="cuda")
+    Yl = torch.zeros((512, rows), device="cuda")
+    Yn = torch.zeros((64, 256), device="cuda")
+    torch.cuda.synchronize()
+    h.launch_only_batch(Xs, Y_dev=Ys, stream=s.cuda_stream)
+    s.synchronize()
+    ref = Ys.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        h.launch_only_batch(Xs, Y_dev=Ys, stream=s.cuda_stream)
+    for bad, Xb, Yb in ((h, Xl, Yl), (h_new, Xs, Yn)):
+        g_bad = torch.cuda.CUDAGraph()
+        with pytest.raises(gq.GqError, match="capture"):
+            with torch.cuda.graph(g_bad, stream=s):
+                bad.launch_only_batch(Xb, Y_dev=Yb, stream=s.cuda_stream)
+        torch.cuda.synchronize()
+    # the larger call grows the workspace (eager)
+    h.launch_only_batch(Xl, Y_dev=Yl, stream=s.cuda_stream)
+    s.synchronize()
+    ref_l = Yl.clone()
+    for i in range(3):
+        Ys.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(Ys, ref), f"replay {i}"
+        h.launch_only_batch(Xl, Y_dev=Yl, stream=s.cuda_stream)
+        s.synchronize()
+        assert torch.equal(Yl, ref_l)

@@ -92,6 +92,15 @@ def test_moe_errors(backend):
     hq = backend.upload_experts(12, syn.make_blocks(12, 4 * 256, 256, seed=2), 256, 256, 4)
     with pytest.raises(gq.GqError):
         backend.moe_ffn(hq, hu, hd, 4, lg, x, 2)       # mixed dtypes
+    # top_k <= 64 even when there are more experts
+    g2, u2, d2 = make(66, 256, 256, seed=3)
+    hg2 = backend.upload_experts(IQ3, g2, 256, 256, 66)
+    hu2 = backend.upload_experts(IQ3, u2, 256, 256, 66)
+    hd2 = backend.upload_experts(IQ3, d2, 256, 256, 66)
+    lg2 = torch.zeros((2, 66), device="cuda")
+    backend.moe_ffn(hg2, hu2, hd2, 66, lg2, x, 8)
+    with pytest.raises(gq.GqError, match="top_k=65"):
+        backend.moe_ffn(hg2, hu2, hd2, 66, lg2, x, 65)
 
 
 def test_moe_routing_ties(backend, orc):

@@ -173,3 +173,56 @@ def test_prefill_next_token_skips_nan(backend):
         gm2.decode(int(t), pos, want_logits=False)
     nxt2, lg2 = gm2.decode(int(toks[-1]), len(toks) - 1)
     assert np.isnan(lg2[0]) and nxt2 == oracle.argmax(lg2)
+
+
+@pytest.mark.parametrize("cfg_name,n_ctx,n", [("SMALL", 100, 64), ("HD128", 70, 130)])
+def test_prefill_q8_0_kv(backend, cfg_name, n_ctx, n):
+    """Prefill into a Q8_0 KV cache (KvDtype::Q8_0, src/model/mod.rs:536-603):
+    run_batch writes each prompt row packed and attends over the unpacked
+    rows (cpu_path.rs:904-906).  Against the oracle stepping the prompt over
+    its own Q8_0 cache: logits to TOL_FP32, the unpacked prompt rows to the
+    bf16-operand bound (row max|err| of the row's max|value|), the uploaded
+    rows untouched (the bound is a few code steps, 1/127 of the row's max
+    each: the bf16 operands move values across the codes' rounding
+    boundaries), every packed block with a nonzero scale holding a code
+    of magnitude 127 (the pack's scale is f16(max|x| / 127)).  Then the
+    oracle takes the GPU's rows and both decode greedily: same tokens."""
+    import gq
+    cfg = dict({"SMALL": SMALL, "HD128": HD128}[cfg_name], kv_dtype="q8_0")
+    w = syn.make_decoder(cfg, 51 + n, embd_scale=1e4)
+    L, kvd = cfg["n_layers"], cfg["n_kv_heads"] * cfg["head_dim"]
+    rng = np.random.default_rng(n)
+    kv = [np.stack([np.stack([npref.pack_q8_0_rows(rng.standard_normal(kvd).astype(np.float32))
+                              for _ in range(n_ctx)]) for _ in range(L)]) for _ in range(2)]
+    hw = syn.upload_decoder(backend, cfg, w)
+    gm = gq.DecodeModel(dict(cfg, max_tokens=64), hw)
+    for l in range(L):
+        gm.kv_upload(l, kv[0][l], kv[1][l])
+    om = oracle.DecoderModel(cfg, w, kv, kv_dtype="q8_0")
+    toks = np.random.default_rng(n + 1).integers(0, cfg["vocab"], n).astype(np.int32)
+    nxt, got = gm.prefill(toks, n_ctx)
+    for i, t in enumerate(toks):
+        ref = om.step(int(t), n_ctx + i)
+    err = float(np.abs(got - ref).max())
+    say(f"q8_0 prefill {cfg_name}: logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
+    assert err <= TOL_FP32 * float(np.abs(ref).max())
+    for l in range(L):
+        k, v = gm.kv_download(l, n_ctx + n)
+        np.testing.assert_array_equal(k[:n_ctx], kv[0][l])
+        np.testing.assert_array_equal(v[:n_ctx], kv[1][l])
+        for nm, got_rows, ref_rows in (("K", k, om.kc[l]), ("V", v, om.vc[l])):
+            blk = got_rows[n_ctx:].reshape(n, -1, 34)
+            codes = blk[:, :, 2:].view(np.int8).astype(np.int32)
+            scale = blk[:, :, 0].astype(np.uint16) | (blk[:, :, 1].astype(np.uint16) << 8)
+            assert np.all(np.abs(codes).max(axis=2)[scale != 0x3C00] == 127), (nm, l)
+            g = npref.unpack_q8_0_rows(got_rows[n_ctx:])
+            r = npref.unpack_q8_0_rows(ref_rows[n_ctx:n_ctx + n])
+            rel = np.abs(g - r).max(axis=1) / np.abs(r).max(axis=1)
+            say(f"  layer {l} {nm} worst row {rel.max():.3g} median {np.median(rel):.3g}")
+            assert rel.max() <= 5e-2 and np.median(rel) <= 2e-2
+            ref_rows[n_ctx:n_ctx + n] = got_rows[n_ctx:]
+    exp, tok = [], nxt
+    for i in range(12):
+        tok = oracle.argmax(om.step(tok, n_ctx + n + i))
+        exp.append(tok)
+    np.testing.assert_array_equal(gm.generate(nxt, n_ctx + n, 12), np.array(exp, np.int32))
