@@ -986,8 +986,9 @@ int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float 
   for (int l = 0; l < L.n_layers; l++) {
     const gq_weight *ws[7] = {L.wq[l], L.wk[l], L.wv[l], L.wo[l], L.wgate[l], L.wup[l], L.wdown[l]};
     for (const gq_weight *w : ws) {
-      if (w->L.dtype != gq::T_Q4_K && w->L.dtype != gq::T_Q6_K)
-        return fail(GQ_EDTYPE, "layer %d: prefill needs Q4_K or Q6_K projection weights, not %s", l,
+      if (w->L.dtype != gq::T_Q4_K && w->L.dtype != gq::T_Q6_K && w->L.dtype != gq::T_Q5_K &&
+          w->L.dtype != gq::T_Q8_0)
+        return fail(GQ_EDTYPE, "layer %d: prefill needs Q4_K, Q5_K, Q6_K or Q8_0 projection weights, not %s", l,
                     type_name(w->L.dtype));
       int rc = gq_ensure_gemm_records(w, s);
       if (rc) return rc;

@@ -236,17 +236,33 @@ __device__ __forceinline__ uint32_t pack_bf16(float a, float b) {
 //                groups, then d (f16); chunks 1-2 = the low 4 bits of the
 //                6-bit codes in the same nibble order as Q4_K; chunk 3 = the
 //                high 2 bits, dword g (16-element group g) holding element
-//                16 g + i at bits 2i, 2i + 1.
+//                16 g + i at bits 2i, 2i + 1;
+//   Q5_K (64 B): chunk 0 = the unit's 16-byte header (as Q4_K); chunks
+//                1-2 = the group's 32 quant bytes (as Q4_K); chunk 3 = the
+//                fifth bits, dword 2 h + qq holding element 32 h + 16 qq + i
+//                at bit i;
+//   Q8_0 (80 B): chunk 0 = the f16 d of the stage's two 32-element blocks;
+//                chunks 1-4 = the 64 int8 codes.
 template <int FMT> struct GemmFmt;
 template <> struct GemmFmt<T_Q4_K> { static constexpr int C = 3; };
 template <> struct GemmFmt<T_Q6_K> { static constexpr int C = 4; };
+template <> struct GemmFmt<T_Q5_K> { static constexpr int C = 4; };
+template <> struct GemmFmt<T_Q8_0> { static constexpr int C = 5; };
 // Bytes of the copy per unit (4 stages) of a row.
-__host__ __device__ constexpr int gemm_unit_bytes(int fmt) { return fmt == T_Q6_K ? 256 : 144; }
+__host__ __device__ constexpr int gemm_unit_bytes(int fmt) {
+  return fmt == T_Q4_K ? 144 : fmt == T_Q8_0 ? 320 : 256;
+}
 // Offset of chunk c of stage s within a row of the copy.
 template <int FMT>
 __device__ __forceinline__ long gemm_chunk_off(int s, int c) {
-  if constexpr (FMT == T_Q6_K) return (long)s * 64 + 16 * c;
-  else return (long)(s >> 2) * 144 + (c == 0 ? 0 : 16 + 32 * (s & 3) + 16 * (c - 1));
+  if constexpr (FMT == T_Q4_K) return (long)(s >> 2) * 144 + (c == 0 ? 0 : 16 + 32 * (s & 3) + 16 * (c - 1));
+  else return (long)s * (16 * GemmFmt<FMT>::C) + 16 * c;
+}
+// The chunk of a stage record holding the quant bytes of dequant task
+// (half h, quarter qq).
+template <int FMT>
+__host__ __device__ constexpr int gemm_qs_chunk(int h, int qq) {
+  return FMT == T_Q8_0 ? 1 + 2 * h + qq : 1 + qq;
 }
 
 // Record of stage j (0..3) of one unit from the unit's ggml bytes u[] (Q6_K:
@@ -281,7 +297,7 @@ __global__ void k_gemm_records(Layout L, const uint8_t *body, const uint16_t *dd
   if (L.dtype == T_Q4_K) {
     for (int c = 0; c < 9; c++)
       *(uint4 *)(dst + 16 * c) = *(const uint4 *)(body + chunk_offset(L, t, j, c));
-  } else {
+  } else if (L.dtype == T_Q6_K) {
     uint8_t ub[210];
     for (int c = 0; c < 13; c++) {
       const uint4 v = *(const uint4 *)(body + chunk_offset(L, t, j, c));
@@ -297,6 +313,39 @@ __global__ void k_gemm_records(Layout L, const uint8_t *body, const uint16_t *dd
         uint4 v;
         __builtin_memcpy(&v, rb + 16 * q, 16);
         *(uint4 *)(dst + 64 * s + 16 * q) = v;
+      }
+    }
+  } else {
+    // Q5_K (the 176 B block) or Q8_0 (8 x 32 codes, then the 8 f16 d)
+    const int nc = L.dtype == T_Q5_K ? 11 : 17;
+    uint8_t ub[272];
+    for (int c = 0; c < nc; c++) {
+      const uint4 v = *(const uint4 *)(body + chunk_offset(L, t, j, c));
+      __builtin_memcpy(ub + 16 * c, &v, 16);
+    }
+    for (int s = 0; s < 4; s++) {
+      uint8_t rb[80];
+      for (int i = 0; i < 80; i++) rb[i] = 0;
+      if (L.dtype == T_Q5_K) {
+        for (int i = 0; i < 16; i++) rb[i] = ub[i];
+        for (int i = 0; i < 32; i++) rb[16 + i] = ub[48 + 32 * s + i];
+        for (int h = 0; h < 2; h++)
+          for (int l = 0; l < 32; l++)  // element 32 h + l of the stage: qh[l] bit 2 s + h
+            rb[48 + 4 * (2 * h + (l >> 4)) + ((l & 15) >> 3)] |=
+                (uint8_t)(((ub[16 + l] >> (2 * s + h)) & 1) << (l & 7));
+        for (int q = 0; q < 4; q++) {
+          uint4 v;
+          __builtin_memcpy(&v, rb + 16 * q, 16);
+          *(uint4 *)(dst + 64 * s + 16 * q) = v;
+        }
+      } else {
+        for (int i = 0; i < 4; i++) rb[i] = ub[256 + 4 * s + i];  // d of blocks 2 s, 2 s + 1
+        for (int i = 0; i < 64; i++) rb[16 + i] = ub[64 * s + i];
+        for (int q = 0; q < 5; q++) {
+          uint4 v;
+          __builtin_memcpy(&v, rb + 16 * q, 16);
+          *(uint4 *)(dst + 80 * s + 16 * q) = v;
+        }
       }
     }
   }
@@ -659,12 +708,13 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
 #pragma unroll
         for (int round = 0; round < 3; round++) {
           const int t = min(lane + 64 * round, R::TASKS - 1);
-          const int rr = t >> 2, qq = t & 1;
+          const int rr = t >> 2, h = (t >> 1) & 1, qq = t & 1;
           ad[3 * round] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr);
-          ad[3 * round + 1] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr + 16 + 16 * qq);
+          ad[3 * round + 1] =
+              (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr + 16 * gemm_qs_chunk<FMT>(h, qq));
           ad[3 * round + 2] = (uint32_t)(uintptr_t)(lds_void_t *)(wg + 16 * C * rr + 48);
         }
-        if constexpr (FMT == T_Q4_K) {
+        if constexpr (FMT == T_Q4_K || FMT == T_Q8_0) {
           const uint32_t a6[6] = {ad[0], ad[1], ad[3], ad[4], ad[6], ad[7]};
           uint4 v[6];
           lds_read6(a6, v);
@@ -703,6 +753,31 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
               const uint32_t qv = (qw[i] >> sh) & 0x0F0F0F0Fu;
               o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(qv), nm), fmaf(ds, cvt_ubyte<1>(qv), nm));
               o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(qv), nm), fmaf(ds, cvt_ubyte<3>(qv), nm));
+            }
+          } else if constexpr (FMT == T_Q5_K) {
+            // dequant_q5_k: d * sc * q - dmin * m, q = low nibble | fifth bit << 4
+            uint32_t sc, mn;
+            scale_min_k4_sel(2 * j + h, hd[round].y, hd[round].z, hd[round].w, sc, mn);
+            const float ds = ok ? h2f(hd[round].x) * (float)sc : 0.f;
+            const float nm = ok ? -(h2f(hd[round].x >> 16) * (float)mn) : 0.f;
+            const int g = 2 * h + qq;
+            const uint32_t hw = g == 0 ? qh[round].x : g == 1 ? qh[round].y : g == 2 ? qh[round].z : qh[round].w;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const uint32_t x4 = (hw >> (4 * i)) & 0xFu;
+              const uint32_t hi = (x4 & 1u) | ((x4 & 2u) << 7) | ((x4 & 4u) << 14) | ((x4 & 8u) << 21);
+              const uint32_t qv = ((qw[i] >> sh) & 0x0F0F0F0Fu) | (hi << 4);
+              o[2 * i] = pack_bf16(fmaf(ds, cvt_ubyte<0>(qv), nm), fmaf(ds, cvt_ubyte<1>(qv), nm));
+              o[2 * i + 1] = pack_bf16(fmaf(ds, cvt_ubyte<2>(qv), nm), fmaf(ds, cvt_ubyte<3>(qv), nm));
+            }
+          } else if constexpr (FMT == T_Q8_0) {
+            // dequant_q8_0: d * q, exact in fp32, then bf16
+            const float d = ok ? h2f(h ? hd[round].x >> 16 : hd[round].x) : 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+              const uint32_t w = qw[i];
+              o[2 * i] = pack_bf16(d * (float)(int8_t)(w & 0xFFu), d * (float)(int8_t)((w >> 8) & 0xFFu));
+              o[2 * i + 1] = pack_bf16(d * (float)(int8_t)((w >> 16) & 0xFFu), d * (float)(int8_t)(w >> 24));
             }
           } else {
             // dequant_q6_k: (d * sc) * (q - 32), one rounding: fma(ds, q, -32 ds)
@@ -1169,7 +1244,8 @@ size_t gemm_part_floats(const gq_weight *const *ws, int count, int n, int num_cu
 size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode, int num_cus) {
   const size_t kpad = (size_t)w->L.units * 256;
   if (mode == GQ_GEMM_BF16) {
-    if (w->L.dtype != T_Q4_K && w->L.dtype != T_Q6_K) return (size_t)-1;
+    if (w->L.dtype != T_Q4_K && w->L.dtype != T_Q6_K && w->L.dtype != T_Q5_K && w->L.dtype != T_Q8_0)
+      return (size_t)-1;
     const size_t xb = (size_t)((n + GEMM_NPAD - 1) / GEMM_NPAD * GEMM_NPAD) * kpad * 2;
     return ((xb + 255) & ~(size_t)255) + gemm_part_floats(&w, 1, n, num_cus, false) * 4 + 256;
   }
@@ -1218,7 +1294,11 @@ hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int co
   const long nb = (long)tb * p.ntiles * p.ksplit;
   if (nb > 0x7fffffffL) return hipErrorInvalidValue;
   void (*kern)(GemmArgs);
-  if (p.direct) kern = fmt == T_Q4_K ? k_gemm_bf16_direct<T_Q4_K> : k_gemm_bf16_direct<T_Q6_K>;
+  // Q5_K and Q8_0 run the direct kernel at every batch size (the ring
+  // kernel's LDS has no room for Q8_0's five-chunk records)
+  if (fmt == T_Q5_K) kern = k_gemm_bf16_direct<T_Q5_K>;
+  else if (fmt == T_Q8_0) kern = k_gemm_bf16_direct<T_Q8_0>;
+  else if (p.direct) kern = fmt == T_Q4_K ? k_gemm_bf16_direct<T_Q4_K> : k_gemm_bf16_direct<T_Q6_K>;
   else if (fmt == T_Q4_K) kern = k_gemm_bf16_ring<160, 256, 3, T_Q4_K>;
   else if (fmt == T_Q6_K) kern = k_gemm_bf16_ring<160, 256, 3, T_Q6_K>;
   else return hipErrorInvalidValue;

@@ -36,7 +36,7 @@ extern "C" {
 #define GQ_TYPE_IQ3_XXS 18
 
 /* gq_gemm modes (batched prefill). */
-#define GQ_GEMM_BF16 0  /* Q4_K tiles dequantized to bf16 in LDS, bf16 MFMA */
+#define GQ_GEMM_BF16 0  /* weight tiles dequantized to bf16 in LDS, bf16 MFMA */
 #define GQ_GEMM_INT8 1  /* activations packed per-32 to Q8, int8 MFMA      */
 
 typedef struct gq_weight gq_weight;
@@ -113,7 +113,8 @@ int gq_dequant_rows_host(const gq_weight *w, int row0, int nrows, float *out_hos
 /* launch_only_batch (src/ops/wgpu_backend/resident.rs:76-104) and the
  * prefill path of WeightMap::matmul_batch_into (src/model/mod.rs:414-464):
  * X_dev [n][in_dim] fp32 token-major -> Y_dev [n][out_dim] fp32.
- * mode GQ_GEMM_BF16 (Q4_K or Q6_K weights) or GQ_GEMM_INT8 (Q4_K weights).
+ * mode GQ_GEMM_BF16 (Q4_K, Q5_K, Q6_K or Q8_0 weights; each dequantized as
+ * dequant_row does, then rounded to bf16) or GQ_GEMM_INT8 (Q4_K weights).
  * The first call on a weight builds its GEMM copy (per-stage records) and
  * synchronizes the stream once.  The packed-X workspace is the stream's own
  * (as gq_moe_ffn's).  Under HIP graph capture a call is accepted only if
@@ -226,8 +227,11 @@ int gq_model_decode(gq_model *m, int token, int pos, float *logits_host, int *ne
  * passes of up to 512 tokens; K/V of every position into the cache;
  * logits_host[vocab] (may be NULL) and the greedy next token (may be NULL)
  * of the last position.  Projection GEMMs run in bf16 (weights: bf16 of the
- * exact dequant; activations: bf16), everything else in fp32.  Needs Q4_K or
- * Q6_K projection weights; the first call builds their GEMM copies.
+ * exact dequant; activations: bf16), everything else in fp32.  Needs Q4_K,
+ * Q5_K, Q6_K or Q8_0 projection weights; the first call builds their GEMM
+ * copies.  With a Q8_0 KV cache (KvDtype::Q8_0) the prompt rows are packed
+ * as the decode step packs them and the attention reads every row unpacked
+ * (code * scale), rounded to f16 for its MFMA operands.
  * Synchronous on `stream`. */
 int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float *logits_host,
                      int *next_token, void *stream);

@@ -248,7 +248,7 @@ def bf16(a):
     return r.astype(np.uint32).view(np.float32).astype(np.float64)
 
 
-def prefill_bf16(cfg, w, kc, vc, tokens, pos0):
+def prefill_bf16(cfg, w, kc, vc, tokens, pos0, kv="f16"):
     """Batched prefill (run_batch: every layer over all prompt tokens at
     once) in float64 with the GPU prefill's operand rounding at each
     projection: weights rounded to bf16 from their fp32 dequant, the
@@ -256,6 +256,9 @@ def prefill_bf16(cfg, w, kc, vc, tokens, pos0):
     silu(g) * u) rounded to fp32 and then to bf16.  RoPE, the f16 K/V cache,
     the causal softmax and the residual adds stay float64; the output head
     is unrounded (the GPU runs it on the matvec).  kc / vc are updated.
+    kv="q8_0": kc / vc hold KvDtype::Q8_0 rows ([layer][ctx][kv_dim/32*34]
+    bytes); the new rows are packed from their fp32 values and every row is
+    read back as f16(code * scale), the GPU's attention operands.
     Returns the logits of the last token."""
     H, hd = cfg["hidden"], cfg["head_dim"]
     nh, nkv, F = cfg["n_heads"], cfg["n_kv_heads"], cfg["ffn"]
@@ -288,10 +291,18 @@ def prefill_bf16(cfg, w, kc, vc, tokens, pos0):
         v = xn @ matb(cfg["attn_type"], w["wv"][L], nkv * hd, H).T
         q = rope(q.reshape(n, nh, hd))
         k = rope(k.reshape(n, nkv, hd)).reshape(n, -1)
-        kc[L, pos0:pos0 + n] = k.astype(np.float16).view(np.uint16)
-        vc[L, pos0:pos0 + n] = v.astype(np.float16).view(np.uint16)
-        K = kc[L, :pos0 + n].view(np.float16).astype(np.float64).reshape(pos0 + n, nkv, hd)
-        V = vc[L, :pos0 + n].view(np.float16).astype(np.float64).reshape(pos0 + n, nkv, hd)
+        if kv == "q8_0":
+            for t in range(n):
+                kc[L, pos0 + t] = pack_q8_0_rows(k[t].astype(np.float32))
+                vc[L, pos0 + t] = pack_q8_0_rows(v[t].astype(np.float32))
+            K = unpack_q8_0_rows(kc[L, :pos0 + n]).astype(np.float16).astype(np.float64)
+            V = unpack_q8_0_rows(vc[L, :pos0 + n]).astype(np.float16).astype(np.float64)
+            K, V = K.reshape(pos0 + n, nkv, hd), V.reshape(pos0 + n, nkv, hd)
+        else:
+            kc[L, pos0:pos0 + n] = k.astype(np.float16).view(np.uint16)
+            vc[L, pos0:pos0 + n] = v.astype(np.float16).view(np.uint16)
+            K = kc[L, :pos0 + n].view(np.float16).astype(np.float64).reshape(pos0 + n, nkv, hd)
+            V = vc[L, :pos0 + n].view(np.float16).astype(np.float64).reshape(pos0 + n, nkv, hd)
         att = np.empty((n, nh, hd))
         for h in range(nh):
             s = q[:, h, :] @ K[:, h // group, :].T / np.sqrt(hd)  # [n, pos0 + n]

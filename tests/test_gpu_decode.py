@@ -184,8 +184,9 @@ def _kv_rows_match(gm, om, cfg, lo, hi):
 
 # A layer computed wrongly must show: zeroing any one layer's o- or
 # down-projection moves the step-0 logits by more than LAYER_SENS of their
-# max (the GPU and the oracle agree to LOGIT_TOL = 1e-4).
-LAYER_SENS = 2e-3
+# max (the GPU and the oracle agree to LOGIT_TOL = 1e-4; observed moves are
+# 0.10 - 0.98).
+LAYER_SENS = 5e-2
 
 
 @pytest.mark.timeout(300)

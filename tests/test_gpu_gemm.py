@@ -120,6 +120,39 @@ def test_gemm_full_config(backend, orc):
         sc, q = orc.quantize_q8_32(X[t])
         Xq[t] = q.astype(np.float64) * np.repeat(sc.view(np.float16).astype(np.float64), 32)
     check(Yi, Xq @ Wf.T, "full int8 vs same-operand fp64")
+    # the fp32 CPU path (WeightMap::matmul_batch_into) on 16 of the 512
+    # tokens: the distance is the operands' rounding (bf16 2^-9 each; per-32
+    # Q8 activations 2^-8)
+    sub = np.arange(0, n, n // 16)
+    ref32 = orc.matmul_batch_into(Q4_K, w, X[sub], rows)
+    check(Yb[sub], ref32, "full bf16 vs fp32 CPU path (16 tokens)", tol=1e-2)
+    check(Yi[sub], ref32, "full int8 vs fp32 CPU path (16 tokens)", tol=3e-2)
+
+
+Q8_0, Q5_K = 8, 13
+# Q8_0 and Q5_K (bf16 mode only): token counts on both sides of the ring /
+# direct kernel boundary (both run the direct kernel), a ragged last unit
+# (Q8_0 k = 288), K splits.
+OTHER_SHAPES = [(Q8_0, 331, 512, 37), (Q8_0, 1024, 2048, 300), (Q8_0, 100, 288, 20),
+                (Q8_0, 8192, 2048, 512), (Q5_K, 331, 512, 37), (Q5_K, 512, 3584, 300),
+                (Q5_K, 40, 768, 3)]
+
+
+@pytest.mark.parametrize("dtype,rows,k,n", OTHER_SHAPES)
+def test_gemm_bf16_q8_0_q5k(backend, orc, dtype, rows, k, n):
+    """WeightMap::matmul_batch_into (src/model/mod.rs:414-464) dequantizes
+    every dtype with dequant_row; the bf16 GEMM of Q8_0 and Q5_K weights
+    against the same-operand fp64 product (1e-4) and the fp32 CPU path
+    (1e-2, bf16 operands).  (8192 x 2048 is BASELINE configs[0]'s Q8_0 FFN-up
+    matrix, here over 512 prompt tokens.)"""
+    import gq
+    say(f"gemm bf16 dtype={dtype} rows={rows} k={k} n={n}")
+    w, X, Wf, Y = run(backend, orc, rows, k, n, gq.GQ_GEMM_BF16, seed=rows + 3 * k + dtype, dtype=dtype)
+    ref = bf16_round(X).astype(np.float64) @ bf16_round(Wf).astype(np.float64).T
+    check(Y, ref, f"bf16 dtype {dtype} vs same-operand fp64")
+    sub = np.arange(0, n, max(1, n // 16))
+    ref32 = orc.matmul_batch_into(dtype, w, X[sub], rows)
+    check(Y[sub], ref32, f"bf16 dtype {dtype} vs fp32 CPU path", tol=1e-2)
 
 
 def test_gemm_errors_and_edges(backend):
@@ -129,10 +162,10 @@ def test_gemm_errors_and_edges(backend):
     h = backend.upload_weight(14, w, 256, 4)
     with pytest.raises(gq.GqError, match="not supported"):
         h.launch_only_batch(torch.zeros((2, 256), device="cuda"), mode=gq.GQ_GEMM_INT8)
-    w8 = syn.make_blocks(8, 4, 256, seed=1)  # Q8_0: no GEMM mode
+    w8 = syn.make_blocks(8, 4, 256, seed=1)  # Q8_0: bf16 only
     h8 = backend.upload_weight(8, w8, 256, 4)
     with pytest.raises(gq.GqError, match="not supported"):
-        h8.launch_only_batch(torch.zeros((2, 256), device="cuda"))
+        h8.launch_only_batch(torch.zeros((2, 256), device="cuda"), mode=gq.GQ_GEMM_INT8)
     w4 = syn.make_blocks(Q4_K, 4, 256, seed=1)
     h4 = backend.upload_weight(Q4_K, w4, 256, 4)
     with pytest.raises(gq.GqError, match="mode"):

@@ -35,6 +35,9 @@ SMALL = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=5
 HD128 = dict(SMALL, hidden=512, n_heads=4, n_kv_heads=1, head_dim=128, ffn=768)
 
 TOL_SAME = 2e-3   # vs the same-rounding reference (logits)
+# A Q8_0 KV cache: a rounding tie flips a code, 1/127 of its block's max
+# (16x an f16 ulp), and later layers inherit it.
+TOL_SAME_Q8KV = 1e-2
 KV_SAME = 1e-2    # K/V rows vs the same-rounding reference (worst row), of max|value|
 KV_MEDIAN = 1e-4  # ... and the median row (rounding ties are rare: observed 0)
 TOL_FP32 = 2e-2   # vs the fp32 CPU path (bf16 operands)
@@ -67,23 +70,39 @@ def _f16(a):
     return a.view(np.float16).astype(np.float32)
 
 
-CASES = [("SMALL", 0, 37), ("SMALL", 100, 64), ("HD128", 70, 130), ("SMALL", 5, 600),
-         ("HD128", 0, 300)]
+# Projection-type mixes beyond Q4_K_M: an all-Q8_0 model (the Llama-3.2-1B
+# Q8_0 file type of BASELINE configs[0]) and a Q5_K_M-like one.
+MIXES = {"Q4_K_M": {}, "Q8_0": dict(attn_type=syn.Q8_0, gate_up_type=syn.Q8_0, down_type=syn.Q8_0,
+                                    head_type=syn.Q8_0),
+         "Q5_K_M": dict(attn_type=syn.Q5_K, gate_up_type=syn.Q5_K, down_type=syn.Q6_K)}
 
 
-@pytest.mark.parametrize("cfg_name,n_ctx,n", CASES)
-def test_prefill_same_rounding(backend, cfg_name, n_ctx, n):
+CASES = [("SMALL", 0, 37, "Q4_K_M"), ("SMALL", 100, 64, "Q4_K_M"), ("HD128", 70, 130, "Q4_K_M"),
+         ("SMALL", 5, 600, "Q4_K_M"), ("HD128", 0, 300, "Q4_K_M"), ("SMALL", 100, 64, "Q8_0"),
+         ("SMALL", 5, 600, "Q8_0"), ("HD128", 70, 300, "Q8_0"), ("SMALL", 30, 200, "Q5_K_M"),
+         ("HD128", 0, 130, "Q5_K_M")]
+# Embedding scale of the same-rounding models.  The all-Q8_0 decoders (zero-
+# mean rows, no per-block bias to dominate the residual) are ill-conditioned
+# at an N(0, 1) embedding: a 1e-7 relative change of the embedding moves the
+# same-rounding reference's own logits by 2e-3 to 4e-3 of their max after
+# two layers, so no two roundings agree to TOL_SAME.  A x100 embedding (the
+# token drives the residual) brings that to <= 4e-5.
+MIX_EMBD = {"Q4_K_M": 1.0, "Q5_K_M": 1.0, "Q8_0": 100.0}
+
+
+@pytest.mark.parametrize("cfg_name,n_ctx,n,mix", CASES)
+def test_prefill_same_rounding(backend, cfg_name, n_ctx, n, mix):
     """Logits and every K/V row written against npref.prefill_bf16; the
     rows before the prompt are untouched.  n = 600 takes two passes."""
-    cfg = {"SMALL": SMALL, "HD128": HD128}[cfg_name]
-    say(f"prefill {cfg_name} n_ctx={n_ctx} n={n}")
-    gm, w, kv, kc, vc = _build(backend, cfg, seed=11 + n, n_ctx=n_ctx, attn_scale=ATTN_SCALE)
+    cfg = dict({"SMALL": SMALL, "HD128": HD128}[cfg_name], **MIXES[mix])
+    say(f"prefill {cfg_name} ({mix}) n_ctx={n_ctx} n={n}")
+    gm, w, kv, kc, vc = _build(backend, cfg, seed=11 + n, n_ctx=n_ctx, attn_scale=ATTN_SCALE,
+                               embd_scale=MIX_EMBD[mix])
     toks = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
     nxt, got = gm.prefill(toks, n_ctx)
     ref = npref.prefill_bf16(cfg, w, kc, vc, toks, n_ctx)
     err = float(np.abs(got - ref).max())
     say(f"  logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
-    assert err <= TOL_SAME * float(np.abs(ref).max())
     assert nxt == int(np.argmax(got))
     for l in range(cfg["n_layers"]):
         k, v = gm.kv_download(l, n_ctx + n)
@@ -97,11 +116,16 @@ def test_prefill_same_rounding(backend, cfg_name, n_ctx, n):
             say(f"  layer {l} {nm} max|err| {rows.max():.3g} median {np.median(rows):.3g} of {top:.3g}")
             assert rows.max() <= KV_SAME * top
             assert np.median(rows) <= KV_MEDIAN * top
+    assert err <= TOL_SAME * float(np.abs(ref).max())
 
 
-@pytest.mark.parametrize("cfg_name,n_ctx,n", [("SMALL", 100, 64), ("HD128", 70, 130)])
-def test_prefill_vs_fp32_oracle(backend, cfg_name, n_ctx, n):
-    cfg = {"SMALL": SMALL, "HD128": HD128}[cfg_name]
+# (The all-Q8_0 model is checked against the same-rounding reference only:
+# its zero-mean rows make logits of order 10, and the near-argmax softmax of
+# the unscaled model moves them by percents between any two roundings.)
+@pytest.mark.parametrize("cfg_name,n_ctx,n,mix", [("SMALL", 100, 64, "Q4_K_M"), ("HD128", 70, 130, "Q4_K_M"),
+                                                  ("SMALL", 30, 200, "Q5_K_M"), ("HD128", 0, 130, "Q5_K_M")])
+def test_prefill_vs_fp32_oracle(backend, cfg_name, n_ctx, n, mix):
+    cfg = dict({"SMALL": SMALL, "HD128": HD128}[cfg_name], **MIXES[mix])
     gm, w, kv, _, _ = _build(backend, cfg, seed=11 + n, n_ctx=n_ctx)
     om = oracle.DecoderModel(cfg, w, kv)
     toks = np.random.default_rng(n).integers(0, cfg["vocab"], n).astype(np.int32)
@@ -109,7 +133,7 @@ def test_prefill_vs_fp32_oracle(backend, cfg_name, n_ctx, n):
     for i, t in enumerate(toks):
         ref = om.step(int(t), n_ctx + i)
     err = float(np.abs(got - ref).max())
-    say(f"fp32 path: logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
+    say(f"fp32 path ({mix}): logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
     assert err <= TOL_FP32 * float(np.abs(ref).max())
     top = np.sort(ref)[-2:]
     if top[1] - top[0] > 2 * err:
@@ -146,10 +170,10 @@ def test_prefill_errors(backend):
         gm.prefill(np.zeros(10, np.int32), SMALL["ctx"] - 5)
     with pytest.raises(gq.GqError, match="at least one token"):
         gm.prefill(np.zeros(0, np.int32), 0)
-    q8 = dict(SMALL, attn_type=syn.Q8_0)
-    gq8 = _build(backend, q8, seed=4, n_ctx=0)[0]
-    with pytest.raises(gq.GqError, match="Q4_K or Q6_K"):
-        gq8.prefill(np.zeros(4, np.int32), 0)
+    iq3 = dict(SMALL, gate_up_type=syn.IQ3_XXS)
+    giq = _build(backend, iq3, seed=4, n_ctx=0)[0]
+    with pytest.raises(gq.GqError, match="Q4_K, Q5_K, Q6_K or Q8_0"):
+        giq.prefill(np.zeros(4, np.int32), 0)
 
 
 def test_prefill_next_token_skips_nan(backend):
@@ -175,52 +199,65 @@ def test_prefill_next_token_skips_nan(backend):
     assert np.isnan(lg2[0]) and nxt2 == oracle.argmax(lg2)
 
 
-@pytest.mark.parametrize("cfg_name,n_ctx,n", [("SMALL", 100, 64), ("HD128", 70, 130)])
-def test_prefill_q8_0_kv(backend, cfg_name, n_ctx, n):
+@pytest.mark.parametrize("cfg_name,n_ctx,n,mix", [("SMALL", 100, 64, "Q4_K_M"), ("HD128", 70, 130, "Q4_K_M"),
+                                                  ("SMALL", 5, 600, "Q4_K_M"), ("HD128", 40, 100, "Q8_0")])
+def test_prefill_q8_0_kv(backend, cfg_name, n_ctx, n, mix):
     """Prefill into a Q8_0 KV cache (KvDtype::Q8_0, src/model/mod.rs:536-603):
     run_batch writes each prompt row packed and attends over the unpacked
-    rows (cpu_path.rs:904-906).  Against the oracle stepping the prompt over
-    its own Q8_0 cache: logits to TOL_FP32, the unpacked prompt rows to the
-    bf16-operand bound (row max|err| of the row's max|value|), the uploaded
-    rows untouched (the bound is a few code steps, 1/127 of the row's max
-    each: the bf16 operands move values across the codes' rounding
-    boundaries), every packed block with a nonzero scale holding a code
-    of magnitude 127 (the pack's scale is f16(max|x| / 127)).  Then the
-    oracle takes the GPU's rows and both decode greedily: same tokens."""
+    rows (cpu_path.rs:904-906).  Against npref.prefill_bf16 with the same
+    cache type (the new rows packed from their fp32 values, every row read
+    as f16(code * scale)): logits to TOL_SAME_Q8KV; the packed prompt rows' codes
+    equal but for rounding ties (a value within an fp32 ulp of a code
+    boundary, and what later layers inherit of them: at most 1% of the
+    codes, and the unpacked rows to KV_SAME of the layer's max); the uploaded
+    rows untouched; every block with a nonzero scale holds a code of
+    magnitude 127 (the scale is f16(max|x| / 127)).  Then the oracle
+    (LlamaModel::run with the Q8_0 cache) takes the GPU's rows and both
+    decode greedily: the same tokens."""
     import gq
-    cfg = dict({"SMALL": SMALL, "HD128": HD128}[cfg_name], kv_dtype="q8_0")
+    cfg = dict({"SMALL": SMALL, "HD128": HD128}[cfg_name], **MIXES[mix], kv_dtype="q8_0")
     w = syn.make_decoder(cfg, 51 + n, embd_scale=1e4)
+    w["attn_norm"] = [np.float32(ATTN_SCALE) * a for a in w["attn_norm"]]
     L, kvd = cfg["n_layers"], cfg["n_kv_heads"] * cfg["head_dim"]
     rng = np.random.default_rng(n)
     kv = [np.stack([np.stack([npref.pack_q8_0_rows(rng.standard_normal(kvd).astype(np.float32))
-                              for _ in range(n_ctx)]) for _ in range(L)]) for _ in range(2)]
+                              for _ in range(n_ctx)]) for _ in range(L)]) if n_ctx else
+          np.zeros((L, 0, kvd // 32 * 34), np.uint8) for _ in range(2)]
     hw = syn.upload_decoder(backend, cfg, w)
     gm = gq.DecodeModel(dict(cfg, max_tokens=64), hw)
-    for l in range(L):
-        gm.kv_upload(l, kv[0][l], kv[1][l])
-    om = oracle.DecoderModel(cfg, w, kv, kv_dtype="q8_0")
+    if n_ctx:
+        for l in range(L):
+            gm.kv_upload(l, kv[0][l], kv[1][l])
+    kc = np.zeros((L, cfg["ctx"], kvd // 32 * 34), np.uint8)
+    vc = kc.copy()
+    kc[:, :n_ctx], vc[:, :n_ctx] = kv[0], kv[1]
     toks = np.random.default_rng(n + 1).integers(0, cfg["vocab"], n).astype(np.int32)
     nxt, got = gm.prefill(toks, n_ctx)
-    for i, t in enumerate(toks):
-        ref = om.step(int(t), n_ctx + i)
+    ref = npref.prefill_bf16(cfg, w, kc, vc, toks, n_ctx, kv="q8_0")
     err = float(np.abs(got - ref).max())
-    say(f"q8_0 prefill {cfg_name}: logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
-    assert err <= TOL_FP32 * float(np.abs(ref).max())
+    say(f"q8_0 prefill {cfg_name} ({mix}): logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
+    assert nxt == int(np.argmax(got))
+    om = oracle.DecoderModel(cfg, w, kv, kv_dtype="q8_0")
     for l in range(L):
         k, v = gm.kv_download(l, n_ctx + n)
         np.testing.assert_array_equal(k[:n_ctx], kv[0][l])
         np.testing.assert_array_equal(v[:n_ctx], kv[1][l])
-        for nm, got_rows, ref_rows in (("K", k, om.kc[l]), ("V", v, om.vc[l])):
+        for nm, got_rows, ref_rows in (("K", k, kc[l]), ("V", v, vc[l])):
             blk = got_rows[n_ctx:].reshape(n, -1, 34)
             codes = blk[:, :, 2:].view(np.int8).astype(np.int32)
             scale = blk[:, :, 0].astype(np.uint16) | (blk[:, :, 1].astype(np.uint16) << 8)
             assert np.all(np.abs(codes).max(axis=2)[scale != 0x3C00] == 127), (nm, l)
+            rcodes = ref_rows[n_ctx:n_ctx + n].reshape(n, -1, 34)[:, :, 2:].view(np.int8).astype(np.int32)
+            frac = float(np.mean(codes != rcodes))
             g = npref.unpack_q8_0_rows(got_rows[n_ctx:])
             r = npref.unpack_q8_0_rows(ref_rows[n_ctx:n_ctx + n])
-            rel = np.abs(g - r).max(axis=1) / np.abs(r).max(axis=1)
-            say(f"  layer {l} {nm} worst row {rel.max():.3g} median {np.median(rel):.3g}")
-            assert rel.max() <= 5e-2 and np.median(rel) <= 2e-2
-            ref_rows[n_ctx:n_ctx + n] = got_rows[n_ctx:]
+            top = float(np.abs(r).max())
+            say(f"  layer {l} {nm}: codes differing {frac:.3g}, max|err| {np.abs(g - r).max():.3g} of {top:.3g}")
+            assert frac <= 1e-2
+            assert np.abs(g - r).max() <= KV_SAME * top
+        om.kc[l, :n_ctx + n] = k
+        om.vc[l, :n_ctx + n] = v
+    assert err <= TOL_SAME_Q8KV * float(np.abs(ref).max())
     exp, tok = [], nxt
     for i in range(12):
         tok = oracle.argmax(om.step(tok, n_ctx + n + i))
