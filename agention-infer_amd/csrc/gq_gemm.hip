@@ -371,6 +371,15 @@ __global__ void k_gemm_records(Layout L, const uint8_t *body, const uint16_t *dd
 // with ksplit > 1 a block covers stages [S*s/ksplit, S*(s+1)/ksplit) and
 // writes a partial product, which gemm_reduce sums in a fixed order.
 
+// Workgroups are dealt to the 8 XCDs round-robin by id (id % 8).  The
+// GEMM's block index is renumbered so that each XCD takes a contiguous range
+// of it: the token tiles (and K splits) of one row tile then run on one XCD
+// and read its W tile through the same L2.
+__device__ __forceinline__ int xcd_block(int id, int n) {
+  const int x = id & 7, j = id >> 3, q = n >> 3, r = n & 7;
+  return x * q + min(x, r) + j;
+}
+
 template <int TBM, int TBN, int NXR, int FMT>
 struct Ring {
   static constexpr int AT_ = TBM / 16, BT_ = TBN / 16;
@@ -402,7 +411,7 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_ring(GemmArgs a) {
   __shared__ __align__(16) uint16_t Xs[NXR][R::B_FR_ * FR16];
   __shared__ __align__(16) uint8_t Wg[4][WR][WSLOTS * 16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = blockIdx.x, split = b % a.ksplit, rest = b / a.ksplit;
+  const int b = xcd_block(blockIdx.x, gridDim.x), split = b % a.ksplit, rest = b / a.ksplit;
   const int ntile = rest % a.ntiles, tile = rest / a.ntiles;
   GemmSeg sg = a.seg[0];
 #pragma unroll
@@ -664,7 +673,7 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
   __shared__ __align__(16) uint16_t As[2][R::A_FR_ * FR16];
   __shared__ __align__(16) uint8_t Wg[4][WR][WSLOTS * 16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int b = blockIdx.x, split = b % a.ksplit, rest = b / a.ksplit;
+  const int b = xcd_block(blockIdx.x, gridDim.x), split = b % a.ksplit, rest = b / a.ksplit;
   const int ntile = rest % a.ntiles, tile = rest / a.ntiles;
   GemmSeg sg = a.seg[0];
 #pragma unroll
@@ -987,7 +996,7 @@ __global__ __launch_bounds__(512) void k_gemm_i8_direct(const uint8_t *rec, int 
   __shared__ __align__(16) uint8_t Aq[2][2 * 10 * 512];      // [buf][ks][row tile] fragments
   __shared__ __align__(16) float2 Ws[2][2][I8M];              // [buf][ks][row] (d sc, dmin m)
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int ntile = blockIdx.x % ntiles, tile = blockIdx.x / ntiles;
+  const int bid = xcd_block(blockIdx.x, gridDim.x), ntile = bid % ntiles, tile = bid / ntiles;
   const int m0 = tile * I8M, n0 = ntile * I8N;
   const int stages = kpad / 64, kb_all = kpad / 32;
   const long row_stride = (long)(stages / 4) * 144;
