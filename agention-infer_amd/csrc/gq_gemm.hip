@@ -1186,6 +1186,85 @@ __global__ __launch_bounds__(512) void k_gemm_i8_direct(const uint8_t *rec, int 
   }
 }
 
+// ----------------------------------------------------------- int8 kernel, Q6_K
+// Q6_K weights against the same per-32 Q8 activation fragments.  A Q6_K
+// code minus 32 is an int8 (-32..31), so the A operand is the codes
+// themselves, read from the GEMM copy's stage records (64 B: 4 int8 group
+// scales and d, the low 4 bits, the high 2 bits).  Its scales change every
+// 16 elements, half a 32-deep MFMA step: each step runs twice with the
+// other group's half of A zeroed (lanes 0-31 hold k 0..15, lanes 32-63 k
+// 16..31), and the two integer dots are combined exactly,
+// sc_a * D_a + sc_b * D_b (|D| <= 16 * 32 * 127), before y += (d xs) * that
+// in fp32.  Block = 64 rows x 64 tokens, 4 waves of 16 rows; a lane loads
+// its own A bytes and its output rows' scales (L2-resident records).
+__global__ __launch_bounds__(256) void k_gemm_i8_q6k(const uint8_t *rec, int rows, const int8_t *xq,
+                                                     const float2 *xr, int n, int kpad, float *Y) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int m0 = blockIdx.x * 64 + 16 * wave, n0 = blockIdx.y * 64;
+  const int kb_all = kpad / 32, stages = kpad / 64;
+  const long row_stride = (long)stages * 64;
+  const int ar = lane & 15, ag = lane >> 4;  // A: row ar, k 8 ag .. 8 ag + 7 of the 32-block
+  const bool aok = m0 + ar < rows;
+  const uint8_t *arow = rec + (long)min(m0 + ar, rows - 1) * row_stride;
+  const int orow0 = m0 + 4 * (lane >> 4);  // D: rows orow0 + r, token lane % 16
+  const uint8_t *orec[4];
+  bool ook[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    ook[r] = orow0 + r < rows;
+    orec[r] = rec + (long)min(orow0 + r, rows - 1) * row_stride;
+  }
+  f32x4_t acc[4];
+#pragma unroll
+  for (int jn = 0; jn < 4; jn++) acc[jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int qq = ag >> 1, i0 = 8 * (ag & 1);
+  for (int kb = 0; kb < kb_all; kb++) {
+    const int s = kb >> 1, h = kb & 1, g = 2 * h + qq;  // this lane's 16-element group
+    const uint8_t *st = arow + (long)s * 64;
+    const uint2 lo = *(const uint2 *)(st + 16 + 16 * qq + i0);
+    const uint32_t hi = *(const uint16_t *)(st + 48 + 4 * g + i0 / 4);
+    uint32_t w[2];
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+      const uint32_t b2 = (hi >> (8 * e)) & 0xFFu;
+      const uint32_t hb = (b2 | (b2 << 6) | (b2 << 12) | (b2 << 18)) & 0x03030303u;
+      const uint32_t q6 = (((e ? lo.y : lo.x) >> (4 * h)) & 0x0F0F0F0Fu) | (hb << 4);
+      w[e] = aok ? (((q6 | 0x80808080u) - 0x20202020u) ^ 0x80808080u) : 0u;  // bytes q - 32
+    }
+    const long a = (long)((unsigned long)w[0] | ((unsigned long)w[1] << 32));
+    const long aa = ag < 2 ? a : 0, ab = ag < 2 ? 0 : a;  // groups 2h and 2h + 1
+    int sca[4], scb[4];
+    float dd[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint8_t *o = orec[r] + (long)s * 64;
+      sca[r] = (int)(int8_t)o[2 * h];
+      scb[r] = (int)(int8_t)o[2 * h + 1];
+      dd[r] = ook[r] ? h2f(*(const uint16_t *)(o + 4)) : 0.f;
+    }
+#pragma unroll
+    for (int jn = 0; jn < 4; jn++) {
+      const long f = (long)((n0 >> 4) + jn) * kb_all + kb;
+      const long b = *(const long *)(xq + f * 512 + lane * 8);
+      const float xs = xr[f * 16 + (lane & 15)].x;
+      const i32x4_t z = {0, 0, 0, 0};
+      const i32x4_t da = __builtin_amdgcn_mfma_i32_16x16x32_i8(aa, b, z, 0, 0, 0);
+      const i32x4_t db = __builtin_amdgcn_mfma_i32_16x16x32_i8(ab, b, z, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        acc[jn][r] = fmaf(dd[r] * xs, (float)(sca[r] * da[r] + scb[r] * db[r]), acc[jn][r]);
+    }
+  }
+#pragma unroll
+  for (int jn = 0; jn < 4; jn++) {
+    const int t = n0 + 16 * jn + (lane & 15);
+    if (t >= n) continue;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+      if (ook[r]) Y[(long)t * rows + orow0 + r] = acc[jn][r];
+  }
+}
+
 // ----------------------------------------------------------- host side
 size_t gemm_records_bytes(const Layout &L) {
   return (size_t)L.rows * L.units * gemm_unit_bytes(L.dtype);
@@ -1258,7 +1337,7 @@ size_t gemm_workspace_bytes(const gq_weight *w, int n, int mode, int num_cus) {
     const size_t xb = (size_t)((n + GEMM_NPAD - 1) / GEMM_NPAD * GEMM_NPAD) * kpad * 2;
     return ((xb + 255) & ~(size_t)255) + gemm_part_floats(&w, 1, n, num_cus, false) * 4 + 256;
   }
-  if (w->L.dtype != T_Q4_K) return (size_t)-1;
+  if (w->L.dtype != T_Q4_K && w->L.dtype != T_Q6_K) return (size_t)-1;
   // int8: fragments [npad/16][kpad/32][512 B] + records [npad/16][kpad/32][16] float2
   const size_t npad = (size_t)(n + I8N - 1) / I8N * I8N;
   return ((npad * kpad + 255) & ~(size_t)255) + npad * (kpad / 32) * 8 + 256;
@@ -1353,6 +1432,12 @@ hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int 
     const long threads = (long)npad * (kpad / 8);
     hipLaunchKernelGGL(k_x_to_q8_frag, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, X,
                        n, npad, L.k, kpad, xq, xr);
+    if (L.dtype == T_Q6_K) {
+      hipLaunchKernelGGL(k_gemm_i8_q6k, dim3((unsigned)((L.rows + 63) / 64), (unsigned)((n + 63) / 64)),
+                         dim3(256), 0, st, (const uint8_t *)w->gemm_raw, L.rows, (const int8_t *)xq,
+                         (const float2 *)xr, n, kpad, Y);
+      return hipGetLastError();
+    }
     const int ntiles = npad / I8N, mtiles = (L.rows + I8M - 1) / I8M;
     hipLaunchKernelGGL(k_gemm_i8_direct, dim3((unsigned)(mtiles * ntiles)), dim3(512), 0, st,
                        (const uint8_t *)w->gemm_raw, L.rows, ntiles, (const int8_t *)xq,

@@ -132,6 +132,23 @@ def gemm_leg(be, gq, syn, torch, cpu):
         tf = flops / (ms * 1e-3) / 1e12
         out[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
                      "peak": MFMA_PEAK_TFLOPS[name], "frac": round(tf / MFMA_PEAK_TFLOPS[name], 4)}
+    # The Q6_K down projection of the same prefill (3584 x 18944, 512 tokens),
+    # both modes (int8: Q6_K codes against the per-32 Q8 activations).
+    rows6, k6 = HID, FFN
+    h6 = be.upload_weight(Q6_K, syn.make_blocks(Q6_K, rows6, k6, seed=33), k6, rows6)
+    X6 = torch.from_numpy(syn.make_x(k6, seed=34, batch=n)).cuda()
+    Y6 = torch.empty(n, rows6, device="cuda")
+    fl6 = 2.0 * rows6 * k6 * n
+    out["q6k_down"] = {"shape": f"W {rows6}x{k6} Q6_K, X {n}x{k6}"}
+    for mode, name in ((gq.GQ_GEMM_BF16, "bf16"), (gq.GQ_GEMM_INT8, "int8")):
+        for _ in range(3):
+            h6.launch_only_batch(X6, mode=mode, Y_dev=Y6)
+        torch.cuda.synchronize()
+        ms = _timed(torch, lambda: h6.launch_only_batch(X6, mode=mode, Y_dev=Y6), 10)
+        tf = fl6 / (ms * 1e-3) / 1e12
+        out["q6k_down"][name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1),
+                                 "frac": round(tf / MFMA_PEAK_TFLOPS[name], 4)}
+    del h6, X6, Y6
     if cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle
@@ -207,7 +224,9 @@ def moe_leg(be, gq, syn, torch, cpu):
     u = be.upload_experts(IQ3, uw, H, F, E)
     d = be.upload_experts(IQ3, dw, F, H, E)
     per_expert = 2 * gq.type_size(IQ3, H) * F + gq.type_size(IQ3, F) * H
-    out = {"shape": f"{E} experts, h {H}, f {F}, top-{K}", "per_expert_bytes": per_expert}
+    out = {"shape": f"{E} experts, h {H}, f {F}, top-{K}", "per_expert_bytes": per_expert,
+           "codebook": "the library's built-in test codebook (ggml's iq3xxs_grid is not in the "
+                       "image); the kernels' speed does not depend on the table values"}
     for T in (1, 4, 16):
         lg = torch.from_numpy(syn.make_x(E, seed=50 + T, batch=T)).cuda()
         x = torch.from_numpy(syn.make_x(H, seed=60 + T, batch=T)).cuda()
@@ -220,7 +239,7 @@ def moe_leg(be, gq, syn, torch, cpu):
     if cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import oracle
-        nthreads = min(len(os.sched_getaffinity(0)), 16)
+        nthreads = host_threads()
         lg1 = syn.make_x(E, seed=51, batch=1)
         x1 = syn.make_x(H, seed=61, batch=1)
         ids, wts = oracle.moe_route(lg1, K)
