@@ -43,16 +43,23 @@ NCOPY = 2
 COLD_BYTES = 320 << 20
 
 
+PROFILE = os.path.join("profiles", "matvec_q6k_head_and_q4k_layer.md")
+
+
 def measured_traffic():
-    """HBM bytes per head launch from the committed rocprof summary, or None."""
-    path = os.path.join(ROOT, "profiles", "matvec_q6k_head_and_q4k_layer.md")
+    """(HBM bytes per head launch, kernel-trace average us) from the committed
+    rocprof summary of this benchmark (FETCH_SIZE / WRITE_SIZE passes of the
+    same command), or (None, None)."""
+    traffic = us = None
     try:
-        for line in open(path):
+        for line in open(os.path.join(ROOT, PROFILE)):
             if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":")[1])
+                traffic = int(line.split(":")[1])
+            elif line.startswith("kernel_trace_avg_us:"):
+                us = float(line.split(":")[1])
     except OSError:
         pass
-    return None
+    return traffic, us
 
 
 def algo_bytes(gq, dtype, out_dim, in_dim):
@@ -510,6 +517,14 @@ def main():
     head_bytes = [b for n, *_, b in mats if n == "head"][0]
     head_us = per["head"]["us"]
     achieved = head_bytes / (head_us * 1e-6) / 1e9
+    # The counters cannot be read inside this process: the traffic comes from
+    # the committed profile, and only if that profile's kernel time agrees
+    # with this run's (within 10%), so a stale profile reports null.
+    traffic, prof_us = measured_traffic()
+    traffic_note = f"{PROFILE} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; kernel-trace {prof_us} us)"
+    if traffic is None or prof_us is None or abs(prof_us - head_us) > 0.1 * head_us:
+        traffic_note = f"null: {PROFILE} kernel time {prof_us} us disagrees with this run's {head_us} us"
+        traffic = None
 
     out = {
         "metric": "Q4_K/Q6_K matvec HBM GB/s (% of peak); 7B-shape Q4_K_M decode tok/s",
@@ -530,8 +545,8 @@ def main():
                    "wall_s": round(wall, 4)},
         "roofline": {"bound": "hbm", "kernel": "k_mvq<Q6_K> (output head 152064x3584)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                     "launch_us": head_us, "algo_bytes": head_bytes},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "traffic_source": traffic_note, "launch_us": head_us, "algo_bytes": head_bytes},
         "per_kernel": per,
     }
     if args.calib_copy:
