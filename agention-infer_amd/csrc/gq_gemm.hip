@@ -1189,79 +1189,141 @@ __global__ __launch_bounds__(512) void k_gemm_i8_direct(const uint8_t *rec, int 
 // ----------------------------------------------------------- int8 kernel, Q6_K
 // Q6_K weights against the same per-32 Q8 activation fragments.  A Q6_K
 // code minus 32 is an int8 (-32..31), so the A operand is the codes
-// themselves, read from the GEMM copy's stage records (64 B: 4 int8 group
-// scales and d, the low 4 bits, the high 2 bits).  Its scales change every
-// 16 elements, half a 32-deep MFMA step: each step runs twice with the
-// other group's half of A zeroed (lanes 0-31 hold k 0..15, lanes 32-63 k
-// 16..31), and the two integer dots are combined exactly,
-// sc_a * D_a + sc_b * D_b (|D| <= 16 * 32 * 127), before y += (d xs) * that
-// in fp32.  Block = 64 rows x 64 tokens, 4 waves of 16 rows; a lane loads
-// its own A bytes and its output rows' scales (L2-resident records).
+// themselves.  Its scales change every 16 elements, half a 32-deep MFMA
+// step: each step runs twice with the other group's half of A zeroed
+// (lanes 0-31 hold k 0..15, lanes 32-63 k 16..31), and the two integer dots
+// are combined exactly, sc_a * D_a + sc_b * D_b (|D| <= 16 * 32 * 127),
+// before y += (d xs) * that in fp32.
+// Block tile 64 rows x 64 tokens, 256 threads; wave w owns rows 16 w ..
+// 16 w + 15 and all 64 tokens (4 MFMA tiles).  Per 64-element stage, a
+// stage ahead, every operand goes through LDS:
+//   * threads 0-127 (row tid / 2, half tid % 2) fetch the stage record's
+//     quant chunks of their row and write the half's 32 codes as int8 A
+//     fragments; threads 128-191 fetch the row's 4 group scales and d;
+//   * every thread fetches 16 bytes of the stage's X fragments (4 KiB) and
+//     threads 0-127 its 128 X scales.
+// One barrier per stage.
+constexpr int Q6M = 64, Q6N = 64, Q6J = Q6N / 16;
 __global__ __launch_bounds__(256) void k_gemm_i8_q6k(const uint8_t *rec, int rows, const int8_t *xq,
                                                      const float2 *xr, int n, int kpad, float *Y) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int m0 = blockIdx.x * 64 + 16 * wave, n0 = blockIdx.y * 64;
-  const int kb_all = kpad / 32, stages = kpad / 64;
+  __shared__ __align__(16) uint8_t Aq[2][2][4][512];  // [buf][half][row tile][lane slot x 8 codes]
+  __shared__ __align__(16) int Sc[2][4][Q6M];         // [buf][group][row] int8 scale
+  __shared__ __align__(16) float Dd[2][Q6M];          // [buf][row] f16 d
+  __shared__ __align__(16) float Xs[2][2][Q6J][16];   // [buf][half][token tile][token] f16 xs
+  __shared__ __align__(16) uint8_t Xb[2][2][Q6J][512];  // [buf][half][token tile] B fragments
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int m0 = blockIdx.x * Q6M, n0 = blockIdx.y * Q6N;
+  const int stages = kpad / 64, kb_all = kpad / 32;
   const long row_stride = (long)stages * 64;
-  const int ar = lane & 15, ag = lane >> 4;  // A: row ar, k 8 ag .. 8 ag + 7 of the 32-block
-  const bool aok = m0 + ar < rows;
-  const uint8_t *arow = rec + (long)min(m0 + ar, rows - 1) * row_stride;
-  const int orow0 = m0 + 4 * (lane >> 4);  // D: rows orow0 + r, token lane % 16
-  const uint8_t *orec[4];
-  bool ook[4];
+  // staging role of this thread
+  const int sr = tid < 128 ? tid >> 1 : tid - 128, sh = tid & 1;
+  const bool sq = tid < 128, ss = tid >= 128 && tid < 192;
+  const bool sok = m0 + sr < rows;
+  const uint8_t *srow = rec + (long)min(m0 + min(sr, Q6M - 1), rows - 1) * row_stride;
+  // the next stage's staged loads: the row's quant chunks (c1, c2, hb) or
+  // its scales and d (c0), one X scale (xsv), 16 bytes of X fragments (xf)
+  uint4 c1 = make_uint4(0, 0, 0, 0), c2 = c1, c0 = c1, xf = c1;
+  uint2 hb = make_uint2(0, 0);
+  float xsv = 0.f;
+  auto load_w = [&](int s) {
+    const uint8_t *rp = srow + (long)s * 64;
+    if (sq) {
+      c1 = *(const uint4 *)(rp + 16);
+      c2 = *(const uint4 *)(rp + 32);
+      hb = *(const uint2 *)(rp + 48 + 8 * sh);
+    } else if (ss) {
+      c0 = *(const uint4 *)rp;
+    }
+    if (tid < 32 * Q6J) {
+      const long f = ((n0 >> 4) + ((tid >> 4) % Q6J)) * kb_all + 2 * s + tid / (16 * Q6J);
+      xsv = xr[f * 16 + (tid & 15)].x;
+    }
+    if (tid < 64 * Q6J) {  // fragment (half, token tile) = tid / 32 (half-major), bytes 16 (tid % 32)
+      const int fi = tid >> 5, h = fi / Q6J, jn = fi % Q6J;
+      const long f = ((n0 >> 4) + jn) * kb_all + 2 * s + h;
+      xf = *(const uint4 *)(xq + f * 512 + 16 * (tid & 31));
+    }
+  };
+  auto store_w = [&](int buf) {
+    if (sq) {
+      // element e = 16 qq + i of half sh: low 4 bits = nibble sh of byte i
+      // of chunk 1 + qq, high 2 bits = bits 2i, 2i + 1 of dword 2 sh + qq
+      const uint32_t lw[2][4] = {{c1.x, c1.y, c1.z, c1.w}, {c2.x, c2.y, c2.z, c2.w}};
+      const uint32_t hw[2] = {hb.x, hb.y};
+      uint8_t *fr = &Aq[buf][sh][sr >> 4][0];
 #pragma unroll
-  for (int r = 0; r < 4; r++) {
-    ook[r] = orow0 + r < rows;
-    orec[r] = rec + (long)min(orow0 + r, rows - 1) * row_stride;
+      for (int j = 0; j < 4; j++) {  // codes 8 j .. 8 j + 7: lane slot (row % 16) + 16 j
+        const int qq = j >> 1;
+        uint32_t out[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+          const int i0 = 8 * (j & 1) + 4 * e;  // first of 4 elements within the 16
+          const uint32_t lo = (lw[qq][i0 >> 2] >> (4 * sh)) & 0x0F0F0F0Fu;
+          const uint32_t b2 = (hw[qq] >> (2 * i0)) & 0xFFu;
+          const uint32_t hi = (b2 | (b2 << 6) | (b2 << 12) | (b2 << 18)) & 0x03030303u;
+          const uint32_t q6 = lo | (hi << 4);
+          out[e] = sok ? (((q6 | 0x80808080u) - 0x20202020u) ^ 0x80808080u) : 0u;  // q - 32
+        }
+        *(uint2 *)(fr + ((sr & 15) + 16 * j) * 8) = make_uint2(out[0], out[1]);
+      }
+    } else if (ss) {
+#pragma unroll
+      for (int g = 0; g < 4; g++) Sc[buf][g][sr] = (int)(int8_t)((c0.x >> (8 * g)) & 0xFFu);
+      Dd[buf][sr] = sok ? h2f(c0.y) : 0.f;
+    }
+    if (tid < 32 * Q6J) Xs[buf][tid / (16 * Q6J)][(tid >> 4) % Q6J][tid & 15] = xsv;
+    if (tid < 64 * Q6J) {
+      const int fi = tid >> 5;
+      *(uint4 *)&Xb[buf][fi / Q6J][fi % Q6J][16 * (tid & 31)] = xf;
+    }
+  };
+  f32x4_t acc[Q6J];
+#pragma unroll
+  for (int jn = 0; jn < Q6J; jn++) acc[jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const int rr0 = 16 * wave + 4 * (lane >> 4);  // this lane's output rows rr0 .. rr0 + 3 (block-local)
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const long a = *(const long *)&Aq[buf][h][wave][lane * 8];
+      const long aa = lane < 32 ? a : 0, ab = lane < 32 ? 0 : a;  // groups 2h and 2h + 1
+      int sca[4], scb[4];
+      float dd[4];
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        sca[r] = Sc[buf][2 * h][rr0 + r];
+        scb[r] = Sc[buf][2 * h + 1][rr0 + r];
+        dd[r] = Dd[buf][rr0 + r];
+      }
+#pragma unroll
+      for (int jn = 0; jn < Q6J; jn++) {
+        const long bx = *(const long *)&Xb[buf][h][jn][lane * 8];
+        const i32x4_t z = {0, 0, 0, 0};
+        const i32x4_t da = __builtin_amdgcn_mfma_i32_16x16x32_i8(aa, bx, z, 0, 0, 0);
+        const i32x4_t db = __builtin_amdgcn_mfma_i32_16x16x32_i8(ab, bx, z, 0, 0, 0);
+        const float xs = Xs[buf][h][jn][lane & 15];
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          acc[jn][r] = fmaf(dd[r] * xs, (float)(sca[r] * da[r] + scb[r] * db[r]), acc[jn][r]);
+      }
+    }
+  };
+  load_w(0);
+  store_w(0);
+  __syncthreads();
+  for (int s = 0; s < stages; s++) {
+    const bool more = s + 1 < stages;
+    if (more) load_w(s + 1);  // a stage ahead
+    compute(s & 1);
+    if (more) store_w((s & 1) ^ 1);
+    __syncthreads();
   }
-  f32x4_t acc[4];
 #pragma unroll
-  for (int jn = 0; jn < 4; jn++) acc[jn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const int qq = ag >> 1, i0 = 8 * (ag & 1);
-  for (int kb = 0; kb < kb_all; kb++) {
-    const int s = kb >> 1, h = kb & 1, g = 2 * h + qq;  // this lane's 16-element group
-    const uint8_t *st = arow + (long)s * 64;
-    const uint2 lo = *(const uint2 *)(st + 16 + 16 * qq + i0);
-    const uint32_t hi = *(const uint16_t *)(st + 48 + 4 * g + i0 / 4);
-    uint32_t w[2];
-#pragma unroll
-    for (int e = 0; e < 2; e++) {
-      const uint32_t b2 = (hi >> (8 * e)) & 0xFFu;
-      const uint32_t hb = (b2 | (b2 << 6) | (b2 << 12) | (b2 << 18)) & 0x03030303u;
-      const uint32_t q6 = (((e ? lo.y : lo.x) >> (4 * h)) & 0x0F0F0F0Fu) | (hb << 4);
-      w[e] = aok ? (((q6 | 0x80808080u) - 0x20202020u) ^ 0x80808080u) : 0u;  // bytes q - 32
-    }
-    const long a = (long)((unsigned long)w[0] | ((unsigned long)w[1] << 32));
-    const long aa = ag < 2 ? a : 0, ab = ag < 2 ? 0 : a;  // groups 2h and 2h + 1
-    int sca[4], scb[4];
-    float dd[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const uint8_t *o = orec[r] + (long)s * 64;
-      sca[r] = (int)(int8_t)o[2 * h];
-      scb[r] = (int)(int8_t)o[2 * h + 1];
-      dd[r] = ook[r] ? h2f(*(const uint16_t *)(o + 4)) : 0.f;
-    }
-#pragma unroll
-    for (int jn = 0; jn < 4; jn++) {
-      const long f = (long)((n0 >> 4) + jn) * kb_all + kb;
-      const long b = *(const long *)(xq + f * 512 + lane * 8);
-      const float xs = xr[f * 16 + (lane & 15)].x;
-      const i32x4_t z = {0, 0, 0, 0};
-      const i32x4_t da = __builtin_amdgcn_mfma_i32_16x16x32_i8(aa, b, z, 0, 0, 0);
-      const i32x4_t db = __builtin_amdgcn_mfma_i32_16x16x32_i8(ab, b, z, 0, 0, 0);
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        acc[jn][r] = fmaf(dd[r] * xs, (float)(sca[r] * da[r] + scb[r] * db[r]), acc[jn][r]);
-    }
-  }
-#pragma unroll
-  for (int jn = 0; jn < 4; jn++) {
+  for (int jn = 0; jn < Q6J; jn++) {
     const int t = n0 + 16 * jn + (lane & 15);
     if (t >= n) continue;
 #pragma unroll
     for (int r = 0; r < 4; r++)
-      if (ook[r]) Y[(long)t * rows + orow0 + r] = acc[jn][r];
+      if (m0 + rr0 + r < rows) Y[(long)t * rows + m0 + rr0 + r] = acc[jn][r];
   }
 }
 
@@ -1433,7 +1495,7 @@ hipError_t launch_gemm(const gq_weight *w, const float *X, int n, float *Y, int 
     hipLaunchKernelGGL(k_x_to_q8_frag, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st, X,
                        n, npad, L.k, kpad, xq, xr);
     if (L.dtype == T_Q6_K) {
-      hipLaunchKernelGGL(k_gemm_i8_q6k, dim3((unsigned)((L.rows + 63) / 64), (unsigned)((n + 63) / 64)),
+      hipLaunchKernelGGL(k_gemm_i8_q6k, dim3((unsigned)((L.rows + Q6M - 1) / Q6M), (unsigned)((n + Q6N - 1) / Q6N)),
                          dim3(256), 0, st, (const uint8_t *)w->gemm_raw, L.rows, (const int8_t *)xq,
                          (const float2 *)xr, n, kpad, Y);
       return hipGetLastError();
