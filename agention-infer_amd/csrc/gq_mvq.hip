@@ -852,6 +852,16 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
   // on the 152064 x 3584 Q6_K head: 67.9 against 70.2 us; smaller launches
   // keep one block per CU).
   if (bpc == 1 && G >= 16 * num_cus) a.blocks = std::max(1, num_cus * 27 / 32);
+  // Small launches: no more blocks than give each wave one item (group x
+  // quad) to stream -- fewer x stagings, and every block's waves busy.
+  // Measured: q/k/v 3584+512+512 x 3584 on 144 blocks 5.30-5.37 against
+  // 5.63-5.65 us on 256; the Q8_0 8192 x 2048 matrix on 128 blocks 6.44-6.52
+  // against 6.81-6.82 us.
+  if (bpc == 1) {
+    const long items = (long)G * ((a.units + 3) / 4) * nt;
+    const int nw = mvq_waves(a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt);
+    a.blocks = (int)std::max(1L, std::min((long)a.blocks, (items + nw - 1) / nw));
+  }
   static const int maxb = [] {
     const char *e = getenv("GQ_MVQ_MAX_BLOCKS");  // tuning override: at most this many blocks
     return e && atoi(e) > 0 ? atoi(e) : 1 << 30;
