@@ -638,6 +638,7 @@ class GgufModel(DecodeModel):
         self.cfg = dict(n_layers=c.block_count, hidden=c.embedding_length, n_heads=c.head_count,
                         n_kv_heads=c.head_count_kv, head_dim=c.head_dim, vocab=c.vocab_size,
                         ctx=c.ctx, eps=c.layer_norm_rms_epsilon, theta=c.rope_freq_base)
+        self.kv_q8 = False  # gqh_model_load builds an f16 KV cache (KvDtype::F16)
         m = ctypes.c_void_p()
         _hcheck(host_lib().gqh_model_handle(h, ctypes.byref(m)))
         self._h = m

@@ -129,3 +129,34 @@ def test_gguf_upload_tensor_matvec(backend, tmp_path, dtype):
     assert np.abs(y - ref).max() <= 1e-4 * np.abs(ref).max()
     with pytest.raises(gq.GgufError):
         f.upload("norm")  # 1-D F32: not a weight the backend multiplies
+
+
+def test_gguf_q8_0_model_prefill_and_generate(backend, tmp_path):
+    """An all-Q8_0 file (the file type of BASELINE configs[0]'s Llama-3.2-1B
+    Q8_0 model; here a small decoder with a Q8_0 head): gq_model_prefill of
+    a 40-token prompt (LlamaModel::run_batch, cpu_path.rs:834-991) against
+    the oracle stepping the same tokens (logits to the bf16-operand bound
+    2e-2 of their max), then, on the GPU's prompt K/V rows, 16 greedy steps
+    equal to the oracle's."""
+    cfg = dict(CFG, attn_type=Q8, gate_up_type=Q8, down_type=Q8, head_type=Q8)
+    types = [[Q8] * 7] * cfg["n_layers"]
+    w = _weights(cfg, types, seed=14)
+    gm = _load(tmp_path, cfg, w, types, head_type=Q8)
+    om = oracle.DecoderModel(cfg, w)
+    toks = np.random.default_rng(14).integers(0, cfg["vocab"], 40).astype(np.int32)
+    nxt, got = gm.prefill(toks, 0)
+    for i, t in enumerate(toks):
+        ref = om.step(int(t), i)
+    err = float(np.abs(got - ref).max())
+    assert err <= 2e-2 * float(np.abs(ref).max()), err
+    top = np.sort(ref)[-2:]
+    if top[1] - top[0] > 2 * err:
+        assert nxt == oracle.argmax(ref)
+    for l in range(cfg["n_layers"]):
+        k, v = gm.kv_download(l, 40)
+        om.kc[l, :40], om.vc[l, :40] = k, v
+    exp, tok = [], nxt
+    for i in range(16):
+        tok = oracle.argmax(om.step(tok, 40 + i))
+        exp.append(tok)
+    np.testing.assert_array_equal(gm.generate(nxt, 40, 16), np.array(exp, np.int32))
