@@ -159,3 +159,49 @@ def test_moe_other_formats(backend, orc, dtype, E, H, F, T, k):
     bound = TOL * float(np.max(np.abs(ref)))
     say(f"  max|err| {err:.3g} bound {bound:.3g}")
     assert err <= bound
+
+
+def test_moe_capture_survives_workspace_growth(backend):
+    """gq_moe_ffn captured in a HIP graph after an eager call of the same
+    size: a later, larger eager call grows the stream's workspace without
+    freeing the captured one, every replay (eager work between) reproduces
+    the eager output, and a call that would grow the workspace under
+    capture fails with GqError instead of allocating."""
+    import gq
+    import torch
+    E, H, F, k = 16, 512, 256, 4
+    gate, up, down = make(E, H, F, seed=71)
+    hg = backend.upload_experts(IQ3, gate, H, F, E)
+    hu = backend.upload_experts(IQ3, up, H, F, E)
+    hd = backend.upload_experts(IQ3, down, F, H, E)
+    s = torch.cuda.Stream()
+    lg2 = torch.from_numpy(syn.make_x(E, seed=72, batch=2)).cuda()
+    x2 = torch.from_numpy(syn.make_x(H, seed=73, batch=2)).cuda()
+    lg8 = torch.from_numpy(syn.make_x(E, seed=74, batch=8)).cuda()
+    x8 = torch.from_numpy(syn.make_x(H, seed=75, batch=8)).cuda()
+    y2 = torch.zeros((2, H), device="cuda")
+    y8 = torch.zeros((8, H), device="cuda")
+    torch.cuda.synchronize()
+    backend.moe_ffn(hg, hu, hd, E, lg2, x2, k, out_dev=y2, stream=s.cuda_stream)
+    s.synchronize()
+    ref2 = y2.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        backend.moe_ffn(hg, hu, hd, E, lg2, x2, k, out_dev=y2, stream=s.cuda_stream)
+    g_bad = torch.cuda.CUDAGraph()
+    with pytest.raises(gq.GqError, match="capture"):
+        with torch.cuda.graph(g_bad, stream=s):
+            backend.moe_ffn(hg, hu, hd, E, lg8, x8, k, out_dev=y8, stream=s.cuda_stream)
+    torch.cuda.synchronize()
+    backend.moe_ffn(hg, hu, hd, E, lg8, x8, k, out_dev=y8, stream=s.cuda_stream)
+    s.synchronize()
+    ref8 = y8.clone()
+    for i in range(3):
+        y2.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y2, ref2), f"replay {i}"
+        backend.moe_ffn(hg, hu, hd, E, lg8, x8, k, out_dev=y8, stream=s.cuda_stream)
+        s.synchronize()
+        assert torch.equal(y8, ref8)
