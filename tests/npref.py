@@ -265,11 +265,16 @@ def prefill_bf16(cfg, w, kc, vc, tokens, pos0, kv="f16"):
     half, group = hd // 2, nh // nkv
     n = len(tokens)
 
+    def mat32(dtype, blob, rows, cols):
+        if cols % 256 == 0:  # whole blocks per row: the rows dequantize as one run
+            return dequant(dtype, np.ascontiguousarray(blob).reshape(-1), rows * cols).reshape(rows, cols)
+        return np.stack([dequant(dtype, blob[r], cols) for r in range(rows)])
+
     def matb(dtype, blob, rows, cols):
-        return bf16(np.stack([dequant(dtype, blob[r], cols) for r in range(rows)]))
+        return bf16(mat32(dtype, blob, rows, cols))
 
     def mat(dtype, blob, rows, cols):
-        return np.stack([dequant(dtype, blob[r], cols) for r in range(rows)]).astype(np.float64)
+        return mat32(dtype, blob, rows, cols).astype(np.float64)
 
     def norm(x, g):  # rows of x
         return g * x / np.sqrt(np.mean(x * x, axis=1, keepdims=True) + cfg["eps"])

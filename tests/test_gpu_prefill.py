@@ -263,3 +263,59 @@ def test_prefill_q8_0_kv(backend, cfg_name, n_ctx, n, mix):
         tok = oracle.argmax(om.step(tok, n_ctx + n + i))
         exp.append(tok)
     np.testing.assert_array_equal(gm.generate(nxt, n_ctx + n, 12), np.array(exp, np.int32))
+
+
+def test_prefill_same_rounding_7b_width(backend):
+    """The same-rounding check at the 7B shapes of the GEMMs and the
+    attention (hidden 3584, 28 / 4 heads of 128, ffn 18944; Q4_K_M types),
+    two layers and a 1000-token vocabulary so that the float64 reference
+    fits: 100 uploaded rows, a 300-token prompt.  At this width the bf16
+    operand roundings make the reference itself sensitive: with attention
+    norms x0.01 and FFN norms x0.006, scaling the embedding by 1 + 1e-6
+    moves its logits by 2e-3 of their maximum and its layer-1 K rows by
+    1e-3 (rms).  With zero-mean Q4_K rows, attention norms x0.001, FFN norms
+    x0.002, embedding x100 and cached V ~ N(0, 30^2), that perturbation
+    moves the logits by 2e-4 and the layer-1 K/V by 3e-4 (rms), while
+    zeroing layer 0's FFN down / attention output moves the logits by 6e-2
+    / 0.48 and the layer-1 K by 6e-2 / 0.9 (rms).  Logits to TOL_SAME;
+    layer 0's K/V rows as in test_prefill_same_rounding; later layers'
+    rows to KV_SAME (worst) and KV_RMS_7B (rms over all values)."""
+    import gq
+    KV_RMS_7B = 2e-3
+    cfg = dict(syn.QWEN25_7B, n_layers=2, vocab=1000, ctx=512)
+    n_ctx, n = 100, 300
+    w = syn.make_decoder(cfg, 61, embd_scale=100.0, centered=True)
+    w["attn_norm"] = [np.float32(0.001) * a for a in w["attn_norm"]]
+    w["ffn_norm"] = [np.float32(0.002) * a for a in w["ffn_norm"]]
+    k0, v0 = syn.make_kv(cfg, n_ctx, 62)
+    v0 = (v0.view(np.float16) * np.float16(30.0)).view(np.uint16)
+    hw = syn.upload_decoder(backend, cfg, w)
+    gm = gq.DecodeModel(dict(cfg, max_tokens=64), hw)
+    kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+    kc = np.zeros((cfg["n_layers"], cfg["ctx"], kvd), np.uint16)
+    vc = kc.copy()
+    for l in range(cfg["n_layers"]):
+        gm.kv_upload(l, k0[l], v0[l])
+        kc[l, :n_ctx], vc[l, :n_ctx] = k0[l], v0[l]
+    toks = np.random.default_rng(63).integers(0, cfg["vocab"], n).astype(np.int32)
+    nxt, got = gm.prefill(toks, n_ctx)
+    ref = npref.prefill_bf16(cfg, w, kc, vc, toks, n_ctx)
+    err = float(np.abs(got - ref).max())
+    say(f"7b width: logits max|err| {err:.3g} of {float(np.abs(ref).max()):.3g}")
+    for l in range(cfg["n_layers"]):
+        k, v = gm.kv_download(l, n_ctx + n)
+        for nm, got_rows, ref_rows in (("K", k, kc[l]), ("V", v, vc[l])):
+            g = _f16(got_rows[n_ctx:]).astype(np.float64)
+            r = _f16(ref_rows[n_ctx:n_ctx + n]).astype(np.float64)
+            rows = np.abs(g - r).max(axis=1)
+            top = float(np.abs(r).max())
+            rms = float(np.sqrt(np.mean((g - r) ** 2) / np.mean(r * r)))
+            say(f"  layer {l} {nm} max|err| {rows.max():.3g} median {np.median(rows):.3g} "
+                f"of {top:.3g}; rms {rms:.3g}")
+            assert rows.max() <= KV_SAME * top
+            if l == 0:
+                assert np.median(rows) <= KV_MEDIAN * top
+            else:
+                assert rms <= KV_RMS_7B
+    assert err <= TOL_SAME * float(np.abs(ref).max())
+    assert nxt == int(np.argmax(got))
