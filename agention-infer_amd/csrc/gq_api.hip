@@ -784,7 +784,7 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   if (!rc && L.kv_q8) rc = dalloc(m, &L.vscale, (size_t)d->n_layers * d->ctx * (kvd / 32));
   float *buf = nullptr;
   const int nb_amax = gq::ARGMAX_SLOTS;
-  const size_t nbuf = 3 * ((size_t)H + 16) + 2 * ((size_t)nh * hd + 16) + 2 * (kvd + 16) +
+  const size_t nbuf = 4 * ((size_t)H + 16) + 2 * ((size_t)nh * hd + 16) + 2 * (kvd + 16) +
                       ((size_t)d->ffn + 16) + ((size_t)d->vocab + 16) +
                       ((size_t)nh * L.att_chunks * (2 + hd) + 16) + (nb_amax + 16) + (hd / 2 + 16);
   int *ibuf = nullptr;
@@ -796,7 +796,7 @@ int gq_model_create(const gq_model_desc *d, gq_model **out) {
   if (rc) { delete m; return rc; }
   size_t o = 0;
   auto take = [&](size_t n) { float *p = buf + o; o += (n + 15) & ~(size_t)15; return p; };
-  L.xa = take(H); L.xb = take(H); L.proj = take(H);
+  L.xa = take(H); L.xb = take(H); L.xc = take(H); L.proj = take(H);
   L.q = take((size_t)nh * hd); L.att = take((size_t)nh * hd);
   L.k = take(kvd); L.v = take(kvd); L.h = take(d->ffn);
   L.logits = take(d->vocab); L.att_part = take((size_t)nh * L.att_chunks * (2 + hd));

@@ -546,16 +546,23 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
   const int hd = m.head_dim, nh = m.n_heads, nkv = m.n_kv_heads;
   const int kvd = nkv * hd, group = nh / nkv;
   hipError_t e;
+  // The down projections split their K range over two sets of blocks
+  // (MvIn::y2): x_b = (x_a + down_0) and proj = down_1, added by the next
+  // norm, which stores x_c = x_b + proj as the residual stream.
   for (int L = 0; L < m.n_layers; L++) {
-    // q, k, v of RMSNorm(x_b)
+    // q, k, v of RMSNorm(x), x the residual stream
     MvIn in;
     in.src = MV_NORM;
     // (layer 0 stores the embedding row as the residual stream x_b; later
-    // layers read x_b = x_a + proj, stored by the previous down launch)
+    // layers store x_c = x_b + proj from the previous down launch's halves,
+    // or read x_b = x_a + down when it did not split)
+    const bool split_in = L && mv_ksplit_ok(m.wdown[L - 1]->L.units);
+    float *xres = !L ? m.xb : split_in ? m.xc : m.xb;  // the stream the o projection adds to
     in.x = L ? m.xb : m.embd;
+    in.r = split_in ? m.proj : nullptr;
     in.tok = L ? nullptr : &m.state->token;
     in.nw = m.attn_norm[L];
-    in.xo = L ? nullptr : m.xb;
+    in.xo = !L || split_in ? xres : nullptr;
     in.eps = m.eps;
     in.q8k = true;  // matmul_qkv_into -> matmul_into (cpu_path.rs:319-321)
     // One launch per distinct dtype among q/k/v (GGUF Q4_K_M files carry
@@ -606,7 +613,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     MvIn ain;
     ain.x = m.att;
     ain.q8k = true;  // matmul_into (cpu_path.rs:757)
-    ain.res = m.xb;  // x_a = x_b + o (cpu_path.rs:780-782)
+    ain.res = xres;  // x_a = x_b + o (cpu_path.rs:780-782)
     const gq_weight *wo[1] = {m.wo[L]};
     float *xa[1] = {m.xa};
     if ((e = matvec_launch(wo, 1, ain, xa, s)) != hipSuccess) return e;
@@ -623,6 +630,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     din.x = m.h;
     din.q8k = true;  // matmul_ffn_into's down: matmul_into (cpu_path.rs:383)
     din.res = m.xa;  // x_b = x_a + down (cpu_path.rs:806-808)
+    if (mv_ksplit_ok(m.wdown[L]->L.units)) din.y2 = m.proj;
     const gq_weight *wd[1] = {m.wdown[L]};
     float *xb[1] = {m.xb};
     if ((e = matvec_launch(wd, 1, din, xb, s)) != hipSuccess) return e;
@@ -631,6 +639,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
   MvIn hin;
   hin.src = MV_NORM;
   hin.x = m.xb;
+  hin.r = m.n_layers && mv_ksplit_ok(m.wdown[m.n_layers - 1]->L.units) ? m.proj : nullptr;
   hin.nw = m.output_norm;
   hin.eps = m.eps;
   hin.q8k = true;  // the head: matmul_into (cpu_path.rs:815)

@@ -67,7 +67,15 @@ struct MvIn {
   // (greedy argmax, sampler.rs:120-131); null: off.
   float *amax_v = nullptr;
   int *amax_i = nullptr;
+  // One-matrix MV_X launches with at least two quads per row: if set, the
+  // blocks split each row's K range in two (quads [0, ts) and [ts, T)), so
+  // that a block stages half of x; half 0 writes res + W_0 . x to y, half 1
+  // writes W_1 . x here (no residual) and the consumer adds the two.
+  float *y2 = nullptr;
 };
+
+// Whether a matvec of this weight can take MvIn::y2 (two quads per row).
+inline bool mv_ksplit_ok(int units) { return (units + 3) / 4 >= 2; }
 
 struct MvArgs {
   MvIn in;
@@ -79,6 +87,8 @@ struct MvArgs {
   int nseg;
   int groups;            // quad layout: 16-row groups of all segments (seg[i].blk_begin
                          // is then the first of segment i)
+  int ksplit;            // in.y2: the first quad of half 1 (0: no split)
+  int blocks0;           // in.y2: blocks [0, blocks0) run half 0, the rest half 1
   MvSeg seg[MV_MAX_SEG];
 };
 
@@ -144,6 +154,7 @@ struct DecodeLaunch {
   int kv_q8;                  // KvDtype::Q8_0 cache
   uint16_t *kscale, *vscale;  // kv_q8: [layer][ctx][kv_dim / 32] f16 block scales
   float *xa, *xb;             // residual stream, ping-pong
+  float *xc;                  // residual stream x_b + proj of the split down launch
   float *q, *k, *v, *att, *proj, *h, *logits, *att_part;
   float *rope_den;            // [head_dim / 2] theta^(2i/head_dim), computed on the host
   float *amax_v;              // per-block argmax partials

@@ -373,12 +373,22 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   //   down:    token p takes blocks [p bpt, (p + 1) bpt) and the h / 16
   //            groups of its top_k experts' down matrices (NM = top_k,
   //            matrix m = slot m, against slot m's input).
+  //   split (a.ksplit > 0, dense one-matrix launches): blocks [0, blocks0)
+  //            take quads [0, ksplit) of their groups, the others quads
+  //            [ksplit, T), each over all groups; a block stages only its
+  //            half's inputs.
   int G, B, b, p = 0, Uw;
+  bool h1 = false;  // split: this block runs half 1
   if constexpr (MODE == MQ_DENSE) {
     G = a.groups;
     B = a.blocks;
     b = blockIdx.x;
     Uw = a.units;
+    if (a.ksplit > 0) {
+      h1 = (int)blockIdx.x >= a.blocks0;
+      B = h1 ? a.blocks - a.blocks0 : a.blocks0;
+      b = h1 ? (int)blockIdx.x - a.blocks0 : (int)blockIdx.x;
+    }
   } else if constexpr (MODE == MQ_GATE_UP) {
     B = mo.bpp;
     p = blockIdx.x / B;
@@ -394,8 +404,13 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   }
   const int NM = MODE == MQ_DOWN ? mo.top_k : NT;  // matrices per group
   const int U = Uw, T = (U + 3) >> 2;              // weight units per row, quads
-  // Staged x: U units (down: top_k slot inputs of 4T units each).
-  const int Ux = MODE == MQ_DOWN ? NM * 4 * T : U, upad = 4 * ((Ux + 3) >> 2);
+  // This block's quads of a row: [tq0, tq0 + Tl) (T without a split).
+  const int tq0 = h1 ? a.ksplit : 0;
+  const int Tl = MODE == MQ_DENSE && a.ksplit > 0 ? (h1 ? T - a.ksplit : a.ksplit) : T;
+  // Staged x: U units (split: the half's units; down: top_k slot inputs of
+  // 4T units each).
+  const int Ux = MODE == MQ_DOWN ? NM * 4 * T : min(U, 4 * (tq0 + Tl)) - 4 * tq0;
+  const int upad = 4 * ((Ux + 3) >> 2);
   const int ngb = (G - b + B - 1) / B;
   // Row sums go to one LDS slot per (group, matrix, quad): (lg NM + m) T + t.
   // down with 4F + 2 units per row and an even top_k (SP): the 2-unit tail
@@ -405,7 +420,7 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   const int F = U >> 2;
   const bool SP = MODE == MQ_DOWN && (U & 3) == 2 && (NM & 1) == 0;
   const int per_sp = (NM / 2) * (2 * F + 1);
-  const int nslots = ngb * NM * T;
+  const int nslots = ngb * NM * Tl;
   const int nitems = SP ? ngb * per_sp : nslots;
   const int rows_blk = ngb * QROWS;
   if (nitems == 0) return;  // (plans give every block a group; uniform per block)
@@ -429,13 +444,13 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
       c.t = k < F ? k : k < 2 * F ? k - F : F;
       c.pair = k == 2 * F;
     } else {
-      const int per = NM * T, gi = it / per, rem = it - gi * per;
+      const int per = NM * Tl, gi = it / per, rem = it - gi * per;
       c.lg = gi;
-      c.m = rem / T;
-      c.t = rem - c.m * T;
+      c.m = rem / Tl;
+      c.t = rem - c.m * Tl;
     }
     c.fg = b + c.lg * B;
-    c.slot = (c.lg * NM + c.m) * T + c.t;
+    c.slot = (c.lg * NM + c.m) * Tl + c.t;
     c.seg = 0;
     if constexpr (MODE == MQ_DENSE && NT == 1) {
 #pragma unroll
@@ -491,10 +506,10 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
         if (q >= 2) sg = s2;
       }
     }
-    const int g = sg.g;
-    const int nr = min(QROWS, sg.rows - QROWS * g), nq = lc.pair ? 2 : min(4, U - 4 * lc.t);
+    const int g = sg.g, tg = tq0 + lc.t;  // (the quad in the row)
+    const int nr = min(QROWS, sg.rows - QROWS * g), nq = lc.pair ? 2 : min(4, U - 4 * tg);
     const int ql = lc.pair ? (q & 1) : q;
-    const long base = (long)g * QROWS * U + (long)lc.t * 4 * nr;  // quad_item_unit
+    const long base = (long)g * QROWS * U + (long)tg * 4 * nr;  // quad_item_unit
     const bool live = r < nr && ql < nq && !idle;
     const int l = live ? nr * ql + r : 0;  // idle lanes re-read lane 0 (same lines)
     const uint8_t *bp = sg.body + base * (C * 16);
@@ -616,6 +631,9 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
   } else if constexpr (SRC == MV_SWIGLU) {
     XSwiGLU<K4> xs{a.in.xg, a.in.xu, a.k};
     stage_all(xs);
+  } else if (a.ksplit > 0) {  // this half's inputs
+    XPlain<K4> xs{a.in.x + 1024 * tq0, min(a.k, 1024 * (tq0 + Tl)) - 1024 * tq0};
+    stage_all(xs);
   } else {
     XPlain<K4> xs{a.in.x, a.k};
     stage_all(xs);
@@ -632,7 +650,7 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
     // lane group j (0..3) works on unit 4t + j of slot m, or for a tail pair
     // on unit 4F + (j & 1) of slot m + j / 2
     const int ql = cc.pair ? (q & 1) : q;
-    const int u = 4 * cc.t + ql;  // this lane's unit in its row
+    const int u = 4 * (tq0 + cc.t) + ql;  // this lane's unit in its row
     // staged unit of lane group j's input (down: in its slot's input)
     auto xunit = [&](int j) {
       const int m = cc.pair ? cc.m + (j >> 1) : cc.m;
@@ -652,7 +670,7 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
     v += __shfl_xor(v, 16, 64);
     if (!cc.pair) v += __shfl_xor(v, 32, 64);
     if (q == 0) S.part[cc.slot * QROWS + r] = v;
-    if (cc.pair && q == 2) S.part[(cc.slot + T) * QROWS + r] = v;  // slot m + 1, same quad
+    if (cc.pair && q == 2) S.part[(cc.slot + Tl) * QROWS + r] = v;  // slot m + 1, same quad
   };
   if constexpr (DEPTH == 3) {
     for (;;) {
@@ -692,8 +710,8 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
 #pragma unroll
       for (int m = 0; m < 2; m++) {
         float s = 0.f;
-        const float *pp = S.part + ((lg * 2 + m) * T) * QROWS + rr;
-        for (int t = 0; t < T; t++) s += pp[t * QROWS];
+        const float *pp = S.part + ((lg * 2 + m) * Tl) * QROWS + rr;
+        for (int t = 0; t < Tl; t++) s += pp[t * QROWS];
         v[m] = s;
       }
       mo.hbuf[(long)p * mo.f + row] = v[0] / (1.0f + expf(-v[0])) * v[1];
@@ -707,8 +725,8 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
       float out = 0.f;
       for (int m = 0; m < NM; m++) {
         float s = 0.f;
-        const float *pp = S.part + ((lg * NM + m) * T) * QROWS + rr;
-        for (int t = 0; t < T; t++) s += pp[t * QROWS];
+        const float *pp = S.part + ((lg * NM + m) * Tl) * QROWS + rr;
+        for (int t = 0; t < Tl; t++) s += pp[t * QROWS];
         out += mo.w[p * NM + m] * s;
       }
       mo.out[(long)p * mo.h + row] = out;
@@ -733,14 +751,14 @@ __device__ __forceinline__ void mvq_body(const MvArgs &a, const MoeArgs &mo) {
 #pragma unroll
     for (int m = 0; m < NT; m++) {
       float s = 0.f;
-      const float *pp = S.part + ((lg * NT + m) * T) * QROWS + rr;
-      for (int t = 0; t < T; t++) s += pp[t * QROWS];
+      const float *pp = S.part + ((lg * NT + m) * Tl) * QROWS + rr;
+      for (int t = 0; t < Tl; t++) s += pp[t * QROWS];
       v[m] = s * rscale;
     }
     float out = v[0];
     if constexpr (NT == 2) out = v[0] / (1.0f + expf(-v[0])) * v[1];
-    if (NT == 1 && a.in.res) out = a.in.res[row] + out;  // (one-matrix launches)
-    sg.y[row] = out;
+    if (NT == 1 && a.in.res && !h1) out = a.in.res[row] + out;  // (one-matrix launches)
+    (h1 ? a.in.y2 : sg.y)[row] = out;
     if (out > bv) {  // rows rise with lr: strict > keeps the first maximum; NaN never wins
       bv = out;
       bi = row;
@@ -796,8 +814,9 @@ hipError_t mvq_launch_o(const MvArgs &a, size_t lds, hipStream_t st) {
 // one staging pass when the input fits one (units <= NTH / 16)
 template <int FMT, bool K4, int SRC, int NT>
 hipError_t mvq_launch_t(const MvArgs &a, size_t lds, hipStream_t st) {
-  return a.units * 16 <= 64 * mvq_waves(FMT) ? mvq_launch_o<FMT, K4, SRC, NT, true>(a, lds, st)
-                                             : mvq_launch_o<FMT, K4, SRC, NT, false>(a, lds, st);
+  const int ux = a.ksplit > 0 ? std::max(4 * a.ksplit, a.units - 4 * a.ksplit) : a.units;
+  return ux * 16 <= 64 * mvq_waves(FMT) ? mvq_launch_o<FMT, K4, SRC, NT, true>(a, lds, st)
+                                        : mvq_launch_o<FMT, K4, SRC, NT, false>(a, lds, st);
 }
 
 template <int FMT>
@@ -842,6 +861,23 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
   }
   if (a.pair) a.seg[1].blk_begin = 0;
   a.groups = G;
+  a.ksplit = 0;
+  a.blocks0 = 0;
+  const int fmt = a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt;
+  const int T = (a.units + 3) / 4;
+  if (a.in.y2) {
+    // K split: half 0 takes quads [0, T / 2), half 1 the rest; the blocks
+    // (at most one per CU, at most G per half) go to the halves in
+    // proportion to their quads.
+    const int ts = T / 2, tot = std::max(2, std::min(2 * G, num_cus));
+    a.ksplit = ts;
+    a.blocks0 = std::max(1, std::min(G, (int)((long)tot * ts / T)));
+    const int b1 = std::max(1, std::min(G, tot - a.blocks0));
+    a.blocks = a.blocks0 + b1;
+    const int ngb = std::max((G + a.blocks0 - 1) / a.blocks0, (G + b1 - 1) / b1);
+    const int ux = std::max(4 * ts, a.units - 4 * ts), tl = std::max(ts, T - ts);
+    return qsmem_layout(aux_per_unit(fmt), ux, ngb * tl * QROWS, nullptr, nullptr);
+  }
   static const int bpc = [] {
     const char *e = getenv("GQ_MVQ_BLOCKS_PER_CU");  // tuning override
     return e && atoi(e) > 0 ? atoi(e) : 1;
@@ -869,8 +905,7 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
   a.blocks = std::min(a.blocks, maxb);
   // The fused argmax writes one partial per block into ARGMAX_SLOTS slots.
   if (a.in.amax_v) a.blocks = std::min(a.blocks, ARGMAX_SLOTS);
-  const int fmt = a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt;
-  const int ngb = (G + a.blocks - 1) / a.blocks, T = (a.units + 3) / 4;
+  const int ngb = (G + a.blocks - 1) / a.blocks;
   return qsmem_layout(aux_per_unit(fmt), a.units, ngb * nt * T * QROWS, nullptr, nullptr);
 }
 
@@ -950,6 +985,10 @@ hipError_t launch_mvq_moe(const MoeArgs &a, int T, int stage, bool route, hipStr
 hipError_t launch_mvq(const MvArgs &a, size_t lds, hipStream_t st) {
   if (lds + mvq_static_lds(a.fmt) > 160 * 1024) return hipErrorInvalidValue;
   if (a.in.amax_v && a.blocks > ARGMAX_SLOTS) return hipErrorInvalidValue;
+  // the split: one matrix, plain x, two quads per row, no argmax
+  if (a.in.y2 && (a.pair || a.nseg != 1 || a.in.src != MV_X || a.in.amax_v || !mv_ksplit_ok(a.units) ||
+                  a.ksplit <= 0))
+    return hipErrorInvalidValue;
   switch (a.fmt) {
   case T_Q4_K: return mvq_launch_f<T_Q4_K>(a, lds, st);
   case T_Q5_K: return a.in.q8k && !a.pair ? mvq_launch_f<T_Q5_K8>(a, lds, st) : mvq_launch_f<T_Q5_K>(a, lds, st);

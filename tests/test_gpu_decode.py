@@ -72,6 +72,30 @@ def test_decode_logits_small(backend, n_ctx):
         np.testing.assert_allclose(vf, ovf, rtol=2e-3, atol=1e-3)
 
 
+@pytest.mark.parametrize("ffn", [1792, 2560])
+def test_decode_split_down(backend, ffn):
+    """Down projections of 2 and 3 quads per row (7 and 10 units: a 3-unit
+    and a 2-unit tail quad) run with their K range split over two sets of
+    blocks, half 1's partial added by the next norm: every step's logits,
+    argmax and K/V rows as in test_decode_logits_small, 8 greedy tokens."""
+    cfg = dict(SMALL, ffn=ffn)
+    gm, om = _build(backend, cfg, seed=11, n_ctx=100, embd_scale=1e4)
+    toks = np.random.default_rng(ffn).integers(0, cfg["vocab"], 3)
+    for pos, token in zip(range(100, 103), toks):
+        ref = om.step(int(token), pos)
+        nxt, got = gm.decode(int(token), pos)
+        err = np.abs(got - ref).max()
+        assert err <= LOGIT_TOL * np.abs(ref).max(), (pos, err)
+        assert nxt == oracle.argmax(ref)
+    for l in range(cfg["n_layers"]):
+        k, v = gm.kv_download(l, 103)
+        for got_rows, ref_rows in ((k, om.kc[l, :103]), (v, om.vc[l, :103])):
+            np.testing.assert_allclose(got_rows.view(np.float16).astype(np.float32),
+                                       ref_rows.view(np.float16).astype(np.float32), rtol=2e-3, atol=1e-3)
+    gm2, om2 = _build(backend, cfg, seed=12, n_ctx=50, embd_scale=1e5)
+    np.testing.assert_array_equal(gm2.generate(7, 50, 8), _oracle_greedy(om2, 7, 50, 8))
+
+
 def test_generate_matches_oracle_and_decode(backend):
     cfg = SMALL
     gm, om = _build(backend, cfg, seed=5, n_ctx=200, embd_scale=1e5)
