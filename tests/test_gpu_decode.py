@@ -72,13 +72,14 @@ def test_decode_logits_small(backend, n_ctx):
         np.testing.assert_allclose(vf, ovf, rtol=2e-3, atol=1e-3)
 
 
-@pytest.mark.parametrize("ffn", [1792, 2560])
-def test_decode_split_down(backend, ffn):
+@pytest.mark.parametrize("ffn,down", [(1792, syn.Q6_K), (2560, syn.Q6_K), (2080, syn.Q8_0)])
+def test_decode_split_down(backend, ffn, down):
     """Down projections of 2 and 3 quads per row (7 and 10 units: a 3-unit
-    and a 2-unit tail quad) run with their K range split over two sets of
+    and a 2-unit tail quad; Q8_0 at 2080 inputs, 65 blocks: half 1 ends
+    inside its last unit) run with their K range split over two sets of
     blocks, half 1's partial added by the next norm: every step's logits,
     argmax and K/V rows as in test_decode_logits_small, 8 greedy tokens."""
-    cfg = dict(SMALL, ffn=ffn)
+    cfg = dict(SMALL, ffn=ffn, down_type=down)
     gm, om = _build(backend, cfg, seed=11, n_ctx=100, embd_scale=1e4)
     toks = np.random.default_rng(ffn).integers(0, cfg["vocab"], 3)
     for pos, token in zip(range(100, 103), toks):
