@@ -72,11 +72,13 @@ def test_decode_logits_small(backend, n_ctx):
         np.testing.assert_allclose(vf, ovf, rtol=2e-3, atol=1e-3)
 
 
-@pytest.mark.parametrize("ffn,down", [(1792, syn.Q6_K), (2560, syn.Q6_K), (2080, syn.Q8_0)])
+@pytest.mark.parametrize("ffn,down", [(1792, syn.Q6_K), (2560, syn.Q6_K), (2080, syn.Q8_0), (1792, syn.Q4_K),
+                                      (2560, syn.Q5_K)])
 def test_decode_split_down(backend, ffn, down):
     """Down projections of 2 and 3 quads per row (7 and 10 units: a 3-unit
     and a 2-unit tail quad; Q8_0 at 2080 inputs, 65 blocks: half 1 ends
-    inside its last unit) run with their K range split over two sets of
+    inside its last unit; Q4_K; Q5_K on the Q8_K route, quantized per unit
+    within each half) run with their K range split over two sets of
     blocks, half 1's partial added by the next norm: every step's logits,
     argmax and K/V rows as in test_decode_logits_small, 8 greedy tokens."""
     cfg = dict(SMALL, ffn=ffn, down_type=down)
