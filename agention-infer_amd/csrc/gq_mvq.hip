@@ -44,7 +44,10 @@
 // Work split: block b owns the row groups b, b + B, b + 2B, ... of the
 // launch (all segments' groups in a row); the waves take its items (group,
 // matrix, quad) in turn from an LDS counter.  Each lane keeps its next item
-// in flight while it computes the current one.
+// in flight while it computes the current one.  A one-matrix launch may
+// split K (MvIn::y2): two sets of blocks, each over all row groups, take the
+// first and the second half of every row's quads and stage only that half
+// of x; the second half's sums go to y2 for the caller to add.
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
