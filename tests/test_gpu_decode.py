@@ -384,3 +384,64 @@ def test_decode_q8_0_kv(backend, cfg_name, n_ctx):
         tok = oracle.argmax(om.step(tok, n_ctx + 3 + i))
         exp.append(tok)
     np.testing.assert_array_equal(got, np.array(exp, np.int32))
+
+
+@pytest.mark.parametrize("n_ctx,kv_dtype", [(8300, "f16"), (20000, "f16"), (20000, "q8_0")])
+def test_decode_long_context(backend, n_ctx, kv_dtype):
+    """Contexts past the merge kernel's first round of loads (8192
+    positions, 128 chunks) and past one chunk per merge thread (16384
+    positions): teacher-forced steps over an uploaded context against the
+    oracle (logits; the new K/V rows), then 6 greedy tokens.  Zero-mean
+    Q4_K rows, an N(0, 1) embedding and attention norms x0.1 keep the
+    scores O(1), so every cached row carries weight: on the oracle, zeroing
+    the rows past 8192 moves the first step's logits far beyond the
+    tolerance (at 20000 positions by 0.94 of their max; a 1e-6 change of
+    the embedding moves them by 1.3e-6)."""
+    import gq
+    import npref
+    cfg = dict(SMALL, ctx=n_ctx + 64, kv_dtype=kv_dtype)
+    w = syn.make_decoder(cfg, 41, centered=True)
+    w["attn_norm"] = [np.float32(0.1) * a for a in w["attn_norm"]]
+    q8 = kv_dtype == "q8_0"
+    if q8:
+        rng = np.random.default_rng(42)
+        kvd = cfg["n_kv_heads"] * cfg["head_dim"]
+        kv = [np.stack([npref.pack_q8_0_rows(rng.standard_normal((n_ctx, kvd)).astype(np.float32))
+                        .reshape(n_ctx, -1) for _ in range(cfg["n_layers"])]) for _ in range(2)]
+    else:
+        kv = syn.make_kv(cfg, n_ctx, 42)
+    hw = syn.upload_decoder(backend, cfg, w)
+    gm = gq.DecodeModel(dict(cfg, max_tokens=64), hw)
+    for l in range(cfg["n_layers"]):
+        gm.kv_upload(l, kv[0][l], kv[1][l])
+    om = oracle.DecoderModel(cfg, w, kv, kv_dtype=kv_dtype)
+    tol = 1e-3 if q8 else LOGIT_TOL
+    toks = np.random.default_rng(n_ctx).integers(0, cfg["vocab"], 3)
+    if not q8:  # the check depends on the rows past 8192
+        kz = [a.copy() for a in kv]
+        for a in kz:
+            a[:, 8192:] = 0
+        r0 = oracle.DecoderModel(cfg, w, kv).step(int(toks[0]), n_ctx)
+        rz = oracle.DecoderModel(cfg, w, kz).step(int(toks[0]), n_ctx)
+        assert np.abs(rz - r0).max() > 100 * tol * np.abs(r0).max()
+    for pos, token in zip(range(n_ctx, n_ctx + 3), toks):
+        ref = om.step(int(token), pos)
+        nxt, got = gm.decode(int(token), pos)
+        err = np.abs(got - ref).max()
+        assert err <= tol * np.abs(ref).max(), (pos, err)
+        assert nxt == oracle.argmax(ref)
+    for l in range(cfg["n_layers"]):
+        k, v = gm.kv_download(l, n_ctx + 3)
+        for got_rows, ref_rows in ((k, om.kc[l, :n_ctx + 3]), (v, om.vc[l, :n_ctx + 3])):
+            np.testing.assert_array_equal(got_rows[:n_ctx], ref_rows[:n_ctx])
+            if q8:
+                a = npref.unpack_q8_0_rows(got_rows[n_ctx:])
+                b = npref.unpack_q8_0_rows(ref_rows[n_ctx:])
+                step = np.repeat(np.abs(b).reshape(3, -1, 32).max(axis=2) / 127.0, 32, axis=1)
+                assert np.all(np.abs(a - b) <= 1.01 * step + 1e-30)
+            else:
+                np.testing.assert_allclose(got_rows[n_ctx:].view(np.float16).astype(np.float32),
+                                           ref_rows[n_ctx:].view(np.float16).astype(np.float32),
+                                           rtol=2e-3, atol=1e-3)
+    got = gm.generate(int(toks[-1]), n_ctx + 3, 6)
+    np.testing.assert_array_equal(got, _oracle_greedy(om, int(toks[-1]), n_ctx + 3, 6))
