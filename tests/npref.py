@@ -179,9 +179,21 @@ def quantize_row_q8_k(x):
     return d, qs.reshape(-1), bs.astype(np.int16)
 
 
+def rope_angles(pos, theta, hd):
+    """RoPE angles as cpu_path.rs:99-133 forms them, in f32: pos as f32
+    divided by powf(theta, 2i/hd) (so at large positions they carry the f32
+    rounding of pos / den, ~1e-3 rad at 20000); the sin / cos that follow
+    are taken in float64.  pos: int or int array; returns float64 [..., hd/2]."""
+    i = np.arange(hd // 2, dtype=np.float32)
+    den = np.power(np.float32(theta), (np.float32(2.0) * i) / np.float32(hd)).astype(np.float32)
+    p = np.asarray(pos, np.float32)[..., None]
+    return (p / den).astype(np.float32).astype(np.float64)
+
+
 def decode_step(cfg, w, kc, vc, token, pos):
     """One decode step of a dense Llama/Qwen2 decoder in float64, written
-    from the model's definition (RMSNorm, NEOX RoPE with theta^(2i/hd),
+    from the model's definition (RMSNorm, NEOX RoPE with theta^(2i/hd) and
+    f32 angles (rope_angles),
     causal softmax attention with grouped KV heads, SwiGLU FFN, residual
     adds), with the weights dequantized by the numpy block decoders above.
     kc / vc: float16 bit arrays [n_layers][ctx][kv_dim], updated at pos
@@ -200,7 +212,7 @@ def decode_step(cfg, w, kc, vc, token, pos):
         return g * x / np.sqrt(np.mean(x * x) + cfg["eps"])
 
     i = np.arange(half)
-    ang = pos / np.power(float(cfg["theta"]), 2.0 * i / hd)
+    ang = rope_angles(pos, cfg["theta"], hd)
     cs, sn = np.cos(ang), np.sin(ang)
 
     def rope(v):  # v [heads, hd]
@@ -253,7 +265,7 @@ def prefill_bf16(cfg, w, kc, vc, tokens, pos0, kv="f16"):
     once) in float64 with the GPU prefill's operand rounding at each
     projection: weights rounded to bf16 from their fp32 dequant, the
     activations entering a projection (normed x, attention output,
-    silu(g) * u) rounded to fp32 and then to bf16.  RoPE, the f16 K/V cache,
+    silu(g) * u) rounded to fp32 and then to bf16.  RoPE (f32 angles, rope_angles), the f16 K/V cache,
     the causal softmax and the residual adds stay float64; the output head
     is unrounded (the GPU runs it on the matvec).  kc / vc are updated.
     kv="q8_0": kc / vc hold KvDtype::Q8_0 rows ([layer][ctx][kv_dim/32*34]
@@ -281,7 +293,7 @@ def prefill_bf16(cfg, w, kc, vc, tokens, pos0, kv="f16"):
 
     pos = pos0 + np.arange(n)
     i = np.arange(half)
-    ang = pos[:, None] / np.power(float(cfg["theta"]), 2.0 * i / hd)[None, :]
+    ang = rope_angles(pos, cfg["theta"], hd)
     cs, sn = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
 
     def rope(v):  # v [n, heads, hd]

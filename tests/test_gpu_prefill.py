@@ -80,7 +80,7 @@ MIXES = {"Q4_K_M": {}, "Q8_0": dict(attn_type=syn.Q8_0, gate_up_type=syn.Q8_0, d
 CASES = [("SMALL", 0, 37, "Q4_K_M"), ("SMALL", 100, 64, "Q4_K_M"), ("HD128", 70, 130, "Q4_K_M"),
          ("SMALL", 5, 600, "Q4_K_M"), ("HD128", 0, 300, "Q4_K_M"), ("SMALL", 100, 64, "Q8_0"),
          ("SMALL", 5, 600, "Q8_0"), ("HD128", 70, 300, "Q8_0"), ("SMALL", 30, 200, "Q5_K_M"),
-         ("HD128", 0, 130, "Q5_K_M")]
+         ("HD128", 0, 130, "Q5_K_M"), ("SMALL", 20000, 64, "Q4_K_M"), ("HD128", 9000, 130, "Q4_K_M")]
 # Embedding scale of the same-rounding models.  The all-Q8_0 decoders (zero-
 # mean rows, no per-block bias to dominate the residual) are ill-conditioned
 # at an N(0, 1) embedding: a 1e-7 relative change of the embedding moves the
@@ -93,8 +93,10 @@ MIX_EMBD = {"Q4_K_M": 1.0, "Q5_K_M": 1.0, "Q8_0": 100.0}
 @pytest.mark.parametrize("cfg_name,n_ctx,n,mix", CASES)
 def test_prefill_same_rounding(backend, cfg_name, n_ctx, n, mix):
     """Logits and every K/V row written against npref.prefill_bf16; the
-    rows before the prompt are untouched.  n = 600 takes two passes."""
+    rows before the prompt are untouched.  n = 600 takes two passes; 20000
+    and 9000 cached positions run the attention over long key ranges."""
     cfg = dict({"SMALL": SMALL, "HD128": HD128}[cfg_name], **MIXES[mix])
+    cfg["ctx"] = max(cfg["ctx"], n_ctx + n + 8)
     say(f"prefill {cfg_name} ({mix}) n_ctx={n_ctx} n={n}")
     gm, w, kv, kc, vc = _build(backend, cfg, seed=11 + n, n_ctx=n_ctx, attn_scale=ATTN_SCALE,
                                embd_scale=MIX_EMBD[mix])
