@@ -59,8 +59,11 @@ def run(backend, orc, E, H, F, T, k, seed, check_tokens=None, weights=None):
 # take the quad layout and the MFMA kernels, others the wave-tiled layout
 # and the v_dot4 kernels; the last three shapes mix the two.
 @pytest.mark.parametrize("E,H,F,T,k", [(16, 512, 256, 3, 4), (8, 256, 768, 5, 2), (4, 1024, 512, 1, 4),
-                                       (4, 200, 40, 2, 2), (4, 208, 40, 3, 2), (4, 200, 48, 2, 3)])
+                                       (4, 200, 40, 2, 2), (4, 208, 40, 3, 2), (4, 200, 48, 2, 3),
+                                       (64, 512, 256, 48, 8), (1100, 256, 32, 6, 4)])
 def test_moe_small(backend, orc, E, H, F, T, k):
+    """(The last two: 384 (token, slot) pairs, more than one block each
+    would fill the GPU with; 1100 experts, routed by the router kernel.)"""
     say(f"moe small E={E} H={H} F={F} T={T} k={k}")
     run(backend, orc, E, H, F, T, k, seed=E + H + T)
 
