@@ -75,39 +75,53 @@ constexpr int NORM_GROUPS = 4;
 // partials part[s][t][c] (s < ksplit) unreduced: x[t] += part[0][t] +
 // part[1][t] + ... (in that order, as k_gemm_reduce) is done here, and the
 // new row is stored back to x.
-__global__ __launch_bounds__(256) void k_norm_to_frag(float *x, const float *w, int n, int H,
-                                                      int kpad, float eps, uint16_t *xb,
-                                                      const float *part, int ksplit) {
+__global__ __launch_bounds__(256) void k_norm_to_frag(float *__restrict__ x, const float *__restrict__ w, int n,
+                                                      int H, int kpad, float eps, uint16_t *__restrict__ xb,
+                                                      const float *__restrict__ part, int ksplit) {
   __shared__ float red[4];
   const int t = blockIdx.x, ksteps = kpad / 32;
   float *xt = x + (long)t * H;
   float v[NORM_GROUPS][8];
-  float ss = 0.f;
+  bool in[NORM_GROUPS];
+  // every group's row loads first, then each split's partials for all
+  // groups (loads in flight together, not one group's chain after another)
 #pragma unroll
   for (int j = 0; j < NORM_GROUPS; j++) {
     const int c = 8 * (threadIdx.x + 256 * j);
-    if (t < n && c < H) {
-      float4 a = *(const float4 *)(xt + c), b = *(const float4 *)(xt + c + 4);
-      if (ksplit > 0) {
-        const long cnt = (long)n * H;
-        for (int k = 0; k < ksplit; k++) {
-          const float *pp = part + k * cnt + (long)t * H + c;
-          const float4 pa = *(const float4 *)pp, pb = *(const float4 *)(pp + 4);
-          a.x += pa.x; a.y += pa.y; a.z += pa.z; a.w += pa.w;
-          b.x += pb.x; b.y += pb.y; b.z += pb.z; b.w += pb.w;
-        }
-        *(float4 *)(xt + c) = a;
-        *(float4 *)(xt + c + 4) = b;
-      }
-      v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
-      v[j][4] = b.x; v[j][5] = b.y; v[j][6] = b.z; v[j][7] = b.w;
-    } else {
+    in[j] = t < n && c < H;
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (in[j]) {
+      a = *(const float4 *)(xt + c);
+      b = *(const float4 *)(xt + c + 4);
+    }
+    v[j][0] = a.x; v[j][1] = a.y; v[j][2] = a.z; v[j][3] = a.w;
+    v[j][4] = b.x; v[j][5] = b.y; v[j][6] = b.z; v[j][7] = b.w;
+  }
+  if (ksplit > 0) {
+    const long cnt = (long)n * H;
+    for (int k = 0; k < ksplit; k++) {
 #pragma unroll
-      for (int e = 0; e < 8; e++) v[j][e] = 0.f;
+      for (int j = 0; j < NORM_GROUPS; j++) {
+        if (!in[j]) continue;
+        const float *pp = part + k * cnt + (long)t * H + 8 * (threadIdx.x + 256 * j);
+        const float4 pa = *(const float4 *)pp, pb = *(const float4 *)(pp + 4);
+        v[j][0] += pa.x; v[j][1] += pa.y; v[j][2] += pa.z; v[j][3] += pa.w;
+        v[j][4] += pb.x; v[j][5] += pb.y; v[j][6] += pb.z; v[j][7] += pb.w;
+      }
     }
 #pragma unroll
-    for (int e = 0; e < 8; e++) ss += v[j][e] * v[j][e];
+    for (int j = 0; j < NORM_GROUPS; j++) {
+      if (!in[j]) continue;
+      const int c = 8 * (threadIdx.x + 256 * j);
+      *(float4 *)(xt + c) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+      *(float4 *)(xt + c + 4) = make_float4(v[j][4], v[j][5], v[j][6], v[j][7]);
+    }
   }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NORM_GROUPS; j++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) ss += v[j][e] * v[j][e];
   ss = block_sum256(ss, red);
   const float rms = sqrtf(ss / (float)H + eps);
 #pragma unroll
