@@ -1006,6 +1006,7 @@ int gq_model_prefill(gq_model *m, const int *tokens_host, int n, int pos, float 
     if (!rc) rc = dalloc(m, &m->pf.u, np * L.ffn);
     if (!rc) rc = dalloc(m, &m->pf.part, std::max<size_t>(1, gq::prefill_part_floats(L, gq::PREFILL_MAX, g_dev.num_cus)));
     if (!rc) rc = dalloc(m, &m->pf.xb, (size_t)gq::GEMM_NPAD * kmax);
+    if (!rc) rc = dalloc(m, &m->pf.xh, (size_t)gq::GEMM_NPAD * ((L.ffn + 255) / 256 * 256));
     if (!rc) rc = dalloc(m, &m->pf.tokens, np);
     if (!rc && L.kv_q8) rc = dalloc(m, &m->pf.kf, (size_t)L.ctx * kvd);
     if (!rc && L.kv_q8) rc = dalloc(m, &m->pf.vf, (size_t)L.ctx * kvd);

@@ -679,7 +679,9 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
 #pragma unroll
   for (int i = 1; i < GEMM_MAX_SEG; i++)
     if (i < a.nseg && tile >= a.seg[i].tile_begin) sg = a.seg[i];
-  const int m0 = (tile - sg.tile_begin) * TBM, n0 = ntile * TBN, rows = sg.rows;
+  // pair: tile rows 0-79 are gate rows m0 .. m0 + 79, 80-159 the same up rows
+  const bool pair = a.pair != 0;
+  const int m0 = (tile - sg.tile_begin) * (pair ? TBM / 2 : TBM), n0 = ntile * TBN, rows = sg.rows;
   const int stages_all = a.kpad / BK;
   const int s0 = (int)((long)stages_all * split / a.ksplit);
   const int stages = (int)((long)stages_all * (split + 1) / a.ksplit) - s0, last = stages - 1;
@@ -687,6 +689,10 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
 
   if (wave >= 4) {
     const int pw = wave - 4;
+    // matrix row of this wave's tile row PROWS * pw + rr (pair: waves 6-7
+    // hold the up rows)
+    const int mrow0 = m0 + PROWS * (pair ? (pw & 1) : pw);
+    const uint8_t *rec = pair && pw >= 2 ? a.seg[1].rec : sg.rec;
     // W chunk slots of this wave: q = 64 i + lane (q < WSLOTS): row
     // PROWS * pw + q / C, chunk q % C of the stage record.
     const uint8_t *wsrc[WINS];
@@ -694,8 +700,8 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < WINS; i++) {
       const int q = min(64 * i + lane, WSLOTS - 1);
-      const int row = min(m0 + PROWS * pw + q / C, rows - 1);
-      wsrc[i] = sg.rec + (long)row * row_stride;
+      const int row = min(mrow0 + q / C, rows - 1);
+      wsrc[i] = rec + (long)row * row_stride;
       wc[i] = q % C;
     }
     auto issue_w = [&](int s) {  // this wave's rows of local stage s (clamped) into slot s % WR
@@ -748,7 +754,7 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
         if (round < R::ROUNDS - 1 || t < R::TASKS) {
           const int rr = t >> 2, h = (t >> 1) & 1, qq = t & 1;
           const int r = PROWS * pw + rr;
-          const bool ok = m0 + r < rows;
+          const bool ok = mrow0 + rr < rows;
           const uint32_t qw[4] = {qs[round].x, qs[round].y, qs[round].z, qs[round].w};
           const uint32_t sh = 4u * (uint32_t)h;
           uint32_t o[8];
@@ -871,6 +877,28 @@ __global__ __launch_bounds__(512) void k_gemm_bf16_direct(GemmArgs a) {
     __builtin_amdgcn_s_barrier();
   }
   // D layout: lane holds rows 4*(lane/16)+r (weight rows) of column lane%16 (token).
+  if (pair) {  // h = silu(g) * u (ffn_gate_up, cpu_path.rs:225-227) as bf16 fragments
+    const int hks = a.hkpad / 32;
+#pragma unroll
+    for (int i = 0; i < AT_ / 2; i++) {
+      const int m = m0 + 16 * i + 4 * (lane >> 4);
+      if (m >= a.hkpad) continue;
+#pragma unroll
+      for (int jn = 0; jn < 4; jn++) {
+        const int t = n0 + 64 * wave + 16 * jn + (lane & 15);
+        float h[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float g = acc[i][jn][r], u = acc[i + AT_ / 2][jn][r];
+          h[r] = t < a.n && m + r < rows ? g / (1.0f + expf(-g)) * u : 0.f;
+        }
+        // columns m .. m + 3 of token t: half of a fragment slot of 8
+        uint16_t *dst = a.hb + (((long)(t >> 4) * hks + (m >> 5)) * 64 + (t & 15) + 16 * ((m & 31) >> 3)) * 8 + (m & 7);
+        *(uint2 *)dst = make_uint2(f2bf(h[0]) | (f2bf(h[1]) << 16), f2bf(h[2]) | (f2bf(h[3]) << 16));
+      }
+    }
+    return;
+  }
   float *Y = a.ksplit > 1 ? sg.part + (long)split * a.n * rows : sg.y;
 #pragma unroll
   for (int i = 0; i < AT_; i++) {
@@ -1471,6 +1499,43 @@ hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int co
   }
   r.blk0[count] = blocks;
   hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)blocks), dim3(256), 0, st, r, p.ksplit, add ? 1 : 0);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_bf16_swiglu(const gq_weight *gate, const gq_weight *up, const uint16_t *xb, int n,
+                                   uint16_t *hb, int num_cus, hipStream_t st) {
+  (void)num_cus;
+  if (n <= 128) return hipErrorNotSupported;  // the ring kernel's batches
+  const Layout &L = gate->L;
+  if (up->L.dtype != L.dtype || up->L.units != L.units || up->L.rows != L.rows || !gate->gemm_raw ||
+      !up->gemm_raw)
+    return hipErrorNotSupported;
+  if (L.dtype != T_Q4_K && L.dtype != T_Q6_K && L.dtype != T_Q5_K && L.dtype != T_Q8_0)
+    return hipErrorNotSupported;
+  GemmArgs a{};
+  a.nseg = 1;
+  a.ntiles = (n + BN - 1) / BN;
+  a.ksplit = 1;
+  a.n = n;
+  a.kpad = L.units * 256;
+  a.xb = xb;
+  a.pair = 1;
+  a.hkpad = (L.rows + 255) / 256 * 256;
+  a.hb = hb;
+  a.seg[0].rec = gate->gemm_raw;
+  a.seg[0].rows = L.rows;
+  a.seg[0].tile_begin = 0;
+  a.seg[1].rec = up->gemm_raw;
+  a.seg[1].rows = L.rows;
+  // 80 output rows per tile, over every padded column of hb (rows past F
+  // give zeros)
+  const long nb = (long)((a.hkpad + BM / 2 - 1) / (BM / 2)) * a.ntiles;
+  if (nb > 0x7fffffffL) return hipErrorInvalidValue;
+  void (*kern)(GemmArgs) = L.dtype == T_Q4_K   ? k_gemm_bf16_direct<T_Q4_K>
+                           : L.dtype == T_Q6_K ? k_gemm_bf16_direct<T_Q6_K>
+                           : L.dtype == T_Q5_K ? k_gemm_bf16_direct<T_Q5_K>
+                                               : k_gemm_bf16_direct<T_Q8_0>;
+  hipLaunchKernelGGL(kern, dim3((unsigned)nb), dim3(512), 0, st, a);
   return hipGetLastError();
 }
 

@@ -173,6 +173,7 @@ struct PrefillBufs {
   float *q, *k, *v, *g, *u;
   float *part;     // GEMM K-split partials (prefill_part_floats)
   uint16_t *xb;    // GEMM X fragments [512][max(hidden, ffn, q_dim) rounded to 256] bf16
+  uint16_t *xh;    // the down GEMM's X from the fused gate/up epilogue [512][ffn rounded to 256]
   int *tokens;     // [PREFILL_MAX]
   uint16_t *kf, *vf;  // Q8_0 KV cache: one layer's rows unpacked to f16 [ctx][kv_dim]
 };
@@ -232,6 +233,12 @@ struct GemmArgs {
   GemmSeg seg[GEMM_MAX_SEG];
   int nseg, ntiles, ksplit, n, kpad;
   const uint16_t *xb;  // X as bf16 MFMA fragments [npad/16][kpad/32][64 lanes][8]
+  // pair (direct kernel, no K split): seg[0] = gate, seg[1] = up of one
+  // shape; a block tile holds 80 rows of each, and the epilogue writes
+  // silu(gate . x) * (up . x) as bf16 fragments hb (the next GEMM's X, hkpad
+  // columns) instead of Y.
+  int pair, hkpad;
+  uint16_t *hb;
 };
 // X fragments must cover n rounded up to GEMM_NPAD (a multiple of the
 // 256-token tile).
@@ -247,6 +254,13 @@ int gemm_ksplit(int tiles, int stages, int num_cus);
 hipError_t launch_gemm_bf16(const gq_weight *const *ws, float *const *ys, int count,
                             const uint16_t *xb, int n, float *part, bool add, int num_cus,
                             hipStream_t st, int *defer = nullptr);
+// The gate/up pair of the SwiGLU on the direct kernel: hb = bf16 fragments
+// of silu(gate . X) * (up . X) ([npad/16][round_up(F, 256)/32][64][8], the
+// next GEMM's X; zero past n and F).  hipErrorNotSupported when the batch
+// takes the ring kernel (n <= 128) or the two differ in type or shape: the
+// caller then runs launch_gemm_bf16 and its own SwiGLU.
+hipError_t launch_gemm_bf16_swiglu(const gq_weight *gate, const gq_weight *up, const uint16_t *xb, int n,
+                                   uint16_t *hb, int num_cus, hipStream_t st);
 size_t gemm_part_floats(const gq_weight *const *ws, int count, int n, int num_cus, bool add);
 // X fp32 [n][k] -> bf16 fragments (kpad = k rounded up to 256, npad = n
 // rounded up to GEMM_NPAD, zero padding).

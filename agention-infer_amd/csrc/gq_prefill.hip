@@ -661,14 +661,25 @@ hipError_t launch_prefill(const DecodeLaunch &m, const PrefillBufs &b, const int
     hipLaunchKernelGGL(k_norm_to_frag, dim3(npad), dim3(256), 0, s, b.x, m.ffn_norm[L], n, H,
                        round_up(H, 256), m.eps, b.xb, b.part, pending);
     pending = 0;
-    const gq_weight *gu[2] = {m.wgate[L], m.wup[L]};
-    float *guo[2] = {b.g, b.u};
-    if ((e = launch_gemm_bf16(gu, guo, 2, b.xb, n, b.part, false, num_cus, s)) != hipSuccess) return e;
-    const int kpf = round_up(F, 256);
-    hipLaunchKernelGGL(k_swiglu_to_frag, dim3((int)(((long)npad / 16 * (kpf / 32) + 3) / 4)), dim3(256), 0,
-                       s, b.g, b.u, n, F, npad, kpf, b.xb);
+    // h = silu(gate . xn) * (up . xn) as the down GEMM's X: in the gate/up
+    // GEMM's epilogue (into xh: other blocks are still reading xb), or,
+    // for batches on the ring kernel and mixed gate/up types, g and u
+    // then k_swiglu_to_frag
+    const uint16_t *hx = b.xh;
+    e = launch_gemm_bf16_swiglu(m.wgate[L], m.wup[L], b.xb, n, b.xh, num_cus, s);
+    if (e == hipErrorNotSupported) {
+      const gq_weight *gu[2] = {m.wgate[L], m.wup[L]};
+      float *guo[2] = {b.g, b.u};
+      if ((e = launch_gemm_bf16(gu, guo, 2, b.xb, n, b.part, false, num_cus, s)) != hipSuccess) return e;
+      const int kpf = round_up(F, 256);
+      hipLaunchKernelGGL(k_swiglu_to_frag, dim3((int)(((long)npad / 16 * (kpf / 32) + 3) / 4)), dim3(256), 0,
+                         s, b.g, b.u, n, F, npad, kpf, b.xb);
+      hx = b.xb;
+    } else if (e != hipSuccess) {
+      return e;
+    }
     // (the next layer's norm does the reduction; the head reads x itself)
-    if ((e = launch_gemm_bf16(&m.wdown[L], xo, 1, b.xb, n, b.part, true, num_cus, s,
+    if ((e = launch_gemm_bf16(&m.wdown[L], xo, 1, hx, n, b.part, true, num_cus, s,
                               L + 1 < m.n_layers ? &pending : nullptr)) != hipSuccess)
       return e;
   }
