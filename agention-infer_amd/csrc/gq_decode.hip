@@ -557,7 +557,7 @@ hipError_t launch_decode_step(const DecodeLaunch &m, hipStream_t s) {
     // layers store x_c = x_b + proj from the previous down launch's halves,
     // or read x_b = x_a + down when it did not split)
     const bool split_in = L && mv_ksplit_ok(m.wdown[L - 1]->L.units);
-    float *xres = !L ? m.xb : split_in ? m.xc : m.xb;  // the stream the o projection adds to
+    float *xres = split_in ? m.xc : m.xb;  // the stream the o projection adds to
     in.x = L ? m.xb : m.embd;
     in.r = split_in ? m.proj : nullptr;
     in.tok = L ? nullptr : &m.state->token;
