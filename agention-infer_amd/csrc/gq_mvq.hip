@@ -901,6 +901,13 @@ size_t mvq_plan(MvArgs &a, int num_cus) {
     const int nw = mvq_waves(a.fmt == T_Q5_K && a.in.q8k && !a.pair ? T_Q5_K8 : a.fmt);
     a.blocks = (int)std::max(1L, std::min((long)a.blocks, (items + nw - 1) / nw));
   }
+  // Even split: as few blocks as give the same largest number of row groups
+  // per block (gate/up, 2368 groups: 237 blocks of 10 instead of 256 of 9 or
+  // 10; measured 15.3 against 15.6-15.8 us).
+  {
+    const int gpb = (G + a.blocks - 1) / a.blocks;
+    a.blocks = (G + gpb - 1) / gpb;
+  }
   static const int maxb = [] {
     const char *e = getenv("GQ_MVQ_MAX_BLOCKS");  // tuning override: at most this many blocks
     return e && atoi(e) > 0 ? atoi(e) : 1 << 30;
