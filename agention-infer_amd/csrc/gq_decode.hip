@@ -391,14 +391,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_gqa(
 }
 
 // Merge of the chunk partials: block (h, y) = query head h, dims
-// 32 y .. 32 y + 31, 256 threads; thread (qq, d) (qq < MQ = 8) sums dim d
+// 16 y .. 16 y + 15, 256 threads; thread (qq, d) (qq < MQ = 16) sums dim d
 // over the chunks c = qq, qq + MQ, ..., then the MQ partial sums are added
-// in order (small blocks: a head's dims spread over HD / 32 of them):
+// in order (small blocks: a head's dims spread over HD / 16 of them; 16
+// dims per block measured 0.15% faster decode than 32):
 //   att[h][d] = sum_c o_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M),
 // M = max_c m_c over the chunks holding positions <= pos.  Every load of
-// the first 16 * MQ chunks (m, l and o: 8192 positions) is issued at the
+// the first 16 * MQ chunks (m, l and o: 16384 positions) is issued at the
 // start; every block of a head computes the head's M and L.
-constexpr int ATT_MERGE_THREADS = 256, ATT_MERGE_DIMS = 32;
+constexpr int ATT_MERGE_THREADS = 256, ATT_MERGE_DIMS = 16;
 template <int HD>
 __global__ __launch_bounds__(ATT_MERGE_THREADS) void k_attn_merge(const DecodeState *st, int nchunk_grid,
                                                              const float *part, float *att) {
